@@ -1,0 +1,186 @@
+/*
+ * diffrast_mi355x: differentiable rasterization for AMD Instinct MI355X
+ * (gfx950).  C ABI of libdiffrast_mi355x.so.
+ *
+ * One entry point per custom-VJP half of the reference's public ops
+ * (mnmly/mlx-swift-diffrast, the Swift files under Sources/MLXDiffRast).  Each replaces
+ * the Forward or VJP closure of one `CustomFunction` together with the
+ * `MLXFast.metalKernel` dispatchers that closure calls:
+ *
+ *   dr_rasterize_fwd     Rasterize.swift:104-108, 123-128  (:823-894)
+ *   dr_rasterize_bwd     Rasterize.swift:109-118, 129-139  (:850-866)
+ *   dr_interpolate_fwd   Interpolate.swift:82-85, 113-119  (:475-500)
+ *   dr_interpolate_bwd   Interpolate.swift:86-91, 120-127  (:502-541)
+ *   dr_texture_mip_*     Texture.swift:144-161, 287-307
+ *   dr_texture_fwd       Texture.swift:187-191, 222-227, 255-260, 309-315
+ *   dr_texture_bwd       Texture.swift:192-199, 229-236, 261-267, 316-324
+ *   dr_antialias_topology Antialias.swift:19-66
+ *   dr_antialias_fwd     Antialias.swift:112-117  (:556-568)
+ *   dr_antialias_bwd     Antialias.swift:118-128  (:570-600)
+ *
+ * Conventions
+ *   - All tensors are device memory (hipMalloc'd), fp32 or int32, row-major,
+ *     channels last, in the reference's layouts:
+ *       pos [N,V,4] clip space (x*w, y*w, z*w, w) or shared [V,4];
+ *       tri [T,3]; rast / rast_db [N,H,W,4] = (u, v, z/w, tri_id+1) and
+ *       (du/dx, du/dy, dv/dx, dv/dy); pixel (h=0, w=0) is the top-left.
+ *   - A "batch stride" argument is the element distance between consecutive
+ *     batch entries of a tensor; 0 means one tensor shared by every batch
+ *     entry (the reference's N-broadcast, without materialising it).
+ *   - The caller allocates every input and output.  Gradient outputs that
+ *     are accumulated by scatter-add are zero-filled by the library first,
+ *     unless DR_ACCUMULATE is set in `flags`, in which case the library adds
+ *     into what the buffer holds.
+ *   - Work is enqueued asynchronously on `stream` (a hipStream_t; NULL is the
+ *     default stream) of the current HIP device.  Internal scratch is kept
+ *     per (device, stream); calls on different streams may overlap.
+ *   - Every call returns DR_OK or an error code and never throws; the message
+ *     of the last error on the calling thread is dr_get_last_error().
+ *   - Host-memory arguments are named *_host; everything else is device
+ *     memory.
+ */
+#ifndef DIFFRAST_MI355X_H
+#define DIFFRAST_MI355X_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DR_ABI_VERSION 1
+
+typedef void* dr_stream_t; /* hipStream_t */
+
+enum {
+  DR_OK = 0,
+  DR_ERR_ARGUMENT = 1, /* a shape or argument precondition failed */
+  DR_ERR_HIP = 2,      /* a HIP runtime call failed */
+  DR_ERR_MEMORY = 3    /* scratch allocation failed */
+};
+
+enum { DR_ACCUMULATE = 1u };
+
+/* Texture.swift:8-17 (BoundaryMode) */
+enum { DR_BOUNDARY_WRAP = 0, DR_BOUNDARY_CLAMP = 1, DR_BOUNDARY_ZERO = 2, DR_BOUNDARY_CUBE = 3 };
+/* Texture.swift:35-40 (FilterMode) */
+enum {
+  DR_FILTER_NEAREST = 0,
+  DR_FILTER_LINEAR = 1,
+  DR_FILTER_LINEAR_MIPMAP_NEAREST = 2,
+  DR_FILTER_LINEAR_MIPMAP_LINEAR = 3
+};
+
+int dr_abi_version(void);
+const char* dr_get_last_error(void);
+/* Frees the scratch memory held for the current device (all streams). */
+int dr_release_scratch(void);
+
+/* ---- rasterize ------------------------------------------------------- */
+
+/* Forward of DiffRast.rasterize (Rasterize.swift:44-144).
+ *   pos_batch_stride: V*4 for instanced pos [N,V,4]; 0 for range mode
+ *     (shared pos [V,4]).
+ *   ranges_host: NULL (every image draws triangles [0,T)), or a host array
+ *     [N,2] of (first triangle, triangle count) per image (range mode).
+ *   peel: NULL, or the rast [N,H,W,4] of the previous layer (depth peeling:
+ *     only depths greater than that layer's are kept).
+ *   rast_db: NULL for gradDB = false.
+ * Unlike the reference, the per-tile triangle lists never overflow (the
+ * reference drops triangles beyond 128 per 16x16 tile), and equal depths
+ * resolve to the lowest triangle index. */
+int dr_rasterize_fwd(const float* pos, int64_t pos_batch_stride, const int32_t* tri,
+                     const int32_t* ranges_host, const float* peel, int N, int V, int T,
+                     int H, int W, float* rast, float* rast_db, dr_stream_t stream);
+
+/* VJP of DiffRast.rasterize: d_pos (same layout and batch stride as pos;
+ * range mode accumulates all images into the shared [V,4]).  d_rast_db may
+ * be NULL (gradDB = false). */
+int dr_rasterize_bwd(const float* pos, int64_t pos_batch_stride, const int32_t* tri,
+                     const float* rast, const float* d_rast, const float* d_rast_db, int N,
+                     int V, int H, int W, float* d_pos, unsigned flags, dr_stream_t stream);
+
+/* ---- interpolate ----------------------------------------------------- */
+
+/* Forward of DiffRast.interpolate (Interpolate.swift:43-132).
+ *   attr [N,V,A] (attr_batch_stride = V*A) or shared [V,A] (stride 0).
+ *   K = 0: basic path (rast_db, diff_idx, out_da unused).
+ *   K > 0: DA path; diff_idx [K] device int32, or NULL for all attributes
+ *     (then K must equal A); out_da [N,H,W,2K]. */
+int dr_interpolate_fwd(const float* attr, int64_t attr_batch_stride, const float* rast,
+                       const float* rast_db, const int32_t* tri, const int32_t* diff_idx,
+                       int K, int N, int H, int W, int V, int A, float* out, float* out_da,
+                       dr_stream_t stream);
+
+/* VJP of DiffRast.interpolate: d_attr (layout/stride d_attr_batch_stride,
+ * 0 = accumulate every image into one [V,A]), d_rast [N,H,W,4] (channels 2,3
+ * are zero), d_rast_db [N,H,W,4] (DA path only, may be NULL). */
+int dr_interpolate_bwd(const float* attr, int64_t attr_batch_stride, const float* rast,
+                       const float* rast_db, const int32_t* tri, const int32_t* diff_idx,
+                       int K, const float* d_out, const float* d_out_da, int N, int H, int W,
+                       int V, int A, float* d_attr, int64_t d_attr_batch_stride, float* d_rast,
+                       float* d_rast_db, unsigned flags, dr_stream_t stream);
+
+/* ---- texture --------------------------------------------------------- */
+
+/* textureConstructMip (Texture.swift:144-161): number of levels (level 0
+ * included) of the 2x2 box pyramid of an [*, H, W, *] texture, capped at
+ * max_level + 1 when max_level >= 0.  Writes each level's H/W (up to 32). */
+int dr_texture_mip_levels(int H, int W, int max_level, int32_t* level_h_host,
+                          int32_t* level_w_host);
+/* Floats needed for levels 1..L-1 of Nt textures (level 0 is the texture). */
+int64_t dr_texture_mip_size(int Nt, int H, int W, int C, int L);
+/* Builds levels 1..L-1 of Nt textures into `pyramid`, level-major:
+ * level k holds [Nt, Hk, Wk, C] starting after levels 1..k-1. */
+int dr_texture_build_mip(const float* tex, int Nt, int H, int W, int C, int L, float* pyramid,
+                         dr_stream_t stream);
+
+/* Forward of DiffRast.texture (Texture.swift:62-131).
+ *   tex: [Nt, Ht, Wt, C], or [Nt, 6, Ht, Wt, C] for DR_BOUNDARY_CUBE; Nt is
+ *     1 (shared by every image) or N.
+ *   pyramid / L: mip levels 1..L-1 from dr_texture_build_mip (mip filters).
+ *   uv: [N,Hi,Wi,2] (cube: direction [N,Hi,Wi,3]).
+ *   uv_da: [N,Hi,Wi,4] (mip filters).
+ *   bias_map: NULL or [N,Hi,Wi] per-pixel mip level bias; bias: scalar
+ *     bias.  Both scale uv_da by 2^bias before the LOD (Texture.swift:104-126).
+ */
+int dr_texture_fwd(const float* tex, const float* pyramid, int Nt, int Ht, int Wt, int C,
+                   int L, const float* uv, const float* uv_da, const float* bias_map,
+                   float bias, int filter, int boundary, int N, int Hi, int Wi, float* out,
+                   dr_stream_t stream);
+
+/* VJP of DiffRast.texture.  d_tex has tex's shape ([Nt,...]: a shared
+ * texture receives the sum over images).  d_uv may be NULL; it is zero for
+ * nearest and cube, as in the reference.  d_uv_da (mip filters) and
+ * d_bias_map (when bias_map is given) may be NULL. */
+int dr_texture_bwd(const float* tex, const float* pyramid, int Nt, int Ht, int Wt, int C,
+                   int L, const float* uv, const float* uv_da, const float* bias_map,
+                   float bias, int filter, int boundary, int N, int Hi, int Wi,
+                   const float* d_out, float* d_tex, float* d_uv, float* d_uv_da,
+                   float* d_bias_map, unsigned flags, dr_stream_t stream);
+
+/* ---- antialias ------------------------------------------------------- */
+
+/* antialiasConstructTopologyHash (Antialias.swift:19-66), on the GPU:
+ * topo[t,k] = the other triangle sharing the edge opposite vertex k, -1
+ * for a boundary edge, -2 for an edge of 3+ triangles.  Bit-identical to the
+ * reference (the result does not depend on any ordering). */
+int dr_antialias_topology(const int32_t* tri, int T, int32_t* topo, dr_stream_t stream);
+
+/* Forward of DiffRast.antialias (Antialias.swift:90-131).  color [N,H,W,C],
+ * rast [N,H,W,4], pos [N,V,4], tri [T,3], topo [T,3] -> out [N,H,W,C]. */
+int dr_antialias_fwd(const float* color, const float* rast, const float* pos,
+                     const int32_t* tri, const int32_t* topo, int N, int H, int W, int C,
+                     int V, int T, float* out, dr_stream_t stream);
+
+/* VJP of DiffRast.antialias: d_color [N,H,W,C], d_pos [N,V,4] (either may
+ * be NULL to skip it). */
+int dr_antialias_bwd(const float* color, const float* rast, const float* pos,
+                     const int32_t* tri, const int32_t* topo, const float* d_out, int N, int H,
+                     int W, int C, int V, int T, float* d_color, float* d_pos, unsigned flags,
+                     dr_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

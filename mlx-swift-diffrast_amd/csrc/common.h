@@ -1,0 +1,147 @@
+// Shared device helpers for the gfx950 kernels (wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "diffrast_mi355x.h"
+
+namespace dr {
+
+// ---------------------------------------------------------------------------
+// errors
+// ---------------------------------------------------------------------------
+
+void set_error(const std::string& msg);
+
+#define DR_CHECK_ARG(cond, msg)              \
+  do {                                       \
+    if (!(cond)) {                           \
+      ::dr::set_error(std::string(msg));     \
+      return DR_ERR_ARGUMENT;                \
+    }                                        \
+  } while (0)
+
+#define DR_CHECK_HIP(expr)                                                         \
+  do {                                                                             \
+    hipError_t e_ = (expr);                                                        \
+    if (e_ != hipSuccess) {                                                        \
+      ::dr::set_error(std::string(#expr) + ": " + hipGetErrorString(e_));          \
+      return DR_ERR_HIP;                                                           \
+    }                                                                              \
+  } while (0)
+
+#define DR_CHECK_LAUNCH() DR_CHECK_HIP(hipGetLastError())
+
+// ---------------------------------------------------------------------------
+// scratch memory, kept per (device, stream), grow-only
+// ---------------------------------------------------------------------------
+
+enum Slot {
+  SLOT_RAST_REC = 0,  // per-triangle screen records
+  SLOT_RAST_RECT,     // per-triangle tile rectangles
+  SLOT_RAST_CNT,      // per-tile counters / offsets
+  SLOT_RAST_LIST,     // tile -> triangle lists
+  SLOT_RAST_ITEMS,    // range-mode item prefix
+  SLOT_TOPO,          // edge hash table
+  SLOT_DPYR,          // mip pyramid gradient
+  SLOT_SMALL,         // small device-side counters
+  SLOT_COUNT
+};
+
+struct Scratch {
+  void* ptr[SLOT_COUNT] = {};
+  size_t cap[SLOT_COUNT] = {};
+  // Bin-list capacity protocol (rasterize): the exact pair count of the
+  // last call is copied to pinned host memory after the call; the next call
+  // reads it (once its copy has landed) to size the list buffer.
+  int64_t* pinned_total = nullptr;
+  hipEvent_t total_event = nullptr;
+  bool total_pending = false;
+};
+
+// Returns the scratch record of (current device, stream); nullptr on error.
+Scratch* scratch_for(hipStream_t stream);
+// Ensures slot `s` holds at least `bytes`; returns its pointer or nullptr.
+void* scratch_get(Scratch* sc, hipStream_t stream, int s, size_t bytes);
+
+// ---------------------------------------------------------------------------
+// device helpers
+// ---------------------------------------------------------------------------
+
+constexpr int kWave = 64;
+
+// `(int)floor(x)` with the conversion GPUs implement (saturate, NaN -> 0);
+// the oracle uses the same definition.
+__device__ __forceinline__ int f2i(float x) {
+  if (x != x) return 0;
+  if (x >= 2147483648.0f) return 2147483647;
+  if (x <= -2147483648.0f) return (-2147483647 - 1);
+  return (int)x;
+}
+
+__device__ __forceinline__ int lane_id() { return (int)__lane_id(); }
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+  return v;
+}
+
+// Scatter-add of M values per lane into addresses that are equal for all
+// lanes with the same (`key`, `key2`).  Lanes sharing a key with at least kGroupMin
+// others are summed across the wave first and written by one lane; other
+// lanes issue their own atomics.  Inactive lanes pass valid = false (every
+// lane of the wave must call this).
+constexpr int kGroupMin = 6;
+
+template <int M>
+__device__ __forceinline__ void group_atomic_add(bool valid, uint64_t key, float* const (&addr)[M],
+                                                 const float (&val)[M], uint32_t key2 = 0) {
+  uint64_t pending = __ballot(valid);
+  const int lane = lane_id();
+  while (pending) {
+    const int leader = __ffsll((long long)pending) - 1;
+    const uint64_t lkey = __shfl(key, leader, kWave);
+    const uint32_t lkey2 = __shfl(key2, leader, kWave);
+    const bool member = valid && key == lkey && key2 == lkey2 && ((pending >> lane) & 1ull);
+    const uint64_t members = __ballot(member);
+    pending &= ~members;
+    if (__popcll(members) >= kGroupMin) {
+#pragma unroll
+      for (int i = 0; i < M; ++i) {
+        float s = wave_sum(member ? val[i] : 0.0f);
+        if (lane == leader && s != 0.0f) unsafeAtomicAdd(addr[i], s);
+      }
+    } else if (member) {
+#pragma unroll
+      for (int i = 0; i < M; ++i)
+        if (val[i] != 0.0f) unsafeAtomicAdd(addr[i], val[i]);
+    }
+  }
+}
+
+template <typename T>
+__global__ void fill_kernel(T* __restrict__ p, T v, int64_t n) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (; i < n; i += stride) p[i] = v;
+}
+
+// Fill with a kernel (not hipMemsetAsync) so the call stays graph-capturable.
+template <typename T>
+inline hipError_t fill_async(T* p, T v, int64_t n, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  int64_t blocks = (n + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  hipLaunchKernelGGL(fill_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, s, p, v, n);
+  return hipGetLastError();
+}
+
+inline unsigned grid_for(int64_t n, int block) {
+  return (unsigned)((n + block - 1) / block);
+}
+
+}  // namespace dr

@@ -1,0 +1,260 @@
+// interpolate: barycentric gather of per-vertex attributes (+ screen-space
+// derivatives), and the fused backward (d_attr scatter, d_rast, d_rast_db in
+// one pass over the pixels instead of three).
+//
+// Semantics follow Sources/MLXDiffRast/Interpolate.swift of the reference:
+//   forward    :137-170 (basic), :175-228 (DA)
+//   backward   :231-264 / :269-324 (d_attr), :327-367 (d_rast),
+//              :370-417 (d_rast_db)
+// u weights vertex 1, v weights vertex 2, bw = 1 - u - v weights vertex 0
+// (CONVENTIONS.md of the reference).
+#include "common.h"
+
+namespace dr {
+
+// Compile-time attribute / derivative counts for the common shapes; 0 means
+// "given at run time".
+template <int AT>
+__device__ __forceinline__ int dimA(int A) { return AT > 0 ? AT : A; }
+
+template <int AT, int KT>
+__global__ void __launch_bounds__(256) k_interp_fwd(
+    const float* __restrict__ attr, int64_t attr_stride, const float* __restrict__ rast,
+    const float* __restrict__ rast_db, const int32_t* __restrict__ tri,
+    const int32_t* __restrict__ diff_idx, int K_, int64_t P, int HW, int A_,
+    float* __restrict__ out, float* __restrict__ out_da) {
+  const int64_t pix = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (pix >= P) return;
+  const int A = dimA<AT>(A_);
+  const int K = KT > 0 ? KT : K_;
+  const float4 r = *reinterpret_cast<const float4*>(rast + pix * 4);
+  const int t = f2i(r.w) - 1;
+  float* o = out + pix * A;
+  float* od = K > 0 ? out_da + pix * 2 * K : nullptr;
+  if (t < 0) {
+    for (int a = 0; a < A; ++a) o[a] = 0.0f;
+    for (int k = 0; k < 2 * K; ++k) od[k] = 0.0f;
+    return;
+  }
+  const int n = (int)(pix / HW);
+  const float* at = attr + (int64_t)n * attr_stride;
+  const int i0 = tri[t * 3 + 0], i1 = tri[t * 3 + 1], i2 = tri[t * 3 + 2];
+  const float* a0p = at + (int64_t)i0 * A;
+  const float* a1p = at + (int64_t)i1 * A;
+  const float* a2p = at + (int64_t)i2 * A;
+  const float u = r.x, v = r.y;
+  const float bw = 1.0f - u - v;
+#pragma unroll
+  for (int a = 0; a < A; ++a) o[a] = bw * a0p[a] + u * a1p[a] + v * a2p[a];
+  if (K > 0) {
+    const float4 db = *reinterpret_cast<const float4*>(rast_db + pix * 4);
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int a = diff_idx ? diff_idx[k] : k;
+      const float d01 = a1p[a] - a0p[a];
+      const float d02 = a2p[a] - a0p[a];
+      od[2 * k + 0] = d01 * db.x + d02 * db.z;
+      od[2 * k + 1] = d01 * db.y + d02 * db.w;
+    }
+  }
+}
+
+// Fused backward.  Pixels are walked in 16x16 tiles, one 8x8 quadrant per
+// wave, so a wave's pixels mostly share a few triangles and their d_attr
+// contributions are summed across the wave before the atomics.
+template <int AT, int KT>
+__global__ void __launch_bounds__(256) k_interp_bwd(
+    const float* __restrict__ attr, int64_t attr_stride, const float* __restrict__ rast,
+    const float* __restrict__ rast_db, const int32_t* __restrict__ tri,
+    const int32_t* __restrict__ diff_idx, int K_, const float* __restrict__ d_out,
+    const float* __restrict__ d_out_da, int N, int H, int W, int ntx, int nty, int A_,
+    float* __restrict__ d_attr, int64_t d_attr_stride, float* __restrict__ d_rast,
+    float* __restrict__ d_rast_db) {
+  const int tiles = ntx * nty;
+  const int b = (int)blockIdx.x;
+  const int n = b / tiles;
+  const int tile = b - n * tiles;
+  const int ty = tile / ntx, tx = tile - ty * ntx;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int qx0 = tx * 16 + (wave & 1) * 8, qy0 = ty * 16 + (wave >> 1) * 8;
+  if (qx0 >= W || qy0 >= H) return;
+  const int pw = qx0 + (lane & 7), ph = qy0 + (lane >> 3);
+  const bool inside = pw < W && ph < H;
+  const int64_t pix = ((int64_t)n * H + min(ph, H - 1)) * W + min(pw, W - 1);
+  const int A = dimA<AT>(A_);
+  const int K = KT > 0 ? KT : K_;
+
+  const float4 r = *reinterpret_cast<const float4*>(rast + pix * 4);
+  const int t = f2i(r.w) - 1;
+  const bool valid = inside && t >= 0;
+  const float u = r.x, v = r.y;
+  const float bw = 1.0f - u - v;
+  int i0 = 0, i1 = 0, i2 = 0;
+  if (valid) {
+    i0 = tri[t * 3 + 0];
+    i1 = tri[t * 3 + 1];
+    i2 = tri[t * 3 + 2];
+  }
+  const float* at = attr + (int64_t)n * attr_stride;
+  float* da = d_attr + (int64_t)n * d_attr_stride;
+  const float* g = d_out + pix * A;
+  float4 db = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (K > 0 && valid) db = *reinterpret_cast<const float4*>(rast_db + pix * 4);
+
+  // d_rast (Interpolate.swift:327-367) and d_rast_db (:370-417).
+  float du = 0.0f, dv = 0.0f;
+  if (valid) {
+    for (int a = 0; a < A; ++a) {
+      const float a0 = at[(int64_t)i0 * A + a], a1 = at[(int64_t)i1 * A + a],
+                  a2 = at[(int64_t)i2 * A + a];
+      du += (a1 - a0) * g[a];
+      dv += (a2 - a0) * g[a];
+    }
+  }
+  float d_udx = 0.0f, d_udy = 0.0f, d_vdx = 0.0f, d_vdy = 0.0f;
+  if (K > 0 && valid) {
+    const float* gd = d_out_da + pix * 2 * K;
+    for (int k = 0; k < K; ++k) {
+      const int a = diff_idx ? diff_idx[k] : k;
+      const float a0 = at[(int64_t)i0 * A + a], a1 = at[(int64_t)i1 * A + a],
+                  a2 = at[(int64_t)i2 * A + a];
+      const float d01 = a1 - a0, d02 = a2 - a0;
+      const float gx = gd[2 * k + 0], gy = gd[2 * k + 1];
+      d_udx += d01 * gx;
+      d_udy += d01 * gy;
+      d_vdx += d02 * gx;
+      d_vdy += d02 * gy;
+    }
+  }
+  if (inside) {
+    *reinterpret_cast<float4*>(d_rast + pix * 4) = make_float4(du, dv, 0.0f, 0.0f);
+    if (K > 0 && d_rast_db)
+      *reinterpret_cast<float4*>(d_rast_db + pix * 4) = make_float4(d_udx, d_udy, d_vdx, d_vdy);
+  }
+
+  // d_attr (Interpolate.swift:231-264, :269-324).
+  const uint64_t key = (uint64_t)(uint32_t)t;
+  if (AT > 0 && (KT > 0 || K == 0)) {
+    constexpr int M = 3 * (AT > 0 ? AT : 1) + 3 * KT;
+    float val[M];
+    float* addr[M];
+#pragma unroll
+    for (int a = 0; a < (AT > 0 ? AT : 1); ++a) {
+      const float ga = valid ? g[a] : 0.0f;
+      val[3 * a + 0] = bw * ga;
+      val[3 * a + 1] = u * ga;
+      val[3 * a + 2] = v * ga;
+      addr[3 * a + 0] = da + (int64_t)i0 * A + a;
+      addr[3 * a + 1] = da + (int64_t)i1 * A + a;
+      addr[3 * a + 2] = da + (int64_t)i2 * A + a;
+    }
+    if (KT > 0) {
+      const float* gd = d_out_da + pix * 2 * K;
+#pragma unroll
+      for (int k = 0; k < (KT > 0 ? KT : 1); ++k) {
+        const int a = diff_idx ? diff_idx[k] : k;
+        const float gx = valid ? gd[2 * k + 0] : 0.0f, gy = valid ? gd[2 * k + 1] : 0.0f;
+        const float u_term = gx * db.x + gy * db.y;
+        const float v_term = gx * db.z + gy * db.w;
+        const int base = 3 * (AT > 0 ? AT : 1) + 3 * k;
+        val[base + 0] = -u_term - v_term;
+        val[base + 1] = u_term;
+        val[base + 2] = v_term;
+        addr[base + 0] = da + (int64_t)i0 * A + a;
+        addr[base + 1] = da + (int64_t)i1 * A + a;
+        addr[base + 2] = da + (int64_t)i2 * A + a;
+      }
+    }
+    group_atomic_add<M>(valid, key, addr, val);
+  } else {
+    for (int a = 0; a < A; ++a) {
+      const float ga = valid ? g[a] : 0.0f;
+      float val[3] = {bw * ga, u * ga, v * ga};
+      float* addr[3] = {da + (int64_t)i0 * A + a, da + (int64_t)i1 * A + a,
+                        da + (int64_t)i2 * A + a};
+      group_atomic_add<3>(valid, key, addr, val);
+    }
+    if (K > 0) {
+      const float* gd = d_out_da + pix * 2 * K;
+      for (int k = 0; k < K; ++k) {
+        const int a = diff_idx ? diff_idx[k] : k;
+        const float gx = valid ? gd[2 * k + 0] : 0.0f, gy = valid ? gd[2 * k + 1] : 0.0f;
+        const float u_term = gx * db.x + gy * db.y;
+        const float v_term = gx * db.z + gy * db.w;
+        float val[3] = {-u_term - v_term, u_term, v_term};
+        float* addr[3] = {da + (int64_t)i0 * A + a, da + (int64_t)i1 * A + a,
+                          da + (int64_t)i2 * A + a};
+        group_atomic_add<3>(valid, key, addr, val);
+      }
+    }
+  }
+}
+
+}  // namespace dr
+
+using namespace dr;
+
+#define DR_INTERP_DISPATCH(KERNEL, GRID, ...)                                              \
+  do {                                                                                     \
+    if (A == 2 && K == 0) hipLaunchKernelGGL((KERNEL<2, 0>), GRID, dim3(256), 0, stream, __VA_ARGS__); \
+    else if (A == 2 && K == 2) hipLaunchKernelGGL((KERNEL<2, 2>), GRID, dim3(256), 0, stream, __VA_ARGS__); \
+    else if (A == 3 && K == 0) hipLaunchKernelGGL((KERNEL<3, 0>), GRID, dim3(256), 0, stream, __VA_ARGS__); \
+    else if (A == 3 && K == 3) hipLaunchKernelGGL((KERNEL<3, 3>), GRID, dim3(256), 0, stream, __VA_ARGS__); \
+    else if (A == 4 && K == 0) hipLaunchKernelGGL((KERNEL<4, 0>), GRID, dim3(256), 0, stream, __VA_ARGS__); \
+    else if (A == 6 && K == 0) hipLaunchKernelGGL((KERNEL<6, 0>), GRID, dim3(256), 0, stream, __VA_ARGS__); \
+    else hipLaunchKernelGGL((KERNEL<0, 0>), GRID, dim3(256), 0, stream, __VA_ARGS__);      \
+  } while (0)
+
+static int check_interp(const float* attr, const float* rast, const int32_t* tri,
+                        const float* rast_db, int K, int N, int H, int W, int V, int A,
+                        int64_t attr_stride, const int32_t* diff_idx) {
+  DR_CHECK_ARG(N >= 1 && H >= 1 && W >= 1 && V >= 0 && A >= 1 && K >= 0,
+               "interpolate: bad sizes");
+  DR_CHECK_ARG(attr && rast && tri, "interpolate: null tensor");
+  DR_CHECK_ARG(attr_stride == 0 || attr_stride == (int64_t)V * A,
+               "interpolate: attr_batch_stride must be 0 or V*A");
+  DR_CHECK_ARG(K == 0 || rast_db, "interpolate: rastDB is required when diffAttrs is set");
+  DR_CHECK_ARG(K == 0 || diff_idx || K == A, "interpolate: diff_idx NULL needs K == A");
+  return DR_OK;
+}
+
+extern "C" int dr_interpolate_fwd(const float* attr, int64_t attr_batch_stride,
+                                  const float* rast, const float* rast_db, const int32_t* tri,
+                                  const int32_t* diff_idx, int K, int N, int H, int W, int V,
+                                  int A, float* out, float* out_da, dr_stream_t stream_) {
+  hipStream_t stream = (hipStream_t)stream_;
+  (void)hipGetLastError();
+  int st = check_interp(attr, rast, tri, rast_db, K, N, H, W, V, A, attr_batch_stride, diff_idx);
+  if (st) return st;
+  DR_CHECK_ARG(out && (K == 0 || out_da), "interpolate: null output");
+  const int64_t P = (int64_t)N * H * W;
+  const dim3 grid(grid_for(P, 256));
+  DR_INTERP_DISPATCH(k_interp_fwd, grid, attr, attr_batch_stride, rast, rast_db, tri, diff_idx,
+                     K, P, H * W, A, out, out_da);
+  DR_CHECK_LAUNCH();
+  return DR_OK;
+}
+
+extern "C" int dr_interpolate_bwd(const float* attr, int64_t attr_batch_stride,
+                                  const float* rast, const float* rast_db, const int32_t* tri,
+                                  const int32_t* diff_idx, int K, const float* d_out,
+                                  const float* d_out_da, int N, int H, int W, int V, int A,
+                                  float* d_attr, int64_t d_attr_batch_stride, float* d_rast,
+                                  float* d_rast_db, unsigned flags, dr_stream_t stream_) {
+  hipStream_t stream = (hipStream_t)stream_;
+  (void)hipGetLastError();
+  int st = check_interp(attr, rast, tri, rast_db, K, N, H, W, V, A, attr_batch_stride, diff_idx);
+  if (st) return st;
+  DR_CHECK_ARG(d_out && d_attr && d_rast && (K == 0 || d_out_da), "interpolate_bwd: null tensor");
+  DR_CHECK_ARG(d_attr_batch_stride == 0 || d_attr_batch_stride == (int64_t)V * A,
+               "interpolate_bwd: d_attr_batch_stride must be 0 or V*A");
+  const int64_t nattr = (d_attr_batch_stride ? (int64_t)N : 1) * V * A;
+  if (!(flags & DR_ACCUMULATE)) DR_CHECK_HIP(fill_async(d_attr, 0.0f, nattr, stream));
+  const int ntx = (W + 15) / 16, nty = (H + 15) / 16;
+  const dim3 grid((unsigned)((int64_t)N * ntx * nty));
+  DR_INTERP_DISPATCH(k_interp_bwd, grid, attr, attr_batch_stride, rast, rast_db, tri, diff_idx, K,
+                     d_out, d_out_da, N, H, W, ntx, nty, A, d_attr, d_attr_batch_stride, d_rast,
+                     d_rast_db);
+  DR_CHECK_LAUNCH();
+  return DR_OK;
+}

@@ -1,0 +1,580 @@
+// rasterize: triangle setup, screen-tile binning, per-tile coverage / depth /
+// barycentric forward (+ rast_db), and the d_pos backward.
+//
+// Semantics follow Sources/MLXDiffRast/Rasterize.swift of the reference:
+//   setup    :280-328   (per-triangle perspective divide, signed area)
+//   binning  :182-240   (16x16 tiles, tile range from the pixel AABB)
+//   forward  :371-477 / :487-599 (inclusive edges, first-hit on equal z)
+//   backward :637-812
+// Differences by design: tile lists never overflow (the reference drops
+// triangles beyond 128 per tile), and equal depths pick the lowest triangle
+// index (the reference picks the first in its atomic bin order).
+//
+// All float expressions are evaluated exactly as the reference writes them
+// (this file is compiled with -ffp-contract=off), so the tri_id channel and
+// the forward floats are bit-identical to a sequential execution of the
+// reference.
+#include "common.h"
+
+namespace dr {
+
+constexpr int kTile = 16;
+
+// Per-triangle record, 4 x float4:
+//   r0 = (sx0, sy0, sx1, sy1)  r1 = (sx2, sy2, sz0, sz1)
+//   r2 = (sz2, area, 1/area, 0) r3 = (minx, maxx, miny, maxy)
+// area == 0 marks a triangle the reference zeroes (w <= 0 or degenerate).
+struct alignas(16) TriRec {
+  float4 r0, r1, r2, r3;
+};
+
+__device__ __forceinline__ int xcd_remap(int b, int B) {
+  // Blocks are dealt round-robin to the 8 XCDs; give each XCD a contiguous
+  // run of tiles so neighbouring tiles share that XCD's L2.
+  if ((B & 7) != 0) return b;
+  return (b & 7) * (B >> 3) + (b >> 3);
+}
+
+// Rasterize.swift:280-328 (+ the AABB and tile range of :191-223).
+__global__ void __launch_bounds__(256) k_setup(const float* __restrict__ pos, int64_t pos_stride,
+                                               const int32_t* __restrict__ tri, int Npos, int T,
+                                               int H, int W, TriRec* __restrict__ rec,
+                                               int4* __restrict__ rect) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)Npos * T) return;
+  const int n = (int)(i / T);
+  const int t = (int)(i - (int64_t)n * T);
+  const float* p = pos + (int64_t)n * pos_stride;
+  const int i0 = tri[t * 3 + 0], i1 = tri[t * 3 + 1], i2 = tri[t * 3 + 2];
+  const float4 v0 = *reinterpret_cast<const float4*>(p + (int64_t)i0 * 4);
+  const float4 v1 = *reinterpret_cast<const float4*>(p + (int64_t)i1 * 4);
+  const float4 v2 = *reinterpret_cast<const float4*>(p + (int64_t)i2 * 4);
+  TriRec r;
+  int4 rc = make_int4(-1, -1, -1, -1);
+  if (v0.w <= 0.0f || v1.w <= 0.0f || v2.w <= 0.0f) {
+    r.r0 = r.r1 = r.r2 = r.r3 = make_float4(0.f, 0.f, 0.f, 0.f);
+  } else {
+    const float sx0 = v0.x / v0.w, sy0 = v0.y / v0.w, sz0 = v0.z / v0.w;
+    const float sx1 = v1.x / v1.w, sy1 = v1.y / v1.w, sz1 = v1.z / v1.w;
+    const float sx2 = v2.x / v2.w, sy2 = v2.y / v2.w, sz2 = v2.z / v2.w;
+    const float area = (sx1 - sx0) * (sy2 - sy0) - (sx2 - sx0) * (sy1 - sy0);
+    const float minx = fminf(sx0, fminf(sx1, sx2));
+    const float maxx = fmaxf(sx0, fmaxf(sx1, sx2));
+    const float miny = fminf(sy0, fminf(sy1, sy2));
+    const float maxy = fmaxf(sy0, fmaxf(sy1, sy2));
+    r.r0 = make_float4(sx0, sy0, sx1, sy1);
+    r.r1 = make_float4(sx2, sy2, sz0, sz1);
+    r.r2 = make_float4(sz2, area, 1.0f / area, 0.0f);
+    r.r3 = make_float4(minx, maxx, miny, maxy);
+    if (area != 0.0f) {
+      const float px_min = (minx + 1.0f) * (float)W * 0.5f - 0.5f;
+      const float px_max = (maxx + 1.0f) * (float)W * 0.5f - 0.5f;
+      const float py_min = (1.0f - maxy) * (float)H * 0.5f - 0.5f;
+      const float py_max = (1.0f - miny) * (float)H * 0.5f - 0.5f;
+      int x0 = f2i(floorf(px_min)), x1 = f2i(floorf(px_max));
+      int y0 = f2i(floorf(py_min)), y1 = f2i(floorf(py_max));
+      if (x0 < 0) x0 = 0;
+      if (x1 >= W) x1 = W - 1;
+      if (y0 < 0) y0 = 0;
+      if (y1 >= H) y1 = H - 1;
+      if (x0 <= x1 && y0 <= y1) rc = make_int4(x0 / kTile, x1 / kTile, y0 / kTile, y1 / kTile);
+    }
+  }
+  rec[i] = r;
+  rect[i] = rc;
+}
+
+// Work item -> (image n, triangle t, record index).  Instanced mode: every
+// image draws [0,T) from its own records.  Range mode: image n draws
+// [start_n, start_n + count_n) from the shared records.
+struct Items {
+  const int64_t* prefix;  // [N+1] range mode, else nullptr
+  const int64_t* start;   // [N]
+  int T;
+};
+
+__device__ __forceinline__ void item_of(const Items& it, int64_t i, int N, int& n, int& t,
+                                        int64_t& r) {
+  if (it.prefix == nullptr) {
+    n = (int)(i / it.T);
+    t = (int)(i - (int64_t)n * it.T);
+    r = i;
+  } else {
+    int lo = 0, hi = N;  // largest n with prefix[n] <= i
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (it.prefix[mid] <= i) lo = mid; else hi = mid;
+    }
+    n = lo;
+    t = (int)(it.start[n] + (i - it.prefix[n]));
+    r = t;
+  }
+}
+
+// Rasterize.swift:227-233, first half: per-tile counts.
+__global__ void __launch_bounds__(256) k_bin_count(Items it, int64_t n_items, int N,
+                                                   const int4* __restrict__ rect, int ntx,
+                                                   int tiles, int* __restrict__ cnt) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n_items) return;
+  int n, t;
+  int64_t r;
+  item_of(it, i, N, n, t, r);
+  const int4 rc = rect[r];
+  if (rc.x < 0) return;
+  int* c = cnt + (int64_t)n * tiles;
+  for (int ty = rc.z; ty <= rc.w; ++ty)
+    for (int tx = rc.x; tx <= rc.y; ++tx) atomicAdd(&c[ty * ntx + tx], 1);
+}
+
+// Each tile reserves its list segment: a wave-wide exclusive scan of the
+// counts, one atomic per wave on the running total.
+__global__ void __launch_bounds__(256) k_bin_alloc(const int* __restrict__ cnt, int64_t n_tiles,
+                                                   int64_t* __restrict__ off,
+                                                   int* __restrict__ fill,
+                                                   unsigned long long* __restrict__ total) {
+  const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int c = j < n_tiles ? cnt[j] : 0;
+  int incl = c;
+  const int lane = lane_id();
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const int y = __shfl_up(incl, d, kWave);
+    if (lane >= d) incl += y;
+  }
+  const int wave_total = __shfl(incl, kWave - 1, kWave);
+  unsigned long long base = 0;
+  if (lane == kWave - 1 && wave_total > 0) base = atomicAdd(total, (unsigned long long)wave_total);
+  base = __shfl(base, kWave - 1, kWave);
+  if (j < n_tiles) {
+    off[j] = (int64_t)base + (incl - c);
+    fill[j] = 0;
+  }
+}
+
+// Rasterize.swift:227-239, second half: append t to each touched tile.
+__global__ void __launch_bounds__(256) k_bin_fill(Items it, int64_t n_items, int N,
+                                                  const int4* __restrict__ rect, int ntx,
+                                                  int tiles, const int64_t* __restrict__ off,
+                                                  int* __restrict__ fill,
+                                                  int* __restrict__ list, int64_t cap) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n_items) return;
+  int n, t;
+  int64_t r;
+  item_of(it, i, N, n, t, r);
+  const int4 rc = rect[r];
+  if (rc.x < 0) return;
+  const int64_t base = (int64_t)n * tiles;
+  for (int ty = rc.z; ty <= rc.w; ++ty)
+    for (int tx = rc.x; tx <= rc.y; ++tx) {
+      const int64_t j = base + ty * ntx + tx;
+      const int s = atomicAdd(&fill[j], 1);
+      const int64_t p = off[j] + s;
+      if (p < cap) list[p] = t;
+    }
+}
+
+struct Best {
+  float z, u, v;
+  int t;
+};
+
+// One candidate against one pixel (Rasterize.swift:417-462).
+__device__ __forceinline__ void test_tri(const TriRec& R, int t, float x, float y, float peel_z,
+                                         Best& b) {
+  const float sx0 = R.r0.x, sy0 = R.r0.y, sx1 = R.r0.z, sy1 = R.r0.w;
+  const float sx2 = R.r1.x, sy2 = R.r1.y, sz0 = R.r1.z, sz1 = R.r1.w;
+  const float sz2 = R.r2.x, area = R.r2.y, inv_area = R.r2.z;
+  if (x < R.r3.x || x > R.r3.y || y < R.r3.z || y > R.r3.w) return;
+  const float e0 = (sx1 - x) * (sy2 - y) - (sx2 - x) * (sy1 - y);
+  const float e1 = (sx2 - x) * (sy0 - y) - (sx0 - x) * (sy2 - y);
+  const float e2 = (sx0 - x) * (sy1 - y) - (sx1 - x) * (sy0 - y);
+  if ((e0 * area) < 0.0f || (e1 * area) < 0.0f || (e2 * area) < 0.0f) return;
+  const float bw = e0 * inv_area;
+  const float u = e1 * inv_area;
+  const float v = e2 * inv_area;
+  const float z = bw * sz0 + u * sz1 + v * sz2;
+  if (z < -1.0f || z > 1.0f) return;
+  if (z <= peel_z) return;
+  if (z < b.z || (z == b.z && t < b.t)) {
+    b.z = z;
+    b.u = u;
+    b.v = v;
+    b.t = t;
+  }
+}
+
+__device__ __forceinline__ TriRec load_rec(const TriRec* __restrict__ rec, int64_t r) {
+  const float4* q = reinterpret_cast<const float4*>(rec + r);
+  TriRec R;
+  R.r0 = q[0];
+  R.r1 = q[1];
+  R.r2 = q[2];
+  R.r3 = q[3];
+  return R;
+}
+
+// Rasterize.swift:371-599.  One workgroup per (image, 16x16 tile); wave w
+// owns the 8x8 quadrant (w&1, w>>1).  The tile's triangle ids and records
+// are wave-uniform, so they travel through the scalar cache; each triangle
+// is first tested against the quadrant's pixel-centre box (exact: the
+// pixel -> NDC map is monotonic), so most of the list costs a few scalar
+// compares.
+template <bool DB, bool PEEL>
+__global__ void __launch_bounds__(256) k_raster(
+    const TriRec* __restrict__ rec, const int4* __restrict__ rect, Items it, int64_t rec_stride,
+    const int* __restrict__ cnt, const int64_t* __restrict__ off, const int* __restrict__ list,
+    int64_t cap, const float* __restrict__ peel, int N, int H, int W, int ntx, int nty,
+    float* __restrict__ rast, float* __restrict__ rast_db) {
+  const int tiles = ntx * nty;
+  const int B = tiles * N;
+  const int b = xcd_remap((int)blockIdx.x, B);
+  const int n = b / tiles;
+  const int tile = b - n * tiles;
+  const int ty = tile / ntx, tx = tile - ty * ntx;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int qx0 = tx * kTile + (wave & 1) * 8;
+  const int qy0 = ty * kTile + (wave >> 1) * 8;
+  if (qx0 >= W || qy0 >= H) return;  // whole quadrant outside the image
+  const int pw = qx0 + (lane & 7);
+  const int ph = qy0 + (lane >> 3);
+  const bool valid = pw < W && ph < H;
+  const int qx1 = min(qx0 + 7, W - 1), qy1 = min(qy0 + 7, H - 1);
+
+  const float x = 2.0f * ((float)pw + 0.5f) / (float)W - 1.0f;
+  const float y = 1.0f - 2.0f * ((float)ph + 0.5f) / (float)H;
+  const float xw0 = 2.0f * ((float)qx0 + 0.5f) / (float)W - 1.0f;
+  const float xw1 = 2.0f * ((float)qx1 + 0.5f) / (float)W - 1.0f;
+  const float yw1 = 1.0f - 2.0f * ((float)qy0 + 0.5f) / (float)H;  // top row: largest y
+  const float yw0 = 1.0f - 2.0f * ((float)qy1 + 0.5f) / (float)H;
+
+  const int64_t pix = ((int64_t)n * H + ph) * W + pw;
+  float peel_z = -1e30f;
+  if (PEEL && valid) {
+    const float4 pl = *reinterpret_cast<const float4*>(peel + pix * 4);
+    if (pl.w > 0.0f) peel_z = pl.z;
+  }
+  Best best = {1e30f, 0.0f, 0.0f, -1};
+  const int64_t rbase = (int64_t)n * rec_stride;
+  const int64_t j = (int64_t)n * tiles + tile;
+  const int count = cnt[j];
+  const int64_t o = off[j];
+  if (o + count <= cap) {
+    const int* ids = list + o;
+    for (int i = 0; i < count; ++i) {
+      const int t = ids[i];
+      const TriRec R = load_rec(rec, rbase + t);
+      if (R.r3.y < xw0 || R.r3.x > xw1 || R.r3.w < yw0 || R.r3.z > yw1) continue;
+      if (valid) test_tri(R, t, x, y, peel_z, best);
+    }
+  } else {
+    // The list did not fit the scratch sized from an earlier call: scan the
+    // image's whole triangle range with the same tile test the binning
+    // uses (same candidate set, so the same result).
+    int t0 = 0, t1 = it.T;
+    if (it.prefix != nullptr) {
+      t0 = (int)it.start[n];
+      t1 = t0 + (int)(it.prefix[n + 1] - it.prefix[n]);
+    }
+    for (int t = t0; t < t1; ++t) {
+      const int4 rc = rect[rbase + t];
+      if (rc.x < 0 || tx < rc.x || tx > rc.y || ty < rc.z || ty > rc.w) continue;
+      const TriRec R = load_rec(rec, rbase + t);
+      if (R.r3.y < xw0 || R.r3.x > xw1 || R.r3.w < yw0 || R.r3.z > yw1) continue;
+      if (valid) test_tri(R, t, x, y, peel_z, best);
+    }
+  }
+  if (!valid) return;
+  float4 o4, d4 = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (best.t < 0) {
+    o4 = make_float4(0.f, 0.f, 0.f, 0.f);
+  } else {
+    o4 = make_float4(best.u, best.v, best.z, (float)(best.t + 1));
+    if (DB) {  // Rasterize.swift:586-598
+      const TriRec R = load_rec(rec, rbase + best.t);
+      const float sx0 = R.r0.x, sy0 = R.r0.y, sx1 = R.r0.z, sy1 = R.r0.w;
+      const float sx2 = R.r1.x, sy2 = R.r1.y;
+      const float inv_area = R.r2.z;
+      const float k_x = 2.0f / (float)W;
+      const float k_y = -2.0f / (float)H;
+      d4 = make_float4((sy2 - sy0) * inv_area * k_x, (sx0 - sx2) * inv_area * k_y,
+                       (sy0 - sy1) * inv_area * k_x, (sx1 - sx0) * inv_area * k_y);
+    }
+  }
+  *reinterpret_cast<float4*>(rast + pix * 4) = o4;
+  if (DB) *reinterpret_cast<float4*>(rast_db + pix * 4) = d4;
+}
+
+// Rasterize.swift:637-812.  Same tile/quadrant layout as the forward so a
+// wave's pixels share few triangles; same-triangle lanes are summed across
+// the wave before the 12 d_pos atomics.
+__global__ void __launch_bounds__(256) k_raster_bwd(
+    const float* __restrict__ pos, int64_t pos_stride, const int32_t* __restrict__ tri,
+    const float* __restrict__ rast, const float* __restrict__ d_rast,
+    const float* __restrict__ d_rast_db, int N, int H, int W, int ntx, int nty,
+    float* __restrict__ d_pos) {
+  const int tiles = ntx * nty;
+  const int b = xcd_remap((int)blockIdx.x, tiles * N);
+  const int n = b / tiles;
+  const int tile = b - n * tiles;
+  const int ty = tile / ntx, tx = tile - ty * ntx;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int qx0 = tx * kTile + (wave & 1) * 8;
+  const int qy0 = ty * kTile + (wave >> 1) * 8;
+  if (qx0 >= W || qy0 >= H) return;
+  const int pw = qx0 + (lane & 7);
+  const int ph = qy0 + (lane >> 3);
+  bool valid = pw < W && ph < H;
+  const int64_t pix = ((int64_t)n * H + min(ph, H - 1)) * W + min(pw, W - 1);
+  const float4 r = *reinterpret_cast<const float4*>(rast + pix * 4);
+  const int t = f2i(r.w) - 1;
+  valid = valid && t >= 0;
+
+  float val[12];
+  float* addr[12];
+#pragma unroll
+  for (int k = 0; k < 12; ++k) {
+    val[k] = 0.0f;
+    addr[k] = d_pos;
+  }
+  if (valid) {
+    const float u_val = r.x, v_val = r.y;
+    const float bw_val = 1.0f - u_val - v_val;
+    const float4 dr = *reinterpret_cast<const float4*>(d_rast + pix * 4);
+    const float d_u = dr.x, d_v = dr.y, d_z = dr.z;
+    float4 ddb = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (d_rast_db) ddb = *reinterpret_cast<const float4*>(d_rast_db + pix * 4);
+    const float d_db0 = ddb.x, d_db1 = ddb.y, d_db2 = ddb.z, d_db3 = ddb.w;
+    const float Px = 2.0f * ((float)pw + 0.5f) / (float)W - 1.0f;
+    const float Py = 1.0f - 2.0f * ((float)ph + 0.5f) / (float)H;
+    const float* p = pos + (int64_t)n * pos_stride;
+    float* dp = d_pos + (int64_t)n * pos_stride;
+    const int i0 = tri[t * 3 + 0], i1 = tri[t * 3 + 1], i2 = tri[t * 3 + 2];
+    const float4 P0 = *reinterpret_cast<const float4*>(p + (int64_t)i0 * 4);
+    const float4 P1 = *reinterpret_cast<const float4*>(p + (int64_t)i1 * 4);
+    const float4 P2 = *reinterpret_cast<const float4*>(p + (int64_t)i2 * 4);
+    const float sx0 = P0.x / P0.w, sy0 = P0.y / P0.w, sz0 = P0.z / P0.w;
+    const float sx1 = P1.x / P1.w, sy1 = P1.y / P1.w, sz1 = P1.z / P1.w;
+    const float sx2 = P2.x / P2.w, sy2 = P2.y / P2.w, sz2 = P2.z / P2.w;
+    const float area = (sx1 - sx0) * (sy2 - sy0) - (sx2 - sx0) * (sy1 - sy0);
+    const float inv_area = 1.0f / area;
+    const float dadsx0 = sy1 - sy2, dadsx1 = sy2 - sy0, dadsx2 = sy0 - sy1;
+    const float dadsy0 = sx2 - sx1, dadsy1 = sx0 - sx2, dadsy2 = sx1 - sx0;
+    const float de1dsx0 = Py - sy2, de1dsx2 = sy0 - Py;
+    const float de1dsy0 = sx2 - Px, de1dsy2 = Px - sx0;
+    const float de2dsx0 = sy1 - Py, de2dsx1 = Py - sy0;
+    const float de2dsy0 = Px - sx1, de2dsy1 = sx0 - Px;
+    const float dudsx0 = (de1dsx0 - u_val * dadsx0) * inv_area;
+    const float dudsx1 = (0.0f - u_val * dadsx1) * inv_area;
+    const float dudsx2 = (de1dsx2 - u_val * dadsx2) * inv_area;
+    const float dudsy0 = (de1dsy0 - u_val * dadsy0) * inv_area;
+    const float dudsy1 = (0.0f - u_val * dadsy1) * inv_area;
+    const float dudsy2 = (de1dsy2 - u_val * dadsy2) * inv_area;
+    const float dvdsx0 = (de2dsx0 - v_val * dadsx0) * inv_area;
+    const float dvdsx1 = (de2dsx1 - v_val * dadsx1) * inv_area;
+    const float dvdsx2 = (0.0f - v_val * dadsx2) * inv_area;
+    const float dvdsy0 = (de2dsy0 - v_val * dadsy0) * inv_area;
+    const float dvdsy1 = (de2dsy1 - v_val * dadsy1) * inv_area;
+    const float dvdsy2 = (0.0f - v_val * dadsy2) * inv_area;
+    const float dsz10 = sz1 - sz0, dsz20 = sz2 - sz0;
+    float dsx0 = d_u * dudsx0 + d_v * dvdsx0 + d_z * (dudsx0 * dsz10 + dvdsx0 * dsz20);
+    float dsx1 = d_u * dudsx1 + d_v * dvdsx1 + d_z * (dudsx1 * dsz10 + dvdsx1 * dsz20);
+    float dsx2 = d_u * dudsx2 + d_v * dvdsx2 + d_z * (dudsx2 * dsz10 + dvdsx2 * dsz20);
+    float dsy0 = d_u * dudsy0 + d_v * dvdsy0 + d_z * (dudsy0 * dsz10 + dvdsy0 * dsz20);
+    float dsy1 = d_u * dudsy1 + d_v * dvdsy1 + d_z * (dudsy1 * dsz10 + dvdsy1 * dsz20);
+    float dsy2 = d_u * dudsy2 + d_v * dvdsy2 + d_z * (dudsy2 * dsz10 + dvdsy2 * dsz20);
+    const float dsz0_s = d_z * bw_val, dsz1_s = d_z * u_val, dsz2_s = d_z * v_val;
+    const float Kx = 2.0f / (float)W;
+    const float Ky = -2.0f / (float)H;
+    const float rdb0 = (sy2 - sy0) * Kx * inv_area;
+    const float rdb1 = (sx0 - sx2) * Ky * inv_area;
+    const float rdb2 = (sy0 - sy1) * Kx * inv_area;
+    const float rdb3 = (sx1 - sx0) * Ky * inv_area;
+    const float s = d_db0 * rdb0 + d_db1 * rdb1 + d_db2 * rdb2 + d_db3 * rdb3;
+    dsx0 += (-s * dadsx0) * inv_area;
+    dsx1 += (-s * dadsx1) * inv_area;
+    dsx2 += (-s * dadsx2) * inv_area;
+    dsy0 += (-s * dadsy0) * inv_area;
+    dsy1 += (-s * dadsy1) * inv_area;
+    dsy2 += (-s * dadsy2) * inv_area;
+    dsy0 += d_db0 * (-Kx) * inv_area;
+    dsy2 += d_db0 * (Kx) * inv_area;
+    dsx0 += d_db1 * (Ky) * inv_area;
+    dsx2 += d_db1 * (-Ky) * inv_area;
+    dsy0 += d_db2 * (Kx) * inv_area;
+    dsy1 += d_db2 * (-Kx) * inv_area;
+    dsx0 += d_db3 * (-Ky) * inv_area;
+    dsx1 += d_db3 * (Ky) * inv_area;
+    const float inv_w0 = 1.0f / P0.w, inv_w1 = 1.0f / P1.w, inv_w2 = 1.0f / P2.w;
+    val[0] = dsx0 * inv_w0;
+    val[1] = dsy0 * inv_w0;
+    val[2] = dsz0_s * inv_w0;
+    val[3] = -(sx0 * dsx0 + sy0 * dsy0 + sz0 * dsz0_s) * inv_w0;
+    val[4] = dsx1 * inv_w1;
+    val[5] = dsy1 * inv_w1;
+    val[6] = dsz1_s * inv_w1;
+    val[7] = -(sx1 * dsx1 + sy1 * dsy1 + sz1 * dsz1_s) * inv_w1;
+    val[8] = dsx2 * inv_w2;
+    val[9] = dsy2 * inv_w2;
+    val[10] = dsz2_s * inv_w2;
+    val[11] = -(sx2 * dsx2 + sy2 * dsy2 + sz2 * dsz2_s) * inv_w2;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      addr[c] = dp + (int64_t)i0 * 4 + c;
+      addr[4 + c] = dp + (int64_t)i1 * 4 + c;
+      addr[8 + c] = dp + (int64_t)i2 * 4 + c;
+    }
+  }
+  group_atomic_add<12>(valid, (uint64_t)(uint32_t)t, addr, val);
+}
+
+}  // namespace dr
+
+using namespace dr;
+
+namespace {
+
+struct RangePlan {
+  int64_t n_items = 0;
+  bool range_mode = false;
+  std::vector<int64_t> host;  // prefix [N+1] then start [N]
+};
+
+}  // namespace
+
+extern "C" int dr_rasterize_fwd(const float* pos, int64_t pos_batch_stride, const int32_t* tri,
+                                const int32_t* ranges_host, const float* peel, int N, int V,
+                                int T, int H, int W, float* rast, float* rast_db,
+                                dr_stream_t stream_) {
+  hipStream_t stream = (hipStream_t)stream_;
+  DR_CHECK_ARG(N >= 1 && V >= 0 && T >= 0 && H >= 1 && W >= 1, "rasterize: bad sizes");
+  DR_CHECK_ARG(pos && tri && rast, "rasterize: null tensor");
+  DR_CHECK_ARG(ranges_host != nullptr || pos_batch_stride == (int64_t)V * 4,
+               "rasterize: instanced pos needs pos_batch_stride = V*4");
+  DR_CHECK_ARG(ranges_host == nullptr || pos_batch_stride == 0,
+               "rasterize: range mode needs a shared pos (pos_batch_stride = 0)");
+  DR_CHECK_ARG((int64_t)N * T < (int64_t)1 << 40, "rasterize: too many triangles");
+  Scratch* sc = scratch_for(stream);
+  if (!sc) return DR_ERR_HIP;
+
+  const int ntx = (W + kTile - 1) / kTile, nty = (H + kTile - 1) / kTile;
+  const int tiles = ntx * nty;
+  const int64_t n_tiles = (int64_t)N * tiles;
+  DR_CHECK_ARG(n_tiles < (int64_t)1 << 31, "rasterize: too many tiles");
+
+  // Items: which (image, triangle) pairs are drawn.
+  Items it{nullptr, nullptr, T};
+  int Npos = N;
+  int64_t n_items = (int64_t)N * T;
+  if (ranges_host) {
+    Npos = 1;
+    std::vector<int64_t> h(2 * (size_t)N + 1);
+    h[0] = 0;
+    for (int n = 0; n < N; ++n) {
+      int64_t s = ranges_host[2 * n], c = ranges_host[2 * n + 1];
+      int64_t lo = s < 0 ? 0 : s, hi = s + c > T ? T : s + c;
+      if (hi < lo) hi = lo;
+      h[n + 1] = h[n] + (hi - lo);
+      h[N + 1 + n] = lo;
+    }
+    n_items = h[N];
+    int64_t* d = (int64_t*)scratch_get(sc, stream, SLOT_RAST_ITEMS, h.size() * sizeof(int64_t));
+    if (!d) return DR_ERR_MEMORY;
+    // Synchronous copy: the host vector dies at the end of this call.
+    DR_CHECK_HIP(hipMemcpyAsync(d, h.data(), h.size() * sizeof(int64_t), hipMemcpyHostToDevice,
+                                stream));
+    DR_CHECK_HIP(hipStreamSynchronize(stream));
+    it.prefix = d;
+    it.start = d + N + 1;
+  }
+  const int64_t n_rec = (int64_t)Npos * T;
+  const int64_t rec_stride = ranges_host ? 0 : T;
+
+  TriRec* rec = (TriRec*)scratch_get(sc, stream, SLOT_RAST_REC, (size_t)n_rec * sizeof(TriRec));
+  int4* rect = (int4*)scratch_get(sc, stream, SLOT_RAST_RECT, (size_t)n_rec * sizeof(int4));
+  char* cbuf = (char*)scratch_get(sc, stream, SLOT_RAST_CNT, (size_t)n_tiles * 16);
+  unsigned long long* total =
+      (unsigned long long*)scratch_get(sc, stream, SLOT_SMALL, 64);
+  if (!rec || !rect || !cbuf || !total) return DR_ERR_MEMORY;
+  int64_t* off = (int64_t*)cbuf;
+  int* cnt = (int*)(cbuf + n_tiles * 8);
+  int* fillc = cnt + n_tiles;
+
+  DR_CHECK_HIP(fill_async(cnt, 0, n_tiles, stream));
+  DR_CHECK_HIP(fill_async(total, 0ull, 1, stream));
+  if (n_rec > 0) {
+    hipLaunchKernelGGL(k_setup, dim3(grid_for(n_rec, 256)), dim3(256), 0, stream, pos,
+                       ranges_host ? (int64_t)0 : pos_batch_stride, tri, Npos, T, H, W, rec, rect);
+    DR_CHECK_LAUNCH();
+  }
+  if (n_items > 0) {
+    hipLaunchKernelGGL(k_bin_count, dim3(grid_for(n_items, 256)), dim3(256), 0, stream, it,
+                       n_items, N, rect, ntx, tiles, cnt);
+    DR_CHECK_LAUNCH();
+  }
+  hipLaunchKernelGGL(k_bin_alloc, dim3(grid_for(n_tiles, 256)), dim3(256), 0, stream, cnt,
+                     n_tiles, off, fillc, total);
+  DR_CHECK_LAUNCH();
+
+  // List capacity: exact on the first call (one host sync); afterwards the
+  // previous call's total sizes the buffer without waiting, and the raster
+  // kernel falls back to a full scan for any tile that did not fit.
+  int64_t need = 0;
+  if (sc->total_pending && hipEventQuery(sc->total_event) == hipSuccess) {
+    need = *sc->pinned_total;
+    sc->total_pending = false;
+  }
+  if (sc->cap[SLOT_RAST_LIST] == 0) {
+    DR_CHECK_HIP(hipMemcpyAsync(sc->pinned_total, total, sizeof(int64_t), hipMemcpyDeviceToHost,
+                                stream));
+    DR_CHECK_HIP(hipStreamSynchronize(stream));
+    need = *sc->pinned_total;
+  }
+  int* list = (int*)scratch_get(sc, stream, SLOT_RAST_LIST, (size_t)(need > 0 ? need : 1) * 4);
+  if (!list) return DR_ERR_MEMORY;
+  const int64_t cap = (int64_t)(sc->cap[SLOT_RAST_LIST] / 4);
+
+  if (n_items > 0) {
+    hipLaunchKernelGGL(k_bin_fill, dim3(grid_for(n_items, 256)), dim3(256), 0, stream, it,
+                       n_items, N, rect, ntx, tiles, off, fillc, list, cap);
+    DR_CHECK_LAUNCH();
+  }
+  const dim3 grid((unsigned)n_tiles), block(256);
+#define DR_RASTER(DBV, PV)                                                                    \
+  hipLaunchKernelGGL((k_raster<DBV, PV>), grid, block, 0, stream, rec, rect, it, rec_stride, \
+                     cnt, off, list, cap, peel, N, H, W, ntx, nty, rast, rast_db)
+  if (rast_db) {
+    if (peel) DR_RASTER(true, true); else DR_RASTER(true, false);
+  } else {
+    if (peel) DR_RASTER(false, true); else DR_RASTER(false, false);
+  }
+#undef DR_RASTER
+  DR_CHECK_LAUNCH();
+  DR_CHECK_HIP(hipMemcpyAsync(sc->pinned_total, total, sizeof(int64_t), hipMemcpyDeviceToHost,
+                              stream));
+  DR_CHECK_HIP(hipEventRecord(sc->total_event, stream));
+  sc->total_pending = true;
+  return DR_OK;
+}
+
+extern "C" int dr_rasterize_bwd(const float* pos, int64_t pos_batch_stride, const int32_t* tri,
+                                const float* rast, const float* d_rast, const float* d_rast_db,
+                                int N, int V, int H, int W, float* d_pos, unsigned flags,
+                                dr_stream_t stream_) {
+  hipStream_t stream = (hipStream_t)stream_;
+  DR_CHECK_ARG(N >= 1 && V >= 0 && H >= 1 && W >= 1, "rasterize_bwd: bad sizes");
+  DR_CHECK_ARG(pos && tri && rast && d_rast && d_pos, "rasterize_bwd: null tensor");
+  DR_CHECK_ARG(pos_batch_stride == 0 || pos_batch_stride == (int64_t)V * 4,
+               "rasterize_bwd: pos_batch_stride must be 0 or V*4");
+  const int64_t npos = (pos_batch_stride ? (int64_t)N : 1) * V * 4;
+  if (!(flags & DR_ACCUMULATE)) DR_CHECK_HIP(fill_async(d_pos, 0.0f, npos, stream));
+  const int ntx = (W + kTile - 1) / kTile, nty = (H + kTile - 1) / kTile;
+  const int64_t blocks = (int64_t)N * ntx * nty;
+  hipLaunchKernelGGL(k_raster_bwd, dim3((unsigned)blocks), dim3(256), 0, stream, pos,
+                     pos_batch_stride, tri, rast, d_rast, d_rast_db, N, H, W, ntx, nty, d_pos);
+  DR_CHECK_LAUNCH();
+  return DR_OK;
+}

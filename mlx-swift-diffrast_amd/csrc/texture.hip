@@ -1,0 +1,708 @@
+// texture: mip pyramid, nearest / bilinear / mip-nearest / trilinear / cube
+// sampling, and one fused backward per filter (d_tex or d_pyramid scatter,
+// d_uv, d_uvDA and the mip-bias gradient in a single pass).
+//
+// Semantics follow Sources/MLXDiffRast/Texture.swift of the reference:
+//   boundary modes     :336-354       bilinear   :359-403, :407-521
+//   nearest            :545-605       cube       :616-738
+//   LOD + levels       :764-790       mip fwd    :795-863
+//   mip backward       :870-1102      pyramid    :144-161 (2x2 mean)
+//   mip bias fold      :104-126 (uvDA * 2^map * 2^bias, folded in-kernel)
+// The pyramid is built once per distinct texture (Nt = 1 serves every
+// image), not once per broadcast copy; d_tex of a shared texture is the sum
+// over images, as MLX's broadcast backward gives.
+#include "common.h"
+
+namespace dr {
+
+constexpr int kMaxLevels = 16;
+
+// Pyramid geometry.  Level 0 is the texture itself; levels 1..L-1 live in
+// one buffer, level-major, each [Nt, Hk, Wk, C].
+struct MipDesc {
+  int L;
+  int h[kMaxLevels];
+  int w[kMaxLevels];
+  int64_t off[kMaxLevels];  // float offset of level k (k >= 1) in the pyramid buffer
+};
+
+// Texture.swift:336-354.
+__device__ __forceinline__ int apply_boundary(int t, int size, int mode, float& oob) {
+  if (mode == DR_BOUNDARY_ZERO) {
+    if (t < 0 || t >= size) {
+      oob = 1.0f;
+      return 0;
+    }
+    oob = 0.0f;
+    return t;
+  }
+  if (mode == DR_BOUNDARY_CLAMP) {
+    oob = 0.0f;
+    return t < 0 ? 0 : (t >= size ? size - 1 : t);
+  }
+  oob = 0.0f;
+  int r = t % size;
+  if (r < 0) r += size;
+  return r;
+}
+
+struct Bilin {
+  int ix0, ix1, iy0, iy1;
+  float fx, fy, m00, m10, m01, m11, w00, w10, w01, w11;
+};
+
+// The bilinear footprint of Texture.swift:372-391 (and its copies).
+__device__ __forceinline__ Bilin bilin(float u, float v, int Wk, int Hk, int mode) {
+  Bilin b;
+  const float tx = u * (float)Wk - 0.5f;
+  const float ty = v * (float)Hk - 0.5f;
+  const int tx0 = f2i(floorf(tx)), ty0 = f2i(floorf(ty));
+  const int tx1 = tx0 + 1, ty1 = ty0 + 1;
+  b.fx = tx - (float)tx0;
+  b.fy = ty - (float)ty0;
+  float ox0, ox1, oy0, oy1;
+  b.ix0 = apply_boundary(tx0, Wk, mode, ox0);
+  b.ix1 = apply_boundary(tx1, Wk, mode, ox1);
+  b.iy0 = apply_boundary(ty0, Hk, mode, oy0);
+  b.iy1 = apply_boundary(ty1, Hk, mode, oy1);
+  b.m00 = (1.0f - ox0) * (1.0f - oy0);
+  b.m10 = (1.0f - ox1) * (1.0f - oy0);
+  b.m01 = (1.0f - ox0) * (1.0f - oy1);
+  b.m11 = (1.0f - ox1) * (1.0f - oy1);
+  const float fx = b.fx, fy = b.fy;
+  b.w00 = (1.0f - fx) * (1.0f - fy) * (1.0f - ox0) * (1.0f - oy0);
+  b.w10 = (fx) * (1.0f - fy) * (1.0f - ox1) * (1.0f - oy0);
+  b.w01 = (1.0f - fx) * (fy) * (1.0f - ox0) * (1.0f - oy1);
+  b.w11 = (fx) * (fy) * (1.0f - ox1) * (1.0f - oy1);
+  return b;
+}
+
+// Texture.swift:616-672: cube face + clamped bilinear footprint.
+__device__ __forceinline__ int cube_bilin(float x, float y, float z, int Wt, int Ht, Bilin& b) {
+  const float ax = fabsf(x), ay = fabsf(y), az = fabsf(z);
+  int face;
+  float sc, tc, ma;
+  if (ax >= ay && ax >= az) {
+    ma = ax;
+    if (x > 0.0f) { face = 0; sc = -z; tc = -y; }
+    else          { face = 1; sc = z;  tc = -y; }
+  } else if (ay >= az) {
+    ma = ay;
+    if (y > 0.0f) { face = 2; sc = x; tc = z; }
+    else          { face = 3; sc = x; tc = -z; }
+  } else {
+    ma = az;
+    if (z > 0.0f) { face = 4; sc = x;  tc = -y; }
+    else          { face = 5; sc = -x; tc = -y; }
+  }
+  const float inv_ma = 1.0f / ma;
+  const float u = (sc * inv_ma + 1.0f) * 0.5f;
+  const float v = (tc * inv_ma + 1.0f) * 0.5f;
+  const float txr = u * (float)Wt - 0.5f;
+  const float tyr = v * (float)Ht - 0.5f;
+  const int tx0 = f2i(floorf(txr)), ty0 = f2i(floorf(tyr));
+  const int tx1 = tx0 + 1, ty1 = ty0 + 1;
+  const float fx = txr - (float)tx0, fy = tyr - (float)ty0;
+  b.fx = fx;
+  b.fy = fy;
+  b.ix0 = max(0, min(Wt - 1, tx0));
+  b.ix1 = max(0, min(Wt - 1, tx1));
+  b.iy0 = max(0, min(Ht - 1, ty0));
+  b.iy1 = max(0, min(Ht - 1, ty1));
+  b.m00 = b.m10 = b.m01 = b.m11 = 1.0f;
+  b.w00 = (1.0f - fx) * (1.0f - fy);
+  b.w10 = fx * (1.0f - fy);
+  b.w01 = (1.0f - fx) * fy;
+  b.w11 = fx * fy;
+  return face;
+}
+
+// Texture.swift:764-790 on the bias-folded derivatives.
+struct Lod {
+  int k0, k1;
+  float frac;
+};
+
+__device__ __forceinline__ Lod mip_lod(float4 da, int Ht, int Wt, int L, bool linear) {
+  const float sx = da.x * (float)Wt, sy = da.y * (float)Wt;
+  const float tx = da.z * (float)Ht, ty = da.w * (float)Ht;
+  const float rho_sq = fmaxf(sx * sx + tx * tx, sy * sy + ty * ty);
+  float lod = 0.5f * log2f(fmaxf(rho_sq, 1e-20f));
+  lod = fmaxf(0.0f, fminf((float)(L - 1), lod));
+  Lod r;
+  if (linear) {
+    r.k0 = f2i(floorf(lod));
+    r.k1 = min(r.k0 + 1, L - 1);
+    r.frac = lod - (float)r.k0;
+  } else {
+    r.k0 = min(f2i(floorf(lod + 0.5f)), L - 1);
+    r.k1 = r.k0;
+    r.frac = 0.0f;
+  }
+  return r;
+}
+
+// uvDA * (2^map * 2^bias) (Texture.swift:109-126).  scale_bias = 2^bias.
+__device__ __forceinline__ float bias_scale(const float* __restrict__ bias_map, int64_t pix,
+                                            float scale_bias, bool has_bias) {
+  if (bias_map) {
+    const float s = exp2f(bias_map[pix]);
+    return has_bias ? s * scale_bias : s;
+  }
+  return scale_bias;
+}
+
+template <int CT>
+__device__ __forceinline__ int dimC(int C) { return CT > 0 ? CT : C; }
+
+// Loads channels [0,C) of one texel.
+template <int CT>
+__device__ __forceinline__ void load_texel(const float* __restrict__ p, int C, float* out) {
+  if (CT == 4) {
+    const float4 q = *reinterpret_cast<const float4*>(p);
+    out[0] = q.x; out[1] = q.y; out[2] = q.z; out[3] = q.w;
+  } else {
+#pragma unroll
+    for (int c = 0; c < dimC<CT>(C); ++c) out[c] = p[c];
+  }
+}
+
+constexpr int kMaxC = 4;  // register arrays for compile-time C; larger C uses CT = 0
+
+// ---------------------------------------------------------------------------
+// forward
+// ---------------------------------------------------------------------------
+
+template <int FILTER, bool CUBE, int CT>
+__global__ void __launch_bounds__(256) k_tex_fwd(
+    const float* __restrict__ tex, const float* __restrict__ pyr, MipDesc md, int64_t tex_stride,
+    int Ht, int Wt, int C_, const float* __restrict__ uv, const float* __restrict__ uv_da,
+    const float* __restrict__ bias_map, float scale_bias, int has_bias, int boundary, int64_t P,
+    int HWi, float* __restrict__ out) {
+  const int64_t pix = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (pix >= P) return;
+  const int C = dimC<CT>(C_);
+  const int n = (int)(pix / HWi);
+  float* o = out + pix * C;
+  if (CUBE) {  // Texture.swift:638-684
+    const float x = uv[pix * 3 + 0], y = uv[pix * 3 + 1], z = uv[pix * 3 + 2];
+    Bilin b;
+    const int face = cube_bilin(x, y, z, Wt, Ht, b);
+    const float* fb = tex + n * tex_stride + (int64_t)face * Ht * Wt * C;
+    for (int c = 0; c < C; ++c) {
+      const float t00 = fb[((int64_t)b.iy0 * Wt + b.ix0) * C + c];
+      const float t10 = fb[((int64_t)b.iy0 * Wt + b.ix1) * C + c];
+      const float t01 = fb[((int64_t)b.iy1 * Wt + b.ix0) * C + c];
+      const float t11 = fb[((int64_t)b.iy1 * Wt + b.ix1) * C + c];
+      o[c] = b.w00 * t00 + b.w10 * t10 + b.w01 * t01 + b.w11 * t11;
+    }
+    return;
+  }
+  const float2 uvp = *reinterpret_cast<const float2*>(uv + pix * 2);
+  if (FILTER == DR_FILTER_NEAREST) {  // Texture.swift:545-572
+    const int tx = f2i(floorf(uvp.x * (float)Wt));
+    const int ty = f2i(floorf(uvp.y * (float)Ht));
+    float ox, oy;
+    const int ix = apply_boundary(tx, Wt, boundary, ox);
+    const int iy = apply_boundary(ty, Ht, boundary, oy);
+    const float mask = (1.0f - ox) * (1.0f - oy);
+    const float* tp = tex + n * tex_stride + ((int64_t)iy * Wt + ix) * C;
+    for (int c = 0; c < C; ++c) o[c] = tp[c] * mask;
+    return;
+  }
+  if (FILTER == DR_FILTER_LINEAR) {  // Texture.swift:359-403
+    const Bilin b = bilin(uvp.x, uvp.y, Wt, Ht, boundary);
+    const float* tb = tex + n * tex_stride;
+    if (CT > 0) {
+      float t00[kMaxC], t10[kMaxC], t01[kMaxC], t11[kMaxC];
+      load_texel<CT>(tb + ((int64_t)b.iy0 * Wt + b.ix0) * C, C, t00);
+      load_texel<CT>(tb + ((int64_t)b.iy0 * Wt + b.ix1) * C, C, t10);
+      load_texel<CT>(tb + ((int64_t)b.iy1 * Wt + b.ix0) * C, C, t01);
+      load_texel<CT>(tb + ((int64_t)b.iy1 * Wt + b.ix1) * C, C, t11);
+#pragma unroll
+      for (int c = 0; c < (CT > 0 ? CT : 1); ++c)
+        o[c] = b.w00 * t00[c] + b.w10 * t10[c] + b.w01 * t01[c] + b.w11 * t11[c];
+    } else {
+      for (int c = 0; c < C; ++c) {
+        const float t00 = tb[((int64_t)b.iy0 * Wt + b.ix0) * C + c];
+        const float t10 = tb[((int64_t)b.iy0 * Wt + b.ix1) * C + c];
+        const float t01 = tb[((int64_t)b.iy1 * Wt + b.ix0) * C + c];
+        const float t11 = tb[((int64_t)b.iy1 * Wt + b.ix1) * C + c];
+        o[c] = b.w00 * t00 + b.w10 * t10 + b.w01 * t01 + b.w11 * t11;
+      }
+    }
+    return;
+  }
+  // Mip filters (Texture.swift:795-863).
+  float4 da = *reinterpret_cast<const float4*>(uv_da + pix * 4);
+  const float s = bias_scale(bias_map, pix, scale_bias, has_bias != 0);
+  if (bias_map || has_bias) da = make_float4(da.x * s, da.y * s, da.z * s, da.w * s);
+  const Lod ld = mip_lod(da, Ht, Wt, md.L, FILTER == DR_FILTER_LINEAR_MIPMAP_LINEAR);
+  const bool shared = tex_stride == 0;
+  for (int li = 0; li < 2; ++li) {
+    const int k = li == 0 ? ld.k0 : ld.k1;
+    const int Hk = md.h[k], Wk = md.w[k];
+    const float* lv = k == 0 ? tex + n * tex_stride
+                             : pyr + md.off[k] + (shared ? 0 : (int64_t)n * Hk * Wk * C);
+    const Bilin b = bilin(uvp.x, uvp.y, Wk, Hk, boundary);
+    const float wgt = li == 0 ? (1.0f - ld.frac) : ld.frac;
+    for (int c = 0; c < C; ++c) {
+      const float t00 = lv[((int64_t)b.iy0 * Wk + b.ix0) * C + c];
+      const float t10 = lv[((int64_t)b.iy0 * Wk + b.ix1) * C + c];
+      const float t01 = lv[((int64_t)b.iy1 * Wk + b.ix0) * C + c];
+      const float t11 = lv[((int64_t)b.iy1 * Wk + b.ix1) * C + c];
+      const float sample = b.w00 * t00 + b.w10 * t10 + b.w01 * t01 + b.w11 * t11;
+      if (li == 0) o[c] = wgt * sample;  // two roundings, as :855 / :858
+      else o[c] = o[c] + wgt * sample;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// backward
+// ---------------------------------------------------------------------------
+
+// Scatter of one bilinear footprint's gradient (w * g * scale) into one
+// level; lanes hitting the same footprint are summed first.
+template <int CT>
+__device__ __forceinline__ void scatter_footprint(bool valid, float* __restrict__ base, int Wk,
+                                                  int C, const Bilin& b, const float* g,
+                                                  float scale) {
+  const int64_t o00 = ((int64_t)b.iy0 * Wk + b.ix0) * C, o10 = ((int64_t)b.iy0 * Wk + b.ix1) * C;
+  const int64_t o01 = ((int64_t)b.iy1 * Wk + b.ix0) * C, o11 = ((int64_t)b.iy1 * Wk + b.ix1) * C;
+  const uint64_t key = (uint64_t)(base + o00);
+  const uint32_t key2 = ((uint32_t)b.ix1 << 16) ^ (uint32_t)b.iy1;
+  if (CT > 0) {
+    float val[4 * (CT > 0 ? CT : 1)];
+    float* addr[4 * (CT > 0 ? CT : 1)];
+#pragma unroll
+    for (int c = 0; c < (CT > 0 ? CT : 1); ++c) {
+      const float gc = valid ? g[c] * scale : 0.0f;
+      val[4 * c + 0] = b.w00 * gc;
+      val[4 * c + 1] = b.w10 * gc;
+      val[4 * c + 2] = b.w01 * gc;
+      val[4 * c + 3] = b.w11 * gc;
+      addr[4 * c + 0] = base + o00 + c;
+      addr[4 * c + 1] = base + o10 + c;
+      addr[4 * c + 2] = base + o01 + c;
+      addr[4 * c + 3] = base + o11 + c;
+    }
+    group_atomic_add<4 * (CT > 0 ? CT : 1)>(valid, key, addr, val, key2);
+  } else {
+    for (int c = 0; c < C; ++c) {
+      const float gc = valid ? g[c] * scale : 0.0f;
+      float val[4] = {b.w00 * gc, b.w10 * gc, b.w01 * gc, b.w11 * gc};
+      float* addr[4] = {base + o00 + c, base + o10 + c, base + o01 + c, base + o11 + c};
+      group_atomic_add<4>(valid, key, addr, val, key2);
+    }
+  }
+}
+
+// d_uv terms of one level (Texture.swift:500-520 / :979-995), summed over C.
+__device__ __forceinline__ void duv_level(const float* __restrict__ lv, int Wk, int C,
+                                          const Bilin& b, const float* g, float scale,
+                                          float& dfx, float& dfy, float& dlod_sample) {
+  dfx = 0.0f;
+  dfy = 0.0f;
+  dlod_sample = 0.0f;
+  for (int c = 0; c < C; ++c) {
+    const float r00 = lv[((int64_t)b.iy0 * Wk + b.ix0) * C + c];
+    const float r10 = lv[((int64_t)b.iy0 * Wk + b.ix1) * C + c];
+    const float r01 = lv[((int64_t)b.iy1 * Wk + b.ix0) * C + c];
+    const float r11 = lv[((int64_t)b.iy1 * Wk + b.ix1) * C + c];
+    const float t00 = r00 * b.m00, t10 = r10 * b.m10, t01 = r01 * b.m01, t11 = r11 * b.m11;
+    const float gc = g[c] * scale;
+    dfx += gc * ((1.0f - b.fy) * (t10 - t00) + b.fy * (t11 - t01));
+    dfy += gc * ((1.0f - b.fx) * (t01 - t00) + b.fx * (t11 - t10));
+    const float sample = b.w00 * r00 + b.w10 * r10 + b.w01 * r01 + b.w11 * r11;
+    dlod_sample += sample * g[c];
+  }
+}
+
+template <int FILTER, bool CUBE, int CT>
+__global__ void __launch_bounds__(256) k_tex_bwd(
+    const float* __restrict__ tex, const float* __restrict__ pyr, MipDesc md, int64_t tex_stride,
+    int Ht, int Wt, int C_, const float* __restrict__ uv, const float* __restrict__ uv_da,
+    const float* __restrict__ bias_map, float scale_bias, int has_bias, int boundary, int N,
+    int Hi, int Wi, int ntx, int nty, const float* __restrict__ d_out, float* __restrict__ d_tex,
+    float* __restrict__ d_pyr, float* __restrict__ d_uv, float* __restrict__ d_uv_da,
+    float* __restrict__ d_bias) {
+  const int tiles = ntx * nty;
+  const int bidx = (int)blockIdx.x;
+  const int n = bidx / tiles;
+  const int tile = bidx - n * tiles;
+  const int ty = tile / ntx, tx = tile - ty * ntx;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int qx0 = tx * 16 + (wave & 1) * 8, qy0 = ty * 16 + (wave >> 1) * 8;
+  if (qx0 >= Wi || qy0 >= Hi) return;
+  const int pw = qx0 + (lane & 7), ph = qy0 + (lane >> 3);
+  const bool valid = pw < Wi && ph < Hi;
+  const int64_t pix = ((int64_t)n * Hi + min(ph, Hi - 1)) * Wi + min(pw, Wi - 1);
+  const int C = dimC<CT>(C_);
+  float g[CT > 0 ? CT : kMaxC];
+  const float* gp = d_out + pix * C;
+  float* dt = d_tex + n * tex_stride;  // tex_stride 0: shared texture
+
+  if (CUBE) {  // Texture.swift:686-738 (d_dir is zero: :196-198)
+    const float x = uv[pix * 3 + 0], y = uv[pix * 3 + 1], z = uv[pix * 3 + 2];
+    Bilin b;
+    const int face = cube_bilin(x, y, z, Wt, Ht, b);
+    float* fb = dt + (int64_t)face * Ht * Wt * C;
+    if (CT > 0) {
+#pragma unroll
+      for (int c = 0; c < (CT > 0 ? CT : 1); ++c) g[c] = gp[c];
+      scatter_footprint<CT>(valid, fb, Wt, C, b, g, 1.0f);
+    } else {
+      for (int c = 0; c < C; ++c) {
+        const float gc = valid ? gp[c] : 0.0f;
+        float val[4] = {b.w00 * gc, b.w10 * gc, b.w01 * gc, b.w11 * gc};
+        float* addr[4] = {fb + ((int64_t)b.iy0 * Wt + b.ix0) * C + c,
+                          fb + ((int64_t)b.iy0 * Wt + b.ix1) * C + c,
+                          fb + ((int64_t)b.iy1 * Wt + b.ix0) * C + c,
+                          fb + ((int64_t)b.iy1 * Wt + b.ix1) * C + c};
+        group_atomic_add<4>(valid, (uint64_t)addr[0], addr, val,
+                            ((uint32_t)b.ix1 << 16) ^ (uint32_t)b.iy1);
+      }
+    }
+    if (d_uv && valid) {
+      d_uv[pix * 3 + 0] = 0.0f;
+      d_uv[pix * 3 + 1] = 0.0f;
+      d_uv[pix * 3 + 2] = 0.0f;
+    }
+    return;
+  }
+
+  const float2 uvp = *reinterpret_cast<const float2*>(uv + pix * 2);
+  if (FILTER == DR_FILTER_NEAREST) {  // Texture.swift:576-605; d_uv = 0 (:234)
+    const int txi = f2i(floorf(uvp.x * (float)Wt));
+    const int tyi = f2i(floorf(uvp.y * (float)Ht));
+    float ox, oy;
+    const int ix = apply_boundary(txi, Wt, boundary, ox);
+    const int iy = apply_boundary(tyi, Ht, boundary, oy);
+    const float mask = (1.0f - ox) * (1.0f - oy);
+    float* tp = dt + ((int64_t)iy * Wt + ix) * C;
+    for (int c = 0; c < C; ++c) {
+      float val[1] = {valid ? gp[c] * mask : 0.0f};
+      float* addr[1] = {tp + c};
+      group_atomic_add<1>(valid, (uint64_t)tp, addr, val);
+    }
+    if (d_uv && valid) *reinterpret_cast<float2*>(d_uv + pix * 2) = make_float2(0.0f, 0.0f);
+    return;
+  }
+
+  for (int c = 0; c < C && c < (CT > 0 ? CT : kMaxC); ++c) g[c] = valid ? gp[c] : 0.0f;
+  const float* gsrc = CT > 0 ? g : gp;  // run-time C reads d_out directly
+
+  if (FILTER == DR_FILTER_LINEAR) {  // Texture.swift:407-521
+    const Bilin b = bilin(uvp.x, uvp.y, Wt, Ht, boundary);
+    const float* tb = tex + n * tex_stride;
+    scatter_footprint<CT>(valid, dt, Wt, C, b, gsrc, 1.0f);
+    if (d_uv && valid) {
+      float dfx, dfy, unused;
+      duv_level(tb, Wt, C, b, gsrc, 1.0f, dfx, dfy, unused);
+      *reinterpret_cast<float2*>(d_uv + pix * 2) = make_float2(dfx * (float)Wt, dfy * (float)Ht);
+    }
+    return;
+  }
+
+  // Mip filters: Texture.swift:870-1102 fused.
+  const float4 da_in = *reinterpret_cast<const float4*>(uv_da + pix * 4);
+  const float s = bias_scale(bias_map, pix, scale_bias, has_bias != 0);
+  const bool scaled = bias_map || has_bias;
+  const float4 da = scaled ? make_float4(da_in.x * s, da_in.y * s, da_in.z * s, da_in.w * s) : da_in;
+  const bool linear = FILTER == DR_FILTER_LINEAR_MIPMAP_LINEAR;
+  const Lod ld = mip_lod(da, Ht, Wt, md.L, linear);
+  const bool shared = tex_stride == 0;
+  auto level_ptr = [&](int k) -> const float* {
+    return k == 0 ? tex + n * tex_stride
+                  : pyr + md.off[k] + (shared ? 0 : (int64_t)n * md.h[k] * md.w[k] * C);
+  };
+  auto dlevel_ptr = [&](int k) -> float* {
+    return k == 0 ? dt : d_pyr + md.off[k] + (shared ? 0 : (int64_t)n * md.h[k] * md.w[k] * C);
+  };
+  float dfx_total = 0.0f, dfy_total = 0.0f;
+  float samp[2] = {0.0f, 0.0f};  // sum_c g_c * sample_c per level (for d_lod)
+  for (int li = 0; li < 2; ++li) {
+    const int k = li == 0 ? ld.k0 : ld.k1;
+    const float scale = li == 0 ? (1.0f - ld.frac) : ld.frac;
+    const int Hk = md.h[k], Wk = md.w[k];
+    const Bilin b = bilin(uvp.x, uvp.y, Wk, Hk, boundary);
+    // A zero weight adds nothing; skip the level's atomics (but keep the
+    // wave convergent for the grouping).
+    scatter_footprint<CT>(valid && scale != 0.0f, dlevel_ptr(k), Wk, C, b, gsrc, scale);
+    if (valid) {
+      float dfx, dfy;
+      duv_level(level_ptr(k), Wk, C, b, gsrc, scale, dfx, dfy, samp[li]);
+      dfx_total += dfx * (float)Wk;
+      dfy_total += dfy * (float)Hk;
+    }
+  }
+  if (!valid) return;
+  if (d_uv) *reinterpret_cast<float2*>(d_uv + pix * 2) = make_float2(dfx_total, dfy_total);
+  if (!d_uv_da && !d_bias) return;
+  // Texture.swift:1011-1102 (mip-nearest also takes this trilinear surrogate).
+  const float sx = da.x * (float)Wt, sy = da.y * (float)Wt;
+  const float tx_ = da.z * (float)Ht, ty_ = da.w * (float)Ht;
+  const float Asq = sx * sx + tx_ * tx_;
+  const float Bsq = sy * sy + ty_ * ty_;
+  const float rho_sq = fmaxf(Asq, Bsq);
+  const float lod_raw = 0.5f * log2f(fmaxf(rho_sq, 1e-20f));
+  float4 d_eff = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (!(lod_raw <= 0.0f || lod_raw >= (float)(md.L - 1))) {
+    float d_lod;
+    const int k0 = f2i(floorf(lod_raw));
+    if (linear) {
+      d_lod = -samp[0] + samp[1];
+    } else {
+      const int k1 = min(k0 + 1, md.L - 1);
+      float s0 = 0.0f, s1 = 0.0f, u0, u1;
+      const Bilin b0 = bilin(uvp.x, uvp.y, md.w[k0], md.h[k0], boundary);
+      duv_level(level_ptr(k0), md.w[k0], C, b0, gsrc, 0.0f, u0, u1, s0);
+      const Bilin b1 = bilin(uvp.x, uvp.y, md.w[k1], md.h[k1], boundary);
+      duv_level(level_ptr(k1), md.w[k1], C, b1, gsrc, 0.0f, u0, u1, s1);
+      d_lod = -s0 + s1;
+    }
+    const float ln2 = 0.6931471805599453f;
+    const float dlod_drho_sq = 1.0f / (2.0f * rho_sq * ln2);
+    const float A_is_max = (Asq >= Bsq) ? 1.0f : 0.0f;
+    const float B_is_max = 1.0f - A_is_max;
+    d_eff = make_float4(d_lod * dlod_drho_sq * A_is_max * 2.0f * sx * (float)Wt,
+                        d_lod * dlod_drho_sq * B_is_max * 2.0f * sy * (float)Wt,
+                        d_lod * dlod_drho_sq * A_is_max * 2.0f * tx_ * (float)Ht,
+                        d_lod * dlod_drho_sq * B_is_max * 2.0f * ty_ * (float)Ht);
+  }
+  // Backward of the bias fold: d_uvDA = d_eff * scale,
+  // d_map = sum_c(d_eff_c * uvDA_c) * scale * ln 2.
+  if (d_uv_da) {
+    const float4 o = scaled ? make_float4(d_eff.x * s, d_eff.y * s, d_eff.z * s, d_eff.w * s) : d_eff;
+    *reinterpret_cast<float4*>(d_uv_da + pix * 4) = o;
+  }
+  if (d_bias && bias_map) {
+    const float gm = d_eff.x * da_in.x + d_eff.y * da_in.y + d_eff.z * da_in.z + d_eff.w * da_in.w;
+    d_bias[pix] = gm * s * 0.6931471805599453f;
+  }
+}
+
+// Texture.swift:156: level k = 2x2 mean of level k-1.
+__global__ void __launch_bounds__(256) k_mip_down(const float* __restrict__ src,
+                                                  float* __restrict__ dst, int Nt, int h, int w,
+                                                  int C) {
+  const int h2 = h / 2, w2 = w / 2;
+  const int64_t total = (int64_t)Nt * h2 * w2 * C;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const int c = (int)(i % C);
+  int64_t r = i / C;
+  const int x = (int)(r % w2);
+  r /= w2;
+  const int y = (int)(r % h2);
+  const int n = (int)(r / h2);
+  const float* s = src + (int64_t)n * h * w * C;
+  const float a = s[((int64_t)(2 * y) * w + 2 * x) * C + c];
+  const float b = s[((int64_t)(2 * y) * w + 2 * x + 1) * C + c];
+  const float d = s[((int64_t)(2 * y + 1) * w + 2 * x) * C + c];
+  const float e = s[((int64_t)(2 * y + 1) * w + 2 * x + 1) * C + c];
+  dst[i] = (((a + b) + d) + e) * 0.25f;
+}
+
+// Backward of the pyramid (MLX autodiff of concatenate + mean): level k's
+// total cotangent is its own gradient plus 1/4 of level k+1's total,
+// accumulated from the coarsest level down; level 0's total is added to
+// d_tex (which already holds level 0's own gradient).
+__global__ void __launch_bounds__(256) k_mip_collapse(const float* __restrict__ d_pyr, MipDesc md,
+                                                      int Nt, int C, float* __restrict__ d_tex) {
+  const int64_t total = (int64_t)Nt * md.h[0] * md.w[0] * C;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total || md.L < 2) return;
+  const int c = (int)(i % C);
+  int64_t r = i / C;
+  const int x = (int)(r % md.w[0]);
+  r /= md.w[0];
+  const int y = (int)(r % md.h[0]);
+  const int n = (int)(r / md.h[0]);
+  const int kL = md.L - 1;
+  auto at = [&](int k) {
+    const int yk = y >> k, xk = x >> k;
+    return d_pyr[md.off[k] + (((int64_t)n * md.h[k] + yk) * md.w[k] + xk) * C + c];
+  };
+  float acc = at(kL);
+  for (int k = kL - 1; k >= 1; --k) acc = at(k) + acc * 0.25f;
+  d_tex[i] = d_tex[i] + acc * 0.25f;
+}
+
+}  // namespace dr
+
+using namespace dr;
+
+static int build_desc(int Ht, int Wt, int C, int Nt, int L, MipDesc& md) {
+  DR_CHECK_ARG(L >= 1 && L <= kMaxLevels, "texture: mip level count out of range");
+  md.L = L;
+  int h = Ht, w = Wt;
+  int64_t off = 0;
+  for (int k = 0; k < L; ++k) {
+    md.h[k] = h;
+    md.w[k] = w;
+    md.off[k] = k == 0 ? 0 : off;
+    if (k > 0) off += (int64_t)Nt * h * w * C;
+    if (k + 1 < L) {
+      DR_CHECK_ARG(h >= 2 && w >= 2 && h % 2 == 0 && w % 2 == 0,
+                   "texture: mip levels need even sizes down to the last level");
+      h /= 2;
+      w /= 2;
+    }
+  }
+  for (int k = L; k < kMaxLevels; ++k) {
+    md.h[k] = md.w[k] = 1;
+    md.off[k] = 0;
+  }
+  return DR_OK;
+}
+
+extern "C" int dr_texture_mip_levels(int H, int W, int max_level, int32_t* level_h,
+                                     int32_t* level_w) {
+  int n = 0;
+  if (level_h) level_h[n] = H;
+  if (level_w) level_w[n] = W;
+  ++n;
+  while (H >= 2 && W >= 2 && H % 2 == 0 && W % 2 == 0 && n < 32) {
+    if (max_level >= 0 && n > max_level) break;
+    H /= 2;
+    W /= 2;
+    if (level_h) level_h[n] = H;
+    if (level_w) level_w[n] = W;
+    ++n;
+  }
+  return n;
+}
+
+extern "C" int64_t dr_texture_mip_size(int Nt, int H, int W, int C, int L) {
+  int64_t s = 0;
+  for (int k = 1; k < L; ++k) {
+    H /= 2;
+    W /= 2;
+    s += (int64_t)Nt * H * W * C;
+  }
+  return s;
+}
+
+extern "C" int dr_texture_build_mip(const float* tex, int Nt, int H, int W, int C, int L,
+                                    float* pyramid, dr_stream_t stream_) {
+  hipStream_t stream = (hipStream_t)stream_;
+  (void)hipGetLastError();
+  DR_CHECK_ARG(tex && Nt >= 1 && C >= 1, "texture_build_mip: bad arguments");
+  MipDesc md;
+  int st = build_desc(H, W, C, Nt, L, md);
+  if (st) return st;
+  if (L > 1) DR_CHECK_ARG(pyramid != nullptr, "texture_build_mip: null pyramid");
+  for (int k = 1; k < L; ++k) {
+    const float* src = k == 1 ? tex : pyramid + md.off[k - 1];
+    const int64_t n = (int64_t)Nt * md.h[k] * md.w[k] * C;
+    hipLaunchKernelGGL(k_mip_down, dim3(grid_for(n, 256)), dim3(256), 0, stream, src,
+                       pyramid + md.off[k], Nt, md.h[k - 1], md.w[k - 1], C);
+    DR_CHECK_LAUNCH();
+  }
+  return DR_OK;
+}
+
+static int check_tex(const float* tex, const float* pyr, int Nt, int N, int Ht, int Wt, int C,
+                     int L, const float* uv, const float* uv_da, int filter, int boundary,
+                     MipDesc& md) {
+  DR_CHECK_ARG(tex && uv && N >= 1 && Ht >= 1 && Wt >= 1 && C >= 1, "texture: bad arguments");
+  DR_CHECK_ARG(Nt == 1 || Nt == N, "texture: tex batch dim incompatible with uv batch");
+  DR_CHECK_ARG(filter >= 0 && filter <= 3 && boundary >= 0 && boundary <= 3,
+               "texture: bad filter / boundary");
+  DR_CHECK_ARG(boundary != DR_BOUNDARY_CUBE || filter == DR_FILTER_LINEAR,
+               "texture: cube textures currently support filterMode .linear only");
+  const bool mip = filter >= DR_FILTER_LINEAR_MIPMAP_NEAREST && boundary != DR_BOUNDARY_CUBE;
+  if (mip) {
+    DR_CHECK_ARG(uv_da != nullptr, "texture: mipmap filterModes require uvDA");
+    DR_CHECK_ARG(L == 1 || pyr != nullptr, "texture: mip pyramid missing");
+    return build_desc(Ht, Wt, C, Nt, L, md);
+  }
+  return build_desc(Ht, Wt, C, Nt, 1, md);
+}
+
+#define DR_TEX_C_DISPATCH(KERNEL, F, CUBEV, GRID, ...)                                       \
+  do {                                                                                        \
+    switch (C) {                                                                              \
+      case 1: hipLaunchKernelGGL((KERNEL<F, CUBEV, 1>), GRID, dim3(256), 0, stream, __VA_ARGS__); break; \
+      case 2: hipLaunchKernelGGL((KERNEL<F, CUBEV, 2>), GRID, dim3(256), 0, stream, __VA_ARGS__); break; \
+      case 3: hipLaunchKernelGGL((KERNEL<F, CUBEV, 3>), GRID, dim3(256), 0, stream, __VA_ARGS__); break; \
+      case 4: hipLaunchKernelGGL((KERNEL<F, CUBEV, 4>), GRID, dim3(256), 0, stream, __VA_ARGS__); break; \
+      default: hipLaunchKernelGGL((KERNEL<F, CUBEV, 0>), GRID, dim3(256), 0, stream, __VA_ARGS__); break; \
+    }                                                                                         \
+  } while (0)
+
+#define DR_TEX_DISPATCH(KERNEL, GRID, ...)                                                              \
+  do {                                                                                                  \
+    if (boundary == DR_BOUNDARY_CUBE) DR_TEX_C_DISPATCH(KERNEL, DR_FILTER_LINEAR, true, GRID, __VA_ARGS__); \
+    else if (filter == DR_FILTER_NEAREST) DR_TEX_C_DISPATCH(KERNEL, DR_FILTER_NEAREST, false, GRID, __VA_ARGS__); \
+    else if (filter == DR_FILTER_LINEAR) DR_TEX_C_DISPATCH(KERNEL, DR_FILTER_LINEAR, false, GRID, __VA_ARGS__); \
+    else if (filter == DR_FILTER_LINEAR_MIPMAP_NEAREST) DR_TEX_C_DISPATCH(KERNEL, DR_FILTER_LINEAR_MIPMAP_NEAREST, false, GRID, __VA_ARGS__); \
+    else DR_TEX_C_DISPATCH(KERNEL, DR_FILTER_LINEAR_MIPMAP_LINEAR, false, GRID, __VA_ARGS__);   \
+  } while (0)
+
+extern "C" int dr_texture_fwd(const float* tex, const float* pyramid, int Nt, int Ht, int Wt,
+                              int C, int L, const float* uv, const float* uv_da,
+                              const float* bias_map, float bias, int filter, int boundary, int N,
+                              int Hi, int Wi, float* out, dr_stream_t stream_) {
+  hipStream_t stream = (hipStream_t)stream_;
+  (void)hipGetLastError();
+  MipDesc md;
+  int st = check_tex(tex, pyramid, Nt, N, Ht, Wt, C, L, uv, uv_da, filter, boundary, md);
+  if (st) return st;
+  DR_CHECK_ARG(out != nullptr && Hi >= 1 && Wi >= 1, "texture: bad output");
+  const bool cube = boundary == DR_BOUNDARY_CUBE;
+  const int64_t tex_stride = Nt == 1 ? 0 : (int64_t)(cube ? 6 : 1) * Ht * Wt * C;
+  const int64_t P = (int64_t)N * Hi * Wi;
+  const float scale_bias = exp2f(bias);
+  const int has_bias = bias != 0.0f;
+  const dim3 grid(grid_for(P, 256));
+  DR_TEX_DISPATCH(k_tex_fwd, grid, tex, pyramid, md, tex_stride, Ht, Wt, C, uv, uv_da, bias_map,
+                  scale_bias, has_bias, boundary, P, Hi * Wi, out);
+  DR_CHECK_LAUNCH();
+  return DR_OK;
+}
+
+extern "C" int dr_texture_bwd(const float* tex, const float* pyramid, int Nt, int Ht, int Wt,
+                              int C, int L, const float* uv, const float* uv_da,
+                              const float* bias_map, float bias, int filter, int boundary, int N,
+                              int Hi, int Wi, const float* d_out, float* d_tex, float* d_uv,
+                              float* d_uv_da, float* d_bias_map, unsigned flags,
+                              dr_stream_t stream_) {
+  hipStream_t stream = (hipStream_t)stream_;
+  (void)hipGetLastError();
+  MipDesc md;
+  int st = check_tex(tex, pyramid, Nt, N, Ht, Wt, C, L, uv, uv_da, filter, boundary, md);
+  if (st) return st;
+  DR_CHECK_ARG(d_out && d_tex && Hi >= 1 && Wi >= 1, "texture_bwd: null tensor");
+  const bool cube = boundary == DR_BOUNDARY_CUBE;
+  const bool mip = !cube && filter >= DR_FILTER_LINEAR_MIPMAP_NEAREST;
+  const int64_t tex_stride = Nt == 1 ? 0 : (int64_t)(cube ? 6 : 1) * Ht * Wt * C;
+  const int64_t ntex = (int64_t)Nt * (cube ? 6 : 1) * Ht * Wt * C;
+  if (!(flags & DR_ACCUMULATE)) DR_CHECK_HIP(fill_async(d_tex, 0.0f, ntex, stream));
+  float* d_pyr = nullptr;
+  if (mip && md.L > 1) {
+    Scratch* sc = scratch_for(stream);
+    if (!sc) return DR_ERR_HIP;
+    const int64_t np = dr_texture_mip_size(Nt, Ht, Wt, C, md.L);
+    d_pyr = (float*)scratch_get(sc, stream, SLOT_DPYR, (size_t)np * sizeof(float));
+    if (!d_pyr) return DR_ERR_MEMORY;
+    DR_CHECK_HIP(fill_async(d_pyr, 0.0f, np, stream));
+  }
+  const float scale_bias = exp2f(bias);
+  const int has_bias = bias != 0.0f;
+  const int ntx = (Wi + 15) / 16, nty = (Hi + 15) / 16;
+  const dim3 grid((unsigned)((int64_t)N * ntx * nty));
+  DR_TEX_DISPATCH(k_tex_bwd, grid, tex, pyramid, md, tex_stride, Ht, Wt, C, uv, uv_da, bias_map,
+                  scale_bias, has_bias, boundary, N, Hi, Wi, ntx, nty, d_out, d_tex, d_pyr, d_uv,
+                  mip ? d_uv_da : nullptr, mip ? d_bias_map : nullptr);
+  DR_CHECK_LAUNCH();
+  if (d_pyr) {
+    const int64_t n0 = (int64_t)Nt * Ht * Wt * C;
+    hipLaunchKernelGGL(k_mip_collapse, dim3(grid_for(n0, 256)), dim3(256), 0, stream, d_pyr, md,
+                       Nt, C, d_tex);
+    DR_CHECK_LAUNCH();
+  }
+  return DR_OK;
+}

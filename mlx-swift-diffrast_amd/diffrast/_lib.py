@@ -1,0 +1,74 @@
+"""ctypes binding of libdiffrast_mi355x.so (the C ABI in include/diffrast_mi355x.h).
+
+There is no fallback: if the library is missing or cannot be loaded, every
+op raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libdiffrast_mi355x.so")
+
+_p = ctypes.c_void_p
+_i = ctypes.c_int
+_i64 = ctypes.c_int64
+_u = ctypes.c_uint
+_f = ctypes.c_float
+
+# Every exported function and its argument types, in header order.
+SIGNATURES = {
+    "dr_abi_version": ([], _i),
+    "dr_get_last_error": ([], ctypes.c_char_p),
+    "dr_release_scratch": ([], _i),
+    "dr_rasterize_fwd": ([_p, _i64, _p, _p, _p, _i, _i, _i, _i, _i, _p, _p, _p], _i),
+    "dr_rasterize_bwd": ([_p, _i64, _p, _p, _p, _p, _i, _i, _i, _i, _p, _u, _p], _i),
+    "dr_interpolate_fwd": ([_p, _i64, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p, _p, _p], _i),
+    "dr_interpolate_bwd": ([_p, _i64, _p, _p, _p, _p, _i, _p, _p, _i, _i, _i, _i, _i, _p, _i64,
+                            _p, _p, _u, _p], _i),
+    "dr_texture_mip_levels": ([_i, _i, _i, _p, _p], _i),
+    "dr_texture_mip_size": ([_i, _i, _i, _i, _i], _i64),
+    "dr_texture_build_mip": ([_p, _i, _i, _i, _i, _i, _p, _p], _i),
+    "dr_texture_fwd": ([_p, _p, _i, _i, _i, _i, _i, _p, _p, _p, _f, _i, _i, _i, _i, _i, _p, _p],
+                       _i),
+    "dr_texture_bwd": ([_p, _p, _i, _i, _i, _i, _i, _p, _p, _p, _f, _i, _i, _i, _i, _i, _p, _p,
+                        _p, _p, _p, _u, _p], _i),
+    "dr_antialias_topology": ([_p, _i, _p, _p], _i),
+    "dr_antialias_fwd": ([_p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p, _p], _i),
+    "dr_antialias_bwd": ([_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p, _p, _u, _p], _i),
+}
+
+DR_OK, DR_ERR_ARGUMENT, DR_ERR_HIP, DR_ERR_MEMORY = 0, 1, 2, 3
+DR_ACCUMULATE = 1
+ABI_VERSION = 1
+
+_lib = None
+
+
+def load():
+    """Loads the library once; raises if it is missing or mismatched."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(
+            f"diffrast: {LIB_PATH} is not built (run `make -C mlx-swift-diffrast_amd`)")
+    lib = ctypes.CDLL(LIB_PATH)
+    for name, (args, res) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = res
+    if lib.dr_abi_version() != ABI_VERSION:
+        raise RuntimeError("diffrast: ABI version mismatch")
+    _lib = lib
+    return lib
+
+
+def check(rc: int) -> None:
+    if rc == DR_OK:
+        return
+    msg = (_lib.dr_get_last_error() or b"").decode(errors="replace")
+    if rc == DR_ERR_ARGUMENT:
+        raise ValueError(msg)
+    raise RuntimeError(f"diffrast error {rc}: {msg}")

@@ -1,0 +1,452 @@
+"""`DiffRast`: the four differentiable rasterization ops on MI355X.
+
+Mirrors the public API of mnmly/mlx-swift-diffrast (the `DiffRast` enum in
+Sources/MLXDiffRast/*.swift): same op names, argument names and meanings,
+output layouts and conventions (clip-space pos, rast = (u, v, z/w,
+tri_id+1), rastDB, instanced / range modes, top-left pixel origin).  Each op
+is a `torch.autograd.Function` whose forward and backward call the C ABI of
+libdiffrast_mi355x.so, the counterpart of the reference's
+`CustomFunction { Forward; VJP }` pairs.  Swift `precondition` failures
+become `ValueError`.
+
+Tensors live on the current ROCm device; there is no CPU path.
+"""
+from __future__ import annotations
+
+import ctypes
+import enum
+from typing import List, Optional, Sequence, Tuple, Union
+
+import torch
+
+from . import _lib
+
+
+class BoundaryMode(enum.IntEnum):
+    """Texture.swift:8-17."""
+    wrap = 0
+    clamp = 1
+    zero = 2
+    cube = 3
+
+
+class FilterMode(enum.IntEnum):
+    """Texture.swift:35-40."""
+    nearest = 0
+    linear = 1
+    linearMipmapNearest = 2
+    linearMipmapLinear = 3
+
+
+_FILTER_NAMES = {"nearest": 0, "linear": 1, "linear-mipmap-nearest": 2,
+                 "linear-mipmap-linear": 3, "linearMipmapNearest": 2, "linearMipmapLinear": 3}
+_BOUNDARY_NAMES = {"wrap": 0, "clamp": 1, "zero": 2, "cube": 3}
+
+
+class DiffAttrs:
+    """Interpolate.swift:15-18: `DiffAttrs.all` or `DiffAttrs.indices([...])`."""
+
+    def __init__(self, indices: Optional[Sequence[int]] = None):
+        self.idx = None if indices is None else [int(i) for i in indices]
+
+    @classmethod
+    def indices(cls, idx: Sequence[int]) -> "DiffAttrs":
+        return cls(list(idx))
+
+    def __eq__(self, other):
+        return isinstance(other, DiffAttrs) and self.idx == other.idx
+
+    def __repr__(self):
+        return "DiffAttrs.all" if self.idx is None else f"DiffAttrs.indices({self.idx})"
+
+
+DiffAttrs.all = DiffAttrs(None)
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _dev_f32(t: torch.Tensor, name: str) -> torch.Tensor:
+    if not isinstance(t, torch.Tensor) or not t.is_cuda:
+        raise ValueError(f"{name} must be a tensor on a ROCm device")
+    return t.detach().to(torch.float32).contiguous()
+
+
+def _dev_i32(t, name: str, device) -> torch.Tensor:
+    if not isinstance(t, torch.Tensor):
+        t = torch.as_tensor(t)
+    return t.detach().to(device=device, dtype=torch.int32).contiguous()
+
+
+# ---------------------------------------------------------------------------
+# rasterize (Rasterize.swift:44-157)
+# ---------------------------------------------------------------------------
+
+class _RasterizeFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, pos, tri, ranges_host, peel, H, W, grad_db):
+        lib = _lib.load()
+        range_mode = ranges_host is not None
+        N = ranges_host.shape[0] if range_mode else pos.shape[0]
+        V = pos.shape[0] if range_mode else pos.shape[1]
+        T = tri.shape[0]
+        posc = pos.contiguous()
+        rast = torch.empty((N, H, W, 4), device=pos.device, dtype=torch.float32)
+        rast_db = torch.empty((N, H, W, 4), device=pos.device, dtype=torch.float32) \
+            if grad_db else torch.empty((N, H, W, 0), device=pos.device, dtype=torch.float32)
+        rng = ranges_host.ctypes.data_as(ctypes.c_void_p) if range_mode else None
+        _lib.check(lib.dr_rasterize_fwd(
+            _ptr(posc), 0 if range_mode else V * 4, _ptr(tri), rng, _ptr(peel), N, V, T, H, W,
+            _ptr(rast), _ptr(rast_db) if grad_db else None, _stream()))
+        ctx.save_for_backward(posc, tri, rast)
+        ctx.meta = (range_mode, N, V, H, W, grad_db)
+        return rast, rast_db
+
+    @staticmethod
+    def backward(ctx, d_rast, d_rast_db):
+        lib = _lib.load()
+        pos, tri, rast = ctx.saved_tensors
+        range_mode, N, V, H, W, grad_db = ctx.meta
+        if d_rast is None:
+            d_rast = torch.zeros_like(rast)
+        d_rast = d_rast.to(torch.float32).contiguous()
+        db = None
+        if grad_db and d_rast_db is not None:
+            db = d_rast_db.to(torch.float32).contiguous()
+        d_pos = torch.empty_like(pos)
+        _lib.check(lib.dr_rasterize_bwd(
+            _ptr(pos), 0 if range_mode else V * 4, _ptr(tri), _ptr(rast), _ptr(d_rast), _ptr(db),
+            N, V, H, W, _ptr(d_pos), 0, _stream()))
+        return d_pos, None, None, None, None, None, None
+
+
+# ---------------------------------------------------------------------------
+# interpolate (Interpolate.swift:43-132)
+# ---------------------------------------------------------------------------
+
+class _InterpolateFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, attr, rast, rast_db, tri, diff_idx, K, shared):
+        lib = _lib.load()
+        N, H, W, _ = rast.shape
+        V, A = attr.shape[-2], attr.shape[-1]
+        stride = 0 if shared else V * A
+        out = torch.empty((N, H, W, A), device=rast.device, dtype=torch.float32)
+        out_da = torch.empty((N, H, W, 2 * K), device=rast.device, dtype=torch.float32)
+        _lib.check(lib.dr_interpolate_fwd(
+            _ptr(attr), stride, _ptr(rast), _ptr(rast_db) if K else None, _ptr(tri),
+            _ptr(diff_idx), K, N, H, W, V, A, _ptr(out), _ptr(out_da) if K else None, _stream()))
+        ctx.save_for_backward(attr, rast, rast_db if K else None, tri, diff_idx)
+        ctx.meta = (K, shared)
+        return out, out_da
+
+    @staticmethod
+    def backward(ctx, d_out, d_out_da):
+        lib = _lib.load()
+        attr, rast, rast_db, tri, diff_idx = ctx.saved_tensors
+        K, shared = ctx.meta
+        N, H, W, _ = rast.shape
+        V, A = attr.shape[-2], attr.shape[-1]
+        stride = 0 if shared else V * A
+        d_out = torch.zeros((N, H, W, A), device=rast.device) if d_out is None \
+            else d_out.to(torch.float32).contiguous()
+        if K:
+            d_out_da = torch.zeros((N, H, W, 2 * K), device=rast.device) if d_out_da is None \
+                else d_out_da.to(torch.float32).contiguous()
+        d_attr = torch.empty_like(attr)
+        d_rast = torch.empty_like(rast)
+        d_rast_db = torch.empty_like(rast) if K else None
+        _lib.check(lib.dr_interpolate_bwd(
+            _ptr(attr), stride, _ptr(rast), _ptr(rast_db), _ptr(tri), _ptr(diff_idx), K,
+            _ptr(d_out), _ptr(d_out_da) if K else None, N, H, W, V, A, _ptr(d_attr), stride,
+            _ptr(d_rast), _ptr(d_rast_db), 0, _stream()))
+        return d_attr, d_rast, d_rast_db, None, None, None, None
+
+
+# ---------------------------------------------------------------------------
+# texture (Texture.swift:62-327)
+# ---------------------------------------------------------------------------
+
+class _TextureFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, tex, uv, uv_da, bias_map, filt, boundary, bias):
+        lib = _lib.load()
+        cube = boundary == BoundaryMode.cube
+        N, Hi, Wi = uv.shape[0], uv.shape[1], uv.shape[2]
+        Nt = tex.shape[0]
+        Ht, Wt, C = (tex.shape[2], tex.shape[3], tex.shape[4]) if cube else \
+            (tex.shape[1], tex.shape[2], tex.shape[3])
+        mip = (not cube) and filt >= FilterMode.linearMipmapNearest
+        L, pyr = 1, None
+        if mip:
+            L = lib.dr_texture_mip_levels(Ht, Wt, -1, None, None)
+            size = lib.dr_texture_mip_size(Nt, Ht, Wt, C, L)
+            pyr = torch.empty(max(size, 1), device=tex.device, dtype=torch.float32)
+            _lib.check(lib.dr_texture_build_mip(_ptr(tex), Nt, Ht, Wt, C, L, _ptr(pyr), _stream()))
+        out = torch.empty((N, Hi, Wi, C), device=uv.device, dtype=torch.float32)
+        _lib.check(lib.dr_texture_fwd(
+            _ptr(tex), _ptr(pyr), Nt, Ht, Wt, C, L, _ptr(uv), _ptr(uv_da), _ptr(bias_map),
+            float(bias), int(filt), int(boundary), N, Hi, Wi, _ptr(out), _stream()))
+        ctx.save_for_backward(tex, uv, uv_da, bias_map, pyr)
+        ctx.meta = (int(filt), int(boundary), float(bias), L, Nt, Ht, Wt, C)
+        return out
+
+    @staticmethod
+    def backward(ctx, d_out):
+        lib = _lib.load()
+        tex, uv, uv_da, bias_map, pyr = ctx.saved_tensors
+        filt, boundary, bias, L, Nt, Ht, Wt, C = ctx.meta
+        N, Hi, Wi = uv.shape[0], uv.shape[1], uv.shape[2]
+        d_out = d_out.to(torch.float32).contiguous()
+        d_tex = torch.empty_like(tex)
+        d_uv = torch.empty_like(uv) if ctx.needs_input_grad[1] else None
+        d_uv_da = torch.empty_like(uv_da) if (uv_da is not None and ctx.needs_input_grad[2]) else None
+        d_bias = torch.empty_like(bias_map) if (bias_map is not None and ctx.needs_input_grad[3]) \
+            else None
+        _lib.check(lib.dr_texture_bwd(
+            _ptr(tex), _ptr(pyr), Nt, Ht, Wt, C, L, _ptr(uv), _ptr(uv_da), _ptr(bias_map),
+            float(bias), filt, boundary, N, Hi, Wi, _ptr(d_out), _ptr(d_tex), _ptr(d_uv),
+            _ptr(d_uv_da), _ptr(d_bias), 0, _stream()))
+        if d_uv_da is None and uv_da is not None and ctx.needs_input_grad[2]:
+            d_uv_da = torch.zeros_like(uv_da)
+        return d_tex, d_uv, d_uv_da, d_bias, None, None, None
+
+
+# ---------------------------------------------------------------------------
+# antialias (Antialias.swift:90-131)
+# ---------------------------------------------------------------------------
+
+class _AntialiasFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, color, pos, rast, tri, topo):
+        lib = _lib.load()
+        N, H, W, C = color.shape
+        V, T = pos.shape[1], tri.shape[0]
+        out = torch.empty_like(color)
+        _lib.check(lib.dr_antialias_fwd(_ptr(color), _ptr(rast), _ptr(pos), _ptr(tri), _ptr(topo),
+                                        N, H, W, C, V, T, _ptr(out), _stream()))
+        ctx.save_for_backward(color, pos, rast, tri, topo)
+        return out
+
+    @staticmethod
+    def backward(ctx, d_out):
+        lib = _lib.load()
+        color, pos, rast, tri, topo = ctx.saved_tensors
+        N, H, W, C = color.shape
+        V, T = pos.shape[1], tri.shape[0]
+        d_out = d_out.to(torch.float32).contiguous()
+        d_color = torch.empty_like(color) if ctx.needs_input_grad[0] else None
+        d_pos = torch.empty_like(pos) if ctx.needs_input_grad[1] else None
+        _lib.check(lib.dr_antialias_bwd(_ptr(color), _ptr(rast), _ptr(pos), _ptr(tri), _ptr(topo),
+                                        _ptr(d_out), N, H, W, C, V, T, _ptr(d_color), _ptr(d_pos),
+                                        0, _stream()))
+        return d_color, d_pos, None, None, None
+
+
+# ---------------------------------------------------------------------------
+# public API
+# ---------------------------------------------------------------------------
+
+class DiffRast:
+    """Namespace of the ops (MLXDiffRast.swift:18)."""
+
+    BoundaryMode = BoundaryMode
+    FilterMode = FilterMode
+    DiffAttrs = DiffAttrs
+
+    @staticmethod
+    def rasterize(pos: torch.Tensor, tri, resolution: Tuple[int, int], gradDB: bool = True,
+                  ranges=None, peelLayer: Optional[torch.Tensor] = None
+                  ) -> Tuple[torch.Tensor, torch.Tensor]:
+        """Rasterize.swift:44-144.  Instanced pos [N,V,4], or range mode: pos
+        [V,4] with ranges [N,2] (start, count) per image.  Returns (rast,
+        rastDB); rastDB is [N,H,W,0] when gradDB is False."""
+        H, W = int(resolution[0]), int(resolution[1])
+        posf = _dev_f32(pos, "rasterize: pos") if not pos.requires_grad else pos.to(torch.float32)
+        if not posf.is_cuda:
+            raise ValueError("rasterize: pos must be on a ROCm device")
+        tri32 = _dev_i32(tri, "tri", posf.device)
+        if tri32.ndim != 2 or tri32.shape[1] != 3:
+            raise ValueError(f"rasterize: tri must be [T, 3] (got {list(tri32.shape)})")
+        ranges_host = None
+        if ranges is not None:
+            if posf.ndim != 2 or posf.shape[1] != 4:
+                raise ValueError(f"rasterize: with `ranges`, pos must be [V, 4] (got {list(posf.shape)})")
+            r = ranges.detach().cpu() if isinstance(ranges, torch.Tensor) else torch.as_tensor(ranges)
+            ranges_host = r.to(torch.int32).contiguous().numpy()
+            if ranges_host.ndim != 2 or ranges_host.shape[1] != 2:
+                raise ValueError(f"rasterize: ranges must be [N, 2] (got {list(ranges_host.shape)})")
+            N = ranges_host.shape[0]
+        else:
+            if posf.ndim != 3 or posf.shape[2] != 4:
+                raise ValueError(f"rasterize: pos must be [N, V, 4] (got {list(posf.shape)})")
+            N = posf.shape[0]
+        peel = None
+        if peelLayer is not None:
+            peel = _dev_f32(peelLayer, "peelLayer")
+            if tuple(peel.shape) != (N, H, W, 4):
+                raise ValueError("rasterize: peelLayer must match rast shape [N, H, W, 4] "
+                                 f"(got {list(peel.shape)})")
+        return _RasterizeFn.apply(posf.contiguous(), tri32, ranges_host, peel, H, W, bool(gradDB))
+
+    @staticmethod
+    def interpolate(attr: torch.Tensor, rast: torch.Tensor, tri, rastDB=None,
+                    diffAttrs: Union[None, DiffAttrs, str, Sequence[int]] = None
+                    ) -> Tuple[torch.Tensor, torch.Tensor]:
+        """Interpolate.swift:43-132.  attr [V,A], [1,V,A] or [N,V,A]."""
+        if rast.ndim != 4 or rast.shape[3] != 4:
+            raise ValueError(f"interpolate: rast must be [N, H, W, 4] (got {list(rast.shape)})")
+        if attr.ndim not in (2, 3):
+            raise ValueError(f"interpolate: attr must be [V, A] or [N, V, A] (got {list(attr.shape)})")
+        N = rast.shape[0]
+        tri32 = _dev_i32(tri, "tri", rast.device)
+        if tri32.ndim != 2 or tri32.shape[1] != 3:
+            raise ValueError(f"interpolate: tri must be [T, 3] (got {list(tri32.shape)})")
+        if attr.ndim == 3 and attr.shape[0] not in (1, N):
+            raise ValueError(f"interpolate: attr batch dim {attr.shape[0]} incompatible with "
+                             f"rast batch {N}")
+        shared = attr.ndim == 2 or attr.shape[0] == 1
+        if attr.ndim == 3 and attr.shape[0] == 1 and N == 1:
+            shared = False
+        A = attr.shape[-1]
+        if isinstance(diffAttrs, str):
+            if diffAttrs != "all":
+                raise ValueError("interpolate: diffAttrs must be 'all' or indices")
+            diffAttrs = DiffAttrs.all
+        elif diffAttrs is not None and not isinstance(diffAttrs, DiffAttrs):
+            diffAttrs = DiffAttrs.indices(diffAttrs)
+        rastf = rast.to(torch.float32).contiguous()
+        attrf = attr.to(torch.float32).contiguous()
+        if diffAttrs is None:
+            out, _ = _InterpolateFn.apply(attrf, rastf, None, tri32, None, 0, shared)
+            return out, torch.zeros((N, rast.shape[1], rast.shape[2], 0), device=rast.device)
+        if rastDB is None:
+            raise ValueError("interpolate: rastDB is required when diffAttrs is set")
+        if tuple(rastDB.shape) != tuple(rast.shape):
+            raise ValueError(f"interpolate: rastDB must match rast shape (got {list(rastDB.shape)} "
+                             f"vs {list(rast.shape)})")
+        if diffAttrs.idx is None:
+            K, didx = A, None
+        else:
+            if len(diffAttrs.idx) == 0:
+                raise ValueError("interpolate: diffAttrs.indices must be non-empty")
+            if any(i < 0 or i >= A for i in diffAttrs.idx):
+                raise ValueError(f"interpolate: diffAttrs.indices values must be in [0, A) (A={A})")
+            K = len(diffAttrs.idx)
+            didx = torch.tensor(diffAttrs.idx, dtype=torch.int32, device=rast.device)
+        return _InterpolateFn.apply(attrf, rastf, rastDB.to(torch.float32).contiguous(), tri32,
+                                    didx, K, shared)
+
+    @staticmethod
+    def texture(tex: torch.Tensor, uv: torch.Tensor, uvDA: Optional[torch.Tensor] = None,
+                filterMode: Union[FilterMode, str] = FilterMode.linear,
+                boundaryMode: Union[BoundaryMode, str] = BoundaryMode.wrap,
+                mipLevelBias: float = 0.0, mipLevelBiasMap: Optional[torch.Tensor] = None
+                ) -> torch.Tensor:
+        """Texture.swift:62-131."""
+        filt = FilterMode(_FILTER_NAMES[filterMode] if isinstance(filterMode, str) else filterMode)
+        bnd = BoundaryMode(_BOUNDARY_NAMES[boundaryMode] if isinstance(boundaryMode, str)
+                           else boundaryMode)
+        texf = tex.to(torch.float32).contiguous()
+        uvf = uv.to(torch.float32).contiguous()
+        if not texf.is_cuda or not uvf.is_cuda:
+            raise ValueError("texture: tensors must be on a ROCm device")
+        if bnd == BoundaryMode.cube:
+            if filt != FilterMode.linear:
+                raise ValueError("texture: cube textures currently support filterMode .linear only")
+            if texf.ndim != 5 or texf.shape[1] != 6:
+                raise ValueError(f"texture: cube tex must be [N, 6, H, W, C] (got {list(texf.shape)})")
+            if uvf.ndim != 4 or uvf.shape[3] != 3:
+                raise ValueError("texture: cube uv must be [N, H_img, W_img, 3] direction vector "
+                                 f"(got {list(uvf.shape)})")
+            if texf.shape[0] not in (1, uvf.shape[0]):
+                raise ValueError("texture: tex batch dim incompatible with uv batch")
+            return _TextureFn.apply(texf, uvf, None, None, filt, bnd, 0.0)
+        if texf.ndim != 4:
+            raise ValueError(f"texture: tex must be [N, H_tex, W_tex, C] (got {list(texf.shape)})")
+        if uvf.ndim != 4 or uvf.shape[3] != 2:
+            raise ValueError(f"texture: uv must be [N, H_img, W_img, 2] (got {list(uvf.shape)})")
+        if texf.shape[0] not in (1, uvf.shape[0]):
+            raise ValueError(f"texture: tex batch dim {texf.shape[0]} incompatible with uv batch "
+                             f"{uvf.shape[0]}")
+        if filt in (FilterMode.nearest, FilterMode.linear):
+            return _TextureFn.apply(texf, uvf, None, None, filt, bnd, 0.0)
+        if uvDA is None:
+            raise ValueError("texture: mipmap filterModes require uvDA")
+        if tuple(uvDA.shape) != tuple(uvf.shape[:3]) + (4,):
+            raise ValueError(f"texture: uvDA must be [N, H_img, W_img, 4] (got {list(uvDA.shape)})")
+        bm = None
+        if mipLevelBiasMap is not None:
+            if tuple(mipLevelBiasMap.shape[:3]) != tuple(uvf.shape[:3]) or \
+                    mipLevelBiasMap.ndim not in (3, 4) or \
+                    (mipLevelBiasMap.ndim == 4 and mipLevelBiasMap.shape[3] != 1):
+                raise ValueError("texture: mipLevelBiasMap must be [N, H_img, W_img] or "
+                                 f"[N, H_img, W_img, 1] (got {list(mipLevelBiasMap.shape)})")
+            bm = mipLevelBiasMap.to(torch.float32).contiguous()
+        return _TextureFn.apply(texf, uvf, uvDA.to(torch.float32).contiguous(), bm, filt, bnd,
+                                float(mipLevelBias))
+
+    @staticmethod
+    def textureConstructMip(tex: torch.Tensor, maxLevel: Optional[int] = None) -> List[torch.Tensor]:
+        """Texture.swift:144-161: [level0 = tex, level1, ...], 2x2 box means."""
+        if tex.ndim != 4:
+            raise ValueError(f"textureConstructMip: tex must be [N, H, W, C] (got {list(tex.shape)})")
+        lib = _lib.load()
+        Nt, H, W, C = tex.shape
+        L = lib.dr_texture_mip_levels(H, W, -1 if maxLevel is None else int(maxLevel), None, None)
+        texf = _dev_f32(tex, "textureConstructMip: tex")
+        size = lib.dr_texture_mip_size(Nt, H, W, C, L)
+        pyr = torch.empty(max(size, 1), device=texf.device, dtype=torch.float32)
+        _lib.check(lib.dr_texture_build_mip(_ptr(texf), Nt, H, W, C, L, _ptr(pyr), _stream()))
+        levels, off, h, w = [tex], 0, H, W
+        for _ in range(1, L):
+            h, w = h // 2, w // 2
+            n = Nt * h * w * C
+            levels.append(pyr[off:off + n].view(Nt, h, w, C))
+            off += n
+        return levels
+
+    @staticmethod
+    def antialiasConstructTopologyHash(tri) -> torch.Tensor:
+        """Antialias.swift:19-66, computed on the GPU."""
+        tri32 = _dev_i32(tri, "tri", torch.device("cuda", torch.cuda.current_device())
+                         if not isinstance(tri, torch.Tensor) or not tri.is_cuda else tri.device)
+        if tri32.ndim != 2 or tri32.shape[1] != 3:
+            raise ValueError("antialiasConstructTopologyHash: tri must be [T, 3] "
+                             f"(got {list(tri32.shape)})")
+        lib = _lib.load()
+        topo = torch.empty_like(tri32)
+        _lib.check(lib.dr_antialias_topology(_ptr(tri32), tri32.shape[0], _ptr(topo), _stream()))
+        return topo
+
+    @staticmethod
+    def antialias(color: torch.Tensor, rast: torch.Tensor, pos: torch.Tensor, tri,
+                  topologyHash: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """Antialias.swift:90-131."""
+        if color.ndim != 4:
+            raise ValueError(f"antialias: color must be [N, H, W, C] (got {list(color.shape)})")
+        if rast.ndim != 4 or rast.shape[3] != 4 or tuple(rast.shape[:3]) != tuple(color.shape[:3]):
+            raise ValueError("antialias: rast must match color in [N, H, W] and have 4 channels")
+        if pos.ndim != 3 or pos.shape[2] != 4:
+            raise ValueError(f"antialias: pos must be [N, V, 4] (got {list(pos.shape)})")
+        tri32 = _dev_i32(tri, "tri", color.device)
+        if tri32.ndim != 2 or tri32.shape[1] != 3:
+            raise ValueError(f"antialias: tri must be [T, 3] (got {list(tri32.shape)})")
+        topo = DiffRast.antialiasConstructTopologyHash(tri32) if topologyHash is None else \
+            _dev_i32(topologyHash, "topologyHash", color.device)
+        return _AntialiasFn.apply(color.to(torch.float32).contiguous(),
+                                  pos.to(torch.float32).contiguous(),
+                                  rast.detach().to(torch.float32).contiguous(), tri32, topo)
+
+
+rasterize = DiffRast.rasterize
+interpolate = DiffRast.interpolate
+texture = DiffRast.texture
+textureConstructMip = DiffRast.textureConstructMip
+antialiasConstructTopologyHash = DiffRast.antialiasConstructTopologyHash
+antialias = DiffRast.antialias

@@ -1,0 +1,72 @@
+"""antialias on the GPU against the CPU oracle: topology hash bit-exact
+(and equal to the O(T^2) brute force), forward within the forward
+tolerance, d_color (gathered here, scattered by the reference) and d_pos
+within the gradient tolerance."""
+import numpy as np
+import pytest
+
+import oracle as O
+import scenes
+from parity import assert_fwd_close, assert_grad_close, dev, host, torch_dev
+from test_oracle_antialias import brute_topology
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("case", ["icosphere", "random", "nonmanifold", "single"])
+def test_topology(case):
+    torch_dev()
+    from diffrast import DiffRast
+    rng = np.random.default_rng(3)
+    if case == "icosphere":
+        _, tri = scenes.icosphere(6)
+    elif case == "random":
+        tri = rng.integers(0, 500, size=(20000, 3)).astype(np.int32)
+    elif case == "nonmanifold":
+        tri = np.array([[0, 1, 2], [0, 1, 3], [0, 1, 4], [1, 2, 3]], np.int32)
+    else:
+        tri = np.array([[0, 1, 2]], np.int32)
+    got = host(DiffRast.antialiasConstructTopologyHash(dev(tri)))
+    ref = O.antialiasConstructTopologyHash(tri)
+    np.testing.assert_array_equal(got, ref)
+    if tri.shape[0] <= 20000 and case != "icosphere":
+        np.testing.assert_array_equal(got, brute_topology(tri))
+
+
+def aa_scene(kind):
+    if kind == "hexpie":
+        sc = scenes.hex_pie(N=3, H=96, W=80)
+        return sc["pos"], sc["tri"], 96, 80
+    if kind == "icosphere":
+        sc = scenes.textured_icosphere(N=2, H=128, W=144, level=4, tex_size=8)
+        return sc["pos"], sc["tri"], 128, 144
+    if kind == "quad":
+        pos = np.array([[-0.45, 0.55, 0, 1], [0.55, 0.55, 0, 1], [0.55, -0.45, 0, 1],
+                        [-0.45, -0.45, 0, 1]], np.float32)[None]
+        return pos, np.array([[0, 1, 2], [0, 2, 3]], np.int32), 4, 4
+    sc = scenes.tier1_triangle(H=61, W=47)
+    return sc["pos"], sc["tri"], 61, 47
+
+
+@pytest.mark.parametrize("kind", ["hexpie", "icosphere", "quad", "tier1"])
+@pytest.mark.parametrize("C", [1, 3, 4])
+def test_antialias(kind, C):
+    torch = torch_dev()
+    from diffrast import DiffRast
+    rng = np.random.default_rng(C + len(kind))
+    pos, tri, H, W = aa_scene(kind)
+    rast, _ = O.rasterize(pos, tri, (H, W), gradDB=False, max_per_tile=0)
+    N = pos.shape[0]
+    color = rng.random((N, H, W, C)).astype(np.float32)
+    c = dev(color).requires_grad_(True)
+    p = dev(pos).requires_grad_(True)
+    out = DiffRast.antialias(c, dev(rast), p, dev(tri))
+    ref = O.antialias(color, rast, pos, tri)
+    assert_fwd_close(host(out), ref)
+    assert (host(out) != color).any()
+    g = rng.normal(size=ref.shape).astype(np.float32)
+    (out * dev(g)).sum().backward()
+    d_color, d_pos = O.antialias_vjp(color, rast, pos, tri, g)
+    assert_grad_close(host(c.grad), d_color, "d_color")
+    assert_grad_close(host(p.grad), d_pos, "d_pos")
+    assert (host(p.grad)[..., 2] == 0).all()

@@ -1,0 +1,131 @@
+"""texture on the GPU against the CPU oracle, every filter x boundary mode,
+shared and per-image textures, C in {1,2,3,4,5}, mip bias (scalar and
+per-pixel), cube maps.  Forward within the forward tolerance (the LOD's
+log2 may differ by an ulp between CPU and GPU, so mip modes are compared
+with tolerance); d_uv / d_uvDA / d_biasMap and the scatter-added d_tex
+within the gradient tolerance."""
+import numpy as np
+import pytest
+
+import oracle as O
+from parity import assert_fwd_close, assert_grad_close, dev, host, torch_dev
+
+pytestmark = pytest.mark.gpu
+
+FILTERS = ["nearest", "linear", "linear-mipmap-nearest", "linear-mipmap-linear"]
+BOUNDS = ["wrap", "clamp", "zero"]
+
+
+def inputs(rng, N, Nt, Ht, Wt, C, Hi, Wi):
+    tex = rng.random((Nt, Ht, Wt, C)).astype(np.float32)
+    uv = rng.uniform(-0.3, 1.3, size=(N, Hi, Wi, 2)).astype(np.float32)
+    uv[:, :3] = 0.0  # a band of "background" pixels sampling one texel (hotspot)
+    da = (rng.normal(size=(N, Hi, Wi, 4)) * rng.choice([0.001, 0.02, 0.2, 2.0],
+                                                       size=(N, Hi, Wi, 1))).astype(np.float32)
+    da[:, :3] = 0.0
+    return tex, uv, da
+
+
+@pytest.mark.parametrize("filt", FILTERS)
+@pytest.mark.parametrize("bnd", BOUNDS)
+@pytest.mark.parametrize("C,Nt", [(4, 1), (3, 2), (1, 2), (5, 1), (2, 1)])
+def test_texture(filt, bnd, C, Nt):
+    torch = torch_dev()
+    from diffrast import DiffRast
+    rng = np.random.default_rng(FILTERS.index(filt) * 100 + BOUNDS.index(bnd) * 10 + C * 2 + Nt)
+    N, Ht, Wt, Hi, Wi = 2, 32, 64, 37, 45
+    tex, uv, da = inputs(rng, N, Nt, Ht, Wt, C, Hi, Wi)
+    mip = "mipmap" in filt
+    t = dev(tex).requires_grad_(True)
+    u = dev(uv).requires_grad_(True)
+    d = dev(da).requires_grad_(True) if mip else None
+    out = DiffRast.texture(t, u, uvDA=d, filterMode=filt, boundaryMode=bnd)
+    ref = O.texture(tex, uv, uvDA=da if mip else None, filterMode=filt, boundaryMode=bnd)
+    if mip:
+        assert_fwd_close(host(out), ref)
+    else:
+        np.testing.assert_array_equal(host(out), ref)
+    g = rng.normal(size=ref.shape).astype(np.float32)
+    (out * dev(g)).sum().backward()
+    d_tex, d_uv, d_da, _ = O.texture_vjp(tex, uv, g, uvDA=da if mip else None, filterMode=filt,
+                                         boundaryMode=bnd)
+    assert tuple(t.grad.shape) == tex.shape
+    assert_grad_close(host(t.grad), d_tex, "d_tex")
+    assert_grad_close(host(u.grad), d_uv, "d_uv")
+    if mip:
+        assert_grad_close(host(d.grad), d_da, "d_uvDA", rtol=1e-3)
+
+
+@pytest.mark.parametrize("filt", ["linear-mipmap-linear", "linear-mipmap-nearest"])
+def test_mip_bias(filt):
+    torch = torch_dev()
+    from diffrast import DiffRast
+    rng = np.random.default_rng(5)
+    tex, uv, da = inputs(rng, 2, 1, 64, 64, 4, 31, 33)
+    bm = rng.uniform(-1, 1, size=(2, 31, 33)).astype(np.float32)
+    t = dev(tex).requires_grad_(True)
+    u = dev(uv).requires_grad_(True)
+    d = dev(da).requires_grad_(True)
+    b = dev(bm).requires_grad_(True)
+    out = DiffRast.texture(t, u, uvDA=d, filterMode=filt, boundaryMode="clamp",
+                           mipLevelBias=0.5, mipLevelBiasMap=b)
+    ref = O.texture(tex, uv, uvDA=da, filterMode=filt, boundaryMode="clamp",
+                    mipLevelBias=0.5, mipLevelBiasMap=bm)
+    assert_fwd_close(host(out), ref)
+    g = rng.normal(size=ref.shape).astype(np.float32)
+    (out * dev(g)).sum().backward()
+    d_tex, d_uv, d_da, d_bm = O.texture_vjp(tex, uv, g, uvDA=da, filterMode=filt,
+                                            boundaryMode="clamp", mipLevelBias=0.5,
+                                            mipLevelBiasMap=bm)
+    assert_grad_close(host(t.grad), d_tex, "d_tex")
+    assert_grad_close(host(u.grad), d_uv, "d_uv")
+    assert_grad_close(host(d.grad), d_da, "d_uvDA", rtol=1e-3)
+    assert_grad_close(host(b.grad), d_bm, "d_biasMap", rtol=1e-3)
+
+
+@pytest.mark.parametrize("C,Nt", [(3, 1), (1, 2), (4, 2)])
+def test_cube(C, Nt):
+    torch = torch_dev()
+    from diffrast import DiffRast
+    rng = np.random.default_rng(C)
+    N, Ht, Wt, Hi, Wi = 2, 16, 16, 19, 23
+    tex = rng.random((Nt, 6, Ht, Wt, C)).astype(np.float32)
+    dirs = rng.normal(size=(N, Hi, Wi, 3)).astype(np.float32)
+    t = dev(tex).requires_grad_(True)
+    u = dev(dirs).requires_grad_(True)
+    out = DiffRast.texture(t, u, boundaryMode="cube")
+    ref = O.texture(tex, dirs, boundaryMode="cube")
+    np.testing.assert_array_equal(host(out), ref)
+    g = rng.normal(size=ref.shape).astype(np.float32)
+    (out * dev(g)).sum().backward()
+    d_tex, d_dir, _, _ = O.texture_vjp(tex, dirs, g, boundaryMode="cube")
+    assert_grad_close(host(t.grad), d_tex, "d_tex")
+    np.testing.assert_array_equal(host(u.grad), 0)
+
+
+def test_construct_mip():
+    torch = torch_dev()
+    from diffrast import DiffRast
+    tex = np.random.default_rng(0).random((2, 64, 32, 3)).astype(np.float32)
+    got = DiffRast.textureConstructMip(dev(tex))
+    ref = O.textureConstructMip(tex)
+    assert len(got) == len(ref) == 6
+    for a, b in zip(got, ref):
+        np.testing.assert_array_equal(host(a), b)
+    got = DiffRast.textureConstructMip(dev(tex), maxLevel=2)
+    assert [tuple(l.shape) for l in got] == [(2, 64, 32, 3), (2, 32, 16, 3), (2, 16, 8, 3)]
+
+
+def test_fixture_parity(fixtures):
+    """ParityTests.swift:92-111 on the GPU: nvdiffrast's texture outputs."""
+    torch_dev()
+    from diffrast import DiffRast
+    tex = np.zeros((1, 8, 8, 3), np.float32)
+    for y in range(8):
+        for x in range(8):
+            tex[0, y, x] = [x / 7, y / 7, (x + y) / 14]
+    out = DiffRast.texture(dev(tex), dev(fixtures["uv"]), boundaryMode="clamp")
+    assert np.abs(host(out) - fixtures["tex_bilinear"]).max() <= 1e-5
+    out = DiffRast.texture(dev(tex), dev(fixtures["uv"]), uvDA=dev(fixtures["uv_da"]),
+                           filterMode="linear-mipmap-linear", boundaryMode="clamp")
+    assert np.abs(host(out) - fixtures["tex_trilinear"]).max() <= 1e-4
