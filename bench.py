@@ -1,0 +1,191 @@
+"""Benchmark: full differentiable-rendering chain, forward + backward.
+
+Workload (one "step"): rasterize (with rast_db) -> interpolate (UV, all
+derivatives) -> texture (trilinear mip, clamp) -> antialias -> MSE loss,
+then the backward pass to pos, the UV attribute and the texture, on
+8 images of 1024x1024 of a level-6 icosphere (40,962 vertices, 81,920
+triangles; spherical UVs, a random rotation per image, fov 45 degrees,
+radius 1 at distance 3) with a 1024x1024 RGBA fp32 value-noise texture.
+Inputs are synthetic and resident on the GPU before timing starts.
+
+Prints one JSON line.  `--gpus N` with N > 1 is not supported (one GPU).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for p in (os.path.join(ROOT, "mlx-swift-diffrast_amd"), os.path.join(ROOT, "tests"),
+          os.path.join(ROOT, "oracle")):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+import numpy as np  # noqa: E402
+
+METRIC = "fwd+bwd Mpix/s (8×1024², 80k tris, full chain); % HBM roofline"
+HBM_PEAK_GBS = 8000.0
+
+
+def make_workload(N, H, W, level, tex_size):
+    import scenes
+    return scenes.textured_icosphere(N=N, H=H, W=W, level=level, tex_size=tex_size)
+
+
+def gpu_run(sc, steps, warmup):
+    import torch
+    from diffrast import DiffRast, _lib
+
+    dev = lambda a: torch.as_tensor(a).cuda()
+    N, H, W = sc["pos"].shape[0], sc["H"], sc["W"]
+    pos = dev(sc["pos"]).requires_grad_(True)
+    tri = dev(sc["tri"])
+    attr = dev(sc["uv"]).requires_grad_(True)        # shared [V,2]
+    tex = dev(sc["tex"]).requires_grad_(True)        # shared [1,Ht,Wt,4]
+    target = dev(sc["target"])
+    topo = DiffRast.antialiasConstructTopologyHash(tri)
+
+    def step():
+        for t in (pos, attr, tex):
+            t.grad = None
+        rast, rast_db = DiffRast.rasterize(pos, tri, (H, W), gradDB=True)
+        uv, uv_da = DiffRast.interpolate(attr, rast, tri, rastDB=rast_db, diffAttrs="all")
+        col = DiffRast.texture(tex, uv, uvDA=uv_da, filterMode="linear-mipmap-linear",
+                               boundaryMode="clamp")
+        out = DiffRast.antialias(col, rast, pos, tri, topologyHash=topo)
+        loss = ((out - target) ** 2).mean()
+        loss.backward()
+        return loss
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    prof = _lib.load()
+    prof.dr_profile_reset()
+    prof.dr_profile_enable(1)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        loss = step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    prof.dr_profile_enable(0)
+    kernels = _lib.profile_report()
+    assert torch.isfinite(loss).item()
+    return (t1 - t0) * 1e3 / steps, kernels
+
+
+def cpu_baseline(sc, seconds_budget=12.0):
+    """The CPU restatement of the reference, on the same inputs: one image of
+    the workload, forward + backward, OpenMP over the host cores."""
+    import oracle as O
+    threads = min(16, os.cpu_count() or 1)
+    O.set_threads(threads)
+    pos = sc["pos"][:1]
+    tri, uva, tex, H, W = sc["tri"], sc["uv"], sc["tex"], sc["H"], sc["W"]
+    topo = O.antialiasConstructTopologyHash(tri)
+    reps, t_total = 0, 0.0
+    while reps == 0 or (t_total < seconds_budget and reps < 40):
+        t0 = time.perf_counter()
+        rast, db = O.rasterize(pos, tri, (H, W), max_per_tile=0)
+        uv, uvda = O.interpolate(uva, rast, tri, rastDB=db, diffAttrs="all")
+        col = O.texture(tex, uv, uvDA=uvda, filterMode="linear-mipmap-linear",
+                        boundaryMode="clamp")
+        out = O.antialias(col, rast, pos, tri, topo)
+        g = (2.0 / out.size) * (out - sc["target"][:1])
+        d_col, d_pos_aa = O.antialias_vjp(col, rast, pos, tri, g, topo)
+        d_tex, d_uv, d_uvda, _ = O.texture_vjp(tex, uv, d_col, uvDA=uvda,
+                                               filterMode="linear-mipmap-linear",
+                                               boundaryMode="clamp")
+        d_attr, d_rast, d_db = O.interpolate_vjp(uva, rast, tri, d_uv, rastDB=db,
+                                                 diffAttrs="all", d_out_da=d_uvda)
+        O.rasterize_vjp(pos, tri, rast, d_rast, d_db)
+        t_total += time.perf_counter() - t0
+        reps += 1
+    O.set_threads(1)
+    per_img = t_total / reps
+    return {"value": round(H * W / per_img / 1e6, 3), "unit": "Mpix/s", "cores": threads,
+            "kind": "port",
+            "sample": f"1 of 8 images ({H}x{W}), full chain fwd+bwd, {reps} rep(s), "
+                      f"{per_img:.2f} s/image"}
+
+
+# Algorithmic HBM bytes per pixel of each kernel (fp32), and the per-launch
+# fixed bytes: what the kernel must read and write at minimum.
+def algorithmic_bytes(name, P, fixed):
+    per_px = {
+        "k_raster": 32,          # write rast + rast_db
+        "k_interp_fwd": 56,      # read rast, rast_db; write uv, uv_da
+        "k_interp_bwd": 88,      # read rast, rast_db, d_uv, d_uvda; write d_rast, d_rast_db
+        "k_tex_fwd": 40,         # read uv, uv_da; write color
+        "k_tex_bwd": 64,         # read uv, uv_da, d_color; write d_uv, d_uvda
+        "k_aa_fwd": 48,          # read color, rast; write out
+        "k_aa_bwd": 64,          # read d_out, color, rast; write d_color
+        "k_raster_bwd": 48,      # read rast, d_rast, d_rast_db
+    }
+    for k, b in per_px.items():
+        if name.startswith(k):
+            return b * P + fixed.get(k, 0)
+    return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--size", type=int, default=1024)
+    ap.add_argument("--batch", type=int, default=8)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported",
+              file=sys.stderr)
+        sys.exit(2)
+
+    N, H, W = args.batch, args.size, args.size
+    sc = make_workload(N, H, W, level=6, tex_size=1024)
+    V, T = sc["pos"].shape[1], sc["tri"].shape[0]
+    ms, kernels = gpu_run(sc, args.steps, args.warmup)
+    P = N * H * W
+    mpix = P / (ms * 1e-3) / 1e6
+
+    # Dominant kernel, timed with HIP events on its own stream over the timed
+    # region; roofline against HBM.
+    fixed = {"k_tex_fwd": 22.4e6, "k_tex_bwd": 2 * 22.4e6,
+             "k_raster_bwd": 2 * N * V * 16, "k_interp_bwd": 2 * V * 8}
+    dom = max(kernels.items(), key=lambda kv: kv[1]["total_ms"]) if kernels else None
+    roofline = None
+    if dom:
+        name, st = dom
+        avg_ms = st["total_ms"] / max(st["count"], 1)
+        algo = algorithmic_bytes(name, P, fixed)
+        if algo is not None:
+            ach = algo / (avg_ms * 1e-3) / 1e9
+            roofline = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
+                        "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+                        "kernel": name, "avg_ms": round(avg_ms, 4)}
+
+    line = {
+        "metric": METRIC, "value": round(mpix, 2), "unit": "Mpix/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (seeded icosphere scene, value-noise texture)",
+        "config": {"workload": "textured icosphere full chain fwd+bwd", "images": N,
+                   "height": H, "width": W, "vertices": int(V), "triangles": int(T),
+                   "texture": "1024x1024x4 f32, 11 mip levels, clamp, linear-mipmap-linear"},
+        "tris_per_s": round(N * T / (ms * 1e-3), 1),
+        "roofline": roofline,
+        "kernels_ms_per_step": {k: round(v["total_ms"] / args.steps, 4)
+                                for k, v in sorted(kernels.items(),
+                                                   key=lambda kv: -kv[1]["total_ms"])},
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(sc)
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

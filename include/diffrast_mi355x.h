@@ -76,6 +76,14 @@ const char* dr_get_last_error(void);
 /* Frees the scratch memory held for the current device (all streams). */
 int dr_release_scratch(void);
 
+/* Kernel timing (no counterpart in the reference; for benchmarks).  While
+ * enabled, every kernel launch is bracketed by HIP events on its stream.
+ * dr_profile_report writes "name launches total_ms" lines into buf and
+ * returns the full report length (it waits for the recorded events). */
+int dr_profile_enable(int on);
+int dr_profile_reset(void);
+int dr_profile_report(char* buf, int len);
+
 /* ---- rasterize ------------------------------------------------------- */
 
 /* Forward of DiffRast.rasterize (Rasterize.swift:44-144).

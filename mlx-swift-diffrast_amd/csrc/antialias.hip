@@ -82,6 +82,7 @@ __global__ void __launch_bounds__(256) k_topo_resolve(const int32_t* __restrict_
 // ---------------------------------------------------------------------------
 
 struct SilDir {
+  bool active;
   float alpha;  // beta > 0 when active
   int ie0, ie1;
   float e0x, e0y, e1x, e1y, t, denom, dbeta;
@@ -99,10 +100,10 @@ __device__ __forceinline__ int tri_at(const AAIn& a, int n, int h, int w) {
   return f2i(a.rast[((((int64_t)n * a.H + h) * a.W + w) << 2) + 3]) - 1;
 }
 
-// Direction dir of pixel (n, ph, pw) whose own triangle is tri_p.
-// Returns false when the pair contributes nothing.
-__device__ __noinline__ bool sil_dir(const AAIn& a, int n, int ph, int pw, int tri_p, int dir,
-                                     SilDir& s) {
+// Direction dir of pixel (n, ph, pw) whose own triangle is tri_p;
+// s.active is false when the pair contributes nothing.
+__device__ __forceinline__ bool sil_dir_impl(const AAIn& a, int n, int ph, int pw, int tri_p,
+                                             int dir, SilDir& s) {
   const int dw = dir == 0 ? 1 : (dir == 2 ? -1 : 0);
   const int dh = dir == 1 ? 1 : (dir == 3 ? -1 : 0);
   const int nh = ph + dh, nw = pw + dw;
@@ -194,6 +195,16 @@ __device__ __noinline__ bool sil_dir(const AAIn& a, int n, int ph, int pw, int t
   return true;
 }
 
+__device__ __forceinline__ SilDir sil_dir(const AAIn& a, int n, int ph, int pw, int tri_p,
+                                          int dir) {
+  SilDir s;
+  s.alpha = 0.0f;
+  s.ie0 = s.ie1 = 0;
+  s.e0x = s.e0y = s.e1x = s.e1y = s.t = s.denom = s.dbeta = 0.0f;
+  s.active = sil_dir_impl(a, n, ph, pw, tri_p, dir, s);
+  return s;
+}
+
 // Antialias.swift:333-358.
 __global__ void __launch_bounds__(256) k_aa_fwd(AAIn a, const float* __restrict__ color, int N,
                                                 int C, float* __restrict__ out) {
@@ -207,17 +218,14 @@ __global__ void __launch_bounds__(256) k_aa_fwd(AAIn a, const float* __restrict_
   float alpha[4];
   int64_t nb[4];
   int any = 0;
+#pragma unroll
   for (int d = 0; d < 4; ++d) {
-    SilDir s;
-    alpha[d] = 0.0f;
-    nb[d] = 0;
-    if (sil_dir(a, n, ph, pw, tri_p, d, s)) {
-      alpha[d] = s.alpha;
-      const int nh = ph + (d == 1 ? 1 : (d == 3 ? -1 : 0));
-      const int nw = pw + (d == 0 ? 1 : (d == 2 ? -1 : 0));
-      nb[d] = (((int64_t)n * a.H + nh) * a.W + nw) * C;
-      any = 1;
-    }
+    const SilDir s = sil_dir(a, n, ph, pw, tri_p, d);
+    alpha[d] = s.active ? s.alpha : 0.0f;
+    const int nh = ph + (d == 1 ? 1 : (d == 3 ? -1 : 0));
+    const int nw = pw + (d == 0 ? 1 : (d == 2 ? -1 : 0));
+    nb[d] = (((int64_t)n * a.H + nh) * a.W + nw) * C;
+    any |= s.active;
   }
   const float* cp = color + pix * C;
   float* o = out + pix * C;
@@ -228,6 +236,7 @@ __global__ void __launch_bounds__(256) k_aa_fwd(AAIn a, const float* __restrict_
   for (int c = 0; c < C; ++c) {
     const float cpc = cp[c];
     float acc = cpc;
+#pragma unroll
     for (int d = 0; d < 4; ++d)
       if (alpha[d] > 0.0f) acc += alpha[d] * (color[nb[d] + c] - cpc);
     o[c] = acc;
@@ -255,11 +264,12 @@ __global__ void __launch_bounds__(256) k_aa_bwd(AAIn a, const float* __restrict_
 
   // 1) own blend weights.
   SilDir sd[4];
-  bool act[4];
   float asum = 0.0f;
+#pragma unroll
   for (int d = 0; d < 4; ++d) {
-    act[d] = inside && sil_dir(a, n, ph, pw, tri_p, d, sd[d]);
-    const float al = act[d] ? sd[d].alpha : 0.0f;
+    sd[d] = sil_dir(a, n, ph, pw, tri_p, d);
+    sd[d].active = sd[d].active && inside;
+    const float al = sd[d].active ? sd[d].alpha : 0.0f;
     s_alpha[d][ly][lx] = al;
     asum += al;
   }
@@ -274,8 +284,8 @@ __global__ void __launch_bounds__(256) k_aa_bwd(AAIn a, const float* __restrict_
     else { qw = x0 + i; qh = y0 + 16; qd = 3; }                 // bottom row, looks -h
     float al = 0.0f;
     if (qh >= 0 && qh < a.H && qw >= 0 && qw < a.W) {
-      SilDir s;
-      if (sil_dir(a, n, qh, qw, tri_at(a, n, qh, qw), qd, s)) al = s.alpha;
+      const SilDir s = sil_dir(a, n, qh, qw, tri_at(a, n, qh, qw), qd);
+      if (s.active) al = s.alpha;
     }
     s_halo[side][i] = al;
   }
@@ -298,6 +308,7 @@ __global__ void __launch_bounds__(256) k_aa_bwd(AAIn a, const float* __restrict_
     float* dc = d_color + pix * C;
     for (int c = 0; c < C; ++c) {
       float acc = g[c] * (1.0f - asum);
+#pragma unroll
       for (int d = 0; d < 4; ++d)
         if (wn[d] > 0.0f) acc += d_out[qn[d] * C + c] * wn[d];
       dc[c] = accumulate ? dc[c] + acc : acc;
@@ -309,8 +320,9 @@ __global__ void __launch_bounds__(256) k_aa_bwd(AAIn a, const float* __restrict_
   const float* p = a.pos + (int64_t)n * a.V * 4;
   float* dp = d_pos + (int64_t)n * a.V * 4;
   const float* cpp = color + pix * C;
+#pragma unroll
   for (int d = 0; d < 4; ++d) {
-    bool on = act[d] && sd[d].alpha > 0.0f && sd[d].alpha < 1.0f;
+    bool on = sd[d].active && sd[d].alpha > 0.0f && sd[d].alpha < 1.0f;
     float dv[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     float* addr[6] = {dp, dp, dp, dp, dp, dp};
     uint64_t key = 0;
@@ -383,9 +395,13 @@ extern "C" int dr_antialias_topology(const int32_t* tri, int T, int32_t* topo,
   int* slot = cnt + S;
   DR_CHECK_HIP(fill_async(keys, kEmpty, (int64_t)S, stream));
   DR_CHECK_HIP(fill_async(cnt, 0, (int64_t)S, stream));
+  {
+  DR_TIMED("k_topo_insert", stream);
   hipLaunchKernelGGL(k_topo_insert, dim3(grid_for(E, 256)), dim3(256), 0, stream, tri, E, keys,
                      cnt, slot, S - 1);
+  }
   DR_CHECK_LAUNCH();
+  DR_TIMED("k_topo_resolve", stream);
   hipLaunchKernelGGL(k_topo_resolve, dim3(grid_for(E, 256)), dim3(256), 0, stream, tri, E, keys,
                      cnt, slot, S - 1, topo);
   DR_CHECK_LAUNCH();
@@ -409,6 +425,7 @@ extern "C" int dr_antialias_fwd(const float* color, const float* rast, const flo
   DR_CHECK_ARG(out != nullptr, "antialias: null output");
   AAIn a{rast, pos, tri, topo, H, W, V};
   const int64_t P = (int64_t)N * H * W;
+  DR_TIMED("k_aa_fwd", stream);
   hipLaunchKernelGGL(k_aa_fwd, dim3(grid_for(P, 256)), dim3(256), 0, stream, a, color, N, C, out);
   DR_CHECK_LAUNCH();
   return DR_OK;
@@ -428,6 +445,7 @@ extern "C" int dr_antialias_bwd(const float* color, const float* rast, const flo
   if (d_pos && !acc) DR_CHECK_HIP(fill_async(d_pos, 0.0f, (int64_t)N * V * 4, stream));
   AAIn a{rast, pos, tri, topo, H, W, V};
   const int ntx = (W + 15) / 16, nty = (H + 15) / 16;
+  DR_TIMED("k_aa_bwd", stream);
   hipLaunchKernelGGL(k_aa_bwd, dim3((unsigned)((int64_t)N * ntx * nty)), dim3(256), 0, stream, a,
                      color, d_out, N, C, ntx, nty, d_color, d_pos, acc ? 1 : 0);
   DR_CHECK_LAUNCH();

@@ -62,10 +62,30 @@ struct Scratch {
   bool total_pending = false;
 };
 
+// Compute units of the current device (cached per device).
+int device_cu_count();
+
 // Returns the scratch record of (current device, stream); nullptr on error.
 Scratch* scratch_for(hipStream_t stream);
 // Ensures slot `s` holds at least `bytes`; returns its pointer or nullptr.
 void* scratch_get(Scratch* sc, hipStream_t stream, int s, size_t bytes);
+
+// ---------------------------------------------------------------------------
+// kernel timing (dr_profile_*): when enabled, each launch made inside a
+// ProfScope is bracketed by HIP events on its stream.
+// ---------------------------------------------------------------------------
+
+extern bool g_prof_enabled;
+
+struct ProfScope {
+  const char* name;
+  hipStream_t stream;
+  hipEvent_t start = nullptr;
+  ProfScope(const char* n, hipStream_t s);
+  ~ProfScope();
+};
+
+#define DR_TIMED(NAME, STREAM) ::dr::ProfScope dr_prof_scope_(NAME, STREAM)
 
 // ---------------------------------------------------------------------------
 // device helpers
@@ -84,6 +104,16 @@ __device__ __forceinline__ int f2i(float x) {
 
 __device__ __forceinline__ int lane_id() { return (int)__lane_id(); }
 
+// Wave-uniform values: keep them in scalar registers.
+__device__ __forceinline__ float uni(float x) {
+  return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(x)));
+}
+__device__ __forceinline__ uint64_t uni(uint64_t x) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)x);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(x >> 32));
+  return ((uint64_t)hi << 32) | lo;
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
@@ -91,35 +121,46 @@ __device__ __forceinline__ float wave_sum(float v) {
 }
 
 // Scatter-add of M values per lane into addresses that are equal for all
-// lanes with the same (`key`, `key2`).  Lanes sharing a key with at least kGroupMin
-// others are summed across the wave first and written by one lane; other
-// lanes issue their own atomics.  Inactive lanes pass valid = false (every
-// lane of the wave must call this).
+// lanes with the same (`key`, `key2`).  Up to kProbes candidate groups are
+// probed (alternating the lowest and highest pending lane as leader); a
+// group of at least kGroupMin lanes is summed across the wave and written by
+// its leader.  Every other lane then issues its own atomics, all lanes in
+// one pass (no per-lane serialisation).  Inactive lanes pass valid = false;
+// every lane of the wave must call this.
 constexpr int kGroupMin = 6;
+constexpr int kProbes = 4;
+
+__device__ __forceinline__ int probe_leader(uint64_t pending, int probe) {
+  return (probe & 1) ? 63 - __clzll((long long)pending) : __ffsll((long long)pending) - 1;
+}
 
 template <int M>
 __device__ __forceinline__ void group_atomic_add(bool valid, uint64_t key, float* const (&addr)[M],
                                                  const float (&val)[M], uint32_t key2 = 0) {
   uint64_t pending = __ballot(valid);
+  bool mine = valid;
   const int lane = lane_id();
-  while (pending) {
-    const int leader = __ffsll((long long)pending) - 1;
+#pragma unroll 1
+  for (int probe = 0; probe < kProbes && pending; ++probe) {
+    const int leader = probe_leader(pending, probe);
     const uint64_t lkey = __shfl(key, leader, kWave);
     const uint32_t lkey2 = __shfl(key2, leader, kWave);
-    const bool member = valid && key == lkey && key2 == lkey2 && ((pending >> lane) & 1ull);
+    const bool member = mine && key == lkey && key2 == lkey2;
     const uint64_t members = __ballot(member);
     pending &= ~members;
     if (__popcll(members) >= kGroupMin) {
 #pragma unroll
       for (int i = 0; i < M; ++i) {
-        float s = wave_sum(member ? val[i] : 0.0f);
+        const float s = wave_sum(member ? val[i] : 0.0f);
         if (lane == leader && s != 0.0f) unsafeAtomicAdd(addr[i], s);
       }
-    } else if (member) {
-#pragma unroll
-      for (int i = 0; i < M; ++i)
-        if (val[i] != 0.0f) unsafeAtomicAdd(addr[i], val[i]);
+      if (member) mine = false;
     }
+  }
+  if (mine) {
+#pragma unroll
+    for (int i = 0; i < M; ++i)
+      if (val[i] != 0.0f) unsafeAtomicAdd(addr[i], val[i]);
   }
 }
 
@@ -136,6 +177,7 @@ inline hipError_t fill_async(T* p, T v, int64_t n, hipStream_t s) {
   if (n <= 0) return hipSuccess;
   int64_t blocks = (n + 255) / 256;
   if (blocks > 4096) blocks = 4096;
+  DR_TIMED("fill", s);
   hipLaunchKernelGGL(fill_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, s, p, v, n);
   return hipGetLastError();
 }

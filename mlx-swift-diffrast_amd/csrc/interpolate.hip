@@ -229,6 +229,7 @@ extern "C" int dr_interpolate_fwd(const float* attr, int64_t attr_batch_stride,
   DR_CHECK_ARG(out && (K == 0 || out_da), "interpolate: null output");
   const int64_t P = (int64_t)N * H * W;
   const dim3 grid(grid_for(P, 256));
+  DR_TIMED("k_interp_fwd", stream);
   DR_INTERP_DISPATCH(k_interp_fwd, grid, attr, attr_batch_stride, rast, rast_db, tri, diff_idx,
                      K, P, H * W, A, out, out_da);
   DR_CHECK_LAUNCH();
@@ -252,6 +253,7 @@ extern "C" int dr_interpolate_bwd(const float* attr, int64_t attr_batch_stride,
   if (!(flags & DR_ACCUMULATE)) DR_CHECK_HIP(fill_async(d_attr, 0.0f, nattr, stream));
   const int ntx = (W + 15) / 16, nty = (H + 15) / 16;
   const dim3 grid((unsigned)((int64_t)N * ntx * nty));
+  DR_TIMED("k_interp_bwd", stream);
   DR_INTERP_DISPATCH(k_interp_bwd, grid, attr, attr_batch_stride, rast, rast_db, tri, diff_idx, K,
                      d_out, d_out_da, N, H, W, ntx, nty, A, d_attr, d_attr_batch_stride, d_rast,
                      d_rast_db);

@@ -506,17 +506,22 @@ extern "C" int dr_rasterize_fwd(const float* pos, int64_t pos_batch_stride, cons
   DR_CHECK_HIP(fill_async(cnt, 0, n_tiles, stream));
   DR_CHECK_HIP(fill_async(total, 0ull, 1, stream));
   if (n_rec > 0) {
+    DR_TIMED("k_setup", stream);
     hipLaunchKernelGGL(k_setup, dim3(grid_for(n_rec, 256)), dim3(256), 0, stream, pos,
                        ranges_host ? (int64_t)0 : pos_batch_stride, tri, Npos, T, H, W, rec, rect);
     DR_CHECK_LAUNCH();
   }
   if (n_items > 0) {
+    DR_TIMED("k_bin_count", stream);
     hipLaunchKernelGGL(k_bin_count, dim3(grid_for(n_items, 256)), dim3(256), 0, stream, it,
                        n_items, N, rect, ntx, tiles, cnt);
     DR_CHECK_LAUNCH();
   }
-  hipLaunchKernelGGL(k_bin_alloc, dim3(grid_for(n_tiles, 256)), dim3(256), 0, stream, cnt,
-                     n_tiles, off, fillc, total);
+  {
+    DR_TIMED("k_bin_alloc", stream);
+    hipLaunchKernelGGL(k_bin_alloc, dim3(grid_for(n_tiles, 256)), dim3(256), 0, stream, cnt,
+                       n_tiles, off, fillc, total);
+  }
   DR_CHECK_LAUNCH();
 
   // List capacity: exact on the first call (one host sync); afterwards the
@@ -538,6 +543,7 @@ extern "C" int dr_rasterize_fwd(const float* pos, int64_t pos_batch_stride, cons
   const int64_t cap = (int64_t)(sc->cap[SLOT_RAST_LIST] / 4);
 
   if (n_items > 0) {
+    DR_TIMED("k_bin_fill", stream);
     hipLaunchKernelGGL(k_bin_fill, dim3(grid_for(n_items, 256)), dim3(256), 0, stream, it,
                        n_items, N, rect, ntx, tiles, off, fillc, list, cap);
     DR_CHECK_LAUNCH();
@@ -546,10 +552,13 @@ extern "C" int dr_rasterize_fwd(const float* pos, int64_t pos_batch_stride, cons
 #define DR_RASTER(DBV, PV)                                                                    \
   hipLaunchKernelGGL((k_raster<DBV, PV>), grid, block, 0, stream, rec, rect, it, rec_stride, \
                      cnt, off, list, cap, peel, N, H, W, ntx, nty, rast, rast_db)
-  if (rast_db) {
-    if (peel) DR_RASTER(true, true); else DR_RASTER(true, false);
-  } else {
-    if (peel) DR_RASTER(false, true); else DR_RASTER(false, false);
+  {
+    DR_TIMED("k_raster", stream);
+    if (rast_db) {
+      if (peel) DR_RASTER(true, true); else DR_RASTER(true, false);
+    } else {
+      if (peel) DR_RASTER(false, true); else DR_RASTER(false, false);
+    }
   }
 #undef DR_RASTER
   DR_CHECK_LAUNCH();
@@ -573,8 +582,11 @@ extern "C" int dr_rasterize_bwd(const float* pos, int64_t pos_batch_stride, cons
   if (!(flags & DR_ACCUMULATE)) DR_CHECK_HIP(fill_async(d_pos, 0.0f, npos, stream));
   const int ntx = (W + kTile - 1) / kTile, nty = (H + kTile - 1) / kTile;
   const int64_t blocks = (int64_t)N * ntx * nty;
-  hipLaunchKernelGGL(k_raster_bwd, dim3((unsigned)blocks), dim3(256), 0, stream, pos,
-                     pos_batch_stride, tri, rast, d_rast, d_rast_db, N, H, W, ntx, nty, d_pos);
+  {
+    DR_TIMED("k_raster_bwd", stream);
+    hipLaunchKernelGGL(k_raster_bwd, dim3((unsigned)blocks), dim3(256), 0, stream, pos,
+                       pos_batch_stride, tri, rast, d_rast, d_rast_db, N, H, W, ntx, nty, d_pos);
+  }
   DR_CHECK_LAUNCH();
   return DR_OK;
 }

@@ -1,7 +1,9 @@
 // Error reporting and per-(device, stream) scratch memory.
 #include <hip/hip_runtime.h>
 
+#include <cstring>
 #include <map>
+#include <vector>
 #include <mutex>
 #include <string>
 #include <utility>
@@ -65,9 +67,102 @@ void* scratch_get(Scratch* sc, hipStream_t stream, int s, size_t bytes) {
   return p;
 }
 
+int device_cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int cu = 0;
+    if (hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cu <= 0)
+      cu = 256;
+    cached[dev] = cu;
+  }
+  return cached[dev];
+}
+
+// ---- kernel timing -------------------------------------------------------
+
+bool g_prof_enabled = false;
+
+struct ProfRec {
+  const char* name;
+  hipEvent_t a, b;
+};
+
+static std::mutex g_prof_mu;
+static std::vector<ProfRec> g_prof;
+static std::vector<hipEvent_t> g_prof_pool;
+
+static hipEvent_t prof_event() {
+  if (!g_prof_pool.empty()) {
+    hipEvent_t e = g_prof_pool.back();
+    g_prof_pool.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+
+ProfScope::ProfScope(const char* n, hipStream_t s) : name(n), stream(s) {
+  if (!g_prof_enabled) return;
+  std::lock_guard<std::mutex> lk(g_prof_mu);
+  start = prof_event();
+  if (start) (void)hipEventRecord(start, stream);
+}
+
+ProfScope::~ProfScope() {
+  if (!start) return;
+  std::lock_guard<std::mutex> lk(g_prof_mu);
+  hipEvent_t end = prof_event();
+  if (!end) return;
+  (void)hipEventRecord(end, stream);
+  g_prof.push_back({name, start, end});
+}
+
 }  // namespace dr
 
 extern "C" {
+
+int dr_profile_enable(int on) {
+  dr::g_prof_enabled = on != 0;
+  return DR_OK;
+}
+
+int dr_profile_reset(void) {
+  std::lock_guard<std::mutex> lk(dr::g_prof_mu);
+  for (auto& r : dr::g_prof) {
+    (void)hipEventSynchronize(r.b);
+    dr::g_prof_pool.push_back(r.a);
+    dr::g_prof_pool.push_back(r.b);
+  }
+  dr::g_prof.clear();
+  return DR_OK;
+}
+
+int dr_profile_report(char* buf, int len) {
+  std::lock_guard<std::mutex> lk(dr::g_prof_mu);
+  std::map<std::string, std::pair<long, double>> agg;
+  for (auto& r : dr::g_prof) {
+    float ms = 0.0f;
+    if (hipEventSynchronize(r.b) != hipSuccess) return -1;
+    if (hipEventElapsedTime(&ms, r.a, r.b) != hipSuccess) return -1;
+    auto& e = agg[r.name];
+    e.first += 1;
+    e.second += ms;
+  }
+  std::string out;
+  for (auto& kv : agg)
+    out += kv.first + " " + std::to_string(kv.second.first) + " " +
+           std::to_string(kv.second.second) + "\n";
+  if (buf && len > 0) {
+    size_t n = out.size() < (size_t)(len - 1) ? out.size() : (size_t)(len - 1);
+    memcpy(buf, out.data(), n);
+    buf[n] = 0;
+  }
+  return (int)out.size();
+}
 
 int dr_abi_version(void) { return DR_ABI_VERSION; }
 

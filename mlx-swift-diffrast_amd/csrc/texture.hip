@@ -262,38 +262,126 @@ __global__ void __launch_bounds__(256) k_tex_fwd(
 // backward
 // ---------------------------------------------------------------------------
 
-// Scatter of one bilinear footprint's gradient (w * g * scale) into one
-// level; lanes hitting the same footprint are summed first.
+// Per-wave accumulator of one bilinear footprint's gradient.  A large group
+// of lanes on one footprint (in practice: every background pixel samples the
+// same clamped texel) adds its wave-summed values here instead of issuing
+// atomics; the accumulator is written out when a different footprint takes
+// its place and when the wave has finished all its tiles.  Wave-uniform.
 template <int CT>
+struct FootAcc {
+  float* p[4];
+  float v[4 * CT];
+  bool on;
+};
+
+template <int CT>
+__device__ __forceinline__ void acc_init(FootAcc<CT>& a) {
+  a.on = false;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) a.p[i] = nullptr;
+#pragma unroll
+  for (int i = 0; i < 4 * CT; ++i) a.v[i] = 0.0f;
+}
+
+template <int CT>
+__device__ __forceinline__ void acc_flush(FootAcc<CT>& a) {
+  if (!a.on) return;
+  if (lane_id() == 0) {
+#pragma unroll
+    for (int c = 0; c < CT; ++c)
+#pragma unroll
+      for (int tap = 0; tap < 4; ++tap)
+        if (a.v[4 * c + tap] != 0.0f) unsafeAtomicAdd(a.p[tap] + c, a.v[4 * c + tap]);
+  }
+  a.on = false;
+}
+
+// Scatter of one bilinear footprint's gradient (w * g * scale) into one
+// level.  Taps that land on the same texel (clamped borders) are merged
+// first; lanes sharing the footprint are summed across the wave.
+template <int CT, bool USE_ACC = true>
 __device__ __forceinline__ void scatter_footprint(bool valid, float* __restrict__ base, int Wk,
                                                   int C, const Bilin& b, const float* g,
-                                                  float scale) {
-  const int64_t o00 = ((int64_t)b.iy0 * Wk + b.ix0) * C, o10 = ((int64_t)b.iy0 * Wk + b.ix1) * C;
-  const int64_t o01 = ((int64_t)b.iy1 * Wk + b.ix0) * C, o11 = ((int64_t)b.iy1 * Wk + b.ix1) * C;
-  const uint64_t key = (uint64_t)(base + o00);
-  const uint32_t key2 = ((uint32_t)b.ix1 << 16) ^ (uint32_t)b.iy1;
+                                                  float scale,
+                                                  FootAcc<(CT > 0 ? CT : 1)>& acc) {
+  float w00 = b.w00, w10 = b.w10, w01 = b.w01, w11 = b.w11;
+  if (b.ix1 == b.ix0) {
+    w00 += w10;
+    w01 += w11;
+    w10 = 0.0f;
+    w11 = 0.0f;
+  }
+  if (b.iy1 == b.iy0) {
+    w00 += w01;
+    w10 += w11;
+    w01 = 0.0f;
+    w11 = 0.0f;
+  }
+  float* const p[4] = {base + ((int64_t)b.iy0 * Wk + b.ix0) * C, base + ((int64_t)b.iy0 * Wk + b.ix1) * C,
+                       base + ((int64_t)b.iy1 * Wk + b.ix0) * C, base + ((int64_t)b.iy1 * Wk + b.ix1) * C};
   if (CT > 0) {
-    float val[4 * (CT > 0 ? CT : 1)];
-    float* addr[4 * (CT > 0 ? CT : 1)];
+    constexpr int M = 4 * (CT > 0 ? CT : 1);
+    float val[M];
 #pragma unroll
     for (int c = 0; c < (CT > 0 ? CT : 1); ++c) {
       const float gc = valid ? g[c] * scale : 0.0f;
-      val[4 * c + 0] = b.w00 * gc;
-      val[4 * c + 1] = b.w10 * gc;
-      val[4 * c + 2] = b.w01 * gc;
-      val[4 * c + 3] = b.w11 * gc;
-      addr[4 * c + 0] = base + o00 + c;
-      addr[4 * c + 1] = base + o10 + c;
-      addr[4 * c + 2] = base + o01 + c;
-      addr[4 * c + 3] = base + o11 + c;
+      val[4 * c + 0] = w00 * gc;
+      val[4 * c + 1] = w10 * gc;
+      val[4 * c + 2] = w01 * gc;
+      val[4 * c + 3] = w11 * gc;
     }
-    group_atomic_add<4 * (CT > 0 ? CT : 1)>(valid, key, addr, val, key2);
+    uint64_t pending = __ballot(valid);
+    bool mine = valid;
+    const int lane = lane_id();
+#pragma unroll 1
+    for (int probe = 0; probe < kProbes && pending; ++probe) {
+      const int leader = probe_leader(pending, probe);
+      float* lp[4];
+      bool same = mine;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        lp[t] = (float*)__shfl((uint64_t)p[t], leader, kWave);
+        same = same && p[t] == lp[t];
+      }
+      const uint64_t members = __ballot(same);
+      pending &= ~members;
+      if (__popcll(members) >= kGroupMin && !USE_ACC) {
+#pragma unroll
+        for (int i = 0; i < M; ++i) {
+          const float sm = wave_sum(same ? val[i] : 0.0f);
+          if (lane == leader && sm != 0.0f) unsafeAtomicAdd(lp[i & 3] + (i >> 2), sm);
+        }
+        if (same) mine = false;
+      } else if (__popcll(members) >= kGroupMin) {
+        const bool hit = acc.on && acc.p[0] == lp[0] && acc.p[1] == lp[1] && acc.p[2] == lp[2] &&
+                         acc.p[3] == lp[3];
+        if (!hit) {
+          acc_flush(acc);
+#pragma unroll
+          for (int t = 0; t < 4; ++t) acc.p[t] = (float*)uni((uint64_t)lp[t]);
+#pragma unroll
+          for (int i = 0; i < M; ++i) acc.v[i] = 0.0f;
+          acc.on = true;
+        }
+#pragma unroll
+        for (int i = 0; i < M; ++i) acc.v[i] = uni(acc.v[i] + wave_sum(same ? val[i] : 0.0f));
+        if (same) mine = false;
+      }
+    }
+    if (mine) {
+#pragma unroll
+      for (int c = 0; c < (CT > 0 ? CT : 1); ++c)
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          if (val[4 * c + t] != 0.0f) unsafeAtomicAdd(p[t] + c, val[4 * c + t]);
+    }
   } else {
+    const uint32_t key2 = ((uint32_t)b.ix1 << 16) ^ (uint32_t)b.iy1;
     for (int c = 0; c < C; ++c) {
       const float gc = valid ? g[c] * scale : 0.0f;
-      float val[4] = {b.w00 * gc, b.w10 * gc, b.w01 * gc, b.w11 * gc};
-      float* addr[4] = {base + o00 + c, base + o10 + c, base + o01 + c, base + o11 + c};
-      group_atomic_add<4>(valid, key, addr, val, key2);
+      float val[4] = {w00 * gc, w10 * gc, w01 * gc, w11 * gc};
+      float* addr[4] = {p[0] + c, p[1] + c, p[2] + c, p[3] + c};
+      group_atomic_add<4>(valid, (uint64_t)p[0], addr, val, key2);
     }
   }
 }
@@ -319,16 +407,46 @@ __device__ __forceinline__ void duv_level(const float* __restrict__ lv, int Wk, 
   }
 }
 
+struct TexBwdArgs {
+  const float* tex;
+  const float* pyr;
+  MipDesc md;
+  int64_t tex_stride;
+  int Ht, Wt, C, boundary, has_bias;
+  const float* uv;
+  const float* uv_da;
+  const float* bias_map;
+  float scale_bias;
+  int N, Hi, Wi, ntx, nty;
+  const float* d_out;
+  float* d_tex;
+  float* d_pyr;
+  float* d_uv;
+  float* d_uv_da;
+  float* d_bias;
+};
+
+// One 16x16 pixel tile of the fused backward (one 8x8 quadrant per wave).
 template <int FILTER, bool CUBE, int CT>
-__global__ void __launch_bounds__(256) k_tex_bwd(
-    const float* __restrict__ tex, const float* __restrict__ pyr, MipDesc md, int64_t tex_stride,
-    int Ht, int Wt, int C_, const float* __restrict__ uv, const float* __restrict__ uv_da,
-    const float* __restrict__ bias_map, float scale_bias, int has_bias, int boundary, int N,
-    int Hi, int Wi, int ntx, int nty, const float* __restrict__ d_out, float* __restrict__ d_tex,
-    float* __restrict__ d_pyr, float* __restrict__ d_uv, float* __restrict__ d_uv_da,
-    float* __restrict__ d_bias) {
+__device__ __forceinline__ void tex_bwd_tile(const TexBwdArgs& A, int bidx,
+                                             FootAcc<(CT > 0 ? CT : 1)>& acc0) {
+  const float* __restrict__ tex = A.tex;
+  const float* __restrict__ pyr = A.pyr;
+  const MipDesc& md = A.md;
+  const int64_t tex_stride = A.tex_stride;
+  const int Ht = A.Ht, Wt = A.Wt, C_ = A.C, boundary = A.boundary, has_bias = A.has_bias;
+  const float* __restrict__ uv = A.uv;
+  const float* __restrict__ uv_da = A.uv_da;
+  const float* __restrict__ bias_map = A.bias_map;
+  const float scale_bias = A.scale_bias;
+  const int Hi = A.Hi, Wi = A.Wi, ntx = A.ntx, nty = A.nty;
+  const float* __restrict__ d_out = A.d_out;
+  float* __restrict__ d_tex = A.d_tex;
+  float* __restrict__ d_pyr = A.d_pyr;
+  float* __restrict__ d_uv = A.d_uv;
+  float* __restrict__ d_uv_da = A.d_uv_da;
+  float* __restrict__ d_bias = A.d_bias;
   const int tiles = ntx * nty;
-  const int bidx = (int)blockIdx.x;
   const int n = bidx / tiles;
   const int tile = bidx - n * tiles;
   const int ty = tile / ntx, tx = tile - ty * ntx;
@@ -351,7 +469,7 @@ __global__ void __launch_bounds__(256) k_tex_bwd(
     if (CT > 0) {
 #pragma unroll
       for (int c = 0; c < (CT > 0 ? CT : 1); ++c) g[c] = gp[c];
-      scatter_footprint<CT>(valid, fb, Wt, C, b, g, 1.0f);
+      scatter_footprint<CT>(valid, fb, Wt, C, b, g, 1.0f, acc0);
     } else {
       for (int c = 0; c < C; ++c) {
         const float gc = valid ? gp[c] : 0.0f;
@@ -396,7 +514,7 @@ __global__ void __launch_bounds__(256) k_tex_bwd(
   if (FILTER == DR_FILTER_LINEAR) {  // Texture.swift:407-521
     const Bilin b = bilin(uvp.x, uvp.y, Wt, Ht, boundary);
     const float* tb = tex + n * tex_stride;
-    scatter_footprint<CT>(valid, dt, Wt, C, b, gsrc, 1.0f);
+    scatter_footprint<CT>(valid, dt, Wt, C, b, gsrc, 1.0f, acc0);
     if (d_uv && valid) {
       float dfx, dfy, unused;
       duv_level(tb, Wt, C, b, gsrc, 1.0f, dfx, dfy, unused);
@@ -429,7 +547,10 @@ __global__ void __launch_bounds__(256) k_tex_bwd(
     const Bilin b = bilin(uvp.x, uvp.y, Wk, Hk, boundary);
     // A zero weight adds nothing; skip the level's atomics (but keep the
     // wave convergent for the grouping).
-    scatter_footprint<CT>(valid && scale != 0.0f, dlevel_ptr(k), Wk, C, b, gsrc, scale);
+    if (li == 0)
+      scatter_footprint<CT, true>(valid && scale != 0.0f, dlevel_ptr(k), Wk, C, b, gsrc, scale, acc0);
+    else
+      scatter_footprint<CT, false>(valid && scale != 0.0f, dlevel_ptr(k), Wk, C, b, gsrc, scale, acc0);
     if (valid) {
       float dfx, dfy;
       duv_level(level_ptr(k), Wk, C, b, gsrc, scale, dfx, dfy, samp[li]);
@@ -483,6 +604,15 @@ __global__ void __launch_bounds__(256) k_tex_bwd(
   }
 }
 
+template <int FILTER, bool CUBE, int CT>
+__global__ void __launch_bounds__(256) k_tex_bwd(TexBwdArgs A, int total_tiles) {
+  FootAcc<(CT > 0 ? CT : 1)> acc0;
+  acc_init(acc0);
+  for (int t = (int)blockIdx.x; t < total_tiles; t += (int)gridDim.x)
+    tex_bwd_tile<FILTER, CUBE, CT>(A, t, acc0);
+  acc_flush(acc0);
+}
+
 // Texture.swift:156: level k = 2x2 mean of level k-1.
 __global__ void __launch_bounds__(256) k_mip_down(const float* __restrict__ src,
                                                   float* __restrict__ dst, int Nt, int h, int w,
@@ -528,6 +658,26 @@ __global__ void __launch_bounds__(256) k_mip_collapse(const float* __restrict__ 
   float acc = at(kL);
   for (int k = kL - 1; k >= 1; --k) acc = at(k) + acc * 0.25f;
   d_tex[i] = d_tex[i] + acc * 0.25f;
+}
+
+// Launches the persistent backward with as many workgroups as fit on the
+// device at once.
+template <int FILTER, bool CUBE, int CT>
+hipError_t launch_tex_bwd(const TexBwdArgs& args, int total_tiles, hipStream_t stream) {
+  static int per_cu = 0;
+  if (per_cu == 0) {
+    int b = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, k_tex_bwd<FILTER, CUBE, CT>, 256, 0) !=
+            hipSuccess ||
+        b <= 0)
+      b = 2;
+    per_cu = b;
+  }
+  const int64_t resident = (int64_t)device_cu_count() * per_cu;
+  const unsigned grid = (unsigned)(total_tiles < resident ? total_tiles : resident);
+  hipLaunchKernelGGL((k_tex_bwd<FILTER, CUBE, CT>), dim3(grid), dim3(256), 0, stream, args,
+                     total_tiles);
+  return hipGetLastError();
 }
 
 }  // namespace dr
@@ -597,6 +747,7 @@ extern "C" int dr_texture_build_mip(const float* tex, int Nt, int H, int W, int 
   for (int k = 1; k < L; ++k) {
     const float* src = k == 1 ? tex : pyramid + md.off[k - 1];
     const int64_t n = (int64_t)Nt * md.h[k] * md.w[k] * C;
+    DR_TIMED("k_mip_down", stream);
     hipLaunchKernelGGL(k_mip_down, dim3(grid_for(n, 256)), dim3(256), 0, stream, src,
                        pyramid + md.off[k], Nt, md.h[k - 1], md.w[k - 1], C);
     DR_CHECK_LAUNCH();
@@ -658,6 +809,7 @@ extern "C" int dr_texture_fwd(const float* tex, const float* pyramid, int Nt, in
   const float scale_bias = exp2f(bias);
   const int has_bias = bias != 0.0f;
   const dim3 grid(grid_for(P, 256));
+  DR_TIMED("k_tex_fwd", stream);
   DR_TEX_DISPATCH(k_tex_fwd, grid, tex, pyramid, md, tex_stride, Ht, Wt, C, uv, uv_da, bias_map,
                   scale_bias, has_bias, boundary, P, Hi * Wi, out);
   DR_CHECK_LAUNCH();
@@ -690,16 +842,60 @@ extern "C" int dr_texture_bwd(const float* tex, const float* pyramid, int Nt, in
     if (!d_pyr) return DR_ERR_MEMORY;
     DR_CHECK_HIP(fill_async(d_pyr, 0.0f, np, stream));
   }
-  const float scale_bias = exp2f(bias);
-  const int has_bias = bias != 0.0f;
   const int ntx = (Wi + 15) / 16, nty = (Hi + 15) / 16;
-  const dim3 grid((unsigned)((int64_t)N * ntx * nty));
-  DR_TEX_DISPATCH(k_tex_bwd, grid, tex, pyramid, md, tex_stride, Ht, Wt, C, uv, uv_da, bias_map,
-                  scale_bias, has_bias, boundary, N, Hi, Wi, ntx, nty, d_out, d_tex, d_pyr, d_uv,
-                  mip ? d_uv_da : nullptr, mip ? d_bias_map : nullptr);
-  DR_CHECK_LAUNCH();
+  TexBwdArgs args;
+  args.tex = tex;
+  args.pyr = pyramid;
+  args.md = md;
+  args.tex_stride = tex_stride;
+  args.Ht = Ht;
+  args.Wt = Wt;
+  args.C = C;
+  args.boundary = boundary;
+  args.has_bias = bias != 0.0f;
+  args.uv = uv;
+  args.uv_da = uv_da;
+  args.bias_map = bias_map;
+  args.scale_bias = exp2f(bias);
+  args.N = N;
+  args.Hi = Hi;
+  args.Wi = Wi;
+  args.ntx = ntx;
+  args.nty = nty;
+  args.d_out = d_out;
+  args.d_tex = d_tex;
+  args.d_pyr = d_pyr;
+  args.d_uv = d_uv;
+  args.d_uv_da = mip ? d_uv_da : nullptr;
+  args.d_bias = mip ? d_bias_map : nullptr;
+  const int64_t total_tiles = (int64_t)N * ntx * nty;
+  DR_CHECK_ARG(total_tiles < (int64_t)1 << 31, "texture_bwd: too many pixels");
+  // Persistent tiles: each wave keeps its footprint accumulator across the
+  // tiles it visits.
+  {
+    DR_TIMED("k_tex_bwd", stream);
+    hipError_t e = hipSuccess;
+#define DR_TB(F, CUBEV, CTV) e = launch_tex_bwd<F, CUBEV, CTV>(args, (int)total_tiles, stream)
+#define DR_TB_C(F, CUBEV)                  \
+  switch (C) {                             \
+    case 1: DR_TB(F, CUBEV, 1); break;     \
+    case 2: DR_TB(F, CUBEV, 2); break;     \
+    case 3: DR_TB(F, CUBEV, 3); break;     \
+    case 4: DR_TB(F, CUBEV, 4); break;     \
+    default: DR_TB(F, CUBEV, 0); break;    \
+  }
+    if (cube) DR_TB_C(DR_FILTER_LINEAR, true)
+    else if (filter == DR_FILTER_NEAREST) DR_TB_C(DR_FILTER_NEAREST, false)
+    else if (filter == DR_FILTER_LINEAR) DR_TB_C(DR_FILTER_LINEAR, false)
+    else if (filter == DR_FILTER_LINEAR_MIPMAP_NEAREST) DR_TB_C(DR_FILTER_LINEAR_MIPMAP_NEAREST, false)
+    else DR_TB_C(DR_FILTER_LINEAR_MIPMAP_LINEAR, false)
+#undef DR_TB_C
+#undef DR_TB
+    DR_CHECK_HIP(e);
+  }
   if (d_pyr) {
     const int64_t n0 = (int64_t)Nt * Ht * Wt * C;
+    DR_TIMED("k_mip_collapse", stream);
     hipLaunchKernelGGL(k_mip_collapse, dim3(grid_for(n0, 256)), dim3(256), 0, stream, d_pyr, md,
                        Nt, C, d_tex);
     DR_CHECK_LAUNCH();

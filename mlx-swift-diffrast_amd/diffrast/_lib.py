@@ -22,6 +22,9 @@ SIGNATURES = {
     "dr_abi_version": ([], _i),
     "dr_get_last_error": ([], ctypes.c_char_p),
     "dr_release_scratch": ([], _i),
+    "dr_profile_enable": ([_i], _i),
+    "dr_profile_reset": ([], _i),
+    "dr_profile_report": ([ctypes.c_char_p, _i], _i),
     "dr_rasterize_fwd": ([_p, _i64, _p, _p, _p, _i, _i, _i, _i, _i, _p, _p, _p], _i),
     "dr_rasterize_bwd": ([_p, _i64, _p, _p, _p, _p, _i, _i, _i, _i, _p, _u, _p], _i),
     "dr_interpolate_fwd": ([_p, _i64, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p, _p, _p], _i),
@@ -72,3 +75,19 @@ def check(rc: int) -> None:
     if rc == DR_ERR_ARGUMENT:
         raise ValueError(msg)
     raise RuntimeError(f"diffrast error {rc}: {msg}")
+
+
+def profile_report():
+    """{kernel: {"count": launches, "total_ms": ms}} of the launches timed
+    since dr_profile_reset while dr_profile_enable(1) was on."""
+    lib = load()
+    n = lib.dr_profile_report(None, 0)
+    if n < 0:
+        raise RuntimeError("dr_profile_report failed")
+    buf = ctypes.create_string_buffer(n + 1)
+    lib.dr_profile_report(buf, n + 1)
+    out = {}
+    for line in buf.value.decode().splitlines():
+        name, cnt, ms = line.split()
+        out[name] = {"count": int(cnt), "total_ms": float(ms)}
+    return out
