@@ -250,6 +250,8 @@ __global__ void __launch_bounds__(256) k_aa_bwd(AAIn a, const float* __restrict_
                                                 float* __restrict__ d_pos, int accumulate) {
   __shared__ float s_alpha[4][16][17];
   __shared__ float s_halo[4][16];
+  __shared__ LdsTable<4, 128> tab;  // d_pos rows touched by this tile
+  lds_table_clear(tab);
   const int tiles = ntx * nty;
   const int b = (int)blockIdx.x;
   const int n = b / tiles;
@@ -314,8 +316,8 @@ __global__ void __launch_bounds__(256) k_aa_bwd(AAIn a, const float* __restrict_
       dc[c] = accumulate ? dc[c] + acc : acc;
     }
   }
-  // 4) d_pos (Antialias.swift:405-495).
-  if (!d_pos) return;
+  // 4) d_pos (Antialias.swift:405-495), summed per vertex in LDS.
+  if (!d_pos) return;  // uniform: no barrier follows
   const float halfW = (float)a.W * 0.5f, halfH = (float)a.H * 0.5f;
   const float* p = a.pos + (int64_t)n * a.V * 4;
   float* dp = d_pos + (int64_t)n * a.V * 4;
@@ -323,9 +325,6 @@ __global__ void __launch_bounds__(256) k_aa_bwd(AAIn a, const float* __restrict_
 #pragma unroll
   for (int d = 0; d < 4; ++d) {
     bool on = sd[d].active && sd[d].alpha > 0.0f && sd[d].alpha < 1.0f;
-    float dv[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    float* addr[6] = {dp, dp, dp, dp, dp, dp};
-    uint64_t key = 0;
     if (on) {
       const int nh = ph + (d == 1 ? 1 : (d == 3 ? -1 : 0));
       const int nw = pw + (d == 0 ? 1 : (d == 2 ? -1 : 0));
@@ -359,18 +358,16 @@ __global__ void __launch_bounds__(256) k_aa_bwd(AAIn a, const float* __restrict_
           const float4 P = *reinterpret_cast<const float4*>(p + (int64_t)iv[e] * 4);
           const float inv_w = 1.0f / P.w;
           const float nd_x = P.x * inv_w, nd_y = P.y * inv_w;
-          dv[3 * e + 0] = d_alpha * dex[e] * halfW * inv_w;
-          dv[3 * e + 1] = d_alpha * dey[e] * (-halfH) * inv_w;
-          dv[3 * e + 2] = d_alpha * (dex[e] * (-halfW * nd_x) + dey[e] * (halfH * nd_y)) * inv_w;
-          addr[3 * e + 0] = dp + (int64_t)iv[e] * 4 + 0;
-          addr[3 * e + 1] = dp + (int64_t)iv[e] * 4 + 1;
-          addr[3 * e + 2] = dp + (int64_t)iv[e] * 4 + 3;
+          const float dv[4] = {
+              d_alpha * dex[e] * halfW * inv_w, d_alpha * dey[e] * (-halfH) * inv_w, 0.0f,
+              d_alpha * (dex[e] * (-halfW * nd_x) + dey[e] * (halfH * nd_y)) * inv_w};
+          lds_table_add(tab, dp + (int64_t)iv[e] * 4, dv);
         }
-        key = ((uint64_t)(uint32_t)s.ie0 << 32) | (uint32_t)s.ie1;
       }
     }
-    group_atomic_add<6>(on, key, addr, dv);
   }
+  __syncthreads();
+  lds_table_flush(tab);
 }
 
 }  // namespace dr

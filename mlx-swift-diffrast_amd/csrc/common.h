@@ -164,6 +164,80 @@ __device__ __forceinline__ void group_atomic_add(bool valid, uint64_t key, float
   }
 }
 
+// ---------------------------------------------------------------------------
+// Workgroup scatter aggregation in LDS.  Contributions are keyed by their
+// destination address; an open-addressing table sums them with LDS
+// atomics, and the flush issues one global atomic per distinct destination
+// and value.  A lane whose probe sequence finds no room adds to global
+// memory directly.
+// ---------------------------------------------------------------------------
+
+constexpr unsigned long long kEmptyKey = ~0ull;
+constexpr int kLdsProbes = 8;
+
+template <int NV, int CAP>
+struct LdsTable {
+  unsigned long long key[CAP];
+  float val[CAP][NV];
+};
+
+__device__ __forceinline__ uint32_t addr_hash(uint64_t k) {
+  return (uint32_t)(((k >> 2) * 0x9E3779B97F4A7C15ull) >> 32);
+}
+
+template <int NV, int CAP>
+__device__ __forceinline__ void lds_table_clear(LdsTable<NV, CAP>& t) {
+  for (int i = threadIdx.x; i < CAP; i += blockDim.x) {
+    t.key[i] = kEmptyKey;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) t.val[i][j] = 0.0f;
+  }
+}
+
+// Adds v[0..NV) to dst[0..NV).
+template <int NV, int CAP>
+__device__ __forceinline__ void lds_table_add(LdsTable<NV, CAP>& t, float* dst, const float* v) {
+  bool any = false;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) any = any || v[j] != 0.0f;
+  if (!any) return;
+  const uint64_t key = (uint64_t)dst;
+  uint32_t h = addr_hash(key) & (CAP - 1);
+#pragma unroll 1
+  for (int probe = 0; probe < kLdsProbes; ++probe) {
+    unsigned long long cur = t.key[h];
+    if (cur == kEmptyKey) cur = atomicCAS(&t.key[h], kEmptyKey, (unsigned long long)key);
+    if (cur == kEmptyKey || cur == key) {
+#pragma unroll
+      for (int j = 0; j < NV; ++j)
+        if (v[j] != 0.0f) atomicAdd(&t.val[h][j], v[j]);
+      return;
+    }
+    h = (h + 1) & (CAP - 1);
+  }
+#pragma unroll
+  for (int j = 0; j < NV; ++j)
+    if (v[j] != 0.0f) unsafeAtomicAdd(dst + j, v[j]);
+}
+
+// Writes the table out (call after a barrier) and leaves it cleared.
+template <int NV, int CAP>
+__device__ __forceinline__ void lds_table_flush(LdsTable<NV, CAP>& t) {
+  for (int i = threadIdx.x; i < CAP; i += blockDim.x) {
+    const unsigned long long k = t.key[i];
+    if (k != kEmptyKey) {
+      float* p = (float*)k;
+#pragma unroll
+      for (int j = 0; j < NV; ++j) {
+        const float v = t.val[i][j];
+        if (v != 0.0f) unsafeAtomicAdd(p + j, v);
+        t.val[i][j] = 0.0f;
+      }
+      t.key[i] = kEmptyKey;
+    }
+  }
+}
+
 template <typename T>
 __global__ void fill_kernel(T* __restrict__ p, T v, int64_t n) {
   int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;

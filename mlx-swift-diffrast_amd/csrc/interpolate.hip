@@ -70,6 +70,10 @@ __global__ void __launch_bounds__(256) k_interp_bwd(
     const float* __restrict__ d_out_da, int N, int H, int W, int ntx, int nty, int A_,
     float* __restrict__ d_attr, int64_t d_attr_stride, float* __restrict__ d_rast,
     float* __restrict__ d_rast_db) {
+  constexpr int NV = AT > 0 ? AT : 1;
+  __shared__ LdsTable<NV, 256> tab;  // d_attr rows (or elements) touched by this tile
+  lds_table_clear(tab);
+  __syncthreads();
   const int tiles = ntx * nty;
   const int b = (int)blockIdx.x;
   const int n = b / tiles;
@@ -77,7 +81,6 @@ __global__ void __launch_bounds__(256) k_interp_bwd(
   const int ty = tile / ntx, tx = tile - ty * ntx;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int qx0 = tx * 16 + (wave & 1) * 8, qy0 = ty * 16 + (wave >> 1) * 8;
-  if (qx0 >= W || qy0 >= H) return;
   const int pw = qx0 + (lane & 7), ph = qy0 + (lane >> 3);
   const bool inside = pw < W && ph < H;
   const int64_t pix = ((int64_t)n * H + min(ph, H - 1)) * W + min(pw, W - 1);
@@ -132,62 +135,58 @@ __global__ void __launch_bounds__(256) k_interp_bwd(
       *reinterpret_cast<float4*>(d_rast_db + pix * 4) = make_float4(d_udx, d_udy, d_vdx, d_vdy);
   }
 
-  // d_attr (Interpolate.swift:231-264, :269-324).
-  const uint64_t key = (uint64_t)(uint32_t)t;
-  if (AT > 0 && (KT > 0 || K == 0)) {
-    constexpr int M = 3 * (AT > 0 ? AT : 1) + 3 * KT;
-    float val[M];
-    float* addr[M];
+  // d_attr (Interpolate.swift:231-264, :269-324), summed per vertex row in
+  // LDS before the global atomics.
+  if (AT > 0) {
+    if (valid) {
+      float r0[NV], r1[NV], r2[NV];
 #pragma unroll
-    for (int a = 0; a < (AT > 0 ? AT : 1); ++a) {
-      const float ga = valid ? g[a] : 0.0f;
-      val[3 * a + 0] = bw * ga;
-      val[3 * a + 1] = u * ga;
-      val[3 * a + 2] = v * ga;
-      addr[3 * a + 0] = da + (int64_t)i0 * A + a;
-      addr[3 * a + 1] = da + (int64_t)i1 * A + a;
-      addr[3 * a + 2] = da + (int64_t)i2 * A + a;
-    }
-    if (KT > 0) {
-      const float* gd = d_out_da + pix * 2 * K;
-#pragma unroll
-      for (int k = 0; k < (KT > 0 ? KT : 1); ++k) {
-        const int a = diff_idx ? diff_idx[k] : k;
-        const float gx = valid ? gd[2 * k + 0] : 0.0f, gy = valid ? gd[2 * k + 1] : 0.0f;
-        const float u_term = gx * db.x + gy * db.y;
-        const float v_term = gx * db.z + gy * db.w;
-        const int base = 3 * (AT > 0 ? AT : 1) + 3 * k;
-        val[base + 0] = -u_term - v_term;
-        val[base + 1] = u_term;
-        val[base + 2] = v_term;
-        addr[base + 0] = da + (int64_t)i0 * A + a;
-        addr[base + 1] = da + (int64_t)i1 * A + a;
-        addr[base + 2] = da + (int64_t)i2 * A + a;
+      for (int a = 0; a < NV; ++a) {
+        const float ga = g[a];
+        r0[a] = bw * ga;
+        r1[a] = u * ga;
+        r2[a] = v * ga;
       }
+      if (KT > 0) {  // identity diff_idx (DiffAttrs.all)
+        const float* gd = d_out_da + pix * 2 * K;
+#pragma unroll
+        for (int k = 0; k < (KT > 0 ? KT : 1); ++k) {
+          const float gx = gd[2 * k + 0], gy = gd[2 * k + 1];
+          const float u_term = gx * db.x + gy * db.y;
+          const float v_term = gx * db.z + gy * db.w;
+          r0[k] += -u_term - v_term;
+          r1[k] += u_term;
+          r2[k] += v_term;
+        }
+      }
+      lds_table_add(tab, da + (int64_t)i0 * A, r0);
+      lds_table_add(tab, da + (int64_t)i1 * A, r1);
+      lds_table_add(tab, da + (int64_t)i2 * A, r2);
     }
-    group_atomic_add<M>(valid, key, addr, val);
-  } else {
+  } else if (valid) {
     for (int a = 0; a < A; ++a) {
-      const float ga = valid ? g[a] : 0.0f;
-      float val[3] = {bw * ga, u * ga, v * ga};
-      float* addr[3] = {da + (int64_t)i0 * A + a, da + (int64_t)i1 * A + a,
-                        da + (int64_t)i2 * A + a};
-      group_atomic_add<3>(valid, key, addr, val);
+      const float ga = g[a];
+      const float v0[1] = {bw * ga}, v1[1] = {u * ga}, v2[1] = {v * ga};
+      lds_table_add(tab, da + (int64_t)i0 * A + a, v0);
+      lds_table_add(tab, da + (int64_t)i1 * A + a, v1);
+      lds_table_add(tab, da + (int64_t)i2 * A + a, v2);
     }
     if (K > 0) {
       const float* gd = d_out_da + pix * 2 * K;
       for (int k = 0; k < K; ++k) {
         const int a = diff_idx ? diff_idx[k] : k;
-        const float gx = valid ? gd[2 * k + 0] : 0.0f, gy = valid ? gd[2 * k + 1] : 0.0f;
+        const float gx = gd[2 * k + 0], gy = gd[2 * k + 1];
         const float u_term = gx * db.x + gy * db.y;
         const float v_term = gx * db.z + gy * db.w;
-        float val[3] = {-u_term - v_term, u_term, v_term};
-        float* addr[3] = {da + (int64_t)i0 * A + a, da + (int64_t)i1 * A + a,
-                          da + (int64_t)i2 * A + a};
-        group_atomic_add<3>(valid, key, addr, val);
+        const float v0[1] = {-u_term - v_term}, v1[1] = {u_term}, v2[1] = {v_term};
+        lds_table_add(tab, da + (int64_t)i0 * A + a, v0);
+        lds_table_add(tab, da + (int64_t)i1 * A + a, v1);
+        lds_table_add(tab, da + (int64_t)i2 * A + a, v2);
       }
     }
   }
+  __syncthreads();
+  lds_table_flush(tab);
 }
 
 }  // namespace dr
@@ -197,9 +196,9 @@ using namespace dr;
 #define DR_INTERP_DISPATCH(KERNEL, GRID, ...)                                              \
   do {                                                                                     \
     if (A == 2 && K == 0) hipLaunchKernelGGL((KERNEL<2, 0>), GRID, dim3(256), 0, stream, __VA_ARGS__); \
-    else if (A == 2 && K == 2) hipLaunchKernelGGL((KERNEL<2, 2>), GRID, dim3(256), 0, stream, __VA_ARGS__); \
+    else if (A == 2 && K == 2 && !diff_idx) hipLaunchKernelGGL((KERNEL<2, 2>), GRID, dim3(256), 0, stream, __VA_ARGS__); \
     else if (A == 3 && K == 0) hipLaunchKernelGGL((KERNEL<3, 0>), GRID, dim3(256), 0, stream, __VA_ARGS__); \
-    else if (A == 3 && K == 3) hipLaunchKernelGGL((KERNEL<3, 3>), GRID, dim3(256), 0, stream, __VA_ARGS__); \
+    else if (A == 3 && K == 3 && !diff_idx) hipLaunchKernelGGL((KERNEL<3, 3>), GRID, dim3(256), 0, stream, __VA_ARGS__); \
     else if (A == 4 && K == 0) hipLaunchKernelGGL((KERNEL<4, 0>), GRID, dim3(256), 0, stream, __VA_ARGS__); \
     else if (A == 6 && K == 0) hipLaunchKernelGGL((KERNEL<6, 0>), GRID, dim3(256), 0, stream, __VA_ARGS__); \
     else hipLaunchKernelGGL((KERNEL<0, 0>), GRID, dim3(256), 0, stream, __VA_ARGS__);      \

@@ -315,6 +315,9 @@ __global__ void __launch_bounds__(256) k_raster_bwd(
     const float* __restrict__ rast, const float* __restrict__ d_rast,
     const float* __restrict__ d_rast_db, int N, int H, int W, int ntx, int nty,
     float* __restrict__ d_pos) {
+  __shared__ LdsTable<4, 256> tab;  // d_pos rows touched by this tile
+  lds_table_clear(tab);
+  __syncthreads();
   const int tiles = ntx * nty;
   const int b = xcd_remap((int)blockIdx.x, tiles * N);
   const int n = b / tiles;
@@ -324,7 +327,6 @@ __global__ void __launch_bounds__(256) k_raster_bwd(
   const int lane = threadIdx.x & 63;
   const int qx0 = tx * kTile + (wave & 1) * 8;
   const int qy0 = ty * kTile + (wave >> 1) * 8;
-  if (qx0 >= W || qy0 >= H) return;
   const int pw = qx0 + (lane & 7);
   const int ph = qy0 + (lane >> 3);
   bool valid = pw < W && ph < H;
@@ -333,13 +335,6 @@ __global__ void __launch_bounds__(256) k_raster_bwd(
   const int t = f2i(r.w) - 1;
   valid = valid && t >= 0;
 
-  float val[12];
-  float* addr[12];
-#pragma unroll
-  for (int k = 0; k < 12; ++k) {
-    val[k] = 0.0f;
-    addr[k] = d_pos;
-  }
   if (valid) {
     const float u_val = r.x, v_val = r.y;
     const float bw_val = 1.0f - u_val - v_val;
@@ -409,6 +404,7 @@ __global__ void __launch_bounds__(256) k_raster_bwd(
     dsx0 += d_db3 * (-Ky) * inv_area;
     dsx1 += d_db3 * (Ky) * inv_area;
     const float inv_w0 = 1.0f / P0.w, inv_w1 = 1.0f / P1.w, inv_w2 = 1.0f / P2.w;
+    float val[12];
     val[0] = dsx0 * inv_w0;
     val[1] = dsy0 * inv_w0;
     val[2] = dsz0_s * inv_w0;
@@ -421,14 +417,12 @@ __global__ void __launch_bounds__(256) k_raster_bwd(
     val[9] = dsy2 * inv_w2;
     val[10] = dsz2_s * inv_w2;
     val[11] = -(sx2 * dsx2 + sy2 * dsy2 + sz2 * dsz2_s) * inv_w2;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      addr[c] = dp + (int64_t)i0 * 4 + c;
-      addr[4 + c] = dp + (int64_t)i1 * 4 + c;
-      addr[8 + c] = dp + (int64_t)i2 * 4 + c;
-    }
+    lds_table_add(tab, dp + (int64_t)i0 * 4, &val[0]);
+    lds_table_add(tab, dp + (int64_t)i1 * 4, &val[4]);
+    lds_table_add(tab, dp + (int64_t)i2 * 4, &val[8]);
   }
-  group_atomic_add<12>(valid, (uint64_t)(uint32_t)t, addr, val);
+  __syncthreads();
+  lds_table_flush(tab);
 }
 
 }  // namespace dr

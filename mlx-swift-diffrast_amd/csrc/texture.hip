@@ -299,11 +299,17 @@ __device__ __forceinline__ void acc_flush(FootAcc<CT>& a) {
 // Scatter of one bilinear footprint's gradient (w * g * scale) into one
 // level.  Taps that land on the same texel (clamped borders) are merged
 // first; lanes sharing the footprint are summed across the wave.
+constexpr int kTexTable = 1024;  // LDS aggregation entries per tile (texels)
+
+template <int CT>
+using TexTable = LdsTable<(CT > 0 ? CT : 1), kTexTable>;
+
 template <int CT, bool USE_ACC = true>
 __device__ __forceinline__ void scatter_footprint(bool valid, float* __restrict__ base, int Wk,
                                                   int C, const Bilin& b, const float* g,
                                                   float scale,
-                                                  FootAcc<(CT > 0 ? CT : 1)>& acc) {
+                                                  FootAcc<(CT > 0 ? CT : 1)>& acc,
+                                                  TexTable<CT>& tab) {
   float w00 = b.w00, w10 = b.w10, w01 = b.w01, w11 = b.w11;
   if (b.ix1 == b.ix0) {
     w00 += w10;
@@ -370,10 +376,12 @@ __device__ __forceinline__ void scatter_footprint(bool valid, float* __restrict_
     }
     if (mine) {
 #pragma unroll
-      for (int c = 0; c < (CT > 0 ? CT : 1); ++c)
+      for (int t = 0; t < 4; ++t) {
+        float v[CT > 0 ? CT : 1];
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
-          if (val[4 * c + t] != 0.0f) unsafeAtomicAdd(p[t] + c, val[4 * c + t]);
+        for (int c = 0; c < (CT > 0 ? CT : 1); ++c) v[c] = val[4 * c + t];
+        lds_table_add(tab, p[t], v);
+      }
     }
   } else {
     const uint32_t key2 = ((uint32_t)b.ix1 << 16) ^ (uint32_t)b.iy1;
@@ -429,7 +437,8 @@ struct TexBwdArgs {
 // One 16x16 pixel tile of the fused backward (one 8x8 quadrant per wave).
 template <int FILTER, bool CUBE, int CT>
 __device__ __forceinline__ void tex_bwd_tile(const TexBwdArgs& A, int bidx,
-                                             FootAcc<(CT > 0 ? CT : 1)>& acc0) {
+                                             FootAcc<(CT > 0 ? CT : 1)>& acc0,
+                                             TexTable<CT>& tab) {
   const float* __restrict__ tex = A.tex;
   const float* __restrict__ pyr = A.pyr;
   const MipDesc& md = A.md;
@@ -469,7 +478,7 @@ __device__ __forceinline__ void tex_bwd_tile(const TexBwdArgs& A, int bidx,
     if (CT > 0) {
 #pragma unroll
       for (int c = 0; c < (CT > 0 ? CT : 1); ++c) g[c] = gp[c];
-      scatter_footprint<CT>(valid, fb, Wt, C, b, g, 1.0f, acc0);
+      scatter_footprint<CT>(valid, fb, Wt, C, b, g, 1.0f, acc0, tab);
     } else {
       for (int c = 0; c < C; ++c) {
         const float gc = valid ? gp[c] : 0.0f;
@@ -499,10 +508,19 @@ __device__ __forceinline__ void tex_bwd_tile(const TexBwdArgs& A, int bidx,
     const int iy = apply_boundary(tyi, Ht, boundary, oy);
     const float mask = (1.0f - ox) * (1.0f - oy);
     float* tp = dt + ((int64_t)iy * Wt + ix) * C;
-    for (int c = 0; c < C; ++c) {
-      float val[1] = {valid ? gp[c] * mask : 0.0f};
-      float* addr[1] = {tp + c};
-      group_atomic_add<1>(valid, (uint64_t)tp, addr, val);
+    if (CT > 0) {
+      if (valid) {
+        float v[CT > 0 ? CT : 1];
+#pragma unroll
+        for (int c = 0; c < (CT > 0 ? CT : 1); ++c) v[c] = gp[c] * mask;
+        lds_table_add(tab, tp, v);
+      }
+    } else {
+      for (int c = 0; c < C; ++c) {
+        float val[1] = {valid ? gp[c] * mask : 0.0f};
+        float* addr[1] = {tp + c};
+        group_atomic_add<1>(valid, (uint64_t)tp, addr, val);
+      }
     }
     if (d_uv && valid) *reinterpret_cast<float2*>(d_uv + pix * 2) = make_float2(0.0f, 0.0f);
     return;
@@ -514,7 +532,7 @@ __device__ __forceinline__ void tex_bwd_tile(const TexBwdArgs& A, int bidx,
   if (FILTER == DR_FILTER_LINEAR) {  // Texture.swift:407-521
     const Bilin b = bilin(uvp.x, uvp.y, Wt, Ht, boundary);
     const float* tb = tex + n * tex_stride;
-    scatter_footprint<CT>(valid, dt, Wt, C, b, gsrc, 1.0f, acc0);
+    scatter_footprint<CT>(valid, dt, Wt, C, b, gsrc, 1.0f, acc0, tab);
     if (d_uv && valid) {
       float dfx, dfy, unused;
       duv_level(tb, Wt, C, b, gsrc, 1.0f, dfx, dfy, unused);
@@ -548,9 +566,11 @@ __device__ __forceinline__ void tex_bwd_tile(const TexBwdArgs& A, int bidx,
     // A zero weight adds nothing; skip the level's atomics (but keep the
     // wave convergent for the grouping).
     if (li == 0)
-      scatter_footprint<CT, true>(valid && scale != 0.0f, dlevel_ptr(k), Wk, C, b, gsrc, scale, acc0);
+      scatter_footprint<CT, true>(valid && scale != 0.0f, dlevel_ptr(k), Wk, C, b, gsrc, scale, acc0,
+                                  tab);
     else
-      scatter_footprint<CT, false>(valid && scale != 0.0f, dlevel_ptr(k), Wk, C, b, gsrc, scale, acc0);
+      scatter_footprint<CT, false>(valid && scale != 0.0f, dlevel_ptr(k), Wk, C, b, gsrc, scale, acc0,
+                                   tab);
     if (valid) {
       float dfx, dfy;
       duv_level(level_ptr(k), Wk, C, b, gsrc, scale, dfx, dfy, samp[li]);
@@ -606,10 +626,17 @@ __device__ __forceinline__ void tex_bwd_tile(const TexBwdArgs& A, int bidx,
 
 template <int FILTER, bool CUBE, int CT>
 __global__ void __launch_bounds__(256) k_tex_bwd(TexBwdArgs A, int total_tiles) {
+  __shared__ TexTable<CT> tab;
   FootAcc<(CT > 0 ? CT : 1)> acc0;
   acc_init(acc0);
-  for (int t = (int)blockIdx.x; t < total_tiles; t += (int)gridDim.x)
-    tex_bwd_tile<FILTER, CUBE, CT>(A, t, acc0);
+  lds_table_clear(tab);
+  __syncthreads();
+  for (int t = (int)blockIdx.x; t < total_tiles; t += (int)gridDim.x) {
+    tex_bwd_tile<FILTER, CUBE, CT>(A, t, acc0, tab);
+    __syncthreads();
+    lds_table_flush(tab);
+    __syncthreads();
+  }
   acc_flush(acc0);
 }
 
