@@ -93,8 +93,20 @@ struct AAIn {
   const float* pos;
   const int32_t* tri;
   const int32_t* topo;
+  const float2* scr;  // [N, V] pixel-space vertex positions
   int H, W, V;
 };
+
+// Pixel-space position of every vertex, with the expressions of
+// Antialias.swift:247-250: x = (x/w + 1) * W/2, y = (1 - y/w) * H/2.
+__global__ void __launch_bounds__(256) k_aa_screen(const float* __restrict__ pos, int64_t NV,
+                                                   int H, int W, float2* __restrict__ scr) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= NV) return;
+  const float4 P = *reinterpret_cast<const float4*>(pos + i * 4);
+  scr[i] = make_float2((P.x / P.w + 1.0f) * (float)W * 0.5f,
+                       (1.0f - P.y / P.w) * (float)H * 0.5f);
+}
 
 __device__ __forceinline__ int tri_at(const AAIn& a, int n, int h, int w) {
   return f2i(a.rast[((((int64_t)n * a.H + h) * a.W + w) << 2) + 3]) - 1;
@@ -124,8 +136,7 @@ __device__ __forceinline__ bool sil_dir_impl(const AAIn& a, int n, int ph, int p
     fg = tri_n;
     target = -1;
   }
-  const float* p = a.pos + (int64_t)n * a.V * 4;
-  const float W = (float)a.W, H = (float)a.H;
+  const float2* sp = a.scr + (int64_t)n * a.V;
   const float pcx = (float)pw + 0.5f, pcy = (float)ph + 0.5f;
   const float ncx = (float)nw + 0.5f, ncy = (float)nh + 0.5f;
   int ie0 = -1, ie1 = -1;
@@ -135,12 +146,8 @@ __device__ __forceinline__ bool sil_dir_impl(const AAIn& a, int n, int ph, int p
     if (a.topo[(int64_t)fg * 3 + kk] != target) continue;
     const int c0 = a.tri[(int64_t)fg * 3 + ((kk + 1) % 3)];
     const int c1 = a.tri[(int64_t)fg * 3 + ((kk + 2) % 3)];
-    const float4 P0 = *reinterpret_cast<const float4*>(p + (int64_t)c0 * 4);
-    const float4 P1 = *reinterpret_cast<const float4*>(p + (int64_t)c1 * 4);
-    const float E0x = (P0.x / P0.w + 1.0f) * W * 0.5f;
-    const float E0y = (1.0f - P0.y / P0.w) * H * 0.5f;
-    const float E1x = (P1.x / P1.w + 1.0f) * W * 0.5f;
-    const float E1y = (1.0f - P1.y / P1.w) * H * 0.5f;
+    const float2 Q0 = sp[c0], Q1 = sp[c1];
+    const float E0x = Q0.x, E0y = Q0.y, E1x = Q1.x, E1y = Q1.y;
     const float ex = E1x - E0x, ey = E1y - E0y;
     const float side_p = ex * (pcy - E0y) - ey * (pcx - E0x);
     const float side_n = ex * (ncy - E0y) - ey * (ncx - E0x);
@@ -405,6 +412,23 @@ extern "C" int dr_antialias_topology(const int32_t* tri, int T, int32_t* topo,
   return DR_OK;
 }
 
+static int aa_screen(const float* pos, int N, int V, int H, int W, hipStream_t stream,
+                     float2** out) {
+  Scratch* sc = scratch_for(stream);
+  if (!sc) return DR_ERR_HIP;
+  const int64_t nv = (int64_t)N * V;
+  float2* scr = (float2*)scratch_get(sc, stream, SLOT_AA_SCREEN, (size_t)(nv > 0 ? nv : 1) * 8);
+  if (!scr) return DR_ERR_MEMORY;
+  if (nv > 0) {
+    DR_TIMED("k_aa_screen", stream);
+    hipLaunchKernelGGL(k_aa_screen, dim3(grid_for(nv, 256)), dim3(256), 0, stream, pos, nv, H, W,
+                       scr);
+  }
+  DR_CHECK_LAUNCH();
+  *out = scr;
+  return DR_OK;
+}
+
 static int check_aa(const float* color, const float* rast, const float* pos, const int32_t* tri,
                     const int32_t* topo, int N, int H, int W, int C, int V, int T) {
   DR_CHECK_ARG(color && rast && pos && tri && topo, "antialias: null tensor");
@@ -420,7 +444,10 @@ extern "C" int dr_antialias_fwd(const float* color, const float* rast, const flo
   int st = check_aa(color, rast, pos, tri, topo, N, H, W, C, V, T);
   if (st) return st;
   DR_CHECK_ARG(out != nullptr, "antialias: null output");
-  AAIn a{rast, pos, tri, topo, H, W, V};
+  float2* scr = nullptr;
+  int st2 = aa_screen(pos, N, V, H, W, stream, &scr);
+  if (st2) return st2;
+  AAIn a{rast, pos, tri, topo, scr, H, W, V};
   const int64_t P = (int64_t)N * H * W;
   DR_TIMED("k_aa_fwd", stream);
   hipLaunchKernelGGL(k_aa_fwd, dim3(grid_for(P, 256)), dim3(256), 0, stream, a, color, N, C, out);
@@ -440,7 +467,10 @@ extern "C" int dr_antialias_bwd(const float* color, const float* rast, const flo
   if (!d_color && !d_pos) return DR_OK;
   const bool acc = (flags & DR_ACCUMULATE) != 0;
   if (d_pos && !acc) DR_CHECK_HIP(fill_async(d_pos, 0.0f, (int64_t)N * V * 4, stream));
-  AAIn a{rast, pos, tri, topo, H, W, V};
+  float2* scr = nullptr;
+  int st2 = aa_screen(pos, N, V, H, W, stream, &scr);
+  if (st2) return st2;
+  AAIn a{rast, pos, tri, topo, scr, H, W, V};
   const int ntx = (W + 15) / 16, nty = (H + 15) / 16;
   DR_TIMED("k_aa_bwd", stream);
   hipLaunchKernelGGL(k_aa_bwd, dim3((unsigned)((int64_t)N * ntx * nty)), dim3(256), 0, stream, a,

@@ -48,6 +48,7 @@ enum Slot {
   SLOT_TOPO,          // edge hash table
   SLOT_DPYR,          // mip pyramid gradient
   SLOT_SMALL,         // small device-side counters
+  SLOT_AA_SCREEN,     // per-vertex pixel-space positions (antialias)
   SLOT_COUNT
 };
 
@@ -114,10 +115,36 @@ __device__ __forceinline__ uint64_t uni(uint64_t x) {
   return ((uint64_t)hi << 32) | lo;
 }
 
+// Wave reductions with DPP row operations (VALU only) and four readlanes:
+// quad xor 1, quad xor 2, row half-mirror and row mirror leave every lane
+// holding its 16-lane row's result; the rows are then combined in scalars.
+template <int CTRL>
+__device__ __forceinline__ int dpp_mov(int v) {
+  return __builtin_amdgcn_update_dpp(v, v, CTRL, 0xF, 0xF, false);
+}
+
+template <typename Op>
+__device__ __forceinline__ int wave_reduce_i(int v, Op op) {
+  v = op(v, dpp_mov<0xB1>(v));   // quad_perm [1,0,3,2]
+  v = op(v, dpp_mov<0x4E>(v));   // quad_perm [2,3,0,1]
+  v = op(v, dpp_mov<0x141>(v));  // row_half_mirror
+  v = op(v, dpp_mov<0x140>(v));  // row_mirror
+  const int r0 = __builtin_amdgcn_readlane(v, 0), r1 = __builtin_amdgcn_readlane(v, 16);
+  const int r2 = __builtin_amdgcn_readlane(v, 32), r3 = __builtin_amdgcn_readlane(v, 48);
+  return op(op(r0, r1), op(r2, r3));
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
-  return v;
+  auto add = [](int a, int b) { return __float_as_int(__int_as_float(a) + __int_as_float(b)); };
+  return __int_as_float(wave_reduce_i(__float_as_int(v), add));
+}
+
+__device__ __forceinline__ int wave_min(int v) {
+  return wave_reduce_i(v, [](int a, int b) { return a < b ? a : b; });
+}
+
+__device__ __forceinline__ int wave_max(int v) {
+  return wave_reduce_i(v, [](int a, int b) { return a > b ? a : b; });
 }
 
 // Scatter-add of M values per lane into addresses that are equal for all
@@ -221,21 +248,21 @@ __device__ __forceinline__ void lds_table_add(LdsTable<NV, CAP>& t, float* dst, 
 }
 
 // Writes the table out (call after a barrier) and leaves it cleared.
+// Consecutive lanes take consecutive values of one entry, so the atomics of
+// an entry share a cache line request.
 template <int NV, int CAP>
 __device__ __forceinline__ void lds_table_flush(LdsTable<NV, CAP>& t) {
-  for (int i = threadIdx.x; i < CAP; i += blockDim.x) {
-    const unsigned long long k = t.key[i];
+  for (int i = threadIdx.x; i < CAP * NV; i += blockDim.x) {
+    const int e = i / NV, j = i - e * NV;
+    const unsigned long long k = t.key[e];
     if (k != kEmptyKey) {
-      float* p = (float*)k;
-#pragma unroll
-      for (int j = 0; j < NV; ++j) {
-        const float v = t.val[i][j];
-        if (v != 0.0f) unsafeAtomicAdd(p + j, v);
-        t.val[i][j] = 0.0f;
-      }
-      t.key[i] = kEmptyKey;
+      const float v = t.val[e][j];
+      if (v != 0.0f) unsafeAtomicAdd((float*)k + j, v);
+      t.val[e][j] = 0.0f;
     }
   }
+  __syncthreads();
+  for (int i = threadIdx.x; i < CAP; i += blockDim.x) t.key[i] = kEmptyKey;
 }
 
 template <typename T>

@@ -401,11 +401,12 @@ __device__ __forceinline__ void duv_level(const float* __restrict__ lv, int Wk, 
   dfx = 0.0f;
   dfy = 0.0f;
   dlod_sample = 0.0f;
+  const float* p00 = lv + (b.iy0 * Wk + b.ix0) * C;
+  const float* p10 = lv + (b.iy0 * Wk + b.ix1) * C;
+  const float* p01 = lv + (b.iy1 * Wk + b.ix0) * C;
+  const float* p11 = lv + (b.iy1 * Wk + b.ix1) * C;
   for (int c = 0; c < C; ++c) {
-    const float r00 = lv[((int64_t)b.iy0 * Wk + b.ix0) * C + c];
-    const float r10 = lv[((int64_t)b.iy0 * Wk + b.ix1) * C + c];
-    const float r01 = lv[((int64_t)b.iy1 * Wk + b.ix0) * C + c];
-    const float r11 = lv[((int64_t)b.iy1 * Wk + b.ix1) * C + c];
+    const float r00 = p00[c], r10 = p10[c], r01 = p01[c], r11 = p11[c];
     const float t00 = r00 * b.m00, t10 = r10 * b.m10, t01 = r01 * b.m01, t11 = r11 * b.m11;
     const float gc = g[c] * scale;
     dfx += gc * ((1.0f - b.fy) * (t10 - t00) + b.fy * (t11 - t01));
@@ -640,6 +641,331 @@ __global__ void __launch_bounds__(256) k_tex_bwd(TexBwdArgs A, int total_tiles) 
   acc_flush(acc0);
 }
 
+// ---------------------------------------------------------------------------
+// Windowed backward for the sampled filters (linear, linear-mipmap-*), C in
+// 1..4.  Per 16x16 pixel tile the texel bounding box of the footprints on
+// the two lowest levels in use is taken, and contributions are summed into
+// dense LDS windows over those boxes (direct indexing, no hashing).  The
+// windows are written out row by row, so consecutive lanes issue atomics to
+// consecutive addresses.  Big groups of lanes on one footprint (the
+// background texel) go to the per-wave accumulator; taps on other levels,
+// or boxes too large for a window, go to the LDS hash table.
+// ---------------------------------------------------------------------------
+
+constexpr int kWinTexels = 1024;
+constexpr int kWinFallback = 256;
+
+struct TapSlot {
+  int k;         // level
+  float scale;   // (1 - frac) or frac; 0 = unused
+  int ix0, ix1, iy0, iy1;
+  float w00, w10, w01, w11;
+};
+
+__device__ __forceinline__ void slot_box(const TapSlot& q, int& x0, int& x1, int& y0, int& y1) {
+  const bool c0 = q.w00 != 0.0f || q.w01 != 0.0f, c1 = q.w10 != 0.0f || q.w11 != 0.0f;
+  const bool r0 = q.w00 != 0.0f || q.w10 != 0.0f, r1 = q.w01 != 0.0f || q.w11 != 0.0f;
+  x0 = 0x7fffffff; x1 = -1; y0 = 0x7fffffff; y1 = -1;
+  if (c0) { x0 = min(x0, q.ix0); x1 = max(x1, q.ix0); }
+  if (c1) { x0 = min(x0, q.ix1); x1 = max(x1, q.ix1); }
+  if (r0) { y0 = min(y0, q.iy0); y1 = max(y1, q.iy0); }
+  if (r1) { y0 = min(y0, q.iy1); y1 = max(y1, q.iy1); }
+}
+
+
+template <int FILTER, int CT>
+__global__ void __launch_bounds__(256) k_tex_bwd_win(TexBwdArgs A, int total_tiles) {
+  __shared__ float win[2][kWinTexels * CT];
+  __shared__ int box[2][4];
+  __shared__ int s_ka;
+  __shared__ LdsTable<CT, kWinFallback> tab;
+  FootAcc<CT> acc;
+  acc_init(acc);
+  const int tid = threadIdx.x;
+  for (int i = tid; i < 2 * kWinTexels * CT; i += 256) (&win[0][0])[i] = 0.0f;
+  lds_table_clear(tab);
+  if (tid == 0) {
+    s_ka = 0x7fffffff;
+    for (int w = 0; w < 2; ++w) {
+      box[w][0] = 0x7fffffff; box[w][1] = -1; box[w][2] = 0x7fffffff; box[w][3] = -1;
+    }
+  }
+  __syncthreads();
+
+  const MipDesc& md = A.md;
+  const bool mip = FILTER == DR_FILTER_LINEAR_MIPMAP_LINEAR || FILTER == DR_FILTER_LINEAR_MIPMAP_NEAREST;
+  const bool shared_tex = A.tex_stride == 0;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int tiles = A.ntx * A.nty;
+
+  for (int bt = (int)blockIdx.x; bt < total_tiles; bt += (int)gridDim.x) {
+    const int n = bt / tiles;
+    const int tile = bt - n * tiles;
+    const int ty = tile / A.ntx, tx = tile - ty * A.ntx;
+    const int pw = tx * 16 + (wave & 1) * 8 + (lane & 7);
+    const int ph = ty * 16 + (wave >> 1) * 8 + (lane >> 3);
+    const bool valid = pw < A.Wi && ph < A.Hi;
+    const int64_t pix = ((int64_t)n * A.Hi + min(ph, A.Hi - 1)) * A.Wi + min(pw, A.Wi - 1);
+    auto level_ptr = [&](int k) -> const float* {
+      return k == 0 ? A.tex + n * A.tex_stride
+                    : A.pyr + md.off[k] + (shared_tex ? 0 : (int64_t)n * md.h[k] * md.w[k] * CT);
+    };
+    auto dlevel_ptr = [&](int k) -> float* {
+      return k == 0 ? A.d_tex + n * A.tex_stride
+                    : A.d_pyr + md.off[k] + (shared_tex ? 0 : (int64_t)n * md.h[k] * md.w[k] * CT);
+    };
+
+    // -- per pixel: footprints, gradients of uv / uvDA ------------------------
+    float g[CT];
+#pragma unroll
+    for (int c = 0; c < CT; ++c) g[c] = valid ? A.d_out[pix * CT + c] : 0.0f;
+    const float2 uvp = *reinterpret_cast<const float2*>(A.uv + pix * 2);
+    TapSlot q[2];
+    float4 da_in = make_float4(0.f, 0.f, 0.f, 0.f), da = da_in;
+    float s = 1.0f;
+    bool scaled = false;
+    if (mip) {
+      da_in = *reinterpret_cast<const float4*>(A.uv_da + pix * 4);
+      s = bias_scale(A.bias_map, pix, A.scale_bias, A.has_bias != 0);
+      scaled = A.bias_map || A.has_bias;
+      da = scaled ? make_float4(da_in.x * s, da_in.y * s, da_in.z * s, da_in.w * s) : da_in;
+      const Lod ld = mip_lod(da, A.Ht, A.Wt, md.L, FILTER == DR_FILTER_LINEAR_MIPMAP_LINEAR);
+      q[0].k = ld.k0;
+      q[0].scale = 1.0f - ld.frac;
+      q[1].k = ld.k1;
+      q[1].scale = ld.frac;
+    } else {
+      q[0].k = 0;
+      q[0].scale = 1.0f;
+      q[1].k = 0;
+      q[1].scale = 0.0f;
+    }
+    float dfx_total = 0.0f, dfy_total = 0.0f, samp[2] = {0.0f, 0.0f};
+#pragma unroll
+    for (int li = 0; li < 2; ++li) {
+      const int k = q[li].k, Hk = md.h[k], Wk = md.w[k];
+      const Bilin b = bilin(uvp.x, uvp.y, Wk, Hk, A.boundary);
+      float w00 = b.w00, w10 = b.w10, w01 = b.w01, w11 = b.w11;
+      if (b.ix1 == b.ix0) { w00 += w10; w01 += w11; w10 = 0.0f; w11 = 0.0f; }
+      if (b.iy1 == b.iy0) { w00 += w01; w10 += w11; w01 = 0.0f; w11 = 0.0f; }
+      q[li].ix0 = b.ix0; q[li].ix1 = b.ix1; q[li].iy0 = b.iy0; q[li].iy1 = b.iy1;
+      const bool on = valid && q[li].scale != 0.0f;
+      q[li].w00 = on ? w00 : 0.0f; q[li].w10 = on ? w10 : 0.0f;
+      q[li].w01 = on ? w01 : 0.0f; q[li].w11 = on ? w11 : 0.0f;
+      if (valid && (mip || li == 0)) {
+        float dfx, dfy;
+        duv_level(level_ptr(k), Wk, CT, b, g, mip ? q[li].scale : 1.0f, dfx, dfy, samp[li]);
+        dfx_total += dfx * (float)Wk;
+        dfy_total += dfy * (float)Hk;
+      }
+    }
+    if (valid && A.d_uv)
+      *reinterpret_cast<float2*>(A.d_uv + pix * 2) = make_float2(dfx_total, dfy_total);
+    if (mip && valid && (A.d_uv_da || A.d_bias)) {  // Texture.swift:1011-1102
+      const float sx = da.x * (float)A.Wt, sy = da.y * (float)A.Wt;
+      const float tx_ = da.z * (float)A.Ht, ty_ = da.w * (float)A.Ht;
+      const float Asq = sx * sx + tx_ * tx_;
+      const float Bsq = sy * sy + ty_ * ty_;
+      const float rho_sq = fmaxf(Asq, Bsq);
+      const float lod_raw = 0.5f * log2f(fmaxf(rho_sq, 1e-20f));
+      float4 d_eff = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (!(lod_raw <= 0.0f || lod_raw >= (float)(md.L - 1))) {
+        float d_lod;
+        if (FILTER == DR_FILTER_LINEAR_MIPMAP_LINEAR) {
+          d_lod = -samp[0] + samp[1];
+        } else {
+          const int k0 = f2i(floorf(lod_raw));
+          const int k1 = min(k0 + 1, md.L - 1);
+          float s0 = 0.0f, s1 = 0.0f, u0, u1;
+          const Bilin b0 = bilin(uvp.x, uvp.y, md.w[k0], md.h[k0], A.boundary);
+          duv_level(level_ptr(k0), md.w[k0], CT, b0, g, 0.0f, u0, u1, s0);
+          const Bilin b1 = bilin(uvp.x, uvp.y, md.w[k1], md.h[k1], A.boundary);
+          duv_level(level_ptr(k1), md.w[k1], CT, b1, g, 0.0f, u0, u1, s1);
+          d_lod = -s0 + s1;
+        }
+        const float ln2 = 0.6931471805599453f;
+        // A gradient: the hardware reciprocal (1 ulp) is well inside tolerance.
+        const float dlod_drho_sq = __builtin_amdgcn_rcpf(2.0f * rho_sq * ln2);
+        const float A_is_max = (Asq >= Bsq) ? 1.0f : 0.0f;
+        const float B_is_max = 1.0f - A_is_max;
+        d_eff = make_float4(d_lod * dlod_drho_sq * A_is_max * 2.0f * sx * (float)A.Wt,
+                            d_lod * dlod_drho_sq * B_is_max * 2.0f * sy * (float)A.Wt,
+                            d_lod * dlod_drho_sq * A_is_max * 2.0f * tx_ * (float)A.Ht,
+                            d_lod * dlod_drho_sq * B_is_max * 2.0f * ty_ * (float)A.Ht);
+      }
+      if (A.d_uv_da) {
+        const float4 o = scaled ? make_float4(d_eff.x * s, d_eff.y * s, d_eff.z * s, d_eff.w * s) : d_eff;
+        *reinterpret_cast<float4*>(A.d_uv_da + pix * 4) = o;
+      }
+      if (A.d_bias && A.bias_map) {
+        const float gm = d_eff.x * da_in.x + d_eff.y * da_in.y + d_eff.z * da_in.z + d_eff.w * da_in.w;
+        A.d_bias[pix] = gm * s * 0.6931471805599453f;
+      }
+    }
+
+    // -- hot footprint of slot 0: big wave groups go to the accumulator ------
+    bool hot = false;
+    {
+      const bool on0 = q[0].w00 != 0.0f || q[0].w10 != 0.0f || q[0].w01 != 0.0f || q[0].w11 != 0.0f;
+      const int Wk = md.w[q[0].k];
+      const uint64_t key = ((uint64_t)q[0].k << 48) | (uint64_t)((int64_t)q[0].iy0 * Wk + q[0].ix0);
+      const uint32_t key2 = ((uint32_t)(q[0].ix1 - q[0].ix0) << 16) ^ (uint32_t)(q[0].iy1 - q[0].iy0);
+      uint64_t pending = __ballot(on0);
+#pragma unroll 1
+      for (int probe = 0; probe < 2 && pending; ++probe) {
+        const int leader = probe_leader(pending, probe);
+        const uint64_t lkey = __shfl(key, leader, kWave);
+        const uint32_t lkey2 = __shfl(key2, leader, kWave);
+        const bool same = on0 && !hot && key == lkey && key2 == lkey2;
+        const uint64_t members = __ballot(same);
+        pending &= ~members;
+        if (__popcll(members) < kGroupMin) continue;
+        const int lk = __shfl(q[0].k, leader, kWave);  // wave-uniform from here on
+        float* base = dlevel_ptr(lk);
+        const int lW = md.w[lk];
+        float* lp[4];
+        const int lix0 = __shfl(q[0].ix0, leader, kWave), lix1 = __shfl(q[0].ix1, leader, kWave);
+        const int liy0 = __shfl(q[0].iy0, leader, kWave), liy1 = __shfl(q[0].iy1, leader, kWave);
+        lp[0] = base + ((int64_t)liy0 * lW + lix0) * CT;
+        lp[1] = base + ((int64_t)liy0 * lW + lix1) * CT;
+        lp[2] = base + ((int64_t)liy1 * lW + lix0) * CT;
+        lp[3] = base + ((int64_t)liy1 * lW + lix1) * CT;
+        const bool hit = acc.on && acc.p[0] == lp[0] && acc.p[1] == lp[1] && acc.p[2] == lp[2] &&
+                         acc.p[3] == lp[3];
+        if (!hit) {
+          acc_flush(acc);
+#pragma unroll
+          for (int t = 0; t < 4; ++t) acc.p[t] = (float*)uni((uint64_t)lp[t]);
+#pragma unroll
+          for (int i = 0; i < 4 * CT; ++i) acc.v[i] = 0.0f;
+          acc.on = true;
+        }
+        const float wt[4] = {q[0].w00, q[0].w10, q[0].w01, q[0].w11};
+#pragma unroll
+        for (int c = 0; c < CT; ++c) {
+          const float gc = g[c] * q[0].scale;
+#pragma unroll
+          for (int t = 0; t < 4; ++t)
+            acc.v[4 * c + t] = uni(acc.v[4 * c + t] + wave_sum(same ? wt[t] * gc : 0.0f));
+        }
+        if (same) hot = true;
+      }
+    }
+
+    // -- lowest level in use, then the boxes of the two windows ---------------
+    const bool use0 = !hot && (q[0].w00 != 0.0f || q[0].w10 != 0.0f || q[0].w01 != 0.0f || q[0].w11 != 0.0f);
+    const bool use1 = q[1].w00 != 0.0f || q[1].w10 != 0.0f || q[1].w01 != 0.0f || q[1].w11 != 0.0f;
+    {
+      int kmin = 0x7fffffff;
+      if (use0) kmin = q[0].k;
+      if (use1) kmin = min(kmin, q[1].k);
+      kmin = wave_min(kmin);
+      if (lane == 0 && kmin != 0x7fffffff) atomicMin(&s_ka, kmin);
+    }
+    __syncthreads();
+    const int ka = s_ka;
+    int wsel[2];
+#pragma unroll
+    for (int li = 0; li < 2; ++li) {
+      const bool u = li == 0 ? use0 : use1;
+      wsel[li] = !u ? -2 : (q[li].k == ka ? 0 : (q[li].k == ka + 1 ? 1 : -1));
+    }
+#pragma unroll
+    for (int w = 0; w < 2; ++w) {
+      int x0 = 0x7fffffff, x1 = -1, y0 = 0x7fffffff, y1 = -1;
+#pragma unroll
+      for (int li = 0; li < 2; ++li) {
+        if (wsel[li] != w) continue;
+        int a0, a1, b0, b1;
+        slot_box(q[li], a0, a1, b0, b1);
+        x0 = min(x0, a0); x1 = max(x1, a1); y0 = min(y0, b0); y1 = max(y1, b1);
+      }
+      x0 = wave_min(x0); x1 = wave_max(x1); y0 = wave_min(y0); y1 = wave_max(y1);
+      if (lane == 0 && x1 >= 0) {
+        atomicMin(&box[w][0], x0); atomicMax(&box[w][1], x1);
+        atomicMin(&box[w][2], y0); atomicMax(&box[w][3], y1);
+      }
+    }
+    __syncthreads();
+    int bx0[2], bw[2], by0[2];
+    bool usable[2];
+#pragma unroll
+    for (int w = 0; w < 2; ++w) {
+      bx0[w] = box[w][0];
+      by0[w] = box[w][2];
+      bw[w] = box[w][1] - box[w][0] + 1;
+      const int bh = box[w][3] - box[w][2] + 1;
+      usable[w] = box[w][1] >= 0 && (int64_t)bw[w] * bh <= kWinTexels;
+    }
+
+    // -- accumulate ------------------------------------------------------------
+#pragma unroll
+    for (int li = 0; li < 2; ++li) {
+      const int w = wsel[li];
+      if (w == -2) continue;
+      const float wt[4] = {q[li].w00, q[li].w10, q[li].w01, q[li].w11};
+      const int tx_[4] = {q[li].ix0, q[li].ix1, q[li].ix0, q[li].ix1};
+      const int ty_[4] = {q[li].iy0, q[li].iy0, q[li].iy1, q[li].iy1};
+      const float sc = mip ? q[li].scale : 1.0f;
+      if (w >= 0 && usable[w]) {
+        float* wb = &win[w][0];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          if (wt[t] == 0.0f) continue;
+          const int o = ((ty_[t] - by0[w]) * bw[w] + (tx_[t] - bx0[w])) * CT;  // < kWinTexels*CT
+#pragma unroll
+          for (int c = 0; c < CT; ++c) {
+            const float v = wt[t] * (g[c] * sc);
+            if (v != 0.0f) atomicAdd(wb + o + c, v);
+          }
+        }
+      } else {
+        float* base = dlevel_ptr(q[li].k);
+        const int Wk = md.w[q[li].k];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          if (wt[t] == 0.0f) continue;
+          float v[CT];
+#pragma unroll
+          for (int c = 0; c < CT; ++c) v[c] = wt[t] * (g[c] * sc);
+          lds_table_add(tab, base + (ty_[t] * Wk + tx_[t]) * CT, v);
+        }
+      }
+    }
+    __syncthreads();
+
+    // -- write the windows out, row by row -----------------------------------
+#pragma unroll
+    for (int w = 0; w < 2; ++w) {
+      if (!usable[w]) continue;
+      const int k = ka + w;
+      if (k >= md.L) continue;
+      float* base = dlevel_ptr(k);
+      const int Wk = md.w[k];
+      const int row = bw[w] * CT;
+      const int bh = box[w][3] - box[w][2] + 1;
+      const int total = row * bh;
+      for (int i = tid; i < total; i += 256) {
+        const float v = win[w][i];
+        if (v != 0.0f) {
+          const int r = i / row, cpos = i - r * row;
+          unsafeAtomicAdd(base + ((by0[w] + r) * Wk + bx0[w]) * CT + cpos, v);
+          win[w][i] = 0.0f;
+        }
+      }
+    }
+    lds_table_flush(tab);  // contains a barrier
+    if (tid == 0) {
+      s_ka = 0x7fffffff;
+      for (int w = 0; w < 2; ++w) {
+        box[w][0] = 0x7fffffff; box[w][1] = -1; box[w][2] = 0x7fffffff; box[w][3] = -1;
+      }
+    }
+    __syncthreads();
+  }
+  acc_flush(acc);
+}
+
 // Texture.swift:156: level k = 2x2 mean of level k-1.
 __global__ void __launch_bounds__(256) k_mip_down(const float* __restrict__ src,
                                                   float* __restrict__ dst, int Nt, int h, int w,
@@ -685,6 +1011,24 @@ __global__ void __launch_bounds__(256) k_mip_collapse(const float* __restrict__ 
   float acc = at(kL);
   for (int k = kL - 1; k >= 1; --k) acc = at(k) + acc * 0.25f;
   d_tex[i] = d_tex[i] + acc * 0.25f;
+}
+
+template <int FILTER, int CT>
+hipError_t launch_tex_bwd_win(const TexBwdArgs& args, int total_tiles, hipStream_t stream) {
+  static int per_cu = 0;
+  if (per_cu == 0) {
+    int b = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, k_tex_bwd_win<FILTER, CT>, 256, 0) !=
+            hipSuccess ||
+        b <= 0)
+      b = 2;
+    per_cu = b;
+  }
+  const int64_t resident = (int64_t)device_cu_count() * per_cu;
+  const unsigned grid = (unsigned)(total_tiles < resident ? total_tiles : resident);
+  hipLaunchKernelGGL((k_tex_bwd_win<FILTER, CT>), dim3(grid), dim3(256), 0, stream, args,
+                     total_tiles);
+  return hipGetLastError();
 }
 
 // Launches the persistent backward with as many workgroups as fit on the
@@ -911,11 +1255,23 @@ extern "C" int dr_texture_bwd(const float* tex, const float* pyramid, int Nt, in
     case 4: DR_TB(F, CUBEV, 4); break;     \
     default: DR_TB(F, CUBEV, 0); break;    \
   }
-    if (cube) DR_TB_C(DR_FILTER_LINEAR, true)
+#define DR_TW(F)                                                   \
+  switch (C) {                                                     \
+    case 1: e = launch_tex_bwd_win<F, 1>(args, (int)total_tiles, stream); break; \
+    case 2: e = launch_tex_bwd_win<F, 2>(args, (int)total_tiles, stream); break; \
+    case 3: e = launch_tex_bwd_win<F, 3>(args, (int)total_tiles, stream); break; \
+    default: e = launch_tex_bwd_win<F, 4>(args, (int)total_tiles, stream); break; \
+  }
+    const bool windowed = !cube && filter != DR_FILTER_NEAREST && C >= 1 && C <= 4;
+    if (windowed && filter == DR_FILTER_LINEAR) DR_TW(DR_FILTER_LINEAR)
+    else if (windowed && filter == DR_FILTER_LINEAR_MIPMAP_NEAREST) DR_TW(DR_FILTER_LINEAR_MIPMAP_NEAREST)
+    else if (windowed) DR_TW(DR_FILTER_LINEAR_MIPMAP_LINEAR)
+    else if (cube) DR_TB_C(DR_FILTER_LINEAR, true)
     else if (filter == DR_FILTER_NEAREST) DR_TB_C(DR_FILTER_NEAREST, false)
     else if (filter == DR_FILTER_LINEAR) DR_TB_C(DR_FILTER_LINEAR, false)
     else if (filter == DR_FILTER_LINEAR_MIPMAP_NEAREST) DR_TB_C(DR_FILTER_LINEAR_MIPMAP_NEAREST, false)
     else DR_TB_C(DR_FILTER_LINEAR_MIPMAP_LINEAR, false)
+#undef DR_TW
 #undef DR_TB_C
 #undef DR_TB
     DR_CHECK_HIP(e);
