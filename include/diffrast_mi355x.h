@@ -81,6 +81,8 @@ int dr_release_scratch(void);
  * dr_profile_report writes "name launches total_ms" lines into buf and
  * returns the full report length (it waits for the recorded events). */
 int dr_profile_enable(int on);
+/* Restricts timing to kernels of this name (NULL: every kernel). */
+int dr_profile_select(const char* kernel);
 int dr_profile_reset(void);
 int dr_profile_report(char* buf, int len);
 

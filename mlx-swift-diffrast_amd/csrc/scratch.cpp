@@ -84,6 +84,7 @@ int device_cu_count() {
 // ---- kernel timing -------------------------------------------------------
 
 bool g_prof_enabled = false;
+static std::string g_prof_only;  // empty: time every kernel
 
 struct ProfRec {
   const char* name;
@@ -107,6 +108,7 @@ static hipEvent_t prof_event() {
 
 ProfScope::ProfScope(const char* n, hipStream_t s) : name(n), stream(s) {
   if (!g_prof_enabled) return;
+  if (!g_prof_only.empty() && g_prof_only != n) return;
   std::lock_guard<std::mutex> lk(g_prof_mu);
   start = prof_event();
   if (start) (void)hipEventRecord(start, stream);
@@ -127,6 +129,12 @@ extern "C" {
 
 int dr_profile_enable(int on) {
   dr::g_prof_enabled = on != 0;
+  return DR_OK;
+}
+
+int dr_profile_select(const char* kernel) {
+  std::lock_guard<std::mutex> lk(dr::g_prof_mu);
+  dr::g_prof_only = kernel ? kernel : "";
   return DR_OK;
 }
 

@@ -988,6 +988,56 @@ __global__ void __launch_bounds__(256) k_mip_down(const float* __restrict__ src,
   dst[i] = (((a + b) + d) + e) * 0.25f;
 }
 
+// Builds up to five levels at once: each workgroup reduces a 2^m x 2^m
+// block of level s through levels s+1..s+m in LDS (m <= 5; the sizes of
+// levels s..s+m-1 are even, so the blocks tile level s exactly).  Same 2x2
+// sums as k_mip_down, in the same order.
+constexpr int kMipMaxC = 4;
+
+__global__ void __launch_bounds__(256) k_mip_block(const float* __restrict__ src,
+                                                   float* __restrict__ pyr, MipDesc md, int s,
+                                                   int m, int Nt, int C) {
+  __shared__ float buf[2][256 * kMipMaxC];
+  const int bs = 1 << m;  // source block edge
+  const int Ws = md.w[s];
+  const int nbx = Ws / bs;
+  const int bx = (int)blockIdx.x % nbx, by = (int)blockIdx.x / nbx;
+  const int n = (int)blockIdx.y;
+  const float* lvl = src + (int64_t)n * md.h[s] * Ws * C;
+  int cur = 0;
+  for (int j = 1; j <= m; ++j) {
+    const int e = bs >> j;  // output edge at this step
+    const int k = s + j;
+    const int Wk = md.w[k];
+    float* dst = pyr + md.off[k] + (int64_t)n * md.h[k] * Wk * C;
+    for (int t = threadIdx.x; t < e * e * C; t += blockDim.x) {
+      const int c = t % C, q = t / C;
+      const int x = q % e, y = q / e;
+      float a, b, d, f;
+      if (j == 1) {
+        const int sx = bx * bs + 2 * x, sy = by * bs + 2 * y;
+        a = lvl[((int64_t)sy * Ws + sx) * C + c];
+        b = lvl[((int64_t)sy * Ws + sx + 1) * C + c];
+        d = lvl[((int64_t)(sy + 1) * Ws + sx) * C + c];
+        f = lvl[((int64_t)(sy + 1) * Ws + sx + 1) * C + c];
+      } else {
+        const int pe = 2 * e;
+        const float* pb = buf[cur ^ 1];
+        a = pb[((2 * y) * pe + 2 * x) * C + c];
+        b = pb[((2 * y) * pe + 2 * x + 1) * C + c];
+        d = pb[((2 * y + 1) * pe + 2 * x) * C + c];
+        f = pb[((2 * y + 1) * pe + 2 * x + 1) * C + c];
+      }
+      const float v = (((a + b) + d) + f) * 0.25f;
+      buf[cur][(y * e + x) * C + c] = v;
+      const int ox = bx * e + x, oy = by * e + y;
+      dst[((int64_t)oy * Wk + ox) * C + c] = v;
+    }
+    __syncthreads();
+    cur ^= 1;
+  }
+}
+
 // Backward of the pyramid (MLX autodiff of concatenate + mean): level k's
 // total cotangent is its own gradient plus 1/4 of level k+1's total,
 // accumulated from the coarsest level down; level 0's total is added to
@@ -1115,6 +1165,21 @@ extern "C" int dr_texture_build_mip(const float* tex, int Nt, int H, int W, int 
   int st = build_desc(H, W, C, Nt, L, md);
   if (st) return st;
   if (L > 1) DR_CHECK_ARG(pyramid != nullptr, "texture_build_mip: null pyramid");
+  if (C <= kMipMaxC) {
+    for (int sl = 0; sl < L - 1;) {
+      const int m = (L - 1 - sl) < 5 ? (L - 1 - sl) : 5;
+      const float* src = sl == 0 ? tex : pyramid + md.off[sl];
+      const int bs = 1 << m;
+      const dim3 grid((unsigned)((md.h[sl] / bs) * (md.w[sl] / bs)), (unsigned)Nt);
+      {
+        DR_TIMED("k_mip_block", stream);
+        hipLaunchKernelGGL(k_mip_block, grid, dim3(256), 0, stream, src, pyramid, md, sl, m, Nt, C);
+      }
+      DR_CHECK_LAUNCH();
+      sl += m;
+    }
+    return DR_OK;
+  }
   for (int k = 1; k < L; ++k) {
     const float* src = k == 1 ? tex : pyramid + md.off[k - 1];
     const int64_t n = (int64_t)Nt * md.h[k] * md.w[k] * C;

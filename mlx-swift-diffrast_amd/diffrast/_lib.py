@@ -23,6 +23,7 @@ SIGNATURES = {
     "dr_get_last_error": ([], ctypes.c_char_p),
     "dr_release_scratch": ([], _i),
     "dr_profile_enable": ([_i], _i),
+    "dr_profile_select": ([ctypes.c_char_p], _i),
     "dr_profile_reset": ([], _i),
     "dr_profile_report": ([ctypes.c_char_p, _i], _i),
     "dr_rasterize_fwd": ([_p, _i64, _p, _p, _p, _i, _i, _i, _i, _i, _p, _p, _p], _i),
