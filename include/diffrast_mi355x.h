@@ -27,10 +27,12 @@
  *   - A "batch stride" argument is the element distance between consecutive
  *     batch entries of a tensor; 0 means one tensor shared by every batch
  *     entry (the reference's N-broadcast, without materialising it).
- *   - The caller allocates every input and output.  Gradient outputs that
- *     are accumulated by scatter-add are zero-filled by the library first,
- *     unless DR_ACCUMULATE is set in `flags`, in which case the library adds
- *     into what the buffer holds.
+ *   - The caller allocates every input and output.  The gradients the
+ *     reference accumulates by scatter-add (d_pos of rasterize and
+ *     antialias, d_attr, d_tex, d_color of antialias) are zero-filled by the
+ *     library first, unless DR_ACCUMULATE is set in `flags`, in which case
+ *     the library adds into what the buffer holds.  Every other output
+ *     (d_rast, d_rast_db, d_uv, d_uv_da, d_bias_map) is overwritten.
  *   - Work is enqueued asynchronously on `stream` (a hipStream_t; NULL is the
  *     default stream) of the current HIP device.  Internal scratch is kept
  *     per (device, stream); calls on different streams may overlap.

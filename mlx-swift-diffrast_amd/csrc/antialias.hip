@@ -78,84 +78,83 @@ __global__ void __launch_bounds__(256) k_topo_resolve(const int32_t* __restrict_
 }
 
 // ---------------------------------------------------------------------------
-// silhouette (Antialias.swift:168-326), one direction at a time
+// silhouette (Antialias.swift:168-326)
 // ---------------------------------------------------------------------------
 
+// Per (image, triangle) record gathered once per call, so a pixel next to a
+// triangle edge needs one 48-byte load instead of the chain topology ->
+// vertex ids -> vertex positions:
+//   s01 = (x0, y0, x1, y1), s2 = (x2, y2, topo[0] bits, topo[1] bits),
+//   tv = (topo[2], v0, v1, v2)
+// with pixel-space vertices from the expressions of Antialias.swift:247-250:
+// x = (x/w + 1) * W/2, y = (1 - y/w) * H/2.
+struct alignas(16) AARec {
+  float4 s01, s2;
+  int4 tv;
+};
+
+__global__ void __launch_bounds__(256) k_aa_rec(const float* __restrict__ pos,
+                                                const int32_t* __restrict__ tri,
+                                                const int32_t* __restrict__ topo, int64_t NT,
+                                                int T, int V, int H, int W,
+                                                AARec* __restrict__ rec) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= NT) return;
+  const int64_t n = i / T;
+  const int t = (int)(i - n * T);
+  const float* p = pos + n * V * 4;
+  const int v0 = tri[(int64_t)t * 3 + 0], v1 = tri[(int64_t)t * 3 + 1],
+            v2 = tri[(int64_t)t * 3 + 2];
+  const float4 P0 = *reinterpret_cast<const float4*>(p + (int64_t)v0 * 4);
+  const float4 P1 = *reinterpret_cast<const float4*>(p + (int64_t)v1 * 4);
+  const float4 P2 = *reinterpret_cast<const float4*>(p + (int64_t)v2 * 4);
+  const float hw = (float)W, hh = (float)H;
+  AARec r;
+  r.s01 = make_float4((P0.x / P0.w + 1.0f) * hw * 0.5f, (1.0f - P0.y / P0.w) * hh * 0.5f,
+                      (P1.x / P1.w + 1.0f) * hw * 0.5f, (1.0f - P1.y / P1.w) * hh * 0.5f);
+  r.s2 = make_float4((P2.x / P2.w + 1.0f) * hw * 0.5f, (1.0f - P2.y / P2.w) * hh * 0.5f,
+                     __int_as_float(topo[(int64_t)t * 3 + 0]),
+                     __int_as_float(topo[(int64_t)t * 3 + 1]));
+  r.tv = make_int4(topo[(int64_t)t * 3 + 2], v0, v1, v2);
+  rec[i] = r;
+}
+
 struct SilDir {
-  bool active;
-  float alpha;  // beta > 0 when active
+  float alpha;  // > 0 when active
   int ie0, ie1;
   float e0x, e0y, e1x, e1y, t, denom, dbeta;
 };
 
-struct AAIn {
-  const float* rast;
-  const float* pos;
-  const int32_t* tri;
-  const int32_t* topo;
-  const float2* scr;  // [N, V] pixel-space vertex positions
-  int H, W, V;
-};
-
-// Pixel-space position of every vertex, with the expressions of
-// Antialias.swift:247-250: x = (x/w + 1) * W/2, y = (1 - y/w) * H/2.
-__global__ void __launch_bounds__(256) k_aa_screen(const float* __restrict__ pos, int64_t NV,
-                                                   int H, int W, float2* __restrict__ scr) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= NV) return;
-  const float4 P = *reinterpret_cast<const float4*>(pos + i * 4);
-  scr[i] = make_float2((P.x / P.w + 1.0f) * (float)W * 0.5f,
-                       (1.0f - P.y / P.w) * (float)H * 0.5f);
-}
-
-__device__ __forceinline__ int tri_at(const AAIn& a, int n, int h, int w) {
-  return f2i(a.rast[((((int64_t)n * a.H + h) * a.W + w) << 2) + 3]) - 1;
-}
-
-// Direction dir of pixel (n, ph, pw) whose own triangle is tri_p;
-// s.active is false when the pair contributes nothing.
-__device__ __forceinline__ bool sil_dir_impl(const AAIn& a, int n, int ph, int pw, int tri_p,
-                                             int dir, SilDir& s) {
+// Pair (pixel (ph, pw), its neighbour in direction dir): the edge of the
+// foreground triangle R whose adjacency entry is `target` and whose line
+// separates the two pixel centres (:227-262), then the blend weight of the
+// pixel (:264-310). Returns false when the pair contributes nothing.
+__device__ __forceinline__ bool sil_geom(const AARec& R, int target, int ph, int pw, int dir,
+                                         SilDir& s) {
   const int dw = dir == 0 ? 1 : (dir == 2 ? -1 : 0);
   const int dh = dir == 1 ? 1 : (dir == 3 ? -1 : 0);
-  const int nh = ph + dh, nw = pw + dw;
-  if (nh < 0 || nh >= a.H || nw < 0 || nw >= a.W) return false;
-  const int tri_n = tri_at(a, n, nh, nw);
-  if (tri_p == tri_n) return false;
-  if (tri_p < 0 && tri_n < 0) return false;
-  int fg, target;
-  if (tri_p >= 0 && tri_n >= 0) {
-    const int32_t* tp = a.topo + (int64_t)tri_p * 3;
-    if (!(tp[0] == tri_n || tp[1] == tri_n || tp[2] == tri_n)) return false;
-    fg = tri_p;
-    target = tri_n;
-  } else if (tri_p >= 0) {
-    fg = tri_p;
-    target = -1;
-  } else {
-    fg = tri_n;
-    target = -1;
-  }
-  const float2* sp = a.scr + (int64_t)n * a.V;
   const float pcx = (float)pw + 0.5f, pcy = (float)ph + 0.5f;
-  const float ncx = (float)nw + 0.5f, ncy = (float)nh + 0.5f;
-  int ie0 = -1, ie1 = -1;
-  float e0x = 0.f, e0y = 0.f, e1x = 0.f, e1y = 0.f;
+  const float ncx = (float)(pw + dw) + 0.5f, ncy = (float)(ph + dh) + 0.5f;
+  const int tk[3] = {__float_as_int(R.s2.z), __float_as_int(R.s2.w), R.tv.x};
+  const float X[3] = {R.s01.x, R.s01.z, R.s2.x};
+  const float Y[3] = {R.s01.y, R.s01.w, R.s2.y};
+  const int VI[3] = {R.tv.y, R.tv.z, R.tv.w};
   bool found = false;
-  for (int kk = 0; kk < 3; ++kk) {  // :240-262
-    if (a.topo[(int64_t)fg * 3 + kk] != target) continue;
-    const int c0 = a.tri[(int64_t)fg * 3 + ((kk + 1) % 3)];
-    const int c1 = a.tri[(int64_t)fg * 3 + ((kk + 2) % 3)];
-    const float2 Q0 = sp[c0], Q1 = sp[c1];
-    const float E0x = Q0.x, E0y = Q0.y, E1x = Q1.x, E1y = Q1.y;
-    const float ex = E1x - E0x, ey = E1y - E0y;
-    const float side_p = ex * (pcy - E0y) - ey * (pcx - E0x);
-    const float side_n = ex * (ncy - E0y) - ey * (ncx - E0x);
-    if (side_p * side_n < 0.0f) {
-      ie0 = c0; ie1 = c1;
-      e0x = E0x; e0y = E0y; e1x = E1x; e1y = E1y;
-      found = true;
-      break;
+  float e0x = 0.f, e0y = 0.f, e1x = 0.f, e1y = 0.f;
+  int ie0 = -1, ie1 = -1;
+#pragma unroll
+  for (int kk = 0; kk < 3; ++kk) {
+    const int k1 = (kk + 1) % 3, k2 = (kk + 2) % 3;
+    if (!found && tk[kk] == target) {
+      const float E0x = X[k1], E0y = Y[k1], E1x = X[k2], E1y = Y[k2];
+      const float ex = E1x - E0x, ey = E1y - E0y;
+      const float side_p = ex * (pcy - E0y) - ey * (pcx - E0x);
+      const float side_n = ex * (ncy - E0y) - ey * (ncx - E0x);
+      if (side_p * side_n < 0.0f) {
+        found = true;
+        ie0 = VI[k1]; ie1 = VI[k2];
+        e0x = E0x; e0y = E0y; e1x = E1x; e1y = E1y;
+      }
     }
   }
   if (!found) return false;
@@ -202,156 +201,318 @@ __device__ __forceinline__ bool sil_dir_impl(const AAIn& a, int n, int ph, int p
   return true;
 }
 
-__device__ __forceinline__ SilDir sil_dir(const AAIn& a, int n, int ph, int pw, int tri_p,
-                                          int dir) {
-  SilDir s;
-  s.alpha = 0.0f;
-  s.ie0 = s.ie1 = 0;
-  s.e0x = s.e0y = s.e1x = s.e1y = s.t = s.denom = s.dbeta = 0.0f;
-  s.active = sil_dir_impl(a, n, ph, pw, tri_p, dir, s);
-  return s;
+// Triangle ids of a 16x16 tile and its 1-pixel border (corners unused).
+// kOut marks a neighbour outside the image; ids outside [0, T) read as empty.
+constexpr int kOut = -2;
+
+struct AATile {
+  int n, x0, y0, lx, ly, pw, ph;
+  bool inside;
+};
+
+__device__ __forceinline__ int aa_tri_id(const float* __restrict__ rast, int n, int h, int w,
+                                         int H, int W, int T) {
+  const int id = f2i(rast[((((int64_t)n * H + h) * W + w) << 2) + 3]) - 1;
+  return (unsigned)id < (unsigned)T ? id : -1;
 }
 
-// Antialias.swift:333-358.
-__global__ void __launch_bounds__(256) k_aa_fwd(AAIn a, const float* __restrict__ color, int N,
-                                                int C, float* __restrict__ out) {
-  const int64_t pix = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t P = (int64_t)N * a.H * a.W;
-  if (pix >= P) return;
-  const int pw = (int)(pix % a.W);
-  const int ph = (int)((pix / a.W) % a.H);
-  const int n = (int)(pix / ((int64_t)a.H * a.W));
-  const int tri_p = tri_at(a, n, ph, pw);
-  float alpha[4];
-  int64_t nb[4];
-  int any = 0;
+__device__ __forceinline__ AATile aa_load_tile(const float* __restrict__ rast, int H, int W, int T,
+                                               int ntx, int nty, int (*s_tri)[18]) {
+  AATile g;
+  const int tiles = ntx * nty;
+  const int b = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+  g.n = b / tiles;
+  const int tile = b - g.n * tiles;
+  const int ty = tile / ntx, tx = tile - ty * ntx;
+  g.x0 = tx * 16;
+  g.y0 = ty * 16;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  g.lx = (wave & 1) * 8 + (lane & 7);
+  g.ly = (wave >> 1) * 8 + (lane >> 3);
+  g.pw = g.x0 + g.lx;
+  g.ph = g.y0 + g.ly;
+  g.inside = g.pw < W && g.ph < H;
+  s_tri[g.ly + 1][g.lx + 1] = g.inside ? aa_tri_id(rast, g.n, g.ph, g.pw, H, W, T) : kOut;
+  if (threadIdx.x < 64) {
+    const int side = threadIdx.x >> 4, i = threadIdx.x & 15;
+    int qh, qw, r, c;
+    if (side == 0) { qw = g.x0 - 1;  qh = g.y0 + i;  r = i + 1; c = 0; }
+    else if (side == 1) { qw = g.x0 + 16; qh = g.y0 + i;  r = i + 1; c = 17; }
+    else if (side == 2) { qw = g.x0 + i;  qh = g.y0 - 1;  r = 0;     c = i + 1; }
+    else { qw = g.x0 + i;  qh = g.y0 + 16; r = 17;    c = i + 1; }
+    const bool in = qh >= 0 && qh < H && qw >= 0 && qw < W;
+    s_tri[r][c] = in ? aa_tri_id(rast, g.n, qh, qw, H, W, T) : kOut;
+  }
+  return g;
+}
+
+// Neighbour of tile cell (r, c) (1-based, border included) in direction d:
+// 0 = +w, 1 = +h, 2 = -w, 3 = -h.
+__device__ __forceinline__ int aa_nb(int (*s_tri)[18], int r, int c, int d) {
+  return d == 0 ? s_tri[r][c + 1] : d == 1 ? s_tri[r + 1][c] : d == 2 ? s_tri[r][c - 1]
+                                                                      : s_tri[r - 1][c];
+}
+
+// Whether the pair (own triangle tp, neighbour tn) is a silhouette
+// candidate (:203-204): inside the image, different, not both empty.
+__device__ __forceinline__ bool aa_cand(int tp, int tn) {
+  return tn != kOut && tn != tp && (tp >= 0 || tn >= 0);
+}
+
+// Full per-direction state of one candidate pair: the foreground is the
+// pixel's own triangle when it has one (record rp), else the neighbour's
+// (:206-222).
+__device__ __forceinline__ bool aa_pair(const AARec* __restrict__ recn, const AARec& rp, int tp,
+                                        int tn, int ph, int pw, int d, SilDir& s) {
+  if (tp >= 0) return sil_geom(rp, tn, ph, pw, d, s);
+  const AARec rn = recn[tn];
+  return sil_geom(rn, -1, ph, pw, d, s);
+}
+
+template <int CT>
+__device__ __forceinline__ void ld_px(const float* __restrict__ p, int C, float* v) {
+  if constexpr (CT == 4) {
+    const float4 q = *reinterpret_cast<const float4*>(p);
+    v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+  } else {
+#pragma unroll
+    for (int c = 0; c < (CT > 0 ? CT : 1); ++c) v[c] = p[c];
+  }
+}
+
+template <int CT>
+__device__ __forceinline__ void st_px(float* __restrict__ p, const float* v) {
+  if constexpr (CT == 4) {
+    *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+  } else {
+#pragma unroll
+    for (int c = 0; c < CT; ++c) p[c] = v[c];
+  }
+}
+
+// Antialias.swift:333-358 on 16x16 tiles: triangle ids of the tile and its
+// border are staged in LDS once; only pixels next to a different triangle
+// load a record. CT = channel count when 1..4 (registers), 0 = any C.
+template <int CT>
+__global__ void __launch_bounds__(256) k_aa_fwd(const float* __restrict__ rast,
+                                                const AARec* __restrict__ rec,
+                                                const float* __restrict__ color, int H, int W,
+                                                int T, int C, int ntx, int nty,
+                                                float* __restrict__ out) {
+  __shared__ int s_tri[18][18];
+  const AATile g = aa_load_tile(rast, H, W, T, ntx, nty, s_tri);
+  __syncthreads();
+  if (!g.inside) return;
+  const int r = g.ly + 1, c = g.lx + 1;
+  const int tp = s_tri[r][c];
+  int tn[4];
+  bool any = false;
 #pragma unroll
   for (int d = 0; d < 4; ++d) {
-    const SilDir s = sil_dir(a, n, ph, pw, tri_p, d);
-    alpha[d] = s.active ? s.alpha : 0.0f;
-    const int nh = ph + (d == 1 ? 1 : (d == 3 ? -1 : 0));
-    const int nw = pw + (d == 0 ? 1 : (d == 2 ? -1 : 0));
-    nb[d] = (((int64_t)n * a.H + nh) * a.W + nw) * C;
-    any |= s.active;
+    tn[d] = aa_nb(s_tri, r, c, d);
+    any = any || aa_cand(tp, tn[d]);
   }
-  const float* cp = color + pix * C;
-  float* o = out + pix * C;
-  if (!any) {
-    for (int c = 0; c < C; ++c) o[c] = cp[c];
-    return;
-  }
-  for (int c = 0; c < C; ++c) {
-    const float cpc = cp[c];
-    float acc = cpc;
+  float alpha[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  bool blend = false;
+  if (any) {
+    const AARec* recn = rec + (int64_t)g.n * T;
+    AARec rp;
+    if (tp >= 0) rp = recn[tp];
 #pragma unroll
-    for (int d = 0; d < 4; ++d)
-      if (alpha[d] > 0.0f) acc += alpha[d] * (color[nb[d] + c] - cpc);
-    o[c] = acc;
+    for (int d = 0; d < 4; ++d) {
+      if (!aa_cand(tp, tn[d])) continue;
+      SilDir s;
+      if (aa_pair(recn, rp, tp, tn[d], g.ph, g.pw, d, s)) {
+        alpha[d] = s.alpha;
+        blend = true;
+      }
+    }
+  }
+  const int64_t pix = ((int64_t)g.n * H + g.ph) * W + g.pw;
+  if constexpr (CT > 0) {
+    float cp[CT];
+    ld_px<CT>(color + pix * CT, CT, cp);
+    if (blend) {
+      float acc[CT];
+#pragma unroll
+      for (int k = 0; k < CT; ++k) acc[k] = cp[k];
+      const int64_t nb[4] = {pix + 1, pix + W, pix - 1, pix - W};
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        if (alpha[d] > 0.0f) {
+          float cn[CT];
+          ld_px<CT>(color + nb[d] * CT, CT, cn);
+#pragma unroll
+          for (int k = 0; k < CT; ++k) acc[k] += alpha[d] * (cn[k] - cp[k]);
+        }
+      }
+      st_px<CT>(out + pix * CT, acc);
+    } else {
+      st_px<CT>(out + pix * CT, cp);
+    }
+  } else {
+    const float* cp = color + pix * C;
+    float* o = out + pix * C;
+    const int64_t nb[4] = {pix + 1, pix + W, pix - 1, pix - W};
+    for (int k = 0; k < C; ++k) {
+      const float cpc = cp[k];
+      float acc = cpc;
+#pragma unroll
+      for (int d = 0; d < 4; ++d)
+        if (alpha[d] > 0.0f) acc += alpha[d] * (color[nb[d] * C + k] - cpc);
+      o[k] = acc;
+    }
   }
 }
 
-// Fused backward on 16x16 tiles (one 8x8 quadrant per wave).
-__global__ void __launch_bounds__(256) k_aa_bwd(AAIn a, const float* __restrict__ color,
-                                                const float* __restrict__ d_out, int N, int C,
-                                                int ntx, int nty, float* __restrict__ d_color,
+// Fused backward on 16x16 tiles (one 8x8 quadrant per wave): d_color
+// (Antialias.swift:498-524) gathered through an LDS exchange of the blend
+// weights, d_pos (:388-496) summed per vertex in LDS.
+template <int CT>
+__global__ void __launch_bounds__(256) k_aa_bwd(const float* __restrict__ rast,
+                                                const AARec* __restrict__ rec,
+                                                const float* __restrict__ pos,
+                                                const float* __restrict__ color,
+                                                const float* __restrict__ d_out, int H, int W,
+                                                int V, int T, int C, int ntx, int nty,
+                                                float* __restrict__ d_color,
                                                 float* __restrict__ d_pos, int accumulate) {
+  __shared__ int s_tri[18][18];
   __shared__ float s_alpha[4][16][17];
   __shared__ float s_halo[4][16];
   __shared__ LdsTable<4, 128> tab;  // d_pos rows touched by this tile
   lds_table_clear(tab);
-  const int tiles = ntx * nty;
-  const int b = (int)blockIdx.x;
-  const int n = b / tiles;
-  const int tile = b - n * tiles;
-  const int ty = tile / ntx, tx = tile - ty * ntx;
-  const int x0 = tx * 16, y0 = ty * 16;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int lx = (wave & 1) * 8 + (lane & 7), ly = (wave >> 1) * 8 + (lane >> 3);
-  const int pw = x0 + lx, ph = y0 + ly;
-  const bool inside = pw < a.W && ph < a.H;
-  const int tri_p = inside ? tri_at(a, n, ph, pw) : -1;
+  const AATile g = aa_load_tile(rast, H, W, T, ntx, nty, s_tri);
+  __syncthreads();
+  const AARec* recn = rec + (int64_t)g.n * T;
+  const int r = g.ly + 1, c = g.lx + 1;
+  const int tp = s_tri[r][c];
 
-  // 1) own blend weights.
-  SilDir sd[4];
+  // 1) own blend weights (the edge state is recomputed in 4) for the few
+  //    pixels that need it rather than held across the barrier).
+  float alpha[4];
   float asum = 0.0f;
+  {
+    int tn[4];
+    bool any = false;
 #pragma unroll
-  for (int d = 0; d < 4; ++d) {
-    sd[d] = sil_dir(a, n, ph, pw, tri_p, d);
-    sd[d].active = sd[d].active && inside;
-    const float al = sd[d].active ? sd[d].alpha : 0.0f;
-    s_alpha[d][ly][lx] = al;
-    asum += al;
+    for (int d = 0; d < 4; ++d) {
+      tn[d] = aa_nb(s_tri, r, c, d);
+      any = any || (g.inside && aa_cand(tp, tn[d]));
+    }
+    AARec rp;
+    if (any && tp >= 0) rp = recn[tp];
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      SilDir s;
+      const bool on = any && aa_cand(tp, tn[d]) && aa_pair(recn, rp, tp, tn[d], g.ph, g.pw, d, s);
+      alpha[d] = on ? s.alpha : 0.0f;
+      s_alpha[d][g.ly][g.lx] = alpha[d];
+      asum += alpha[d];
+    }
   }
-  // 2) halo: the one direction of each outside neighbour that points into
+  // 2) border: the one direction of each outside neighbour that points into
   //    the tile.
   if (threadIdx.x < 64) {
     const int side = threadIdx.x >> 4, i = threadIdx.x & 15;
-    int qh, qw, qd;
-    if (side == 0) { qw = x0 - 1;  qh = y0 + i; qd = 0; }       // left column, looks +w
-    else if (side == 1) { qw = x0 + 16; qh = y0 + i; qd = 2; }  // right column, looks -w
-    else if (side == 2) { qw = x0 + i; qh = y0 - 1;  qd = 1; }  // top row, looks +h
-    else { qw = x0 + i; qh = y0 + 16; qd = 3; }                 // bottom row, looks -h
+    int qh, qw, rr, cc, qd;
+    if (side == 0) { qw = g.x0 - 1;  qh = g.y0 + i;  rr = i + 1; cc = 0;     qd = 0; }
+    else if (side == 1) { qw = g.x0 + 16; qh = g.y0 + i;  rr = i + 1; cc = 17;    qd = 2; }
+    else if (side == 2) { qw = g.x0 + i;  qh = g.y0 - 1;  rr = 0;     cc = i + 1; qd = 1; }
+    else { qw = g.x0 + i;  qh = g.y0 + 16; rr = 17;    cc = i + 1; qd = 3; }
     float al = 0.0f;
-    if (qh >= 0 && qh < a.H && qw >= 0 && qw < a.W) {
-      const SilDir s = sil_dir(a, n, qh, qw, tri_at(a, n, qh, qw), qd);
-      if (s.active) al = s.alpha;
+    const int tq = s_tri[rr][cc];
+    if (tq != kOut) {
+      const int tn = aa_nb(s_tri, rr, cc, qd);
+      if (aa_cand(tq, tn)) {
+        AARec rq;
+        if (tq >= 0) rq = recn[tq];
+        SilDir s;
+        if (aa_pair(recn, rq, tq, tn, qh, qw, qd, s)) al = s.alpha;
+      }
     }
     s_halo[side][i] = al;
   }
   __syncthreads();
 
-  const int64_t pix = ((int64_t)n * a.H + min(ph, a.H - 1)) * a.W + min(pw, a.W - 1);
-  const float* g = d_out + pix * C;
+  const int64_t pix = ((int64_t)g.n * H + min(g.ph, H - 1)) * W + min(g.pw, W - 1);
+  const int lx = g.lx, ly = g.ly;
+  const int Cn = CT > 0 ? CT : C;
   // 3) d_color: own term + what each neighbour's blend sends here.
-  if (d_color && inside) {
+  if (d_color && g.inside) {
     float wn[4];
-    int64_t qn[4];
     wn[0] = lx < 15 ? s_alpha[2][ly][lx + 1] : s_halo[1][ly];  // right neighbour, its dir 2
     wn[1] = ly < 15 ? s_alpha[3][ly + 1][lx] : s_halo[3][lx];  // lower neighbour, its dir 3
     wn[2] = lx > 0 ? s_alpha[0][ly][lx - 1] : s_halo[0][ly];   // left neighbour, its dir 0
     wn[3] = ly > 0 ? s_alpha[1][ly - 1][lx] : s_halo[2][lx];   // upper neighbour, its dir 1
-    qn[0] = pix + 1;
-    qn[1] = pix + a.W;
-    qn[2] = pix - 1;
-    qn[3] = pix - a.W;
-    float* dc = d_color + pix * C;
-    for (int c = 0; c < C; ++c) {
-      float acc = g[c] * (1.0f - asum);
+    const int64_t qn[4] = {pix + 1, pix + W, pix - 1, pix - W};
+    if constexpr (CT > 0) {
+      float gv[CT], acc[CT];
+      ld_px<CT>(d_out + pix * CT, CT, gv);
 #pragma unroll
-      for (int d = 0; d < 4; ++d)
-        if (wn[d] > 0.0f) acc += d_out[qn[d] * C + c] * wn[d];
-      dc[c] = accumulate ? dc[c] + acc : acc;
+      for (int k = 0; k < CT; ++k) acc[k] = gv[k] * (1.0f - asum);
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        if (wn[d] > 0.0f) {
+          float gq[CT];
+          ld_px<CT>(d_out + qn[d] * CT, CT, gq);
+#pragma unroll
+          for (int k = 0; k < CT; ++k) acc[k] += gq[k] * wn[d];
+        }
+      }
+      if (accumulate) {
+        float old[CT];
+        ld_px<CT>(d_color + pix * CT, CT, old);
+#pragma unroll
+        for (int k = 0; k < CT; ++k) acc[k] = old[k] + acc[k];
+      }
+      st_px<CT>(d_color + pix * CT, acc);
+    } else {
+      const float* gp = d_out + pix * C;
+      float* dc = d_color + pix * C;
+      for (int k = 0; k < C; ++k) {
+        float acc = gp[k] * (1.0f - asum);
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+          if (wn[d] > 0.0f) acc += d_out[qn[d] * C + k] * wn[d];
+        dc[k] = accumulate ? dc[k] + acc : acc;
+      }
     }
   }
   // 4) d_pos (Antialias.swift:405-495), summed per vertex in LDS.
   if (!d_pos) return;  // uniform: no barrier follows
-  const float halfW = (float)a.W * 0.5f, halfH = (float)a.H * 0.5f;
-  const float* p = a.pos + (int64_t)n * a.V * 4;
-  float* dp = d_pos + (int64_t)n * a.V * 4;
-  const float* cpp = color + pix * C;
+  const float halfW = (float)W * 0.5f, halfH = (float)H * 0.5f;
+  const float* p = pos + (int64_t)g.n * V * 4;
+  float* dp = d_pos + (int64_t)g.n * V * 4;
+  const float* gp = d_out + pix * Cn;
+  const float* cpp = color + pix * Cn;
 #pragma unroll
   for (int d = 0; d < 4; ++d) {
-    bool on = sd[d].active && sd[d].alpha > 0.0f && sd[d].alpha < 1.0f;
+    bool on = alpha[d] > 0.0f && alpha[d] < 1.0f;
     if (on) {
-      const int nh = ph + (d == 1 ? 1 : (d == 3 ? -1 : 0));
-      const int nw = pw + (d == 0 ? 1 : (d == 2 ? -1 : 0));
-      const float* cnp = color + (((int64_t)n * a.H + nh) * a.W + nw) * C;
+      const int64_t q = d == 0 ? pix + 1 : d == 1 ? pix + W : d == 2 ? pix - 1 : pix - W;
+      const float* cnp = color + q * Cn;
       float d_alpha = 0.0f;
-      for (int c = 0; c < C; ++c) d_alpha += g[c] * (cnp[c] - cpp[c]);
+      for (int k = 0; k < Cn; ++k) d_alpha += gp[k] * (cnp[k] - cpp[k]);
       on = d_alpha != 0.0f;
+      SilDir s;
       if (on) {
-        const SilDir& s = sd[d];
+        AARec rp;
+        if (tp >= 0) rp = recn[tp];
+        on = aa_pair(recn, rp, tp, aa_nb(s_tri, r, c, d), g.ph, g.pw, d, s);
+      }
+      if (on) {
         float dade0x, dade0y, dade1x, dade1y;
         const float inv_denom_sq = 1.0f / (s.denom * s.denom);
         if (d == 0 || d == 2) {
-          const float row_y = (float)ph + 0.5f;
+          const float row_y = (float)g.ph + 0.5f;
           const float ex_diff = s.e1x - s.e0x;
           dade0x = s.dbeta * (1.0f - s.t);
           dade1x = s.dbeta * s.t;
           dade0y = s.dbeta * ex_diff * (row_y - s.e1y) * inv_denom_sq;
           dade1y = s.dbeta * (-ex_diff) * (row_y - s.e0y) * inv_denom_sq;
         } else {
-          const float col_x = (float)pw + 0.5f;
+          const float col_x = (float)g.pw + 0.5f;
           const float ey_diff = s.e1y - s.e0y;
           dade0y = s.dbeta * (1.0f - s.t);
           dade1y = s.dbeta * s.t;
@@ -412,20 +573,21 @@ extern "C" int dr_antialias_topology(const int32_t* tri, int T, int32_t* topo,
   return DR_OK;
 }
 
-static int aa_screen(const float* pos, int N, int V, int H, int W, hipStream_t stream,
-                     float2** out) {
+static int aa_records(const float* pos, const int32_t* tri, const int32_t* topo, int N, int V,
+                      int T, int H, int W, hipStream_t stream, AARec** out) {
   Scratch* sc = scratch_for(stream);
   if (!sc) return DR_ERR_HIP;
-  const int64_t nv = (int64_t)N * V;
-  float2* scr = (float2*)scratch_get(sc, stream, SLOT_AA_SCREEN, (size_t)(nv > 0 ? nv : 1) * 8);
-  if (!scr) return DR_ERR_MEMORY;
-  if (nv > 0) {
-    DR_TIMED("k_aa_screen", stream);
-    hipLaunchKernelGGL(k_aa_screen, dim3(grid_for(nv, 256)), dim3(256), 0, stream, pos, nv, H, W,
-                       scr);
+  const int64_t nt = (int64_t)N * T;
+  AARec* rec = (AARec*)scratch_get(sc, stream, SLOT_AA_REC,
+                                   (size_t)(nt > 0 ? nt : 1) * sizeof(AARec));
+  if (!rec) return DR_ERR_MEMORY;
+  if (nt > 0) {
+    DR_TIMED("k_aa_rec", stream);
+    hipLaunchKernelGGL(k_aa_rec, dim3(grid_for(nt, 256)), dim3(256), 0, stream, pos, tri, topo,
+                       nt, T, V, H, W, rec);
   }
   DR_CHECK_LAUNCH();
-  *out = scr;
+  *out = rec;
   return DR_OK;
 }
 
@@ -436,6 +598,23 @@ static int check_aa(const float* color, const float* rast, const float* pos, con
   return DR_OK;
 }
 
+// Channel count as a template argument when it fits in registers (float4
+// accesses need 16-byte aligned rows).
+static int aa_ct(int C, const void* a, const void* b, const void* c) {
+  const bool al = (((uintptr_t)a | (uintptr_t)b | (uintptr_t)c) & 15) == 0;
+  if (C == 4) return al ? 4 : 0;
+  return C <= 3 ? C : 0;
+}
+
+#define DR_AA_DISPATCH(KER, CT, ...)                                               \
+  switch (CT) {                                                                   \
+    case 1: hipLaunchKernelGGL((KER<1>), __VA_ARGS__); break;                     \
+    case 2: hipLaunchKernelGGL((KER<2>), __VA_ARGS__); break;                     \
+    case 3: hipLaunchKernelGGL((KER<3>), __VA_ARGS__); break;                     \
+    case 4: hipLaunchKernelGGL((KER<4>), __VA_ARGS__); break;                     \
+    default: hipLaunchKernelGGL((KER<0>), __VA_ARGS__); break;                    \
+  }
+
 extern "C" int dr_antialias_fwd(const float* color, const float* rast, const float* pos,
                                 const int32_t* tri, const int32_t* topo, int N, int H, int W,
                                 int C, int V, int T, float* out, dr_stream_t stream_) {
@@ -444,13 +623,15 @@ extern "C" int dr_antialias_fwd(const float* color, const float* rast, const flo
   int st = check_aa(color, rast, pos, tri, topo, N, H, W, C, V, T);
   if (st) return st;
   DR_CHECK_ARG(out != nullptr, "antialias: null output");
-  float2* scr = nullptr;
-  int st2 = aa_screen(pos, N, V, H, W, stream, &scr);
+  AARec* rec = nullptr;
+  int st2 = aa_records(pos, tri, topo, N, V, T, H, W, stream, &rec);
   if (st2) return st2;
-  AAIn a{rast, pos, tri, topo, scr, H, W, V};
-  const int64_t P = (int64_t)N * H * W;
+  const int ntx = (W + 15) / 16, nty = (H + 15) / 16;
+  const dim3 grid((unsigned)((int64_t)N * ntx * nty)), block(256);
+  const int ct = aa_ct(C, color, out, color);
   DR_TIMED("k_aa_fwd", stream);
-  hipLaunchKernelGGL(k_aa_fwd, dim3(grid_for(P, 256)), dim3(256), 0, stream, a, color, N, C, out);
+  DR_AA_DISPATCH(k_aa_fwd, ct, grid, block, 0, stream, rast, rec, color, H, W, T, C, ntx, nty,
+                 out);
   DR_CHECK_LAUNCH();
   return DR_OK;
 }
@@ -467,14 +648,15 @@ extern "C" int dr_antialias_bwd(const float* color, const float* rast, const flo
   if (!d_color && !d_pos) return DR_OK;
   const bool acc = (flags & DR_ACCUMULATE) != 0;
   if (d_pos && !acc) DR_CHECK_HIP(fill_async(d_pos, 0.0f, (int64_t)N * V * 4, stream));
-  float2* scr = nullptr;
-  int st2 = aa_screen(pos, N, V, H, W, stream, &scr);
+  AARec* rec = nullptr;
+  int st2 = aa_records(pos, tri, topo, N, V, T, H, W, stream, &rec);
   if (st2) return st2;
-  AAIn a{rast, pos, tri, topo, scr, H, W, V};
   const int ntx = (W + 15) / 16, nty = (H + 15) / 16;
+  const dim3 grid((unsigned)((int64_t)N * ntx * nty)), block(256);
+  const int ct = aa_ct(C, color, d_out, d_color);
   DR_TIMED("k_aa_bwd", stream);
-  hipLaunchKernelGGL(k_aa_bwd, dim3((unsigned)((int64_t)N * ntx * nty)), dim3(256), 0, stream, a,
-                     color, d_out, N, C, ntx, nty, d_color, d_pos, acc ? 1 : 0);
+  DR_AA_DISPATCH(k_aa_bwd, ct, grid, block, 0, stream, rast, rec, pos, color, d_out, H, W, V, T,
+                 C, ntx, nty, d_color, d_pos, acc ? 1 : 0);
   DR_CHECK_LAUNCH();
   return DR_OK;
 }

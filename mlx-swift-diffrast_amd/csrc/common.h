@@ -48,7 +48,7 @@ enum Slot {
   SLOT_TOPO,          // edge hash table
   SLOT_DPYR,          // mip pyramid gradient
   SLOT_SMALL,         // small device-side counters
-  SLOT_AA_SCREEN,     // per-vertex pixel-space positions (antialias)
+  SLOT_AA_REC,        // per (image, triangle) silhouette records (antialias)
   SLOT_COUNT
 };
 
@@ -101,6 +101,13 @@ __device__ __forceinline__ int f2i(float x) {
   if (x >= 2147483648.0f) return 2147483647;
   if (x <= -2147483648.0f) return (-2147483647 - 1);
   return (int)x;
+}
+
+__device__ __forceinline__ int xcd_remap(int b, int B) {
+  // Blocks are dealt round-robin to the 8 XCDs; give each XCD a contiguous
+  // run of tiles so neighbouring tiles share that XCD's L2.
+  if ((B & 7) != 0) return b;
+  return (b & 7) * (B >> 3) + (b >> 3);
 }
 
 __device__ __forceinline__ int lane_id() { return (int)__lane_id(); }

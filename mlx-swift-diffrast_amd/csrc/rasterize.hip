@@ -28,13 +28,6 @@ struct alignas(16) TriRec {
   float4 r0, r1, r2, r3;
 };
 
-__device__ __forceinline__ int xcd_remap(int b, int B) {
-  // Blocks are dealt round-robin to the 8 XCDs; give each XCD a contiguous
-  // run of tiles so neighbouring tiles share that XCD's L2.
-  if ((B & 7) != 0) return b;
-  return (b & 7) * (B >> 3) + (b >> 3);
-}
-
 // Rasterize.swift:280-328 (+ the AABB and tile range of :191-223).
 __global__ void __launch_bounds__(256) k_setup(const float* __restrict__ pos, int64_t pos_stride,
                                                const int32_t* __restrict__ tri, int Npos, int T,

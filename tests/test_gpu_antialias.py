@@ -49,7 +49,7 @@ def aa_scene(kind):
 
 
 @pytest.mark.parametrize("kind", ["hexpie", "icosphere", "quad", "tier1"])
-@pytest.mark.parametrize("C", [1, 3, 4])
+@pytest.mark.parametrize("C", [1, 2, 3, 4, 5])
 def test_antialias(kind, C):
     torch = torch_dev()
     from diffrast import DiffRast
@@ -70,3 +70,20 @@ def test_antialias(kind, C):
     assert_grad_close(host(c.grad), d_color, "d_color")
     assert_grad_close(host(p.grad), d_pos, "d_pos")
     assert (host(p.grad)[..., 2] == 0).all()
+
+
+def test_antialias_unaligned_rows():
+    """Color rows that are not 16-byte aligned take the any-C kernel."""
+    torch = torch_dev()
+    from diffrast import DiffRast
+    rng = np.random.default_rng(11)
+    pos, tri, H, W = aa_scene("tier1")
+    rast, _ = O.rasterize(pos, tri, (H, W), gradDB=False, max_per_tile=0)
+    N = pos.shape[0]
+    color = rng.random((N, H, W, 4)).astype(np.float32)
+    buf = torch.empty(color.size + 1, device="cuda")
+    c = buf[1:].view(color.shape)
+    c.copy_(dev(color))
+    assert c.data_ptr() % 16 != 0
+    out = DiffRast.antialias(c, dev(rast), dev(pos), dev(tri))
+    assert_fwd_close(host(out), O.antialias(color, rast, pos, tri))
