@@ -299,7 +299,7 @@ __device__ __forceinline__ void acc_flush(FootAcc<CT>& a) {
 // Scatter of one bilinear footprint's gradient (w * g * scale) into one
 // level.  Taps that land on the same texel (clamped borders) are merged
 // first; lanes sharing the footprint are summed across the wave.
-constexpr int kTexTable = 1024;  // LDS aggregation entries per tile (texels)
+constexpr int kTexTable = 512;  // LDS aggregation entries per tile (texels)
 
 template <int CT>
 using TexTable = LdsTable<(CT > 0 ? CT : 1), kTexTable>;
@@ -645,15 +645,15 @@ __global__ void __launch_bounds__(256) k_tex_bwd(TexBwdArgs A, int total_tiles) 
 // Windowed backward for the sampled filters (linear, linear-mipmap-*), C in
 // 1..4.  Per 16x16 pixel tile the texel bounding box of the footprints on
 // the two lowest levels in use is taken, and contributions are summed into
-// dense LDS windows over those boxes (direct indexing, no hashing).  The
-// windows are written out row by row, so consecutive lanes issue atomics to
-// consecutive addresses.  Big groups of lanes on one footprint (the
+// dense fp64 LDS windows over those boxes (direct indexing, no hashing; the
+// two windows share one pool).  The windows are written out row by row, so
+// consecutive lanes issue atomics to consecutive addresses.  Big groups of lanes on one footprint (the
 // background texel) go to the per-wave accumulator; taps on other levels,
 // or boxes too large for a window, go to the LDS hash table.
 // ---------------------------------------------------------------------------
 
-constexpr int kWinTexels = 1024;
-constexpr int kWinFallback = 256;
+constexpr int kWinTexels = 1024;  // texels of the two windows together
+constexpr int kWinFallback = 128;
 
 struct TapSlot {
   int k;         // level
@@ -675,14 +675,14 @@ __device__ __forceinline__ void slot_box(const TapSlot& q, int& x0, int& x1, int
 
 template <int FILTER, int CT>
 __global__ void __launch_bounds__(256) k_tex_bwd_win(TexBwdArgs A, int total_tiles) {
-  __shared__ float win[2][kWinTexels * CT];
+  __shared__ double win[kWinTexels * CT];
   __shared__ int box[2][4];
   __shared__ int s_ka;
   __shared__ LdsTable<CT, kWinFallback> tab;
   FootAcc<CT> acc;
   acc_init(acc);
   const int tid = threadIdx.x;
-  for (int i = tid; i < 2 * kWinTexels * CT; i += 256) (&win[0][0])[i] = 0.0f;
+  for (int i = tid; i < kWinTexels * CT; i += 256) win[i] = 0.0;
   lds_table_clear(tab);
   if (tid == 0) {
     s_ka = 0x7fffffff;
@@ -887,16 +887,21 @@ __global__ void __launch_bounds__(256) k_tex_bwd_win(TexBwdArgs A, int total_til
       }
     }
     __syncthreads();
-    int bx0[2], bw[2], by0[2];
+    int bx0[2], bw[2], by0[2], bh[2], wbase[2];
     bool usable[2];
+    int64_t area[2];
 #pragma unroll
     for (int w = 0; w < 2; ++w) {
       bx0[w] = box[w][0];
       by0[w] = box[w][2];
       bw[w] = box[w][1] - box[w][0] + 1;
-      const int bh = box[w][3] - box[w][2] + 1;
-      usable[w] = box[w][1] >= 0 && (int64_t)bw[w] * bh <= kWinTexels;
+      bh[w] = box[w][3] - box[w][2] + 1;
+      area[w] = box[w][1] >= 0 ? (int64_t)bw[w] * bh[w] : 0;
     }
+    usable[0] = box[0][1] >= 0 && area[0] <= kWinTexels;
+    wbase[0] = 0;
+    usable[1] = box[1][1] >= 0 && (usable[0] ? area[0] : 0) + area[1] <= kWinTexels;
+    wbase[1] = usable[0] ? (int)area[0] * CT : 0;
 
     // -- accumulate ------------------------------------------------------------
 #pragma unroll
@@ -908,15 +913,15 @@ __global__ void __launch_bounds__(256) k_tex_bwd_win(TexBwdArgs A, int total_til
       const int ty_[4] = {q[li].iy0, q[li].iy0, q[li].iy1, q[li].iy1};
       const float sc = mip ? q[li].scale : 1.0f;
       if (w >= 0 && usable[w]) {
-        float* wb = &win[w][0];
+        double* wb = win + wbase[w];
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
           if (wt[t] == 0.0f) continue;
-          const int o = ((ty_[t] - by0[w]) * bw[w] + (tx_[t] - bx0[w])) * CT;  // < kWinTexels*CT
+          const int o = ((ty_[t] - by0[w]) * bw[w] + (tx_[t] - bx0[w])) * CT;  // < area[w]*CT
 #pragma unroll
           for (int c = 0; c < CT; ++c) {
             const float v = wt[t] * (g[c] * sc);
-            if (v != 0.0f) atomicAdd(wb + o + c, v);
+            if (v != 0.0f) atomicAdd(wb + o + c, (double)v);
           }
         }
       } else {
@@ -943,14 +948,14 @@ __global__ void __launch_bounds__(256) k_tex_bwd_win(TexBwdArgs A, int total_til
       float* base = dlevel_ptr(k);
       const int Wk = md.w[k];
       const int row = bw[w] * CT;
-      const int bh = box[w][3] - box[w][2] + 1;
-      const int total = row * bh;
+      const int total = row * bh[w];
+      double* wb = win + wbase[w];
       for (int i = tid; i < total; i += 256) {
-        const float v = win[w][i];
-        if (v != 0.0f) {
+        const double v = wb[i];
+        if (v != 0.0) {
           const int r = i / row, cpos = i - r * row;
-          unsafeAtomicAdd(base + ((by0[w] + r) * Wk + bx0[w]) * CT + cpos, v);
-          win[w][i] = 0.0f;
+          unsafeAtomicAdd(base + ((by0[w] + r) * Wk + bx0[w]) * CT + cpos, (float)v);
+          wb[i] = 0.0;
         }
       }
     }
