@@ -141,6 +141,47 @@ __device__ __forceinline__ int wave_reduce_i(int v, Op op) {
   return op(op(r0, r1), op(r2, r3));
 }
 
+// Shift within 16-lane rows (row_shr:n = 0x110 + n, row_shl:n = 0x100 + n);
+// lanes whose source is outside the row read 0.
+template <int CTRL>
+__device__ __forceinline__ int dpp_shift(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, true);
+}
+
+template <int D, int M>
+__device__ __forceinline__ void run_scan_step(int l8, int s, float (&v)[M]) {
+#pragma unroll
+  for (int i = 0; i < M; ++i) {
+    const float o = __int_as_float(dpp_shift<0x110 + D>(__float_as_int(v[i])));
+    if (l8 - D >= s) v[i] += o;
+  }
+}
+
+// Runs of equal `key` along each 8-lane row (lanes 8r..8r+7 hold one pixel
+// row of an 8x8 quadrant): every lane's v[] becomes the sum of its run's
+// values up to itself (a segmented Hillis-Steele scan over DPP row shifts),
+// and the run's last lane, which then holds the run total, gets true.  All
+// 64 lanes must execute this; give each inactive lane a key of its own.
+template <int M>
+__device__ __forceinline__ bool row_run_sum(int key, float (&v)[M]) {
+  const int l8 = lane_id() & 7;
+  const int kp = dpp_shift<0x111>(key);  // key of lane - 1
+  const int kn = dpp_shift<0x101>(key);  // key of lane + 1
+  int s = (l8 == 0 || kp != key) ? l8 : 0;  // run start: max-scan of head positions
+  {
+    const int a = dpp_shift<0x111>(s);
+    if (l8 >= 1) s = max(s, a);
+    const int b = dpp_shift<0x112>(s);
+    if (l8 >= 2) s = max(s, b);
+    const int c = dpp_shift<0x114>(s);
+    if (l8 >= 4) s = max(s, c);
+  }
+  run_scan_step<1>(l8, s, v);
+  run_scan_step<2>(l8, s, v);
+  run_scan_step<4>(l8, s, v);
+  return l8 == 7 || kn != key;
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
   auto add = [](int a, int b) { return __float_as_int(__int_as_float(a) + __int_as_float(b)); };
   return __int_as_float(wave_reduce_i(__float_as_int(v), add));
@@ -285,13 +326,35 @@ __global__ void fill_kernel(T* __restrict__ p, T v, int64_t n) {
   for (; i < n; i += stride) p[i] = v;
 }
 
+// 16-byte stores for a 16-byte aligned run of 4-byte values; the n % 4 tail
+// is written by the first threads.
+template <typename T>
+__global__ void fill4_kernel(T* __restrict__ p, T v, int64_t n) {
+  static_assert(sizeof(T) == 4, "4-byte values");
+  const int64_t n4 = n >> 2;
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  const uint32_t b = __builtin_bit_cast(uint32_t, v);
+  uint4* q = reinterpret_cast<uint4*>(p);
+  for (int64_t j = i; j < n4; j += stride) q[j] = make_uint4(b, b, b, b);
+  if (i < (n & 3)) p[n4 * 4 + i] = v;
+}
+
 // Fill with a kernel (not hipMemsetAsync) so the call stays graph-capturable.
 template <typename T>
 inline hipError_t fill_async(T* p, T v, int64_t n, hipStream_t s) {
   if (n <= 0) return hipSuccess;
+  DR_TIMED("fill", s);
+  if constexpr (sizeof(T) == 4) {
+    if (((uintptr_t)p & 15) == 0 && n >= 1024) {
+      int64_t blocks = (n / 4 + 255) / 256;
+      if (blocks > 8192) blocks = 8192;
+      hipLaunchKernelGGL(fill4_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, s, p, v, n);
+      return hipGetLastError();
+    }
+  }
   int64_t blocks = (n + 255) / 256;
   if (blocks > 4096) blocks = 4096;
-  DR_TIMED("fill", s);
   hipLaunchKernelGGL(fill_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, s, p, v, n);
   return hipGetLastError();
 }

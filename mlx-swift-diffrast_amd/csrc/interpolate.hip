@@ -138,14 +138,16 @@ __global__ void __launch_bounds__(256) k_interp_bwd(
   // d_attr (Interpolate.swift:231-264, :269-324), summed per vertex row in
   // LDS before the global atomics.
   if (AT > 0) {
+    float rv[3 * NV];  // rows of i0, i1, i2
+#pragma unroll
+    for (int q = 0; q < 3 * NV; ++q) rv[q] = 0.0f;
     if (valid) {
-      float r0[NV], r1[NV], r2[NV];
 #pragma unroll
       for (int a = 0; a < NV; ++a) {
         const float ga = g[a];
-        r0[a] = bw * ga;
-        r1[a] = u * ga;
-        r2[a] = v * ga;
+        rv[a] = bw * ga;
+        rv[NV + a] = u * ga;
+        rv[2 * NV + a] = v * ga;
       }
       if (KT > 0) {  // identity diff_idx (DiffAttrs.all)
         const float* gd = d_out_da + pix * 2 * K;
@@ -154,14 +156,19 @@ __global__ void __launch_bounds__(256) k_interp_bwd(
           const float gx = gd[2 * k + 0], gy = gd[2 * k + 1];
           const float u_term = gx * db.x + gy * db.y;
           const float v_term = gx * db.z + gy * db.w;
-          r0[k] += -u_term - v_term;
-          r1[k] += u_term;
-          r2[k] += v_term;
+          rv[k] += -u_term - v_term;
+          rv[NV + k] += u_term;
+          rv[2 * NV + k] += v_term;
         }
       }
-      lds_table_add(tab, da + (int64_t)i0 * A, r0);
-      lds_table_add(tab, da + (int64_t)i1 * A, r1);
-      lds_table_add(tab, da + (int64_t)i2 * A, r2);
+    }
+    // Runs of same-triangle lanes along a pixel row add into the same rows:
+    // sum each run first, its last lane adds the total.
+    const bool tail = row_run_sum(valid ? t : -2 - lane, rv);
+    if (valid && tail) {
+      lds_table_add(tab, da + (int64_t)i0 * A, &rv[0]);
+      lds_table_add(tab, da + (int64_t)i1 * A, &rv[NV]);
+      lds_table_add(tab, da + (int64_t)i2 * A, &rv[2 * NV]);
     }
   } else if (valid) {
     for (int a = 0; a < A; ++a) {

@@ -208,6 +208,24 @@ __device__ __forceinline__ TriRec load_rec(const TriRec* __restrict__ rec, int64
   return R;
 }
 
+__device__ __forceinline__ float rdl(float v, int j) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j));
+}
+
+__device__ __forceinline__ float4 rdl4(float4 v, int j) {
+  return make_float4(rdl(v.x, j), rdl(v.y, j), rdl(v.z, j), rdl(v.w, j));
+}
+
+// Lane j's record, in scalar registers.
+__device__ __forceinline__ TriRec bcast_rec(const TriRec& R, int j) {
+  TriRec o;
+  o.r0 = rdl4(R.r0, j);
+  o.r1 = rdl4(R.r1, j);
+  o.r2 = rdl4(R.r2, j);
+  o.r3 = rdl4(R.r3, j);
+  return o;
+}
+
 // Rasterize.swift:371-599.  One workgroup per (image, 16x16 tile); wave w
 // owns the 8x8 quadrant (w&1, w>>1).  The tile's triangle ids and records
 // are wave-uniform, so they travel through the scalar cache; each triangle
@@ -255,12 +273,29 @@ __global__ void __launch_bounds__(256) k_raster(
   const int count = cnt[j];
   const int64_t o = off[j];
   if (o + count <= cap) {
+    // 64 candidates at a time: each lane loads one candidate's record
+    // (vector gathers, one round trip for all 64) and tests it against the
+    // quadrant's box; the survivors are then taken one by one, their
+    // records broadcast with readlane.
     const int* ids = list + o;
-    for (int i = 0; i < count; ++i) {
-      const int t = ids[i];
-      const TriRec R = load_rec(rec, rbase + t);
-      if (R.r3.y < xw0 || R.r3.x > xw1 || R.r3.w < yw0 || R.r3.z > yw1) continue;
-      if (valid) test_tri(R, t, x, y, peel_z, best);
+    for (int c0 = 0; c0 < count; c0 += kWave) {
+      const int nb = min(kWave, count - c0);
+      int myt = 0;
+      TriRec Rl;
+      bool hit = false;
+      if (lane < nb) {
+        myt = ids[c0 + lane];
+        Rl = load_rec(rec, rbase + myt);
+        hit = !(Rl.r3.y < xw0 || Rl.r3.x > xw1 || Rl.r3.w < yw0 || Rl.r3.z > yw1);
+      }
+      uint64_t m = __ballot(hit);
+      while (m) {
+        const int j = __ffsll((long long)m) - 1;
+        m &= m - 1;
+        const int t = __builtin_amdgcn_readlane(myt, j);
+        const TriRec R = bcast_rec(Rl, j);
+        if (valid) test_tri(R, t, x, y, peel_z, best);
+      }
     }
   } else {
     // The list did not fit the scratch sized from an earlier call: scan the
@@ -301,8 +336,8 @@ __global__ void __launch_bounds__(256) k_raster(
 }
 
 // Rasterize.swift:637-812.  Same tile/quadrant layout as the forward so a
-// wave's pixels share few triangles; same-triangle lanes are summed across
-// the wave before the 12 d_pos atomics.
+// wave's pixels share few triangles; runs of same-triangle lanes along a
+// pixel row are summed before the LDS table adds the 12 d_pos terms.
 __global__ void __launch_bounds__(256) k_raster_bwd(
     const float* __restrict__ pos, int64_t pos_stride, const int32_t* __restrict__ tri,
     const float* __restrict__ rast, const float* __restrict__ d_rast,
@@ -327,7 +362,12 @@ __global__ void __launch_bounds__(256) k_raster_bwd(
   const float4 r = *reinterpret_cast<const float4*>(rast + pix * 4);
   const int t = f2i(r.w) - 1;
   valid = valid && t >= 0;
-
+  float val[12];
+  int i0 = 0, i1 = 0, i2 = 0;
+#pragma unroll
+  for (int q = 0; q < 12; ++q) val[q] = 0.0f;
+  const float* p = pos + (int64_t)n * pos_stride;
+  float* dp = d_pos + (int64_t)n * pos_stride;
   if (valid) {
     const float u_val = r.x, v_val = r.y;
     const float bw_val = 1.0f - u_val - v_val;
@@ -338,9 +378,9 @@ __global__ void __launch_bounds__(256) k_raster_bwd(
     const float d_db0 = ddb.x, d_db1 = ddb.y, d_db2 = ddb.z, d_db3 = ddb.w;
     const float Px = 2.0f * ((float)pw + 0.5f) / (float)W - 1.0f;
     const float Py = 1.0f - 2.0f * ((float)ph + 0.5f) / (float)H;
-    const float* p = pos + (int64_t)n * pos_stride;
-    float* dp = d_pos + (int64_t)n * pos_stride;
-    const int i0 = tri[t * 3 + 0], i1 = tri[t * 3 + 1], i2 = tri[t * 3 + 2];
+    i0 = tri[t * 3 + 0];
+    i1 = tri[t * 3 + 1];
+    i2 = tri[t * 3 + 2];
     const float4 P0 = *reinterpret_cast<const float4*>(p + (int64_t)i0 * 4);
     const float4 P1 = *reinterpret_cast<const float4*>(p + (int64_t)i1 * 4);
     const float4 P2 = *reinterpret_cast<const float4*>(p + (int64_t)i2 * 4);
@@ -397,7 +437,6 @@ __global__ void __launch_bounds__(256) k_raster_bwd(
     dsx0 += d_db3 * (-Ky) * inv_area;
     dsx1 += d_db3 * (Ky) * inv_area;
     const float inv_w0 = 1.0f / P0.w, inv_w1 = 1.0f / P1.w, inv_w2 = 1.0f / P2.w;
-    float val[12];
     val[0] = dsx0 * inv_w0;
     val[1] = dsy0 * inv_w0;
     val[2] = dsz0_s * inv_w0;
@@ -410,6 +449,11 @@ __global__ void __launch_bounds__(256) k_raster_bwd(
     val[9] = dsy2 * inv_w2;
     val[10] = dsz2_s * inv_w2;
     val[11] = -(sx2 * dsx2 + sy2 * dsy2 + sz2 * dsz2_s) * inv_w2;
+  }
+  // Lanes of a row on the same triangle add into the same three rows: sum
+  // each run first, its last lane adds the total.
+  const bool tail = row_run_sum(valid ? t : -2 - lane, val);
+  if (valid && tail) {
     lds_table_add(tab, dp + (int64_t)i0 * 4, &val[0]);
     lds_table_add(tab, dp + (int64_t)i1 * 4, &val[4]);
     lds_table_add(tab, dp + (int64_t)i2 * 4, &val[8]);

@@ -24,7 +24,21 @@ struct MipDesc {
   int h[kMaxLevels];
   int w[kMaxLevels];
   int64_t off[kMaxLevels];  // float offset of level k (k >= 1) in the pyramid buffer
+  int64_t nc;               // Nt * C
 };
+
+// Level k's size and pyramid offset computed from level 0 (every level
+// halves both sizes exactly), so a per-lane level never indexes the
+// descriptor arrays in kernel-argument memory.  Valid for 0 <= k < L.
+__device__ __forceinline__ int mip_h(const MipDesc& m, int k) { return m.h[0] >> k; }
+__device__ __forceinline__ int mip_w(const MipDesc& m, int k) { return m.w[0] >> k; }
+__device__ __forceinline__ int64_t mip_off(const MipDesc& m, int k) {
+  // sum_{j=1}^{k-1} Nt*C*(H*W / 4^j) = Nt*C*(H*W - H_{k-1}*W_{k-1}) / 3
+  const int j = k > 0 ? k - 1 : 0;
+  const int64_t a = (int64_t)m.h[0] * m.w[0];
+  const int64_t b = (int64_t)(m.h[0] >> j) * (m.w[0] >> j);
+  return m.nc * ((a - b) / 3);
+}
 
 // Texture.swift:336-354.
 __device__ __forceinline__ int apply_boundary(int t, int size, int mode, float& oob) {
@@ -241,9 +255,9 @@ __global__ void __launch_bounds__(256) k_tex_fwd(
   const bool shared = tex_stride == 0;
   for (int li = 0; li < 2; ++li) {
     const int k = li == 0 ? ld.k0 : ld.k1;
-    const int Hk = md.h[k], Wk = md.w[k];
+    const int Hk = mip_h(md, k), Wk = mip_w(md, k);
     const float* lv = k == 0 ? tex + n * tex_stride
-                             : pyr + md.off[k] + (shared ? 0 : (int64_t)n * Hk * Wk * C);
+                             : pyr + mip_off(md, k) + (shared ? 0 : (int64_t)n * Hk * Wk * C);
     const Bilin b = bilin(uvp.x, uvp.y, Wk, Hk, boundary);
     const float wgt = li == 0 ? (1.0f - ld.frac) : ld.frac;
     for (int c = 0; c < C; ++c) {
@@ -552,17 +566,17 @@ __device__ __forceinline__ void tex_bwd_tile(const TexBwdArgs& A, int bidx,
   const bool shared = tex_stride == 0;
   auto level_ptr = [&](int k) -> const float* {
     return k == 0 ? tex + n * tex_stride
-                  : pyr + md.off[k] + (shared ? 0 : (int64_t)n * md.h[k] * md.w[k] * C);
+                  : pyr + mip_off(md, k) + (shared ? 0 : (int64_t)n * mip_h(md, k) * mip_w(md, k) * C);
   };
   auto dlevel_ptr = [&](int k) -> float* {
-    return k == 0 ? dt : d_pyr + md.off[k] + (shared ? 0 : (int64_t)n * md.h[k] * md.w[k] * C);
+    return k == 0 ? dt : d_pyr + mip_off(md, k) + (shared ? 0 : (int64_t)n * mip_h(md, k) * mip_w(md, k) * C);
   };
   float dfx_total = 0.0f, dfy_total = 0.0f;
   float samp[2] = {0.0f, 0.0f};  // sum_c g_c * sample_c per level (for d_lod)
   for (int li = 0; li < 2; ++li) {
     const int k = li == 0 ? ld.k0 : ld.k1;
     const float scale = li == 0 ? (1.0f - ld.frac) : ld.frac;
-    const int Hk = md.h[k], Wk = md.w[k];
+    const int Hk = mip_h(md, k), Wk = mip_w(md, k);
     const Bilin b = bilin(uvp.x, uvp.y, Wk, Hk, boundary);
     // A zero weight adds nothing; skip the level's atomics (but keep the
     // wave convergent for the grouping).
@@ -598,10 +612,10 @@ __device__ __forceinline__ void tex_bwd_tile(const TexBwdArgs& A, int bidx,
     } else {
       const int k1 = min(k0 + 1, md.L - 1);
       float s0 = 0.0f, s1 = 0.0f, u0, u1;
-      const Bilin b0 = bilin(uvp.x, uvp.y, md.w[k0], md.h[k0], boundary);
-      duv_level(level_ptr(k0), md.w[k0], C, b0, gsrc, 0.0f, u0, u1, s0);
-      const Bilin b1 = bilin(uvp.x, uvp.y, md.w[k1], md.h[k1], boundary);
-      duv_level(level_ptr(k1), md.w[k1], C, b1, gsrc, 0.0f, u0, u1, s1);
+      const Bilin b0 = bilin(uvp.x, uvp.y, mip_w(md, k0), mip_h(md, k0), boundary);
+      duv_level(level_ptr(k0), mip_w(md, k0), C, b0, gsrc, 0.0f, u0, u1, s0);
+      const Bilin b1 = bilin(uvp.x, uvp.y, mip_w(md, k1), mip_h(md, k1), boundary);
+      duv_level(level_ptr(k1), mip_w(md, k1), C, b1, gsrc, 0.0f, u0, u1, s1);
       d_lod = -s0 + s1;
     }
     const float ln2 = 0.6931471805599453f;
@@ -676,20 +690,16 @@ __device__ __forceinline__ void slot_box(const TapSlot& q, int& x0, int& x1, int
 template <int FILTER, int CT>
 __global__ void __launch_bounds__(256) k_tex_bwd_win(TexBwdArgs A, int total_tiles) {
   __shared__ double win[kWinTexels * CT];
-  __shared__ int box[2][4];
-  __shared__ int s_ka;
+  __shared__ int s_wk[4];          // per wave: lowest level in use
+  __shared__ int s_wbox[4][2][4];  // per wave: boxes on that level and the next
+  __shared__ int s_tab_used[2];    // per tile parity: the table took entries
   __shared__ LdsTable<CT, kWinFallback> tab;
   FootAcc<CT> acc;
   acc_init(acc);
   const int tid = threadIdx.x;
   for (int i = tid; i < kWinTexels * CT; i += 256) win[i] = 0.0;
   lds_table_clear(tab);
-  if (tid == 0) {
-    s_ka = 0x7fffffff;
-    for (int w = 0; w < 2; ++w) {
-      box[w][0] = 0x7fffffff; box[w][1] = -1; box[w][2] = 0x7fffffff; box[w][3] = -1;
-    }
-  }
+  if (tid < 2) s_tab_used[tid] = 0;
   __syncthreads();
 
   const MipDesc& md = A.md;
@@ -698,7 +708,8 @@ __global__ void __launch_bounds__(256) k_tex_bwd_win(TexBwdArgs A, int total_til
   const int wave = tid >> 6, lane = tid & 63;
   const int tiles = A.ntx * A.nty;
 
-  for (int bt = (int)blockIdx.x; bt < total_tiles; bt += (int)gridDim.x) {
+  int it = 0;
+  for (int bt = (int)blockIdx.x; bt < total_tiles; bt += (int)gridDim.x, ++it) {
     const int n = bt / tiles;
     const int tile = bt - n * tiles;
     const int ty = tile / A.ntx, tx = tile - ty * A.ntx;
@@ -708,11 +719,11 @@ __global__ void __launch_bounds__(256) k_tex_bwd_win(TexBwdArgs A, int total_til
     const int64_t pix = ((int64_t)n * A.Hi + min(ph, A.Hi - 1)) * A.Wi + min(pw, A.Wi - 1);
     auto level_ptr = [&](int k) -> const float* {
       return k == 0 ? A.tex + n * A.tex_stride
-                    : A.pyr + md.off[k] + (shared_tex ? 0 : (int64_t)n * md.h[k] * md.w[k] * CT);
+                    : A.pyr + mip_off(md, k) + (shared_tex ? 0 : (int64_t)n * mip_h(md, k) * mip_w(md, k) * CT);
     };
     auto dlevel_ptr = [&](int k) -> float* {
       return k == 0 ? A.d_tex + n * A.tex_stride
-                    : A.d_pyr + md.off[k] + (shared_tex ? 0 : (int64_t)n * md.h[k] * md.w[k] * CT);
+                    : A.d_pyr + mip_off(md, k) + (shared_tex ? 0 : (int64_t)n * mip_h(md, k) * mip_w(md, k) * CT);
     };
 
     // -- per pixel: footprints, gradients of uv / uvDA ------------------------
@@ -743,7 +754,7 @@ __global__ void __launch_bounds__(256) k_tex_bwd_win(TexBwdArgs A, int total_til
     float dfx_total = 0.0f, dfy_total = 0.0f, samp[2] = {0.0f, 0.0f};
 #pragma unroll
     for (int li = 0; li < 2; ++li) {
-      const int k = q[li].k, Hk = md.h[k], Wk = md.w[k];
+      const int k = q[li].k, Hk = mip_h(md, k), Wk = mip_w(md, k);
       const Bilin b = bilin(uvp.x, uvp.y, Wk, Hk, A.boundary);
       float w00 = b.w00, w10 = b.w10, w01 = b.w01, w11 = b.w11;
       if (b.ix1 == b.ix0) { w00 += w10; w01 += w11; w10 = 0.0f; w11 = 0.0f; }
@@ -777,10 +788,10 @@ __global__ void __launch_bounds__(256) k_tex_bwd_win(TexBwdArgs A, int total_til
           const int k0 = f2i(floorf(lod_raw));
           const int k1 = min(k0 + 1, md.L - 1);
           float s0 = 0.0f, s1 = 0.0f, u0, u1;
-          const Bilin b0 = bilin(uvp.x, uvp.y, md.w[k0], md.h[k0], A.boundary);
-          duv_level(level_ptr(k0), md.w[k0], CT, b0, g, 0.0f, u0, u1, s0);
-          const Bilin b1 = bilin(uvp.x, uvp.y, md.w[k1], md.h[k1], A.boundary);
-          duv_level(level_ptr(k1), md.w[k1], CT, b1, g, 0.0f, u0, u1, s1);
+          const Bilin b0 = bilin(uvp.x, uvp.y, mip_w(md, k0), mip_h(md, k0), A.boundary);
+          duv_level(level_ptr(k0), mip_w(md, k0), CT, b0, g, 0.0f, u0, u1, s0);
+          const Bilin b1 = bilin(uvp.x, uvp.y, mip_w(md, k1), mip_h(md, k1), A.boundary);
+          duv_level(level_ptr(k1), mip_w(md, k1), CT, b1, g, 0.0f, u0, u1, s1);
           d_lod = -s0 + s1;
         }
         const float ln2 = 0.6931471805599453f;
@@ -807,7 +818,7 @@ __global__ void __launch_bounds__(256) k_tex_bwd_win(TexBwdArgs A, int total_til
     bool hot = false;
     {
       const bool on0 = q[0].w00 != 0.0f || q[0].w10 != 0.0f || q[0].w01 != 0.0f || q[0].w11 != 0.0f;
-      const int Wk = md.w[q[0].k];
+      const int Wk = mip_w(md, q[0].k);
       const uint64_t key = ((uint64_t)q[0].k << 48) | (uint64_t)((int64_t)q[0].iy0 * Wk + q[0].ix0);
       const uint32_t key2 = ((uint32_t)(q[0].ix1 - q[0].ix0) << 16) ^ (uint32_t)(q[0].iy1 - q[0].iy0);
       uint64_t pending = __ballot(on0);
@@ -822,7 +833,7 @@ __global__ void __launch_bounds__(256) k_tex_bwd_win(TexBwdArgs A, int total_til
         if (__popcll(members) < kGroupMin) continue;
         const int lk = __shfl(q[0].k, leader, kWave);  // wave-uniform from here on
         float* base = dlevel_ptr(lk);
-        const int lW = md.w[lk];
+        const int lW = mip_w(md, lk);
         float* lp[4];
         const int lix0 = __shfl(q[0].ix0, leader, kWave), lix1 = __shfl(q[0].ix1, leader, kWave);
         const int liy0 = __shfl(q[0].iy0, leader, kWave), liy1 = __shfl(q[0].iy1, leader, kWave);
@@ -852,55 +863,68 @@ __global__ void __launch_bounds__(256) k_tex_bwd_win(TexBwdArgs A, int total_til
       }
     }
 
-    // -- lowest level in use, then the boxes of the two windows ---------------
+    // -- per wave: lowest level in use and the boxes on it and the next; the
+    //    block's windows are the two lowest levels over all waves ------------
     const bool use0 = !hot && (q[0].w00 != 0.0f || q[0].w10 != 0.0f || q[0].w01 != 0.0f || q[0].w11 != 0.0f);
     const bool use1 = q[1].w00 != 0.0f || q[1].w10 != 0.0f || q[1].w01 != 0.0f || q[1].w11 != 0.0f;
+    const int par = it & 1;
     {
       int kmin = 0x7fffffff;
       if (use0) kmin = q[0].k;
       if (use1) kmin = min(kmin, q[1].k);
-      kmin = wave_min(kmin);
-      if (lane == 0 && kmin != 0x7fffffff) atomicMin(&s_ka, kmin);
+      const int kw = wave_min(kmin);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        int x0 = 0x7fffffff, x1 = -1, y0 = 0x7fffffff, y1 = -1;
+#pragma unroll
+        for (int li = 0; li < 2; ++li) {
+          const bool u = li == 0 ? use0 : use1;
+          if (!u || q[li].k - kw != j) continue;
+          int a0, a1, b0, b1;
+          slot_box(q[li], a0, a1, b0, b1);
+          x0 = min(x0, a0); x1 = max(x1, a1); y0 = min(y0, b0); y1 = max(y1, b1);
+        }
+        x0 = wave_min(x0); x1 = wave_max(x1); y0 = wave_min(y0); y1 = wave_max(y1);
+        if (lane == 0) {
+          s_wbox[wave][j][0] = x0; s_wbox[wave][j][1] = x1;
+          s_wbox[wave][j][2] = y0; s_wbox[wave][j][3] = y1;
+        }
+      }
+      if (lane == 0) s_wk[wave] = kw;
     }
     __syncthreads();
-    const int ka = s_ka;
+    if (tid == 0) s_tab_used[par ^ 1] = 0;  // read by every thread before the last barrier
+    const int ka = min(min(s_wk[0], s_wk[1]), min(s_wk[2], s_wk[3]));
     int wsel[2];
 #pragma unroll
     for (int li = 0; li < 2; ++li) {
       const bool u = li == 0 ? use0 : use1;
-      wsel[li] = !u ? -2 : (q[li].k == ka ? 0 : (q[li].k == ka + 1 ? 1 : -1));
+      wsel[li] = !u ? -2 : (q[li].k == ka ? 0 : (q[li].k - ka == 1 ? 1 : -1));
     }
-#pragma unroll
-    for (int w = 0; w < 2; ++w) {
-      int x0 = 0x7fffffff, x1 = -1, y0 = 0x7fffffff, y1 = -1;
-#pragma unroll
-      for (int li = 0; li < 2; ++li) {
-        if (wsel[li] != w) continue;
-        int a0, a1, b0, b1;
-        slot_box(q[li], a0, a1, b0, b1);
-        x0 = min(x0, a0); x1 = max(x1, a1); y0 = min(y0, b0); y1 = max(y1, b1);
-      }
-      x0 = wave_min(x0); x1 = wave_max(x1); y0 = wave_min(y0); y1 = wave_max(y1);
-      if (lane == 0 && x1 >= 0) {
-        atomicMin(&box[w][0], x0); atomicMax(&box[w][1], x1);
-        atomicMin(&box[w][2], y0); atomicMax(&box[w][3], y1);
-      }
-    }
-    __syncthreads();
     int bx0[2], bw[2], by0[2], bh[2], wbase[2];
     bool usable[2];
     int64_t area[2];
 #pragma unroll
     for (int w = 0; w < 2; ++w) {
-      bx0[w] = box[w][0];
-      by0[w] = box[w][2];
-      bw[w] = box[w][1] - box[w][0] + 1;
-      bh[w] = box[w][3] - box[w][2] + 1;
-      area[w] = box[w][1] >= 0 ? (int64_t)bw[w] * bh[w] : 0;
+      int x0 = 0x7fffffff, x1 = -1, y0 = 0x7fffffff, y1 = -1;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int kv = s_wk[v];
+        const int j = w - (kv - ka);  // wave v's box j lies on level ka + w
+        if (kv == 0x7fffffff || j < 0 || j > 1) continue;
+        x0 = min(x0, s_wbox[v][j][0]); x1 = max(x1, s_wbox[v][j][1]);
+        y0 = min(y0, s_wbox[v][j][2]); y1 = max(y1, s_wbox[v][j][3]);
+      }
+      bx0[w] = x0;
+      by0[w] = y0;
+      bw[w] = x1 - x0 + 1;
+      bh[w] = y1 - y0 + 1;
+      area[w] = x1 >= 0 ? (int64_t)bw[w] * bh[w] : 0;
+      usable[w] = x1 >= 0;
     }
-    usable[0] = box[0][1] >= 0 && area[0] <= kWinTexels;
+    usable[0] = usable[0] && area[0] <= kWinTexels;
     wbase[0] = 0;
-    usable[1] = box[1][1] >= 0 && (usable[0] ? area[0] : 0) + area[1] <= kWinTexels;
+    usable[1] = usable[1] && (usable[0] ? area[0] : 0) + area[1] <= kWinTexels;
     wbase[1] = usable[0] ? (int)area[0] * CT : 0;
 
     // -- accumulate ------------------------------------------------------------
@@ -926,7 +950,8 @@ __global__ void __launch_bounds__(256) k_tex_bwd_win(TexBwdArgs A, int total_til
         }
       } else {
         float* base = dlevel_ptr(q[li].k);
-        const int Wk = md.w[q[li].k];
+        const int Wk = mip_w(md, q[li].k);
+        s_tab_used[par] = 1;
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
           if (wt[t] == 0.0f) continue;
@@ -946,7 +971,7 @@ __global__ void __launch_bounds__(256) k_tex_bwd_win(TexBwdArgs A, int total_til
       const int k = ka + w;
       if (k >= md.L) continue;
       float* base = dlevel_ptr(k);
-      const int Wk = md.w[k];
+      const int Wk = mip_w(md, k);
       const int row = bw[w] * CT;
       const int total = row * bh[w];
       double* wb = win + wbase[w];
@@ -959,14 +984,7 @@ __global__ void __launch_bounds__(256) k_tex_bwd_win(TexBwdArgs A, int total_til
         }
       }
     }
-    lds_table_flush(tab);  // contains a barrier
-    if (tid == 0) {
-      s_ka = 0x7fffffff;
-      for (int w = 0; w < 2; ++w) {
-        box[w][0] = 0x7fffffff; box[w][1] = -1; box[w][2] = 0x7fffffff; box[w][3] = -1;
-      }
-    }
-    __syncthreads();
+    if (s_tab_used[par]) lds_table_flush(tab);  // uniform; contains a barrier
   }
   acc_flush(acc);
 }
@@ -1048,24 +1066,23 @@ __global__ void __launch_bounds__(256) k_mip_block(const float* __restrict__ src
 // accumulated from the coarsest level down; level 0's total is added to
 // d_tex (which already holds level 0's own gradient).
 __global__ void __launch_bounds__(256) k_mip_collapse(const float* __restrict__ d_pyr, MipDesc md,
-                                                      int Nt, int C, float* __restrict__ d_tex) {
-  const int64_t total = (int64_t)Nt * md.h[0] * md.w[0] * C;
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= total || md.L < 2) return;
-  const int c = (int)(i % C);
-  int64_t r = i / C;
-  const int x = (int)(r % md.w[0]);
-  r /= md.w[0];
-  const int y = (int)(r % md.h[0]);
-  const int n = (int)(r / md.h[0]);
+                                                      int C, int bpr, float* __restrict__ d_tex) {
+  // one thread per texel of level 0: block = 256 texels of one row
+  const int64_t row = (int64_t)blockIdx.x / bpr;  // n * H + y
+  const int x = (int)((int64_t)blockIdx.x - row * bpr) * 256 + (int)threadIdx.x;
+  if (x >= md.w[0] || md.L < 2) return;
+  const int y = (int)(row % md.h[0]);
+  const int n = (int)(row / md.h[0]);
   const int kL = md.L - 1;
-  auto at = [&](int k) {
-    const int yk = y >> k, xk = x >> k;
-    return d_pyr[md.off[k] + (((int64_t)n * md.h[k] + yk) * md.w[k] + xk) * C + c];
-  };
-  float acc = at(kL);
-  for (int k = kL - 1; k >= 1; --k) acc = at(k) + acc * 0.25f;
-  d_tex[i] = d_tex[i] + acc * 0.25f;
+  float* dt = d_tex + (row * md.w[0] + x) * C;
+  for (int c = 0; c < C; ++c) {
+    auto at = [&](int k) {
+      return d_pyr[md.off[k] + (((int64_t)n * md.h[k] + (y >> k)) * md.w[k] + (x >> k)) * C + c];
+    };
+    float acc = at(kL);
+    for (int k = kL - 1; k >= 1; --k) acc = at(k) + acc * 0.25f;
+    dt[c] = dt[c] + acc * 0.25f;
+  }
 }
 
 template <int FILTER, int CT>
@@ -1113,6 +1130,7 @@ using namespace dr;
 static int build_desc(int Ht, int Wt, int C, int Nt, int L, MipDesc& md) {
   DR_CHECK_ARG(L >= 1 && L <= kMaxLevels, "texture: mip level count out of range");
   md.L = L;
+  md.nc = (int64_t)Nt * C;
   int h = Ht, w = Wt;
   int64_t off = 0;
   for (int k = 0; k < L; ++k) {
@@ -1347,10 +1365,10 @@ extern "C" int dr_texture_bwd(const float* tex, const float* pyramid, int Nt, in
     DR_CHECK_HIP(e);
   }
   if (d_pyr) {
-    const int64_t n0 = (int64_t)Nt * Ht * Wt * C;
+    const int bpr = (Wt + 255) / 256;
     DR_TIMED("k_mip_collapse", stream);
-    hipLaunchKernelGGL(k_mip_collapse, dim3(grid_for(n0, 256)), dim3(256), 0, stream, d_pyr, md,
-                       Nt, C, d_tex);
+    hipLaunchKernelGGL(k_mip_collapse, dim3((unsigned)((int64_t)Nt * Ht * bpr)), dim3(256), 0,
+                       stream, d_pyr, md, C, bpr, d_tex);
     DR_CHECK_LAUNCH();
   }
   return DR_OK;

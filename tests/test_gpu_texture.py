@@ -129,3 +129,40 @@ def test_fixture_parity(fixtures):
     out = DiffRast.texture(dev(tex), dev(fixtures["uv"]), uvDA=dev(fixtures["uv_da"]),
                            filterMode="linear-mipmap-linear", boundaryMode="clamp")
     assert np.abs(host(out) - fixtures["tex_trilinear"]).max() <= 1e-4
+
+
+@pytest.mark.parametrize("filt", ["linear-mipmap-linear", "linear-mipmap-nearest", "linear"])
+@pytest.mark.parametrize("bnd", ["clamp", "wrap"])
+def test_smooth_lod_ramp(filt, bnd):
+    """A smooth uv field whose LOD rises across the image (~1.1 to ~3.2), so
+    16x16 tiles hold one, two or three levels and waves of one tile start on
+    different levels; a background band samples one texel."""
+    torch = torch_dev()
+    from diffrast import DiffRast
+    rng = np.random.default_rng(7)
+    N, Hi, Wi, Ht, Wt, C = 2, 96, 112, 256, 256, 4
+    x = (np.arange(Wi, dtype=np.float32) + 0.5)[None, :] * np.ones((Hi, 1), np.float32)
+    y = (np.arange(Hi, dtype=np.float32) + 0.5)[:, None] * np.ones((1, Wi), np.float32)
+    u = 2.0 * (x / Wi) ** 2 + 0.01
+    v = y / Hi * 0.8 + 0.1
+    uv = np.stack([u, v], -1)[None].repeat(N, 0).astype(np.float32)
+    da = np.stack([4.0 * x / Wi ** 2, np.zeros_like(x), np.zeros_like(x),
+                   np.full_like(x, 0.8 / Hi)], -1)[None].repeat(N, 0).astype(np.float32)
+    uv[:, :, :5] = 0.0
+    da[:, :, :5] = 0.0
+    tex = rng.random((1, Ht, Wt, C)).astype(np.float32)
+    mip = "mipmap" in filt
+    t = dev(tex).requires_grad_(True)
+    uu = dev(uv).requires_grad_(True)
+    d = dev(da).requires_grad_(True) if mip else None
+    out = DiffRast.texture(t, uu, uvDA=d, filterMode=filt, boundaryMode=bnd)
+    ref = O.texture(tex, uv, uvDA=da if mip else None, filterMode=filt, boundaryMode=bnd)
+    assert_fwd_close(host(out), ref)
+    g = rng.normal(size=ref.shape).astype(np.float32)
+    (out * dev(g)).sum().backward()
+    d_tex, d_uv, d_da, _ = O.texture_vjp(tex, uv, g, uvDA=da if mip else None, filterMode=filt,
+                                         boundaryMode=bnd)
+    assert_grad_close(host(t.grad), d_tex, "d_tex")
+    assert_grad_close(host(uu.grad), d_uv, "d_uv")
+    if mip:
+        assert_grad_close(host(d.grad), d_da, "d_uvDA", rtol=1e-3)
