@@ -381,7 +381,8 @@ __global__ void __launch_bounds__(256) k_aa_bwd(const float* __restrict__ rast,
   __shared__ float s_alpha[4][16][17];
   __shared__ float s_halo[4][16];
   __shared__ LdsTable<4, 128> tab;  // d_pos rows touched by this tile
-  lds_table_clear(tab);
+  __shared__ int s_need;            // some pixel has a partial blend (d_pos terms)
+  if (threadIdx.x == 0) s_need = 0;
   const AATile g = aa_load_tile(rast, H, W, T, ntx, nty, s_tri);
   __syncthreads();
   const AARec* recn = rec + (int64_t)g.n * T;
@@ -411,10 +412,14 @@ __global__ void __launch_bounds__(256) k_aa_bwd(const float* __restrict__ rast,
       asum += alpha[d];
     }
   }
+  bool partial = false;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) partial = partial || (alpha[d] > 0.0f && alpha[d] < 1.0f);
+  if (d_pos && partial) s_need = 1;
   // 2) border: the one direction of each outside neighbour that points into
-  //    the tile.
-  if (threadIdx.x < 64) {
-    const int side = threadIdx.x >> 4, i = threadIdx.x & 15;
+  //    the tile; lanes 0..15 of each wave take one side.
+  if ((threadIdx.x & 63) < 16) {
+    const int side = threadIdx.x >> 6, i = threadIdx.x & 15;
     int qh, qw, rr, cc, qd;
     if (side == 0) { qw = g.x0 - 1;  qh = g.y0 + i;  rr = i + 1; cc = 0;     qd = 0; }
     else if (side == 1) { qw = g.x0 + 16; qh = g.y0 + i;  rr = i + 1; cc = 17;    qd = 2; }
@@ -479,8 +484,11 @@ __global__ void __launch_bounds__(256) k_aa_bwd(const float* __restrict__ rast,
       }
     }
   }
-  // 4) d_pos (Antialias.swift:405-495), summed per vertex in LDS.
-  if (!d_pos) return;  // uniform: no barrier follows
+  // 4) d_pos (Antialias.swift:405-495), summed per vertex in LDS; only
+  //    tiles with a partial blend have terms.
+  if (!d_pos || !s_need) return;  // uniform: no barrier follows
+  lds_table_clear(tab);
+  __syncthreads();
   const float halfW = (float)W * 0.5f, halfH = (float)H * 0.5f;
   const float* p = pos + (int64_t)g.n * V * 4;
   float* dp = d_pos + (int64_t)g.n * V * 4;

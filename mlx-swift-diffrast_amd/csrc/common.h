@@ -187,9 +187,54 @@ __device__ __forceinline__ float wave_sum(float v) {
   return __int_as_float(wave_reduce_i(__float_as_int(v), add));
 }
 
+template <int CTRL>
+__device__ __forceinline__ float dpp_movf(float v) {
+  return __int_as_float(dpp_mov<CTRL>(__float_as_int(v)));
+}
+
+// Sixteen wave sums at once.  A transposing butterfly (row mirror, half-row
+// mirror, then the two quad swaps; each step keeps half of the values and
+// adds the partner's half) leaves lane l with value (l & 15) summed over
+// its 16-lane row, and two exchanges across rows finish it: every lane
+// returns the total of value (lane & 15).  About 70 instructions instead of
+// 16 separate reductions.  All 64 lanes must execute this.
+__device__ __forceinline__ float wave_sum16(const float (&a)[16]) {
+  const int l = lane_id();
+  float v8[8], v4[4], v2[2];
+  const bool b3 = (l >> 3) & 1, b2 = (l >> 2) & 1, b1 = (l >> 1) & 1, b0 = l & 1;
+#pragma unroll
+  for (int i = 0; i < 8; ++i)  // row_mirror: partner 15 - (l & 15)
+    v8[i] = (b3 ? a[i + 8] : a[i]) + dpp_movf<0x140>(b3 ? a[i] : a[i + 8]);
+#pragma unroll
+  for (int i = 0; i < 4; ++i)  // row_half_mirror: partner 7 - (l & 7)
+    v4[i] = (b2 ? v8[i + 4] : v8[i]) + dpp_movf<0x141>(b2 ? v8[i] : v8[i + 4]);
+#pragma unroll
+  for (int i = 0; i < 2; ++i)  // quad_perm [2,3,0,1]
+    v2[i] = (b1 ? v4[i + 2] : v4[i]) + dpp_movf<0x4E>(b1 ? v4[i] : v4[i + 2]);
+  float v = (b0 ? v2[1] : v2[0]) + dpp_movf<0xB1>(b0 ? v2[0] : v2[1]);  // quad_perm [1,0,3,2]
+  v += __shfl_xor(v, 16, kWave);
+  v += __shfl_xor(v, 32, kWave);
+  return v;
+}
+
 __device__ __forceinline__ int wave_min(int v) {
   return wave_reduce_i(v, [](int a, int b) { return a < b ? a : b; });
 }
+
+// Per-half minimum of two signed 16-bit values packed in an int.
+__device__ __forceinline__ int wave_min_pk16(int v) {
+  typedef short short2_t __attribute__((ext_vector_type(2)));
+  return wave_reduce_i(v, [](int a, int b) {
+    return __builtin_bit_cast(int, __builtin_elementwise_min(__builtin_bit_cast(short2_t, a),
+                                                             __builtin_bit_cast(short2_t, b)));
+  });
+}
+
+__device__ __forceinline__ int pack16(int lo, int hi) {
+  return (int)(((uint32_t)(uint16_t)(int16_t)lo) | ((uint32_t)(uint16_t)(int16_t)hi << 16));
+}
+__device__ __forceinline__ int unpack16_lo(int v) { return (int)(int16_t)(v & 0xffff); }
+__device__ __forceinline__ int unpack16_hi(int v) { return (int)(int16_t)((uint32_t)v >> 16); }
 
 __device__ __forceinline__ int wave_max(int v) {
   return wave_reduce_i(v, [](int a, int b) { return a > b ? a : b; });

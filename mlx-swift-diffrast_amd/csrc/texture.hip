@@ -283,8 +283,8 @@ __global__ void __launch_bounds__(256) k_tex_fwd(
 // its place and when the wave has finished all its tiles.  Wave-uniform.
 template <int CT>
 struct FootAcc {
-  float* p[4];
-  float v[4 * CT];
+  float* p[4];  // the footprint's four texels (wave-uniform)
+  float v;      // lane j < 4*CT: running sum of value j = 4 * channel + tap
   bool on;
 };
 
@@ -293,21 +293,29 @@ __device__ __forceinline__ void acc_init(FootAcc<CT>& a) {
   a.on = false;
 #pragma unroll
   for (int i = 0; i < 4; ++i) a.p[i] = nullptr;
-#pragma unroll
-  for (int i = 0; i < 4 * CT; ++i) a.v[i] = 0.0f;
+  a.v = 0.0f;
 }
 
 template <int CT>
 __device__ __forceinline__ void acc_flush(FootAcc<CT>& a) {
   if (!a.on) return;
-  if (lane_id() == 0) {
-#pragma unroll
-    for (int c = 0; c < CT; ++c)
-#pragma unroll
-      for (int tap = 0; tap < 4; ++tap)
-        if (a.v[4 * c + tap] != 0.0f) unsafeAtomicAdd(a.p[tap] + c, a.v[4 * c + tap]);
+  const int l = lane_id();
+  if (l < 4 * CT && a.v != 0.0f) {
+    const int tap = l & 3;
+    float* q = tap == 0 ? a.p[0] : tap == 1 ? a.p[1] : tap == 2 ? a.p[2] : a.p[3];
+    unsafeAtomicAdd(q + (l >> 2), a.v);
   }
   a.on = false;
+}
+
+// Adds the wave sums of val[0..M) (M <= 16) to the accumulator.
+template <int CT, int M>
+__device__ __forceinline__ void acc_add(FootAcc<CT>& a, const float (&val)[M], bool member) {
+  static_assert(M <= 16, "at most 16 values");
+  float x[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) x[i] = (i < M && member) ? val[i < M ? i : 0] : 0.0f;
+  a.v += wave_sum16(x);
 }
 
 // Scatter of one bilinear footprint's gradient (w * g * scale) into one
@@ -379,12 +387,10 @@ __device__ __forceinline__ void scatter_footprint(bool valid, float* __restrict_
           acc_flush(acc);
 #pragma unroll
           for (int t = 0; t < 4; ++t) acc.p[t] = (float*)uni((uint64_t)lp[t]);
-#pragma unroll
-          for (int i = 0; i < M; ++i) acc.v[i] = 0.0f;
+          acc.v = 0.0f;
           acc.on = true;
         }
-#pragma unroll
-        for (int i = 0; i < M; ++i) acc.v[i] = uni(acc.v[i] + wave_sum(same ? val[i] : 0.0f));
+        acc_add(acc, val, same);
         if (same) mine = false;
       }
     }
@@ -824,19 +830,22 @@ __global__ void __launch_bounds__(256) k_tex_bwd_win(TexBwdArgs A, int total_til
       uint64_t pending = __ballot(on0);
 #pragma unroll 1
       for (int probe = 0; probe < 2 && pending; ++probe) {
-        const int leader = probe_leader(pending, probe);
-        const uint64_t lkey = __shfl(key, leader, kWave);
-        const uint32_t lkey2 = __shfl(key2, leader, kWave);
+        const int leader = probe_leader(pending, probe);  // wave-uniform: readlane
+        const uint64_t lkey = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(key >> 32), leader) << 32) |
+                              (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)key, leader);
+        const uint32_t lkey2 = (uint32_t)__builtin_amdgcn_readlane((int)key2, leader);
         const bool same = on0 && !hot && key == lkey && key2 == lkey2;
         const uint64_t members = __ballot(same);
         pending &= ~members;
         if (__popcll(members) < kGroupMin) continue;
-        const int lk = __shfl(q[0].k, leader, kWave);  // wave-uniform from here on
+        const int lk = __builtin_amdgcn_readlane(q[0].k, leader);
         float* base = dlevel_ptr(lk);
         const int lW = mip_w(md, lk);
         float* lp[4];
-        const int lix0 = __shfl(q[0].ix0, leader, kWave), lix1 = __shfl(q[0].ix1, leader, kWave);
-        const int liy0 = __shfl(q[0].iy0, leader, kWave), liy1 = __shfl(q[0].iy1, leader, kWave);
+        const int lix0 = __builtin_amdgcn_readlane(q[0].ix0, leader);
+        const int lix1 = __builtin_amdgcn_readlane(q[0].ix1, leader);
+        const int liy0 = __builtin_amdgcn_readlane(q[0].iy0, leader);
+        const int liy1 = __builtin_amdgcn_readlane(q[0].iy1, leader);
         lp[0] = base + ((int64_t)liy0 * lW + lix0) * CT;
         lp[1] = base + ((int64_t)liy0 * lW + lix1) * CT;
         lp[2] = base + ((int64_t)liy1 * lW + lix0) * CT;
@@ -847,18 +856,18 @@ __global__ void __launch_bounds__(256) k_tex_bwd_win(TexBwdArgs A, int total_til
           acc_flush(acc);
 #pragma unroll
           for (int t = 0; t < 4; ++t) acc.p[t] = (float*)uni((uint64_t)lp[t]);
-#pragma unroll
-          for (int i = 0; i < 4 * CT; ++i) acc.v[i] = 0.0f;
+          acc.v = 0.0f;
           acc.on = true;
         }
         const float wt[4] = {q[0].w00, q[0].w10, q[0].w01, q[0].w11};
+        float val[4 * CT];
 #pragma unroll
         for (int c = 0; c < CT; ++c) {
           const float gc = g[c] * q[0].scale;
 #pragma unroll
-          for (int t = 0; t < 4; ++t)
-            acc.v[4 * c + t] = uni(acc.v[4 * c + t] + wave_sum(same ? wt[t] * gc : 0.0f));
+          for (int t = 0; t < 4; ++t) val[4 * c + t] = wt[t] * gc;
         }
+        acc_add(acc, val, same);
         if (same) hot = true;
       }
     }
@@ -875,7 +884,9 @@ __global__ void __launch_bounds__(256) k_tex_bwd_win(TexBwdArgs A, int total_til
       const int kw = wave_min(kmin);
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        int x0 = 0x7fffffff, x1 = -1, y0 = 0x7fffffff, y1 = -1;
+        // texel coordinates fit in 16 bits (window path needs sizes <= 32767):
+        // (x0, -x1) and (y0, -y1) are reduced as packed 16-bit minima
+        int x0 = 32767, x1 = -32767, y0 = 32767, y1 = -32767;
 #pragma unroll
         for (int li = 0; li < 2; ++li) {
           const bool u = li == 0 ? use0 : use1;
@@ -884,10 +895,11 @@ __global__ void __launch_bounds__(256) k_tex_bwd_win(TexBwdArgs A, int total_til
           slot_box(q[li], a0, a1, b0, b1);
           x0 = min(x0, a0); x1 = max(x1, a1); y0 = min(y0, b0); y1 = max(y1, b1);
         }
-        x0 = wave_min(x0); x1 = wave_max(x1); y0 = wave_min(y0); y1 = wave_max(y1);
+        const int px = wave_min_pk16(pack16(x0, -x1)), py = wave_min_pk16(pack16(y0, -y1));
         if (lane == 0) {
-          s_wbox[wave][j][0] = x0; s_wbox[wave][j][1] = x1;
-          s_wbox[wave][j][2] = y0; s_wbox[wave][j][3] = y1;
+          const int X1 = -unpack16_hi(px), Y1 = -unpack16_hi(py);
+          s_wbox[wave][j][0] = unpack16_lo(px); s_wbox[wave][j][1] = X1 < 0 ? -1 : X1;
+          s_wbox[wave][j][2] = unpack16_lo(py); s_wbox[wave][j][3] = Y1 < 0 ? -1 : Y1;
         }
       }
       if (lane == 0) s_wk[wave] = kw;
@@ -1350,7 +1362,8 @@ extern "C" int dr_texture_bwd(const float* tex, const float* pyramid, int Nt, in
     case 3: e = launch_tex_bwd_win<F, 3>(args, (int)total_tiles, stream); break; \
     default: e = launch_tex_bwd_win<F, 4>(args, (int)total_tiles, stream); break; \
   }
-    const bool windowed = !cube && filter != DR_FILTER_NEAREST && C >= 1 && C <= 4;
+    const bool windowed = !cube && filter != DR_FILTER_NEAREST && C >= 1 && C <= 4 &&
+                          Wt <= 32767 && Ht <= 32767;  // window boxes use 16-bit texel coordinates
     if (windowed && filter == DR_FILTER_LINEAR) DR_TW(DR_FILTER_LINEAR)
     else if (windowed && filter == DR_FILTER_LINEAR_MIPMAP_NEAREST) DR_TW(DR_FILTER_LINEAR_MIPMAP_NEAREST)
     else if (windowed) DR_TW(DR_FILTER_LINEAR_MIPMAP_LINEAR)
