@@ -301,6 +301,11 @@ __global__ void __launch_bounds__(256) k_aa_fwd(const float* __restrict__ rast,
                                                 float* __restrict__ out) {
   __shared__ int s_tri[18][18];
   const AATile g = aa_load_tile(rast, H, W, T, ntx, nty, s_tri);
+  const int64_t pix = ((int64_t)g.n * H + min(g.ph, H - 1)) * W + min(g.pw, W - 1);
+  float cp[CT > 0 ? CT : 1];
+  if constexpr (CT > 0) {  // own colour: needed by every pixel, issued before the barrier
+    if (g.inside) ld_px<CT>(color + pix * CT, CT, cp);
+  }
   __syncthreads();
   if (!g.inside) return;
   const int r = g.ly + 1, c = g.lx + 1;
@@ -328,10 +333,7 @@ __global__ void __launch_bounds__(256) k_aa_fwd(const float* __restrict__ rast,
       }
     }
   }
-  const int64_t pix = ((int64_t)g.n * H + g.ph) * W + g.pw;
   if constexpr (CT > 0) {
-    float cp[CT];
-    ld_px<CT>(color + pix * CT, CT, cp);
     if (blend) {
       float acc[CT];
 #pragma unroll
@@ -365,9 +367,54 @@ __global__ void __launch_bounds__(256) k_aa_fwd(const float* __restrict__ rast,
   }
 }
 
-// Fused backward on 16x16 tiles (one 8x8 quadrant per wave): d_color
-// (Antialias.swift:498-524) gathered through an LDS exchange of the blend
-// weights, d_pos (:388-496) summed per vertex in LDS.
+// d_pos terms of one partial blend (Antialias.swift:405-495): the blend
+// weight's gradient d_alpha = sum_c g * (c_neighbour - c_own) through the
+// crossing point into the edge's two clip-space vertices.
+__device__ __forceinline__ bool aa_dpos_terms(const SilDir& s, int d, int ph, int pw, int Cn,
+                                              const float* __restrict__ gp,
+                                              const float* __restrict__ cpp,
+                                              const float* __restrict__ cnp,
+                                              const float* __restrict__ p, float* __restrict__ dp,
+                                              float halfW, float halfH, LdsTable<4, 128>& tab) {
+  float d_alpha = 0.0f;
+  for (int k = 0; k < Cn; ++k) d_alpha += gp[k] * (cnp[k] - cpp[k]);
+  if (d_alpha == 0.0f) return false;
+  float dade0x, dade0y, dade1x, dade1y;
+  const float inv_denom_sq = 1.0f / (s.denom * s.denom);
+  if (d == 0 || d == 2) {
+    const float row_y = (float)ph + 0.5f;
+    const float ex_diff = s.e1x - s.e0x;
+    dade0x = s.dbeta * (1.0f - s.t);
+    dade1x = s.dbeta * s.t;
+    dade0y = s.dbeta * ex_diff * (row_y - s.e1y) * inv_denom_sq;
+    dade1y = s.dbeta * (-ex_diff) * (row_y - s.e0y) * inv_denom_sq;
+  } else {
+    const float col_x = (float)pw + 0.5f;
+    const float ey_diff = s.e1y - s.e0y;
+    dade0y = s.dbeta * (1.0f - s.t);
+    dade1y = s.dbeta * s.t;
+    dade0x = s.dbeta * ey_diff * (col_x - s.e1x) * inv_denom_sq;
+    dade1x = s.dbeta * (-ey_diff) * (col_x - s.e0x) * inv_denom_sq;
+  }
+  const int iv[2] = {s.ie0, s.ie1};
+  const float dex[2] = {dade0x, dade1x}, dey[2] = {dade0y, dade1y};
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const float4 P = *reinterpret_cast<const float4*>(p + (int64_t)iv[e] * 4);
+    const float inv_w = 1.0f / P.w;
+    const float nd_x = P.x * inv_w, nd_y = P.y * inv_w;
+    const float dv[4] = {
+        d_alpha * dex[e] * halfW * inv_w, d_alpha * dey[e] * (-halfH) * inv_w, 0.0f,
+        d_alpha * (dex[e] * (-halfW * nd_x) + dey[e] * (halfH * nd_y)) * inv_w};
+    lds_table_add(tab, dp + (int64_t)iv[e] * 4, dv);
+  }
+  return true;
+}
+
+// Fused backward on 16x16 tiles (one 8x8 quadrant per wave): each pixel's
+// blend weights and the d_pos terms of its partial blends (summed per
+// vertex in LDS) come first; d_color (Antialias.swift:498-524) is then
+// gathered through an LDS exchange of the blend weights.
 template <int CT>
 __global__ void __launch_bounds__(256) k_aa_bwd(const float* __restrict__ rast,
                                                 const AARec* __restrict__ rec,
@@ -381,16 +428,25 @@ __global__ void __launch_bounds__(256) k_aa_bwd(const float* __restrict__ rast,
   __shared__ float s_alpha[4][16][17];
   __shared__ float s_halo[4][16];
   __shared__ LdsTable<4, 128> tab;  // d_pos rows touched by this tile
-  __shared__ int s_need;            // some pixel has a partial blend (d_pos terms)
+  __shared__ int s_need;            // the table holds terms
+  if (d_pos) lds_table_clear(tab);
   if (threadIdx.x == 0) s_need = 0;
   const AATile g = aa_load_tile(rast, H, W, T, ntx, nty, s_tri);
+  const int64_t pix = ((int64_t)g.n * H + min(g.ph, H - 1)) * W + min(g.pw, W - 1);
+  float gv[CT > 0 ? CT : 1], old[CT > 0 ? CT : 1];
+  if constexpr (CT > 0) {  // own cotangent: needed by every pixel, issued before the barrier
+    if (d_color && g.inside) {
+      ld_px<CT>(d_out + pix * CT, CT, gv);
+      if (accumulate) ld_px<CT>(d_color + pix * CT, CT, old);
+    }
+  }
   __syncthreads();
   const AARec* recn = rec + (int64_t)g.n * T;
   const int r = g.ly + 1, c = g.lx + 1;
   const int tp = s_tri[r][c];
+  const int Cn = CT > 0 ? CT : C;
 
-  // 1) own blend weights (the edge state is recomputed in 4) for the few
-  //    pixels that need it rather than held across the barrier).
+  // 1) own blend weights, and the d_pos terms of the partial ones.
   float alpha[4];
   float asum = 0.0f;
   {
@@ -403,6 +459,8 @@ __global__ void __launch_bounds__(256) k_aa_bwd(const float* __restrict__ rast,
     }
     AARec rp;
     if (any && tp >= 0) rp = recn[tp];
+    const float halfW = (float)W * 0.5f, halfH = (float)H * 0.5f;
+    bool need = false;
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
       SilDir s;
@@ -410,12 +468,15 @@ __global__ void __launch_bounds__(256) k_aa_bwd(const float* __restrict__ rast,
       alpha[d] = on ? s.alpha : 0.0f;
       s_alpha[d][g.ly][g.lx] = alpha[d];
       asum += alpha[d];
+      if (d_pos && on && s.alpha < 1.0f) {
+        const int64_t q = d == 0 ? pix + 1 : d == 1 ? pix + W : d == 2 ? pix - 1 : pix - W;
+        need = aa_dpos_terms(s, d, g.ph, g.pw, Cn, d_out + pix * Cn, color + pix * Cn,
+                             color + q * Cn, pos + (int64_t)g.n * V * 4,
+                             d_pos + (int64_t)g.n * V * 4, halfW, halfH, tab) || need;
+      }
     }
+    if (need) s_need = 1;
   }
-  bool partial = false;
-#pragma unroll
-  for (int d = 0; d < 4; ++d) partial = partial || (alpha[d] > 0.0f && alpha[d] < 1.0f);
-  if (d_pos && partial) s_need = 1;
   // 2) border: the one direction of each outside neighbour that points into
   //    the tile; lanes 0..15 of each wave take one side.
   if ((threadIdx.x & 63) < 16) {
@@ -440,9 +501,7 @@ __global__ void __launch_bounds__(256) k_aa_bwd(const float* __restrict__ rast,
   }
   __syncthreads();
 
-  const int64_t pix = ((int64_t)g.n * H + min(g.ph, H - 1)) * W + min(g.pw, W - 1);
   const int lx = g.lx, ly = g.ly;
-  const int Cn = CT > 0 ? CT : C;
   // 3) d_color: own term + what each neighbour's blend sends here.
   if (d_color && g.inside) {
     float wn[4];
@@ -452,8 +511,7 @@ __global__ void __launch_bounds__(256) k_aa_bwd(const float* __restrict__ rast,
     wn[3] = ly > 0 ? s_alpha[1][ly - 1][lx] : s_halo[2][lx];   // upper neighbour, its dir 1
     const int64_t qn[4] = {pix + 1, pix + W, pix - 1, pix - W};
     if constexpr (CT > 0) {
-      float gv[CT], acc[CT];
-      ld_px<CT>(d_out + pix * CT, CT, gv);
+      float acc[CT];
 #pragma unroll
       for (int k = 0; k < CT; ++k) acc[k] = gv[k] * (1.0f - asum);
 #pragma unroll
@@ -466,8 +524,6 @@ __global__ void __launch_bounds__(256) k_aa_bwd(const float* __restrict__ rast,
         }
       }
       if (accumulate) {
-        float old[CT];
-        ld_px<CT>(d_color + pix * CT, CT, old);
 #pragma unroll
         for (int k = 0; k < CT; ++k) acc[k] = old[k] + acc[k];
       }
@@ -484,66 +540,8 @@ __global__ void __launch_bounds__(256) k_aa_bwd(const float* __restrict__ rast,
       }
     }
   }
-  // 4) d_pos (Antialias.swift:405-495), summed per vertex in LDS; only
-  //    tiles with a partial blend have terms.
-  if (!d_pos || !s_need) return;  // uniform: no barrier follows
-  lds_table_clear(tab);
-  __syncthreads();
-  const float halfW = (float)W * 0.5f, halfH = (float)H * 0.5f;
-  const float* p = pos + (int64_t)g.n * V * 4;
-  float* dp = d_pos + (int64_t)g.n * V * 4;
-  const float* gp = d_out + pix * Cn;
-  const float* cpp = color + pix * Cn;
-#pragma unroll
-  for (int d = 0; d < 4; ++d) {
-    bool on = alpha[d] > 0.0f && alpha[d] < 1.0f;
-    if (on) {
-      const int64_t q = d == 0 ? pix + 1 : d == 1 ? pix + W : d == 2 ? pix - 1 : pix - W;
-      const float* cnp = color + q * Cn;
-      float d_alpha = 0.0f;
-      for (int k = 0; k < Cn; ++k) d_alpha += gp[k] * (cnp[k] - cpp[k]);
-      on = d_alpha != 0.0f;
-      SilDir s;
-      if (on) {
-        AARec rp;
-        if (tp >= 0) rp = recn[tp];
-        on = aa_pair(recn, rp, tp, aa_nb(s_tri, r, c, d), g.ph, g.pw, d, s);
-      }
-      if (on) {
-        float dade0x, dade0y, dade1x, dade1y;
-        const float inv_denom_sq = 1.0f / (s.denom * s.denom);
-        if (d == 0 || d == 2) {
-          const float row_y = (float)g.ph + 0.5f;
-          const float ex_diff = s.e1x - s.e0x;
-          dade0x = s.dbeta * (1.0f - s.t);
-          dade1x = s.dbeta * s.t;
-          dade0y = s.dbeta * ex_diff * (row_y - s.e1y) * inv_denom_sq;
-          dade1y = s.dbeta * (-ex_diff) * (row_y - s.e0y) * inv_denom_sq;
-        } else {
-          const float col_x = (float)g.pw + 0.5f;
-          const float ey_diff = s.e1y - s.e0y;
-          dade0y = s.dbeta * (1.0f - s.t);
-          dade1y = s.dbeta * s.t;
-          dade0x = s.dbeta * ey_diff * (col_x - s.e1x) * inv_denom_sq;
-          dade1x = s.dbeta * (-ey_diff) * (col_x - s.e0x) * inv_denom_sq;
-        }
-        const int iv[2] = {s.ie0, s.ie1};
-        const float dex[2] = {dade0x, dade1x}, dey[2] = {dade0y, dade1y};
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-          const float4 P = *reinterpret_cast<const float4*>(p + (int64_t)iv[e] * 4);
-          const float inv_w = 1.0f / P.w;
-          const float nd_x = P.x * inv_w, nd_y = P.y * inv_w;
-          const float dv[4] = {
-              d_alpha * dex[e] * halfW * inv_w, d_alpha * dey[e] * (-halfH) * inv_w, 0.0f,
-              d_alpha * (dex[e] * (-halfW * nd_x) + dey[e] * (halfH * nd_y)) * inv_w};
-          lds_table_add(tab, dp + (int64_t)iv[e] * 4, dv);
-        }
-      }
-    }
-  }
-  __syncthreads();
-  lds_table_flush(tab);
+  // 4) write the d_pos sums out (every term was added before the barrier).
+  if (d_pos && s_need) lds_table_flush(tab);  // uniform; contains a barrier
 }
 
 }  // namespace dr

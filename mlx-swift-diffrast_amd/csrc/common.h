@@ -149,37 +149,63 @@ __device__ __forceinline__ int dpp_shift(int v) {
 }
 
 template <int D, int M>
-__device__ __forceinline__ void run_scan_step(int l8, int s, float (&v)[M]) {
+__device__ __forceinline__ void run_scan_step(int li, int s, float (&v)[M]) {
 #pragma unroll
   for (int i = 0; i < M; ++i) {
     const float o = __int_as_float(dpp_shift<0x110 + D>(__float_as_int(v[i])));
-    if (l8 - D >= s) v[i] += o;
+    if (li - D >= s) v[i] += o;
   }
 }
 
-// Runs of equal `key` along each 8-lane row (lanes 8r..8r+7 hold one pixel
-// row of an 8x8 quadrant): every lane's v[] becomes the sum of its run's
-// values up to itself (a segmented Hillis-Steele scan over DPP row shifts),
-// and the run's last lane, which then holds the run total, gets true.  All
-// 64 lanes must execute this; give each inactive lane a key of its own.
+// Runs of equal keys along each 16-lane row (the row of pixels a wave row
+// holds): every lane's v[] becomes the sum of its run's values up to
+// itself (a segmented Hillis-Steele scan over DPP row shifts), and the
+// run's last lane, which then holds the run total, gets true.  Summing a
+// run before it meets an LDS atomic matters: lanes of one instruction that
+// hit one address are serialised (~11 cycles each for fp64 adds).  All 64
+// lanes must execute this; give each inactive lane a key of its own.
+struct RowRun {
+  int li, s;  // lane within its 16-lane row, start of its run
+  bool tail;  // last lane of its run
+};
+
+__device__ __forceinline__ RowRun row_run(uint64_t key) {
+  RowRun r;
+  r.li = lane_id() & 15;
+  const int li = r.li;
+  const int klo = (int)(uint32_t)key, khi = (int)(uint32_t)(key >> 32);
+  // every lane must execute the shifts (a DPP read of a lane that is
+  // switched off returns 0), so no short-circuit evaluation here
+  const int plo = dpp_shift<0x111>(klo), phi = dpp_shift<0x111>(khi);
+  const int nlo = dpp_shift<0x101>(klo), nhi = dpp_shift<0x101>(khi);
+  const bool head = (li == 0) | (plo != klo) | (phi != khi);
+  r.tail = (li == 15) | (nlo != klo) | (nhi != khi);
+  int s = head ? li : 0;  // run start: max-scan of head positions
+  int a = dpp_shift<0x111>(s);
+  if (li >= 1) s = max(s, a);
+  a = dpp_shift<0x112>(s);
+  if (li >= 2) s = max(s, a);
+  a = dpp_shift<0x114>(s);
+  if (li >= 4) s = max(s, a);
+  a = dpp_shift<0x118>(s);
+  if (li >= 8) s = max(s, a);
+  r.s = s;
+  return r;
+}
+
 template <int M>
-__device__ __forceinline__ bool row_run_sum(int key, float (&v)[M]) {
-  const int l8 = lane_id() & 7;
-  const int kp = dpp_shift<0x111>(key);  // key of lane - 1
-  const int kn = dpp_shift<0x101>(key);  // key of lane + 1
-  int s = (l8 == 0 || kp != key) ? l8 : 0;  // run start: max-scan of head positions
-  {
-    const int a = dpp_shift<0x111>(s);
-    if (l8 >= 1) s = max(s, a);
-    const int b = dpp_shift<0x112>(s);
-    if (l8 >= 2) s = max(s, b);
-    const int c = dpp_shift<0x114>(s);
-    if (l8 >= 4) s = max(s, c);
-  }
-  run_scan_step<1>(l8, s, v);
-  run_scan_step<2>(l8, s, v);
-  run_scan_step<4>(l8, s, v);
-  return l8 == 7 || kn != key;
+__device__ __forceinline__ void row_run_scan(const RowRun& r, float (&v)[M]) {
+  run_scan_step<1>(r.li, r.s, v);
+  run_scan_step<2>(r.li, r.s, v);
+  run_scan_step<4>(r.li, r.s, v);
+  run_scan_step<8>(r.li, r.s, v);
+}
+
+template <int M>
+__device__ __forceinline__ bool row_run_sum(uint64_t key, float (&v)[M]) {
+  const RowRun r = row_run(key);
+  row_run_scan(r, v);
+  return r.tail;
 }
 
 __device__ __forceinline__ float wave_sum(float v) {

@@ -59,9 +59,9 @@ __global__ void __launch_bounds__(256) k_interp_fwd(
   }
 }
 
-// Fused backward.  Pixels are walked in 16x16 tiles, one 8x8 quadrant per
-// wave, so a wave's pixels mostly share a few triangles and their d_attr
-// contributions are summed across the wave before the atomics.
+// Fused backward.  Pixels are walked in 16x16 tiles, a 16x4 strip per wave;
+// runs of one triangle along a pixel row are summed before their d_attr
+// terms meet the LDS table.
 template <int AT, int KT>
 __global__ void __launch_bounds__(256) k_interp_bwd(
     const float* __restrict__ attr, int64_t attr_stride, const float* __restrict__ rast,
@@ -80,8 +80,8 @@ __global__ void __launch_bounds__(256) k_interp_bwd(
   const int tile = b - n * tiles;
   const int ty = tile / ntx, tx = tile - ty * ntx;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int qx0 = tx * 16 + (wave & 1) * 8, qy0 = ty * 16 + (wave >> 1) * 8;
-  const int pw = qx0 + (lane & 7), ph = qy0 + (lane >> 3);
+  // 16x4 strip per wave: each 16-lane row holds one pixel row
+  const int pw = tx * 16 + (lane & 15), ph = ty * 16 + wave * 4 + (lane >> 4);
   const bool inside = pw < W && ph < H;
   const int64_t pix = ((int64_t)n * H + min(ph, H - 1)) * W + min(pw, W - 1);
   const int A = dimA<AT>(A_);
@@ -164,7 +164,7 @@ __global__ void __launch_bounds__(256) k_interp_bwd(
     }
     // Runs of same-triangle lanes along a pixel row add into the same rows:
     // sum each run first, its last lane adds the total.
-    const bool tail = row_run_sum(valid ? t : -2 - lane, rv);
+    const bool tail = row_run_sum(valid ? (uint64_t)t : (1ull << 63) | (uint64_t)lane, rv);
     if (valid && tail) {
       lds_table_add(tab, da + (int64_t)i0 * A, &rv[0]);
       lds_table_add(tab, da + (int64_t)i1 * A, &rv[NV]);

@@ -335,9 +335,9 @@ __global__ void __launch_bounds__(256) k_raster(
   if (DB) *reinterpret_cast<float4*>(rast_db + pix * 4) = d4;
 }
 
-// Rasterize.swift:637-812.  Same tile/quadrant layout as the forward so a
-// wave's pixels share few triangles; runs of same-triangle lanes along a
-// pixel row are summed before the LDS table adds the 12 d_pos terms.
+// Rasterize.swift:637-812.  16x16 tiles, a 16x4 strip per wave; runs of
+// same-triangle lanes along a pixel row are summed before the LDS table
+// adds the 12 d_pos terms.
 __global__ void __launch_bounds__(256) k_raster_bwd(
     const float* __restrict__ pos, int64_t pos_stride, const int32_t* __restrict__ tri,
     const float* __restrict__ rast, const float* __restrict__ d_rast,
@@ -353,10 +353,10 @@ __global__ void __launch_bounds__(256) k_raster_bwd(
   const int ty = tile / ntx, tx = tile - ty * ntx;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int qx0 = tx * kTile + (wave & 1) * 8;
-  const int qy0 = ty * kTile + (wave >> 1) * 8;
-  const int pw = qx0 + (lane & 7);
-  const int ph = qy0 + (lane >> 3);
+  // 16x4 strip per wave: each 16-lane row holds one pixel row, so runs of
+  // one triangle along a row are summed with DPP row shifts.
+  const int pw = tx * kTile + (lane & 15);
+  const int ph = ty * kTile + wave * 4 + (lane >> 4);
   bool valid = pw < W && ph < H;
   const int64_t pix = ((int64_t)n * H + min(ph, H - 1)) * W + min(pw, W - 1);
   const float4 r = *reinterpret_cast<const float4*>(rast + pix * 4);
@@ -452,7 +452,7 @@ __global__ void __launch_bounds__(256) k_raster_bwd(
   }
   // Lanes of a row on the same triangle add into the same three rows: sum
   // each run first, its last lane adds the total.
-  const bool tail = row_run_sum(valid ? t : -2 - lane, val);
+  const bool tail = row_run_sum(valid ? (uint64_t)t : (1ull << 63) | (uint64_t)lane, val);
   if (valid && tail) {
     lds_table_add(tab, dp + (int64_t)i0 * 4, &val[0]);
     lds_table_add(tab, dp + (int64_t)i1 * 4, &val[4]);

@@ -719,8 +719,8 @@ __global__ void __launch_bounds__(256) k_tex_bwd_win(TexBwdArgs A, int total_til
     const int n = bt / tiles;
     const int tile = bt - n * tiles;
     const int ty = tile / A.ntx, tx = tile - ty * A.ntx;
-    const int pw = tx * 16 + (wave & 1) * 8 + (lane & 7);
-    const int ph = ty * 16 + (wave >> 1) * 8 + (lane >> 3);
+    const int pw = tx * 16 + (lane & 15);  // 16x4 strip per wave, one pixel row per 16 lanes
+    const int ph = ty * 16 + wave * 4 + (lane >> 4);
     const bool valid = pw < A.Wi && ph < A.Hi;
     const int64_t pix = ((int64_t)n * A.Hi + min(ph, A.Hi - 1)) * A.Wi + min(pw, A.Wi - 1);
     auto level_ptr = [&](int k) -> const float* {
@@ -939,38 +939,43 @@ __global__ void __launch_bounds__(256) k_tex_bwd_win(TexBwdArgs A, int total_til
     usable[1] = usable[1] && (usable[0] ? area[0] : 0) + area[1] <= kWinTexels;
     wbase[1] = usable[0] ? (int)area[0] * CT : 0;
 
-    // -- accumulate ------------------------------------------------------------
+    // -- accumulate: runs of one footprint along a pixel row are summed
+    //    first (lanes of one LDS atomic on one address are serialised), the
+    //    run's last lane adds the totals ----------------------------------------
 #pragma unroll
     for (int li = 0; li < 2; ++li) {
       const int w = wsel[li];
-      if (w == -2) continue;
       const float wt[4] = {q[li].w00, q[li].w10, q[li].w01, q[li].w11};
-      const int tx_[4] = {q[li].ix0, q[li].ix1, q[li].ix0, q[li].ix1};
-      const int ty_[4] = {q[li].iy0, q[li].iy0, q[li].iy1, q[li].iy1};
       const float sc = mip ? q[li].scale : 1.0f;
-      if (w >= 0 && usable[w]) {
-        double* wb = win + wbase[w];
+      // level and the four texel coordinates (each < 32767 on the window
+      // path) fix the taps; an unused slot gets a key no footprint has
+      const uint64_t key =
+          w == -2 ? (0x7FFFull << 45) | (uint64_t)lane
+                  : ((uint64_t)q[li].k << 60) | ((uint64_t)q[li].ix0 << 45) |
+                        ((uint64_t)q[li].ix1 << 30) | ((uint64_t)q[li].iy0 << 15) | (uint64_t)q[li].iy1;
+      const RowRun run = row_run(key);
+      const bool adds = w != -2 && run.tail;
+      const bool in_win = w >= 0 && usable[w];
+      double* wb = win + (w >= 0 ? wbase[w] : 0);
+      float* base = dlevel_ptr(q[li].k);
+      const int Wk = mip_w(md, q[li].k);
+      if (adds && !in_win) s_tab_used[par] = 1;
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          if (wt[t] == 0.0f) continue;
-          const int o = ((ty_[t] - by0[w]) * bw[w] + (tx_[t] - bx0[w])) * CT;  // < area[w]*CT
+      for (int t = 0; t < 4; ++t) {
+        float v[CT];
 #pragma unroll
-          for (int c = 0; c < CT; ++c) {
-            const float v = wt[t] * (g[c] * sc);
-            if (v != 0.0f) atomicAdd(wb + o + c, (double)v);
-          }
-        }
-      } else {
-        float* base = dlevel_ptr(q[li].k);
-        const int Wk = mip_w(md, q[li].k);
-        s_tab_used[par] = 1;
+        for (int c = 0; c < CT; ++c) v[c] = w == -2 ? 0.0f : wt[t] * (g[c] * sc);
+        row_run_scan(run, v);
+        if (!adds) continue;
+        const int tx_ = (t & 1) ? q[li].ix1 : q[li].ix0;
+        const int ty_ = (t & 2) ? q[li].iy1 : q[li].iy0;
+        if (in_win) {
+          const int o = ((ty_ - by0[w]) * bw[w] + (tx_ - bx0[w])) * CT;  // < area[w]*CT
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          if (wt[t] == 0.0f) continue;
-          float v[CT];
-#pragma unroll
-          for (int c = 0; c < CT; ++c) v[c] = wt[t] * (g[c] * sc);
-          lds_table_add(tab, base + (ty_[t] * Wk + tx_[t]) * CT, v);
+          for (int c = 0; c < CT; ++c)
+            if (v[c] != 0.0f) atomicAdd(wb + o + c, (double)v[c]);
+        } else {
+          lds_table_add(tab, base + (ty_ * Wk + tx_) * CT, v);
         }
       }
     }
