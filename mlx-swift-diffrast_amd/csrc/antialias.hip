@@ -411,10 +411,20 @@ __device__ __forceinline__ bool aa_dpos_terms(const SilDir& s, int d, int ph, in
   return true;
 }
 
+// A partial blend queued for its d_pos terms: the edge state and where.
+struct PosItem {
+  float e0x, e0y, e1x, e1y, t, denom, dbeta;
+  int ie0, ie1;
+  int where;  // local pixel (ly * 16 + lx) * 4 + direction
+};
+constexpr int kPosQueue = 256;
+
 // Fused backward on 16x16 tiles (one 8x8 quadrant per wave): each pixel's
-// blend weights and the d_pos terms of its partial blends (summed per
-// vertex in LDS) come first; d_color (Antialias.swift:498-524) is then
-// gathered through an LDS exchange of the blend weights.
+// blend weights come first, its partial blends are queued in LDS; d_color
+// (Antialias.swift:498-524) is gathered through an LDS exchange of the
+// blend weights; then every thread takes one queued blend and adds its
+// d_pos terms (summed per vertex in LDS), so the few lanes with partial
+// blends do not each walk the whole chain of loads while the rest idle.
 template <int CT>
 __global__ void __launch_bounds__(256) k_aa_bwd(const float* __restrict__ rast,
                                                 const AARec* __restrict__ rec,
@@ -428,9 +438,11 @@ __global__ void __launch_bounds__(256) k_aa_bwd(const float* __restrict__ rast,
   __shared__ float s_alpha[4][16][17];
   __shared__ float s_halo[4][16];
   __shared__ LdsTable<4, 128> tab;  // d_pos rows touched by this tile
+  __shared__ PosItem s_q[kPosQueue];
+  __shared__ int s_nq;              // queued partial blends
   __shared__ int s_need;            // the table holds terms
   if (d_pos) lds_table_clear(tab);
-  if (threadIdx.x == 0) s_need = 0;
+  if (threadIdx.x == 0) { s_need = 0; s_nq = 0; }
   const AATile g = aa_load_tile(rast, H, W, T, ntx, nty, s_tri);
   const int64_t pix = ((int64_t)g.n * H + min(g.ph, H - 1)) * W + min(g.pw, W - 1);
   float gv[CT > 0 ? CT : 1], old[CT > 0 ? CT : 1];
@@ -446,9 +458,10 @@ __global__ void __launch_bounds__(256) k_aa_bwd(const float* __restrict__ rast,
   const int tp = s_tri[r][c];
   const int Cn = CT > 0 ? CT : C;
 
-  // 1) own blend weights, and the d_pos terms of the partial ones.
+  // 1) own blend weights; the partial ones are queued for their d_pos terms.
   float alpha[4];
   float asum = 0.0f;
+  int ovf = 0;
   {
     int tn[4];
     bool any = false;
@@ -459,8 +472,6 @@ __global__ void __launch_bounds__(256) k_aa_bwd(const float* __restrict__ rast,
     }
     AARec rp;
     if (any && tp >= 0) rp = recn[tp];
-    const float halfW = (float)W * 0.5f, halfH = (float)H * 0.5f;
-    bool need = false;
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
       SilDir s;
@@ -469,14 +480,21 @@ __global__ void __launch_bounds__(256) k_aa_bwd(const float* __restrict__ rast,
       s_alpha[d][g.ly][g.lx] = alpha[d];
       asum += alpha[d];
       if (d_pos && on && s.alpha < 1.0f) {
-        const int64_t q = d == 0 ? pix + 1 : d == 1 ? pix + W : d == 2 ? pix - 1 : pix - W;
-        need = aa_dpos_terms(s, d, g.ph, g.pw, Cn, d_out + pix * Cn, color + pix * Cn,
-                             color + q * Cn, pos + (int64_t)g.n * V * 4,
-                             d_pos + (int64_t)g.n * V * 4, halfW, halfH, tab) || need;
+        const int slot = atomicAdd(&s_nq, 1);
+        if (slot < kPosQueue) {
+          PosItem it;
+          it.e0x = s.e0x; it.e0y = s.e0y; it.e1x = s.e1x; it.e1y = s.e1y;
+          it.t = s.t; it.denom = s.denom; it.dbeta = s.dbeta;
+          it.ie0 = s.ie0; it.ie1 = s.ie1;
+          it.where = ((g.ly * 16 + g.lx) << 2) | d;
+          s_q[slot] = it;
+        } else {
+          ovf |= 1 << d;  // queue full: this lane adds these terms itself, below
+        }
       }
     }
-    if (need) s_need = 1;
   }
+  if (ovf) s_need = 1;
   // 2) border: the one direction of each outside neighbour that points into
   //    the tile; lanes 0..15 of each wave take one side.
   if ((threadIdx.x & 63) < 16) {
@@ -540,8 +558,41 @@ __global__ void __launch_bounds__(256) k_aa_bwd(const float* __restrict__ rast,
       }
     }
   }
-  // 4) write the d_pos sums out (every term was added before the barrier).
-  if (d_pos && s_need) lds_table_flush(tab);  // uniform; contains a barrier
+  // 4) d_pos terms of the queued partial blends, one per thread, then the
+  //    per-vertex sums are written out.
+  if (!d_pos) return;  // uniform
+  const int nq = min(s_nq, kPosQueue);
+  if (nq == 0 && !s_need) return;  // uniform: both read after the barrier
+  for (int i = threadIdx.x; i < nq; i += blockDim.x) {
+    const PosItem it = s_q[i];
+    SilDir s;
+    s.e0x = it.e0x; s.e0y = it.e0y; s.e1x = it.e1x; s.e1y = it.e1y;
+    s.t = it.t; s.denom = it.denom; s.dbeta = it.dbeta;
+    s.ie0 = it.ie0; s.ie1 = it.ie1;
+    const int d = it.where & 3, lp = it.where >> 2;
+    const int qlx = lp & 15, qly = lp >> 4;
+    const int qph = g.y0 + qly, qpw = g.x0 + qlx;
+    const int64_t qp = ((int64_t)g.n * H + qph) * W + qpw;
+    const int64_t qn = d == 0 ? qp + 1 : d == 1 ? qp + W : d == 2 ? qp - 1 : qp - W;
+    aa_dpos_terms(s, d, qph, qpw, Cn, d_out + qp * Cn, color + qp * Cn, color + qn * Cn,
+                  pos + (int64_t)g.n * V * 4, d_pos + (int64_t)g.n * V * 4, (float)W * 0.5f,
+                  (float)H * 0.5f, tab);
+  }
+  if (ovf) {  // blends that did not fit the queue: recompute the edge state
+    AARec rp;
+    if (tp >= 0) rp = recn[tp];
+    for (int d = 0; d < 4; ++d) {
+      if (!((ovf >> d) & 1)) continue;
+      SilDir s;
+      if (!aa_pair(recn, rp, tp, aa_nb(s_tri, r, c, d), g.ph, g.pw, d, s)) continue;
+      const int64_t qn = d == 0 ? pix + 1 : d == 1 ? pix + W : d == 2 ? pix - 1 : pix - W;
+      aa_dpos_terms(s, d, g.ph, g.pw, Cn, d_out + pix * Cn, color + pix * Cn, color + qn * Cn,
+                    pos + (int64_t)g.n * V * 4, d_pos + (int64_t)g.n * V * 4, (float)W * 0.5f,
+                    (float)H * 0.5f, tab);
+    }
+  }
+  __syncthreads();
+  lds_table_flush(tab);  // contains a barrier
 }
 
 }  // namespace dr

@@ -87,3 +87,31 @@ def test_antialias_unaligned_rows():
     assert c.data_ptr() % 16 != 0
     out = DiffRast.antialias(c, dev(rast), dev(pos), dev(tri))
     assert_fwd_close(host(out), O.antialias(color, rast, pos, tri))
+
+
+@pytest.mark.parametrize("C", [4, 3])
+def test_antialias_dense_edges(C):
+    """Triangles of a few pixels: about 40% of the pixels blend, up to ~220
+    of a 16x16 tile's 256, most in more than one direction, so some tiles
+    hold more partial blends than the d_pos queue (256) and the overflow
+    path runs too."""
+    torch = torch_dev()
+    from diffrast import DiffRast
+    rng = np.random.default_rng(21 + C)
+    sc = scenes.textured_icosphere(N=2, H=128, W=128, level=5, tex_size=8)
+    pos, tri, H, W = sc["pos"], sc["tri"], 128, 128
+    rast, _ = O.rasterize(pos, tri, (H, W), gradDB=False, max_per_tile=0)
+    N = pos.shape[0]
+    color = rng.random((N, H, W, C)).astype(np.float32)
+    ref = O.antialias(color, rast, pos, tri)
+    blended = (ref != color).any(-1).sum(axis=(1, 2))
+    assert blended.min() > 4000, blended
+    c = dev(color).requires_grad_(True)
+    p = dev(pos).requires_grad_(True)
+    out = DiffRast.antialias(c, dev(rast), p, dev(tri))
+    assert_fwd_close(host(out), ref)
+    g = rng.normal(size=ref.shape).astype(np.float32)
+    (out * dev(g)).sum().backward()
+    d_color, d_pos = O.antialias_vjp(color, rast, pos, tri, g)
+    assert_grad_close(host(c.grad), d_color, "d_color")
+    assert_grad_close(host(p.grad), d_pos, "d_pos")
