@@ -55,12 +55,13 @@ enum Slot {
 struct Scratch {
   void* ptr[SLOT_COUNT] = {};
   size_t cap[SLOT_COUNT] = {};
-  // Bin-list capacity protocol (rasterize): the exact pair count of the
-  // last call is copied to pinned host memory after the call; the next call
-  // reads it (once its copy has landed) to size the list buffer.
+  // Tile-list capacity protocol (rasterize): the largest per-tile count of
+  // a call is copied to pinned host memory after the call; a later call
+  // reads it (once its copy has landed) and raises the capacity if needed.
   int64_t* pinned_total = nullptr;
   hipEvent_t total_event = nullptr;
   bool total_pending = false;
+  int bin_cap = 0;  // slots per tile list, 0 = not known yet
 };
 
 // Compute units of the current device (cached per device).

@@ -104,68 +104,112 @@ __device__ __forceinline__ void item_of(const Items& it, int64_t i, int N, int& 
   }
 }
 
+// Binning atomics.  Consecutive triangles are neighbours in the mesh and
+// mostly land in the same tile, and lanes of one atomic instruction on one
+// address are serialised; so each triangle's first kHeld tiles are taken one
+// at a time across the wave, runs of one tile along each 16-lane row are
+// counted with DPP, and only the run's last lane issues the atomic.
+constexpr int kHeld = 4;
+
+// Tile k of a triangle's tile rectangle (row-major), or -1.
+__device__ __forceinline__ int rect_tile(int4 rc, int ntx, int base, int k) {
+  if (rc.x < 0) return -1;
+  const int w = rc.y - rc.x + 1, h = rc.w - rc.z + 1;
+  if (k >= w * h) return -1;
+  return base + (rc.z + k / w) * ntx + rc.x + k % w;
+}
+
+__device__ __forceinline__ int rect_tiles(int4 rc) {
+  return rc.x < 0 ? 0 : (rc.y - rc.x + 1) * (rc.w - rc.z + 1);
+}
+
+// Key of tile j for a run search: lanes without a tile get keys of their own.
+__device__ __forceinline__ uint64_t tile_key(int j, int lane) {
+  return j >= 0 ? (uint64_t)(uint32_t)j : (0xFFFFFFFF00000000ull | (uint64_t)lane);
+}
+
 // Rasterize.swift:227-233, first half: per-tile counts.
 __global__ void __launch_bounds__(256) k_bin_count(Items it, int64_t n_items, int N,
                                                    const int4* __restrict__ rect, int ntx,
                                                    int tiles, int* __restrict__ cnt) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= n_items) return;
-  int n, t;
-  int64_t r;
-  item_of(it, i, N, n, t, r);
-  const int4 rc = rect[r];
-  if (rc.x < 0) return;
-  int* c = cnt + (int64_t)n * tiles;
-  for (int ty = rc.z; ty <= rc.w; ++ty)
-    for (int tx = rc.x; tx <= rc.y; ++tx) atomicAdd(&c[ty * ntx + tx], 1);
-}
-
-// Each tile reserves its list segment: a wave-wide exclusive scan of the
-// counts, one atomic per wave on the running total.
-__global__ void __launch_bounds__(256) k_bin_alloc(const int* __restrict__ cnt, int64_t n_tiles,
-                                                   int64_t* __restrict__ off,
-                                                   int* __restrict__ fill,
-                                                   unsigned long long* __restrict__ total) {
-  const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int c = j < n_tiles ? cnt[j] : 0;
-  int incl = c;
   const int lane = lane_id();
+  int4 rc = make_int4(-1, -1, -1, -1);
+  int base = 0;
+  if (i < n_items) {
+    int n, t;
+    int64_t r;
+    item_of(it, i, N, n, t, r);
+    rc = rect[r];
+    base = n * tiles;
+  }
 #pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    const int y = __shfl_up(incl, d, kWave);
-    if (lane >= d) incl += y;
+  for (int k = 0; k < kHeld; ++k) {  // every lane takes part (row shifts)
+    const int j = rect_tile(rc, ntx, base, k);
+    const RowRun run = row_run(tile_key(j, lane));
+    if (j >= 0 && run.tail) atomicAdd(&cnt[j], run.li - run.s + 1);
   }
-  const int wave_total = __shfl(incl, kWave - 1, kWave);
-  unsigned long long base = 0;
-  if (lane == kWave - 1 && wave_total > 0) base = atomicAdd(total, (unsigned long long)wave_total);
-  base = __shfl(base, kWave - 1, kWave);
-  if (j < n_tiles) {
-    off[j] = (int64_t)base + (incl - c);
-    fill[j] = 0;
-  }
+  const int nt = rect_tiles(rc);
+  for (int k = kHeld; k < nt; ++k) atomicAdd(&cnt[rect_tile(rc, ntx, base, k)], 1);
 }
 
-// Rasterize.swift:227-239, second half: append t to each touched tile.
+// Largest per-tile count (sizes the next call's per-tile list capacity).
+__global__ void __launch_bounds__(256) k_tile_max(const int* __restrict__ c, int64_t n,
+                                                  int* __restrict__ out) {
+  const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int m = wave_max(j < n ? c[j] : 0);
+  if (lane_id() == 0) atomicMax(out, m);
+}
+
+// Rasterize.swift:227-239, second half: append t to each touched tile's
+// list of `cap` slots (tile j's list starts at j * cap; a tile whose count
+// ends above cap is rasterized by a full scan instead).  The last lane of a
+// run reserves the run's slots; the others take theirs from it by rank.
 __global__ void __launch_bounds__(256) k_bin_fill(Items it, int64_t n_items, int N,
                                                   const int4* __restrict__ rect, int ntx,
-                                                  int tiles, const int64_t* __restrict__ off,
-                                                  int* __restrict__ fill,
-                                                  int* __restrict__ list, int64_t cap) {
+                                                  int tiles, int* __restrict__ fill,
+                                                  int* __restrict__ list, int cap) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= n_items) return;
-  int n, t;
-  int64_t r;
-  item_of(it, i, N, n, t, r);
-  const int4 rc = rect[r];
-  if (rc.x < 0) return;
-  const int64_t base = (int64_t)n * tiles;
-  for (int ty = rc.z; ty <= rc.w; ++ty)
-    for (int tx = rc.x; tx <= rc.y; ++tx) {
-      const int64_t j = base + ty * ntx + tx;
-      const int s = atomicAdd(&fill[j], 1);
-      const int64_t p = off[j] + s;
-      if (p < cap) list[p] = t;
+  const int lane = lane_id();
+  int4 rc = make_int4(-1, -1, -1, -1);
+  int base = 0, t = 0;
+  if (i < n_items) {
+    int n;
+    int64_t r;
+    item_of(it, i, N, n, t, r);
+    rc = rect[r];
+    base = n * tiles;
+  }
+#pragma unroll
+  for (int k = 0; k < kHeld; ++k) {  // every lane takes part (row shifts, shuffle)
+    const int j = rect_tile(rc, ntx, base, k);
+    const RowRun run = row_run(tile_key(j, lane));
+    // position of the run's last lane: the first tail at or after this lane
+    int tp = run.tail ? run.li : 16;
+    {
+      int a = dpp_shift<0x101>(tp);
+      if (run.li + 1 <= 15) tp = min(tp, a);
+      a = dpp_shift<0x102>(tp);
+      if (run.li + 2 <= 15) tp = min(tp, a);
+      a = dpp_shift<0x104>(tp);
+      if (run.li + 4 <= 15) tp = min(tp, a);
+      a = dpp_shift<0x108>(tp);
+      if (run.li + 8 <= 15) tp = min(tp, a);
     }
+    int slot0 = 0;
+    if (j >= 0 && run.tail) slot0 = atomicAdd(&fill[j], run.li - run.s + 1);
+    slot0 = __shfl(slot0, (lane & ~15) + min(tp, 15), kWave);
+    if (j >= 0) {
+      const int p = slot0 + (run.li - run.s);
+      if (p < cap) list[(int64_t)j * cap + p] = t;
+    }
+  }
+  const int nt = rect_tiles(rc);
+  for (int k = kHeld; k < nt; ++k) {
+    const int j = rect_tile(rc, ntx, base, k);
+    const int p = atomicAdd(&fill[j], 1);
+    if (p < cap) list[(int64_t)j * cap + p] = t;
+  }
 }
 
 struct Best {
@@ -235,8 +279,8 @@ __device__ __forceinline__ TriRec bcast_rec(const TriRec& R, int j) {
 template <bool DB, bool PEEL>
 __global__ void __launch_bounds__(256) k_raster(
     const TriRec* __restrict__ rec, const int4* __restrict__ rect, Items it, int64_t rec_stride,
-    const int* __restrict__ cnt, const int64_t* __restrict__ off, const int* __restrict__ list,
-    int64_t cap, const float* __restrict__ peel, int N, int H, int W, int ntx, int nty,
+    const int* __restrict__ cnt, const int* __restrict__ list, int cap,
+    const float* __restrict__ peel, int N, int H, int W, int ntx, int nty,
     float* __restrict__ rast, float* __restrict__ rast_db) {
   const int tiles = ntx * nty;
   const int B = tiles * N;
@@ -271,8 +315,8 @@ __global__ void __launch_bounds__(256) k_raster(
   const int64_t rbase = (int64_t)n * rec_stride;
   const int64_t j = (int64_t)n * tiles + tile;
   const int count = cnt[j];
-  const int64_t o = off[j];
-  if (o + count <= cap) {
+  const int64_t o = j * (int64_t)cap;
+  if (count <= cap) {
     // 64 candidates at a time: each lane loads one candidate's record
     // (vector gathers, one round trip for all 64) and tests it against the
     // quadrant's box; the survivors are then taken one by one, their
@@ -298,9 +342,9 @@ __global__ void __launch_bounds__(256) k_raster(
       }
     }
   } else {
-    // The list did not fit the scratch sized from an earlier call: scan the
-    // image's whole triangle range with the same tile test the binning
-    // uses (same candidate set, so the same result).
+    // The tile's list overflowed its capacity (sized from an earlier
+    // call): scan the image's whole triangle range with the same tile test
+    // the binning uses (same candidate set, so the same result).
     int t0 = 0, t1 = it.T;
     if (it.prefix != nullptr) {
       t0 = (int)it.start[n];
@@ -530,59 +574,64 @@ extern "C" int dr_rasterize_fwd(const float* pos, int64_t pos_batch_stride, cons
   unsigned long long* total =
       (unsigned long long*)scratch_get(sc, stream, SLOT_SMALL, 64);
   if (!rec || !rect || !cbuf || !total) return DR_ERR_MEMORY;
-  int64_t* off = (int64_t*)cbuf;
-  int* cnt = (int*)(cbuf + n_tiles * 8);
+  int* cnt = (int*)cbuf;
   int* fillc = cnt + n_tiles;
+  int* tmax = (int*)total;
 
-  DR_CHECK_HIP(fill_async(cnt, 0, n_tiles, stream));
-  DR_CHECK_HIP(fill_async(total, 0ull, 1, stream));
   if (n_rec > 0) {
     DR_TIMED("k_setup", stream);
     hipLaunchKernelGGL(k_setup, dim3(grid_for(n_rec, 256)), dim3(256), 0, stream, pos,
                        ranges_host ? (int64_t)0 : pos_batch_stride, tri, Npos, T, H, W, rec, rect);
     DR_CHECK_LAUNCH();
   }
-  if (n_items > 0) {
-    DR_TIMED("k_bin_count", stream);
-    hipLaunchKernelGGL(k_bin_count, dim3(grid_for(n_items, 256)), dim3(256), 0, stream, it,
-                       n_items, N, rect, ntx, tiles, cnt);
-    DR_CHECK_LAUNCH();
-  }
-  {
-    DR_TIMED("k_bin_alloc", stream);
-    hipLaunchKernelGGL(k_bin_alloc, dim3(grid_for(n_tiles, 256)), dim3(256), 0, stream, cnt,
-                       n_tiles, off, fillc, total);
-  }
-  DR_CHECK_LAUNCH();
 
-  // List capacity: exact on the first call (one host sync); afterwards the
-  // previous call's total sizes the buffer without waiting, and the raster
-  // kernel falls back to a full scan for any tile that did not fit.
-  int64_t need = 0;
+  // Per-tile list capacity: the largest tile count seen so far plus a
+  // quarter.  The first call counts exactly (one host sync); afterwards the
+  // previous call's largest count, read back asynchronously through pinned
+  // memory, only ever raises it, and a tile that overflows is rasterized by
+  // a full scan, so results never depend on the capacity.
+  auto grow = [](int64_t m) { return (int)std::min<int64_t>(((m + m / 4) + 31) / 32 * 32 + 32, 1 << 30); };
+  int C = sc->bin_cap;
   if (sc->total_pending && hipEventQuery(sc->total_event) == hipSuccess) {
-    need = *sc->pinned_total;
+    const int64_t mx = *sc->pinned_total;
     sc->total_pending = false;
+    if (mx > C) C = grow(mx);
   }
-  if (sc->cap[SLOT_RAST_LIST] == 0) {
-    DR_CHECK_HIP(hipMemcpyAsync(sc->pinned_total, total, sizeof(int64_t), hipMemcpyDeviceToHost,
-                                stream));
+  if (C == 0) {
+    DR_CHECK_HIP(fill_async(cnt, 0, n_tiles, stream));
+    DR_CHECK_HIP(fill_async(tmax, 0, 1, stream));
+    if (n_items > 0) {
+      DR_TIMED("k_bin_count", stream);
+      hipLaunchKernelGGL(k_bin_count, dim3(grid_for(n_items, 256)), dim3(256), 0, stream, it,
+                         n_items, N, rect, ntx, tiles, cnt);
+      DR_CHECK_LAUNCH();
+    }
+    hipLaunchKernelGGL(k_tile_max, dim3(grid_for(n_tiles, 256)), dim3(256), 0, stream, cnt,
+                       n_tiles, tmax);
+    DR_CHECK_LAUNCH();
+    *sc->pinned_total = 0;
+    DR_CHECK_HIP(hipMemcpyAsync(sc->pinned_total, tmax, sizeof(int), hipMemcpyDeviceToHost, stream));
     DR_CHECK_HIP(hipStreamSynchronize(stream));
-    need = *sc->pinned_total;
+    C = grow(*sc->pinned_total);
   }
-  int* list = (int*)scratch_get(sc, stream, SLOT_RAST_LIST, (size_t)(need > 0 ? need : 1) * 4);
+  // at most 256 MiB of lists; a tile above the capacity takes the full scan
+  const int64_t c_budget = std::max<int64_t>(32, ((int64_t)64 << 20) / std::max<int64_t>(n_tiles, 1));
+  C = (int)std::min<int64_t>(C, c_budget);
+  if (C > sc->bin_cap) sc->bin_cap = C;
+  int* list = (int*)scratch_get(sc, stream, SLOT_RAST_LIST, (size_t)n_tiles * C * 4);
   if (!list) return DR_ERR_MEMORY;
-  const int64_t cap = (int64_t)(sc->cap[SLOT_RAST_LIST] / 4);
 
+  DR_CHECK_HIP(fill_async(fillc, 0, n_tiles, stream));
   if (n_items > 0) {
     DR_TIMED("k_bin_fill", stream);
     hipLaunchKernelGGL(k_bin_fill, dim3(grid_for(n_items, 256)), dim3(256), 0, stream, it,
-                       n_items, N, rect, ntx, tiles, off, fillc, list, cap);
+                       n_items, N, rect, ntx, tiles, fillc, list, C);
     DR_CHECK_LAUNCH();
   }
   const dim3 grid((unsigned)n_tiles), block(256);
 #define DR_RASTER(DBV, PV)                                                                    \
   hipLaunchKernelGGL((k_raster<DBV, PV>), grid, block, 0, stream, rec, rect, it, rec_stride, \
-                     cnt, off, list, cap, peel, N, H, W, ntx, nty, rast, rast_db)
+                     fillc, list, C, peel, N, H, W, ntx, nty, rast, rast_db)
   {
     DR_TIMED("k_raster", stream);
     if (rast_db) {
@@ -593,10 +642,17 @@ extern "C" int dr_rasterize_fwd(const float* pos, int64_t pos_batch_stride, cons
   }
 #undef DR_RASTER
   DR_CHECK_LAUNCH();
-  DR_CHECK_HIP(hipMemcpyAsync(sc->pinned_total, total, sizeof(int64_t), hipMemcpyDeviceToHost,
-                              stream));
-  DR_CHECK_HIP(hipEventRecord(sc->total_event, stream));
-  sc->total_pending = true;
+  if (!sc->total_pending) {  // largest count of this call, for the next one
+    DR_CHECK_HIP(fill_async(tmax, 0, 1, stream));
+    hipLaunchKernelGGL(k_tile_max, dim3(grid_for(n_tiles, 256)), dim3(256), 0, stream, fillc,
+                       n_tiles, tmax);
+    DR_CHECK_LAUNCH();
+    *sc->pinned_total = 0;
+    DR_CHECK_HIP(hipMemcpyAsync(sc->pinned_total, tmax, sizeof(int), hipMemcpyDeviceToHost,
+                                stream));
+    DR_CHECK_HIP(hipEventRecord(sc->total_event, stream));
+    sc->total_pending = true;
+  }
   return DR_OK;
 }
 

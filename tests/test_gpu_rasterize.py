@@ -142,3 +142,24 @@ def test_backward(name, gradDB):
     rr = host(r)
     ref = O.rasterize_vjp(pos, tri, rr, g, gdb, ranges=ranges)
     assert_grad_close(host(p.grad), ref, f"d_pos {name}")
+
+
+def test_tile_capacity_overflow():
+    """Per-tile list capacity comes from the largest count seen so far: a
+    fresh scratch sized on a sparse scene, then a tile with 300 candidates,
+    must take the full-scan path and still match; later calls (capacity
+    raised from the read-back count) match too."""
+    torch = torch_dev()
+    from diffrast import _lib
+    torch.cuda.synchronize()
+    assert _lib.load().dr_release_scratch() == 0
+    sc = scenes.tier1_triangle(H=32, W=32)
+    check_fwd(sc["pos"], sc["tri"], 32, 32)
+    T = 300
+    p = np.tile(np.array([[-3, 3, 0, 1], [-3, -3, 0, 1], [3, 0, 0, 1]], np.float32), (T, 1))
+    p[:, 2] = np.repeat(np.linspace(0.9, -0.9, T), 3)
+    tri = np.arange(3 * T, dtype=np.int32).reshape(T, 3)
+    for _ in range(3):
+        r = check_fwd(p[None], tri, 32, 32)
+        assert (r[..., 3] == T).all()
+        torch.cuda.synchronize()
