@@ -672,7 +672,7 @@ __global__ void __launch_bounds__(256) k_tex_bwd(TexBwdArgs A, int total_tiles) 
 // or boxes too large for a window, go to the LDS hash table.
 // ---------------------------------------------------------------------------
 
-constexpr int kWinTexels = 1024;  // texels of the two windows together
+constexpr int kWinTexels = 768;  // texels of the two windows together (~30 KB of LDS with the table)
 constexpr int kWinFallback = 128;
 
 struct TapSlot {
@@ -694,7 +694,9 @@ __device__ __forceinline__ void slot_box(const TapSlot& q, int& x0, int& x1, int
 
 
 template <int FILTER, int CT>
-__global__ void __launch_bounds__(256) k_tex_bwd_win(TexBwdArgs A, int total_tiles) {
+// Five workgroups per CU (the register budget this asks for costs a few
+// spilled values, measured cheaper than four resident workgroups).
+__global__ void __launch_bounds__(256, 5) k_tex_bwd_win(TexBwdArgs A, int total_tiles) {
   __shared__ double win[kWinTexels * CT];
   __shared__ int s_wk[4];          // per wave: lowest level in use
   __shared__ int s_wbox[4][2][4];  // per wave: boxes on that level and the next
