@@ -17,45 +17,113 @@ namespace dr {
 template <int AT>
 __device__ __forceinline__ int dimA(int A) { return AT > 0 ? AT : A; }
 
+// Stores n consecutive floats; two or four at a time when the count and the
+// (16-byte aligned) buffers allow.
+template <int NC>
+__device__ __forceinline__ void st_run(float* __restrict__ p, const float* v, int n) {
+  if constexpr (NC == 2) {
+    *reinterpret_cast<float2*>(p) = make_float2(v[0], v[1]);
+  } else if constexpr (NC == 4) {
+    *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+  } else {
+    for (int i = 0; i < n; ++i) p[i] = v[i];
+  }
+}
+
+constexpr int kInterpPix = 2;  // pixels per thread (more loads in flight)
+
 template <int AT, int KT>
 __global__ void __launch_bounds__(256) k_interp_fwd(
     const float* __restrict__ attr, int64_t attr_stride, const float* __restrict__ rast,
     const float* __restrict__ rast_db, const int32_t* __restrict__ tri,
     const int32_t* __restrict__ diff_idx, int K_, int64_t P, int HW, int A_,
     float* __restrict__ out, float* __restrict__ out_da) {
-  const int64_t pix = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (pix >= P) return;
+  constexpr int NA = AT > 0 ? AT : 8;       // register slots for attributes
+  constexpr int NK = KT > 0 ? 2 * KT : 8;   // and for derivative outputs
   const int A = dimA<AT>(A_);
   const int K = KT > 0 ? KT : K_;
-  const float4 r = *reinterpret_cast<const float4*>(rast + pix * 4);
-  const int t = f2i(r.w) - 1;
-  float* o = out + pix * A;
-  float* od = K > 0 ? out_da + pix * 2 * K : nullptr;
-  if (t < 0) {
-    for (int a = 0; a < A; ++a) o[a] = 0.0f;
-    for (int k = 0; k < 2 * K; ++k) od[k] = 0.0f;
-    return;
+  const int64_t base = (int64_t)blockIdx.x * (256 * kInterpPix) + threadIdx.x;
+  float4 r[kInterpPix];
+  int t[kInterpPix];
+#pragma unroll
+  for (int q = 0; q < kInterpPix; ++q) {
+    const int64_t pix = base + q * 256;
+    r[q] = pix < P ? *reinterpret_cast<const float4*>(rast + pix * 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+    t[q] = pix < P ? f2i(r[q].w) - 1 : -1;
   }
-  const int n = (int)(pix / HW);
-  const float* at = attr + (int64_t)n * attr_stride;
-  const int i0 = tri[t * 3 + 0], i1 = tri[t * 3 + 1], i2 = tri[t * 3 + 2];
-  const float* a0p = at + (int64_t)i0 * A;
-  const float* a1p = at + (int64_t)i1 * A;
-  const float* a2p = at + (int64_t)i2 * A;
-  const float u = r.x, v = r.y;
-  const float bw = 1.0f - u - v;
+  int iv[kInterpPix][3];
 #pragma unroll
-  for (int a = 0; a < A; ++a) o[a] = bw * a0p[a] + u * a1p[a] + v * a2p[a];
-  if (K > 0) {
-    const float4 db = *reinterpret_cast<const float4*>(rast_db + pix * 4);
-#pragma unroll
-    for (int k = 0; k < K; ++k) {
-      const int a = diff_idx ? diff_idx[k] : k;
-      const float d01 = a1p[a] - a0p[a];
-      const float d02 = a2p[a] - a0p[a];
-      od[2 * k + 0] = d01 * db.x + d02 * db.z;
-      od[2 * k + 1] = d01 * db.y + d02 * db.w;
+  for (int q = 0; q < kInterpPix; ++q) {
+    iv[q][0] = iv[q][1] = iv[q][2] = 0;
+    if (t[q] >= 0) {
+      iv[q][0] = tri[t[q] * 3 + 0];
+      iv[q][1] = tri[t[q] * 3 + 1];
+      iv[q][2] = tri[t[q] * 3 + 2];
     }
+  }
+#pragma unroll
+  for (int q = 0; q < kInterpPix; ++q) {
+    const int64_t pix = base + q * 256;
+    if (pix >= P) continue;
+    float* o = out + pix * A;
+    float* od = K > 0 ? out_da + pix * 2 * K : nullptr;
+    if (AT == 0 || KT == 0 && K > 0) {  // any shape: element by element
+      if (t[q] < 0) {
+        for (int a = 0; a < A; ++a) o[a] = 0.0f;
+        for (int k = 0; k < 2 * K; ++k) od[k] = 0.0f;
+        continue;
+      }
+      const float* at = attr + (int64_t)(pix / HW) * attr_stride;
+      const float* a0p = at + (int64_t)iv[q][0] * A;
+      const float* a1p = at + (int64_t)iv[q][1] * A;
+      const float* a2p = at + (int64_t)iv[q][2] * A;
+      const float u = r[q].x, v = r[q].y;
+      const float bw = 1.0f - u - v;
+      for (int a = 0; a < A; ++a) o[a] = bw * a0p[a] + u * a1p[a] + v * a2p[a];
+      if (K > 0) {
+        const float4 db = *reinterpret_cast<const float4*>(rast_db + pix * 4);
+        for (int k = 0; k < K; ++k) {
+          const int a = diff_idx ? diff_idx[k] : k;
+          const float d01 = a1p[a] - a0p[a];
+          const float d02 = a2p[a] - a0p[a];
+          od[2 * k + 0] = d01 * db.x + d02 * db.z;
+          od[2 * k + 1] = d01 * db.y + d02 * db.w;
+        }
+      }
+      continue;
+    }
+    // compile-time shape (identity diff_idx when KT > 0)
+    float ov[NA], odv[NK];
+#pragma unroll
+    for (int a = 0; a < NA; ++a) ov[a] = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NK; ++k) odv[k] = 0.0f;
+    if (t[q] >= 0) {
+      const float* at = attr + (int64_t)(pix / HW) * attr_stride;
+      float a0[NA], a1[NA], a2[NA];
+#pragma unroll
+      for (int a = 0; a < NA; ++a) {
+        a0[a] = at[(int64_t)iv[q][0] * NA + a];
+        a1[a] = at[(int64_t)iv[q][1] * NA + a];
+        a2[a] = at[(int64_t)iv[q][2] * NA + a];
+      }
+      const float u = r[q].x, v = r[q].y;
+      const float bw = 1.0f - u - v;
+#pragma unroll
+      for (int a = 0; a < NA; ++a) ov[a] = bw * a0[a] + u * a1[a] + v * a2[a];
+      if (KT > 0) {
+        const float4 db = *reinterpret_cast<const float4*>(rast_db + pix * 4);
+#pragma unroll
+        for (int k = 0; k < (KT > 0 ? KT : 1); ++k) {
+          const float d01 = a1[k] - a0[k];
+          const float d02 = a2[k] - a0[k];
+          odv[2 * k + 0] = d01 * db.x + d02 * db.z;
+          odv[2 * k + 1] = d01 * db.y + d02 * db.w;
+        }
+      }
+    }
+    st_run<NA>(o, ov, NA);
+    if (KT > 0) st_run<NK>(od, odv, NK);
   }
 }
 
@@ -234,10 +302,16 @@ extern "C" int dr_interpolate_fwd(const float* attr, int64_t attr_batch_stride,
   if (st) return st;
   DR_CHECK_ARG(out && (K == 0 || out_da), "interpolate: null output");
   const int64_t P = (int64_t)N * H * W;
-  const dim3 grid(grid_for(P, 256));
+  const dim3 grid(grid_for(P, 256 * kInterpPix));
   DR_TIMED("k_interp_fwd", stream);
-  DR_INTERP_DISPATCH(k_interp_fwd, grid, attr, attr_batch_stride, rast, rast_db, tri, diff_idx,
-                     K, P, H * W, A, out, out_da);
+  // the compile-time shapes store with 8/16-byte vector writes
+  const bool aligned = (((uintptr_t)out | (uintptr_t)(out_da ? out_da : out)) & 15) == 0;
+  if (!aligned)
+    hipLaunchKernelGGL((k_interp_fwd<0, 0>), grid, dim3(256), 0, stream, attr, attr_batch_stride,
+                       rast, rast_db, tri, diff_idx, K, P, H * W, A, out, out_da);
+  else
+    DR_INTERP_DISPATCH(k_interp_fwd, grid, attr, attr_batch_stride, rast, rast_db, tri, diff_idx,
+                       K, P, H * W, A, out, out_da);
   DR_CHECK_LAUNCH();
   return DR_OK;
 }
