@@ -188,12 +188,11 @@ constexpr int kMaxC = 4;  // register arrays for compile-time C; larger C uses C
 // ---------------------------------------------------------------------------
 
 template <int FILTER, bool CUBE, int CT>
-__global__ void __launch_bounds__(256) k_tex_fwd(
-    const float* __restrict__ tex, const float* __restrict__ pyr, MipDesc md, int64_t tex_stride,
-    int Ht, int Wt, int C_, const float* __restrict__ uv, const float* __restrict__ uv_da,
-    const float* __restrict__ bias_map, float scale_bias, int has_bias, int boundary, int64_t P,
-    int HWi, float* __restrict__ out) {
-  const int64_t pix = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+__device__ __forceinline__ void tex_fwd_px(
+    const float* __restrict__ tex, const float* __restrict__ pyr, const MipDesc& md,
+    int64_t tex_stride, int Ht, int Wt, int C_, const float* __restrict__ uv,
+    const float* __restrict__ uv_da, const float* __restrict__ bias_map, float scale_bias,
+    int has_bias, int boundary, int64_t P, int HWi, float* __restrict__ out, int64_t pix) {
   if (pix >= P) return;
   const int C = dimC<CT>(C_);
   const int n = (int)(pix / HWi);
@@ -253,6 +252,35 @@ __global__ void __launch_bounds__(256) k_tex_fwd(
   if (bias_map || has_bias) da = make_float4(da.x * s, da.y * s, da.z * s, da.w * s);
   const Lod ld = mip_lod(da, Ht, Wt, md.L, FILTER == DR_FILTER_LINEAR_MIPMAP_LINEAR);
   const bool shared = tex_stride == 0;
+  if constexpr (CT > 0) {  // texels as vectors, the sum in registers
+    float acc[CT];
+#pragma unroll
+    for (int li = 0; li < 2; ++li) {
+      const int k = li == 0 ? ld.k0 : ld.k1;
+      const int Hk = mip_h(md, k), Wk = mip_w(md, k);
+      const float* lv = k == 0 ? tex + n * tex_stride
+                               : pyr + mip_off(md, k) + (shared ? 0 : (int64_t)n * Hk * Wk * C);
+      const Bilin b = bilin(uvp.x, uvp.y, Wk, Hk, boundary);
+      const float wgt = li == 0 ? (1.0f - ld.frac) : ld.frac;
+      float t00[kMaxC], t10[kMaxC], t01[kMaxC], t11[kMaxC];
+      load_texel<CT>(lv + ((int64_t)b.iy0 * Wk + b.ix0) * C, C, t00);
+      load_texel<CT>(lv + ((int64_t)b.iy0 * Wk + b.ix1) * C, C, t10);
+      load_texel<CT>(lv + ((int64_t)b.iy1 * Wk + b.ix0) * C, C, t01);
+      load_texel<CT>(lv + ((int64_t)b.iy1 * Wk + b.ix1) * C, C, t11);
+#pragma unroll
+      for (int c = 0; c < CT; ++c) {
+        const float sample = b.w00 * t00[c] + b.w10 * t10[c] + b.w01 * t01[c] + b.w11 * t11[c];
+        acc[c] = li == 0 ? wgt * sample : acc[c] + wgt * sample;  // two roundings, as :855 / :858
+      }
+    }
+    if constexpr (CT == 4) {
+      *reinterpret_cast<float4*>(o) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    } else {
+#pragma unroll
+      for (int c = 0; c < CT; ++c) o[c] = acc[c];
+    }
+    return;
+  }
   for (int li = 0; li < 2; ++li) {
     const int k = li == 0 ? ld.k0 : ld.k1;
     const int Hk = mip_h(md, k), Wk = mip_w(md, k);
@@ -270,6 +298,17 @@ __global__ void __launch_bounds__(256) k_tex_fwd(
       else o[c] = o[c] + wgt * sample;
     }
   }
+}
+
+template <int FILTER, bool CUBE, int CT>
+__global__ void __launch_bounds__(256) k_tex_fwd(
+    const float* __restrict__ tex, const float* __restrict__ pyr, MipDesc md, int64_t tex_stride,
+    int Ht, int Wt, int C_, const float* __restrict__ uv, const float* __restrict__ uv_da,
+    const float* __restrict__ bias_map, float scale_bias, int has_bias, int boundary, int64_t P,
+    int HWi, float* __restrict__ out) {
+  tex_fwd_px<FILTER, CUBE, CT>(tex, pyr, md, tex_stride, Ht, Wt, C_, uv, uv_da, bias_map,
+                               scale_bias, has_bias, boundary, P, HWi, out,
+                               (int64_t)blockIdx.x * blockDim.x + threadIdx.x);
 }
 
 // ---------------------------------------------------------------------------
