@@ -614,8 +614,8 @@ extern "C" int dr_rasterize_fwd(const float* pos, int64_t pos_batch_stride, cons
     DR_CHECK_HIP(hipStreamSynchronize(stream));
     C = grow(*sc->pinned_total);
   }
-  // at most 256 MiB of lists; a tile above the capacity takes the full scan
-  const int64_t c_budget = std::max<int64_t>(32, ((int64_t)64 << 20) / std::max<int64_t>(n_tiles, 1));
+  // at most 1 GiB of lists; a tile above the capacity takes the full scan
+  const int64_t c_budget = std::max<int64_t>(32, ((int64_t)256 << 20) / std::max<int64_t>(n_tiles, 1));
   C = (int)std::min<int64_t>(C, c_budget);
   if (C > sc->bin_cap) sc->bin_cap = C;
   int* list = (int*)scratch_get(sc, stream, SLOT_RAST_LIST, (size_t)n_tiles * C * 4);
