@@ -62,7 +62,8 @@ def gpu_run(sc, steps, warmup):
     target = dev(sc["target"])
     topo = DiffRast.antialiasConstructTopologyHash(tri)
 
-    inv_n = 1.0 / float(target.numel())
+    lib = _lib.load()
+    loss = torch.empty((), device="cuda", dtype=torch.float32)
 
     def step():
         for t in (pos, attr, tex):
@@ -72,11 +73,12 @@ def gpu_run(sc, steps, warmup):
         col = DiffRast.texture(tex, uv, uvDA=uv_da, filterMode="linear-mipmap-linear",
                                boundaryMode="clamp")
         out = DiffRast.antialias(col, rast, pos, tri, topologyHash=topo)
-        # MSE loss and its gradient 2/n (out - target) in three elementwise /
-        # reduction kernels
-        diff = (out.detach() - target).view(-1)
-        loss = torch.dot(diff, diff) * inv_n
-        out.backward(diff.mul_(2.0 * inv_n).view_as(out))
+        # MSE loss and its gradient 2/n (out - target) in one pass
+        d_out = torch.empty_like(out)
+        _lib.check(lib.dr_mse_loss(out.data_ptr(), target.data_ptr(), out.numel(),
+                                   loss.data_ptr(), d_out.data_ptr(),
+                                   torch.cuda.current_stream().cuda_stream))
+        out.backward(d_out)
         return loss
 
     prof = _lib.load()

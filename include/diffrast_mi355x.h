@@ -18,6 +18,12 @@
  *   dr_antialias_fwd     Antialias.swift:112-117  (:556-568)
  *   dr_antialias_bwd     Antialias.swift:118-128  (:570-600)
  *
+ * and the loss and optimizer step of the reference's inverse-rendering
+ * samples (Sources/{ColorFit,PoseFit,MeshFit}Example, MLXDiffRastExamples/Adam.swift):
+ *
+ *   dr_mse_loss          ColorFitExample/main.swift:62-66 and its gradient
+ *   dr_adam_step         Adam.swift:36-43
+ *
  * Conventions
  *   - All tensors are device memory (hipMalloc'd), fp32 or int32, row-major,
  *     channels last, in the reference's layouts:
@@ -191,6 +197,28 @@ int dr_antialias_bwd(const float* color, const float* rast, const float* pos,
                      const int32_t* tri, const int32_t* topo, const float* d_out, int N, int H,
                      int W, int C, int V, int T, float* d_color, float* d_pos, unsigned flags,
                      dr_stream_t stream);
+
+/* ---- loss and optimizer of the inverse-rendering samples -------------- */
+
+/* MSE loss of the samples' `lossFn`, `((out - target)^2).mean()`
+ * (ColorFitExample/main.swift:62-66, PoseFitExample/main.swift:93-97,
+ * MeshFitExample/main.swift:87-91), and its gradient.
+ *   loss: one device float; the squares are summed in fp64 in a fixed order
+ *     (the same loss on every call), then loss = (float)sum * (1/n).
+ *   d_out: NULL, or [n]: d loss / d out = 2 * ((out - target) * (1/n)),
+ *     overwritten. */
+int dr_mse_loss(const float* out, const float* target, int64_t n, float* loss, float* d_out,
+                dr_stream_t stream);
+
+/* One step of the samples' Adam (MLXDiffRastExamples/Adam.swift:36-43):
+ *   g = grad (* grad_mask if given);  m = b1*m + (1-b1)*g;
+ *   v = b2*v + (1-b2)*g*g;  param_out = param - lr*(m/c1)/(sqrt(v/c2)+eps),
+ * with c = 1 - beta^step (step counts from 1), each operation rounded to
+ * fp32 in that order.  m and v are updated in place; param_out may be
+ * param. */
+int dr_adam_step(const float* param, const float* grad, const float* grad_mask, float* m,
+                 float* v, float* param_out, int64_t n, int step, float lr, float beta1,
+                 float beta2, float eps, dr_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -41,6 +41,8 @@ SIGNATURES = {
     "dr_antialias_topology": ([_p, _i, _p, _p], _i),
     "dr_antialias_fwd": ([_p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p, _p], _i),
     "dr_antialias_bwd": ([_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p, _p, _u, _p], _i),
+    "dr_mse_loss": ([_p, _p, _i64, _p, _p, _p], _i),
+    "dr_adam_step": ([_p, _p, _p, _p, _p, _p, _i64, _i, _f, _f, _f, _f, _p], _i),
 }
 
 DR_OK, DR_ERR_ARGUMENT, DR_ERR_HIP, DR_ERR_MEMORY = 0, 1, 2, 3

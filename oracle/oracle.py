@@ -517,3 +517,59 @@ def antialias_vjp(color, rast, pos, tri, d_out, topologyHash=None):
     L.orc_aa_bwd_pos(fp(color), fp(rast), fp(pos), ip(tri), ip(topo), fp(g), N, H, W, C, V,
                      fp(d_pos))
     return d_color, d_pos
+
+
+# ---------------------------------------------------------------------------
+# loss and optimizer of the inverse-rendering samples
+# ---------------------------------------------------------------------------
+
+def mse_loss(out, target):
+    """The samples' `lossFn` (ColorFitExample/main.swift:62-66): mean of
+    the fp32 squares of (out - target), summed in float64 here.  Returns
+    (loss, d_out) with d_out the gradient MLX autodiff forms for it:
+    g = (out - target) * (1/n) in fp32, then g + g (the product rule of
+    diff * diff)."""
+    o = c32(out).ravel()
+    t = c32(target).ravel()
+    n = o.size
+    d = (o - t).astype(np.float32)
+    sq = (d * d).astype(np.float32)
+    inv_n = np.float32(1.0) / np.float32(n)
+    loss = np.float32(np.float32(sq.astype(np.float64).sum()) * inv_n)
+    g = (d * inv_n).astype(np.float32)
+    return loss, (g + g).astype(np.float32).reshape(np.shape(out))
+
+
+def _pow_f32(b, t):
+    """b**t (b fp32, t a positive integer) correctly rounded to fp32: the
+    exact rational power, rounded to the nearest fp32 (ties to even)."""
+    from fractions import Fraction
+    exact = Fraction(float(b)) ** int(t)
+    x = np.float32(float(exact))
+    best = None
+    for c in (np.nextafter(x, np.float32(-np.inf)), x, np.nextafter(x, np.float32(np.inf))):
+        err = abs(Fraction(float(c)) - exact)
+        key = (err, int(np.frombuffer(np.float32(c).tobytes(), np.uint32)[0]) & 1)
+        if best is None or key < best[0]:
+            best = (key, c)
+    return np.float32(best[1])
+
+
+def adam_step(param, grad, m, v, t, lr=1e-2, beta1=0.9, beta2=0.999, eps=1e-8, mask=None):
+    """One step of `Adam.step` (MLXDiffRastExamples/Adam.swift:36-43) in
+    fp32, each operation rounded in the order written there.  t is the step
+    count after the increment (1 on the first call).  Returns
+    (new_param, new_m, new_v)."""
+    f = np.float32
+    g = c32(grad)
+    if mask is not None:
+        g = (g * c32(mask)).astype(f)
+    b1, b2, lr, eps = f(beta1), f(beta2), f(lr), f(eps)
+    m = (b1 * c32(m) + (f(1) - b1) * g).astype(f)
+    v = (b2 * c32(v) + (f(1) - b2) * (g * g)).astype(f)
+    c1 = f(1) - _pow_f32(b1, t)
+    c2 = f(1) - _pow_f32(b2, t)
+    m_hat = (m / c1).astype(f)
+    v_hat = (v / c2).astype(f)
+    p = (c32(param) - lr * m_hat / (np.sqrt(v_hat) + eps)).astype(f)
+    return p, m, v
