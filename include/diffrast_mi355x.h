@@ -111,6 +111,18 @@ int dr_rasterize_fwd(const float* pos, int64_t pos_batch_stride, const int32_t* 
                      const int32_t* ranges_host, const float* peel, int N, int V, int T,
                      int H, int W, float* rast, float* rast_db, dr_stream_t stream);
 
+/* Binning report (no counterpart call in the reference; it exposes the
+ * reference's bin counts, Rasterize.swift:227-239).  counts [N, ceil(H/16),
+ * ceil(W/16)] (device int32) receives, per 16x16 tile, the number of drawn
+ * triangles with nonzero area whose clamped pixel bounding box touches it:
+ * the reference's bins[tile, 0].  Tiles above 128 are where the reference
+ * drops triangles (MAX_PER_TILE, Rasterize.swift:164-171); this library does
+ * not.  max_count_host: NULL, or receives the largest count (this waits for
+ * the stream).  Arguments as dr_rasterize_fwd. */
+int dr_rasterize_tile_counts(const float* pos, int64_t pos_batch_stride, const int32_t* tri,
+                             const int32_t* ranges_host, int N, int V, int T, int H, int W,
+                             int32_t* counts, int64_t* max_count_host, dr_stream_t stream);
+
 /* VJP of DiffRast.rasterize: d_pos (same layout and batch stride as pos;
  * range mode accumulates all images into the shared [V,4]).  d_rast_db may
  * be NULL (gradDB = false). */

@@ -47,7 +47,8 @@ enum Slot {
   SLOT_RAST_ITEMS,    // range-mode item prefix
   SLOT_TOPO,          // edge hash table
   SLOT_DPYR,          // mip pyramid gradient
-  SLOT_SMALL,         // small device-side partial sums (loss)
+  SLOT_SMALL,         // small device-side counters
+  SLOT_LOSS,          // partial sums of the loss
   SLOT_AA_REC,        // per (image, triangle) silhouette records (antialias)
   SLOT_COUNT
 };

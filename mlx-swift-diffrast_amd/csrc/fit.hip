@@ -116,7 +116,7 @@ extern "C" int dr_mse_loss(const float* out, const float* target, int64_t n, flo
   DR_CHECK_ARG(out && target && loss, "mse_loss: null tensor");
   Scratch* sc = scratch_for(stream);
   if (!sc) return DR_ERR_MEMORY;
-  double* partial = (double*)scratch_get(sc, stream, SLOT_SMALL, kMseBlocks * sizeof(double));
+  double* partial = (double*)scratch_get(sc, stream, SLOT_LOSS, kMseBlocks * sizeof(double));
   if (!partial) return DR_ERR_MEMORY;
   const float inv_n = 1.0f / (float)n;
   const bool vec =

@@ -510,61 +510,120 @@ __global__ void __launch_bounds__(256) k_raster_bwd(
 
 using namespace dr;
 
-namespace {
+// The (image, triangle) items a call draws: every (n, t) in instanced mode;
+// in range mode, each image's clamped range, listed through a prefix sum
+// that is copied to the device (synchronously: the host vector is local).
+static int plan_items(Scratch* sc, hipStream_t stream, const int32_t* ranges_host, int N, int T,
+                      Items& it, int64_t& n_items) {
+  it = Items{nullptr, nullptr, T};
+  n_items = (int64_t)N * T;
+  if (!ranges_host) return DR_OK;
+  std::vector<int64_t> h(2 * (size_t)N + 1);
+  h[0] = 0;
+  for (int n = 0; n < N; ++n) {
+    int64_t s = ranges_host[2 * n], c = ranges_host[2 * n + 1];
+    int64_t lo = s < 0 ? 0 : s, hi = s + c > T ? T : s + c;
+    if (hi < lo) hi = lo;
+    h[n + 1] = h[n] + (hi - lo);
+    h[N + 1 + n] = lo;
+  }
+  n_items = h[N];
+  int64_t* d = (int64_t*)scratch_get(sc, stream, SLOT_RAST_ITEMS, h.size() * sizeof(int64_t));
+  if (!d) return DR_ERR_MEMORY;
+  DR_CHECK_HIP(hipMemcpyAsync(d, h.data(), h.size() * sizeof(int64_t), hipMemcpyHostToDevice,
+                              stream));
+  DR_CHECK_HIP(hipStreamSynchronize(stream));
+  it.prefix = d;
+  it.start = d + N + 1;
+  return DR_OK;
+}
 
-struct RangePlan {
+static int check_raster_args(const float* pos, int64_t pos_batch_stride, const int32_t* tri,
+                             const int32_t* ranges_host, int N, int V, int T, int H, int W) {
+  DR_CHECK_ARG(N >= 1 && V >= 0 && T >= 0 && H >= 1 && W >= 1, "rasterize: bad sizes");
+  DR_CHECK_ARG(pos && tri, "rasterize: null tensor");
+  DR_CHECK_ARG(ranges_host != nullptr || pos_batch_stride == (int64_t)V * 4,
+               "rasterize: instanced pos needs pos_batch_stride = V*4");
+  DR_CHECK_ARG(ranges_host == nullptr || pos_batch_stride == 0,
+               "rasterize: range mode needs a shared pos (pos_batch_stride = 0)");
+  DR_CHECK_ARG((int64_t)N * T < (int64_t)1 << 40, "rasterize: too many triangles");
+  const int64_t n_tiles =
+      (int64_t)N * ((W + kTile - 1) / kTile) * (int64_t)((H + kTile - 1) / kTile);
+  DR_CHECK_ARG(n_tiles < (int64_t)1 << 31, "rasterize: too many tiles");
+  return DR_OK;
+}
+
+extern "C" int dr_rasterize_tile_counts(const float* pos, int64_t pos_batch_stride,
+                                        const int32_t* tri, const int32_t* ranges_host, int N,
+                                        int V, int T, int H, int W, int32_t* counts,
+                                        int64_t* max_count_host, dr_stream_t stream_) {
+  hipStream_t stream = (hipStream_t)stream_;
+  int st = check_raster_args(pos, pos_batch_stride, tri, ranges_host, N, V, T, H, W);
+  if (st) return st;
+  DR_CHECK_ARG(counts, "rasterize_tile_counts: null counts");
+  Scratch* sc = scratch_for(stream);
+  if (!sc) return DR_ERR_HIP;
+  const int ntx = (W + kTile - 1) / kTile, nty = (H + kTile - 1) / kTile;
+  const int tiles = ntx * nty;
+  const int64_t n_tiles = (int64_t)N * tiles;
+  Items it;
   int64_t n_items = 0;
-  bool range_mode = false;
-  std::vector<int64_t> host;  // prefix [N+1] then start [N]
-};
-
-}  // namespace
+  st = plan_items(sc, stream, ranges_host, N, T, it, n_items);
+  if (st) return st;
+  const int Npos = ranges_host ? 1 : N;
+  const int64_t n_rec = (int64_t)Npos * T;
+  TriRec* rec = (TriRec*)scratch_get(sc, stream, SLOT_RAST_REC, (size_t)n_rec * sizeof(TriRec));
+  int4* rect = (int4*)scratch_get(sc, stream, SLOT_RAST_RECT, (size_t)n_rec * sizeof(int4));
+  int* small = (int*)scratch_get(sc, stream, SLOT_SMALL, 64);
+  if (!rec || !rect || !small) return DR_ERR_MEMORY;
+  if (n_rec > 0) {
+    DR_TIMED("k_setup", stream);
+    hipLaunchKernelGGL(k_setup, dim3(grid_for(n_rec, 256)), dim3(256), 0, stream, pos,
+                       ranges_host ? (int64_t)0 : pos_batch_stride, tri, Npos, T, H, W, rec, rect);
+    DR_CHECK_LAUNCH();
+  }
+  DR_CHECK_HIP(fill_async(counts, 0, n_tiles, stream));
+  if (n_items > 0) {
+    DR_TIMED("k_bin_count", stream);
+    hipLaunchKernelGGL(k_bin_count, dim3(grid_for(n_items, 256)), dim3(256), 0, stream, it,
+                       n_items, N, rect, ntx, tiles, (int*)counts);
+    DR_CHECK_LAUNCH();
+  }
+  if (max_count_host) {
+    int* tmax = small + 8;  // apart from the forward's read-back counter
+    DR_CHECK_HIP(fill_async(tmax, 0, 1, stream));
+    hipLaunchKernelGGL(k_tile_max, dim3(grid_for(n_tiles, 256)), dim3(256), 0, stream,
+                       (const int*)counts, n_tiles, tmax);
+    DR_CHECK_LAUNCH();
+    int mx = 0;
+    DR_CHECK_HIP(hipMemcpyAsync(&mx, tmax, sizeof(int), hipMemcpyDeviceToHost, stream));
+    DR_CHECK_HIP(hipStreamSynchronize(stream));
+    *max_count_host = mx;
+  }
+  return DR_OK;
+}
 
 extern "C" int dr_rasterize_fwd(const float* pos, int64_t pos_batch_stride, const int32_t* tri,
                                 const int32_t* ranges_host, const float* peel, int N, int V,
                                 int T, int H, int W, float* rast, float* rast_db,
                                 dr_stream_t stream_) {
   hipStream_t stream = (hipStream_t)stream_;
-  DR_CHECK_ARG(N >= 1 && V >= 0 && T >= 0 && H >= 1 && W >= 1, "rasterize: bad sizes");
-  DR_CHECK_ARG(pos && tri && rast, "rasterize: null tensor");
-  DR_CHECK_ARG(ranges_host != nullptr || pos_batch_stride == (int64_t)V * 4,
-               "rasterize: instanced pos needs pos_batch_stride = V*4");
-  DR_CHECK_ARG(ranges_host == nullptr || pos_batch_stride == 0,
-               "rasterize: range mode needs a shared pos (pos_batch_stride = 0)");
-  DR_CHECK_ARG((int64_t)N * T < (int64_t)1 << 40, "rasterize: too many triangles");
+  int st = check_raster_args(pos, pos_batch_stride, tri, ranges_host, N, V, T, H, W);
+  if (st) return st;
+  DR_CHECK_ARG(rast, "rasterize: null tensor");
   Scratch* sc = scratch_for(stream);
   if (!sc) return DR_ERR_HIP;
 
   const int ntx = (W + kTile - 1) / kTile, nty = (H + kTile - 1) / kTile;
   const int tiles = ntx * nty;
   const int64_t n_tiles = (int64_t)N * tiles;
-  DR_CHECK_ARG(n_tiles < (int64_t)1 << 31, "rasterize: too many tiles");
 
   // Items: which (image, triangle) pairs are drawn.
-  Items it{nullptr, nullptr, T};
-  int Npos = N;
-  int64_t n_items = (int64_t)N * T;
-  if (ranges_host) {
-    Npos = 1;
-    std::vector<int64_t> h(2 * (size_t)N + 1);
-    h[0] = 0;
-    for (int n = 0; n < N; ++n) {
-      int64_t s = ranges_host[2 * n], c = ranges_host[2 * n + 1];
-      int64_t lo = s < 0 ? 0 : s, hi = s + c > T ? T : s + c;
-      if (hi < lo) hi = lo;
-      h[n + 1] = h[n] + (hi - lo);
-      h[N + 1 + n] = lo;
-    }
-    n_items = h[N];
-    int64_t* d = (int64_t*)scratch_get(sc, stream, SLOT_RAST_ITEMS, h.size() * sizeof(int64_t));
-    if (!d) return DR_ERR_MEMORY;
-    // Synchronous copy: the host vector dies at the end of this call.
-    DR_CHECK_HIP(hipMemcpyAsync(d, h.data(), h.size() * sizeof(int64_t), hipMemcpyHostToDevice,
-                                stream));
-    DR_CHECK_HIP(hipStreamSynchronize(stream));
-    it.prefix = d;
-    it.start = d + N + 1;
-  }
+  Items it;
+  int64_t n_items = 0;
+  st = plan_items(sc, stream, ranges_host, N, T, it, n_items);
+  if (st) return st;
+  const int Npos = ranges_host ? 1 : N;
   const int64_t n_rec = (int64_t)Npos * T;
   const int64_t rec_stride = ranges_host ? 0 : T;
 

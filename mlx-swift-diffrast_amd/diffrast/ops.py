@@ -172,9 +172,44 @@ class _InterpolateFn(torch.autograd.Function):
 # texture (Texture.swift:62-327)
 # ---------------------------------------------------------------------------
 
+def _packed_pyramid(levels, tex):
+    """(L, packed levels 1..L-1) of a `textureConstructMip` list: its levels
+    are views of one buffer in the library's packing, used as they are; any
+    other list of [Nt, Hk, Wk, C] levels is packed by a copy."""
+    levels = list(levels)
+    if not levels:
+        raise ValueError("texture: mip must hold at least level 0")
+    Nt, H, W, C = tex.shape
+    if tuple(levels[0].shape) != (Nt, H, W, C):
+        raise ValueError(f"texture: mip[0] must be the texture's shape {[Nt, H, W, C]}")
+    h, w = H, W
+    for k, lv in enumerate(levels[1:], 1):
+        h, w = h // 2, w // 2
+        if tuple(lv.shape) != (Nt, h, w, C) or not lv.is_cuda:
+            raise ValueError(f"texture: mip[{k}] must be [{Nt}, {h}, {w}, {C}] on the device "
+                             f"(got {list(lv.shape)})")
+    L = len(levels)
+    if L > 1 and h < 1:
+        raise ValueError("texture: mip has more levels than the texture allows")
+    if L == 1:
+        return 1, torch.empty(1, device=tex.device, dtype=torch.float32)
+    first = levels[1]
+    packed = all(lv.dtype == torch.float32 and lv.is_contiguous() for lv in levels[1:])
+    off = 0
+    for lv in levels[1:]:
+        if not packed or lv.data_ptr() != first.data_ptr() + 4 * off:
+            packed = False
+            break
+        off += lv.numel()
+    if packed:
+        n = sum(lv.numel() for lv in levels[1:])
+        return L, first.reshape(-1).as_strided((n,), (1,))
+    return L, torch.cat([lv.detach().to(torch.float32).reshape(-1) for lv in levels[1:]])
+
+
 class _TextureFn(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, tex, uv, uv_da, bias_map, filt, boundary, bias):
+    def forward(ctx, tex, uv, uv_da, bias_map, filt, boundary, bias, cached):
         lib = _lib.load()
         cube = boundary == BoundaryMode.cube
         N, Hi, Wi = uv.shape[0], uv.shape[1], uv.shape[2]
@@ -183,7 +218,9 @@ class _TextureFn(torch.autograd.Function):
             (tex.shape[1], tex.shape[2], tex.shape[3])
         mip = (not cube) and filt >= FilterMode.linearMipmapNearest
         L, pyr = 1, None
-        if mip:
+        if mip and cached is not None:
+            L, pyr = cached
+        elif mip:
             L = lib.dr_texture_mip_levels(Ht, Wt, -1, None, None)
             size = lib.dr_texture_mip_size(Nt, Ht, Wt, C, L)
             pyr = torch.empty(max(size, 1), device=tex.device, dtype=torch.float32)
@@ -214,7 +251,7 @@ class _TextureFn(torch.autograd.Function):
             _ptr(d_uv_da), _ptr(d_bias), 0, _stream()))
         if d_uv_da is None and uv_da is not None and ctx.needs_input_grad[2]:
             d_uv_da = torch.zeros_like(uv_da)
-        return d_tex, d_uv, d_uv_da, d_bias, None, None, None
+        return d_tex, d_uv, d_uv_da, d_bias, None, None, None, None
 
 
 # ---------------------------------------------------------------------------
@@ -295,6 +332,42 @@ class DiffRast:
         return _RasterizeFn.apply(posf.contiguous(), tri32, ranges_host, peel, H, W, bool(gradDB))
 
     @staticmethod
+    def rasterizeTileCounts(pos: torch.Tensor, tri, resolution: Tuple[int, int],
+                            ranges=None) -> torch.Tensor:
+        """Binning report: per 16x16 tile, the number of triangles binned to
+        it, [N, ceil(H/16), ceil(W/16)] int32 -- the reference's bin counts
+        (Rasterize.swift:227-239).  Tiles above 128 are those where the
+        reference drops triangles (MAX_PER_TILE, :164-171); rasterize here
+        keeps them all.  Same layouts as `rasterize`."""
+        H, W = int(resolution[0]), int(resolution[1])
+        posf = _dev_f32(pos.detach() if isinstance(pos, torch.Tensor) else pos,
+                        "rasterizeTileCounts: pos")
+        tri32 = _dev_i32(tri, "tri", posf.device)
+        if tri32.ndim != 2 or tri32.shape[1] != 3:
+            raise ValueError(f"rasterizeTileCounts: tri must be [T, 3] (got {list(tri32.shape)})")
+        rng = None
+        if ranges is not None:
+            if posf.ndim != 2 or posf.shape[1] != 4:
+                raise ValueError("rasterizeTileCounts: with `ranges`, pos must be [V, 4]")
+            r = ranges.detach().cpu() if isinstance(ranges, torch.Tensor) else torch.as_tensor(ranges)
+            rng = r.to(torch.int32).contiguous().numpy()
+            if rng.ndim != 2 or rng.shape[1] != 2:
+                raise ValueError("rasterizeTileCounts: ranges must be [N, 2]")
+            N, V = rng.shape[0], posf.shape[0]
+        else:
+            if posf.ndim != 3 or posf.shape[2] != 4:
+                raise ValueError("rasterizeTileCounts: pos must be [N, V, 4]")
+            N, V = posf.shape[0], posf.shape[1]
+        lib = _lib.load()
+        counts = torch.empty((N, (H + 15) // 16, (W + 15) // 16), device=posf.device,
+                             dtype=torch.int32)
+        _lib.check(lib.dr_rasterize_tile_counts(
+            _ptr(posf), 0 if rng is not None else V * 4, _ptr(tri32),
+            rng.ctypes.data_as(ctypes.c_void_p) if rng is not None else None, N, V,
+            tri32.shape[0], H, W, _ptr(counts), None, _stream()))
+        return counts
+
+    @staticmethod
     def interpolate(attr: torch.Tensor, rast: torch.Tensor, tri, rastDB=None,
                     diffAttrs: Union[None, DiffAttrs, str, Sequence[int]] = None
                     ) -> Tuple[torch.Tensor, torch.Tensor]:
@@ -346,9 +419,17 @@ class DiffRast:
     def texture(tex: torch.Tensor, uv: torch.Tensor, uvDA: Optional[torch.Tensor] = None,
                 filterMode: Union[FilterMode, str] = FilterMode.linear,
                 boundaryMode: Union[BoundaryMode, str] = BoundaryMode.wrap,
-                mipLevelBias: float = 0.0, mipLevelBiasMap: Optional[torch.Tensor] = None
-                ) -> torch.Tensor:
-        """Texture.swift:62-131."""
+                mipLevelBias: float = 0.0, mipLevelBiasMap: Optional[torch.Tensor] = None,
+                mip: Optional[Sequence[torch.Tensor]] = None) -> torch.Tensor:
+        """Texture.swift:62-131.
+
+        `mip` (mip filters only; no counterpart argument in the reference):
+        a pyramid `[tex, level1, ...]` from `textureConstructMip(tex)`, kept
+        across calls with the same texture so it is not rebuilt
+        (Texture.swift:141-143 suggests such caching).  Its levels are read
+        as given (fewer levels cap the LOD); the gradient still flows to
+        `tex` through the 2x2 box backward, as for a pyramid built in the
+        call."""
         filt = FilterMode(_FILTER_NAMES[filterMode] if isinstance(filterMode, str) else filterMode)
         bnd = BoundaryMode(_BOUNDARY_NAMES[boundaryMode] if isinstance(boundaryMode, str)
                            else boundaryMode)
@@ -366,7 +447,7 @@ class DiffRast:
                                  f"(got {list(uvf.shape)})")
             if texf.shape[0] not in (1, uvf.shape[0]):
                 raise ValueError("texture: tex batch dim incompatible with uv batch")
-            return _TextureFn.apply(texf, uvf, None, None, filt, bnd, 0.0)
+            return _TextureFn.apply(texf, uvf, None, None, filt, bnd, 0.0, None)
         if texf.ndim != 4:
             raise ValueError(f"texture: tex must be [N, H_tex, W_tex, C] (got {list(texf.shape)})")
         if uvf.ndim != 4 or uvf.shape[3] != 2:
@@ -375,7 +456,7 @@ class DiffRast:
             raise ValueError(f"texture: tex batch dim {texf.shape[0]} incompatible with uv batch "
                              f"{uvf.shape[0]}")
         if filt in (FilterMode.nearest, FilterMode.linear):
-            return _TextureFn.apply(texf, uvf, None, None, filt, bnd, 0.0)
+            return _TextureFn.apply(texf, uvf, None, None, filt, bnd, 0.0, None)
         if uvDA is None:
             raise ValueError("texture: mipmap filterModes require uvDA")
         if tuple(uvDA.shape) != tuple(uvf.shape[:3]) + (4,):
@@ -388,8 +469,9 @@ class DiffRast:
                 raise ValueError("texture: mipLevelBiasMap must be [N, H_img, W_img] or "
                                  f"[N, H_img, W_img, 1] (got {list(mipLevelBiasMap.shape)})")
             bm = mipLevelBiasMap.to(torch.float32).contiguous()
+        cached = None if mip is None else _packed_pyramid(mip, texf)
         return _TextureFn.apply(texf, uvf, uvDA.to(torch.float32).contiguous(), bm, filt, bnd,
-                                float(mipLevelBias))
+                                float(mipLevelBias), cached)
 
     @staticmethod
     def textureConstructMip(tex: torch.Tensor, maxLevel: Optional[int] = None) -> List[torch.Tensor]:

@@ -188,6 +188,21 @@ def rasterize(pos, tri, resolution, gradDB=True, ranges=None, peelLayer=None,
     return rast, rast_db
 
 
+def rasterize_tile_counts(pos, tri, resolution, ranges=None):
+    """The reference's bin counts bins[tile, 0] (Rasterize.swift:182-240,
+    after the precompute :280-328) as [N, ceil(H/16), ceil(W/16)] int32."""
+    H, W = resolution
+    pos_n, tri, ranges, N, V, T = _raster_layout(pos, tri, ranges)
+    L = lib()
+    screen = np.empty((N, T, 10), np.float32)
+    L.orc_rast_precompute(fp(pos_n), V * 4, ip(tri), ip(ranges), N, V, T, fp(screen))
+    ntx = (W + TILE_SIZE - 1) // TILE_SIZE
+    nty = (H + TILE_SIZE - 1) // TILE_SIZE
+    counts = np.zeros((N, nty * ntx), np.int32)
+    L.orc_rast_bin_count(fp(screen), N, T, H, W, ip(counts))
+    return counts.reshape(N, nty, ntx)
+
+
 def rasterize_vjp(pos, tri, rast, d_rast, d_rast_db=None, ranges=None):
     """VJP closure (Rasterize.swift:109-118, 129-139) -> d_pos, shaped like pos.
 

@@ -78,6 +78,51 @@ def test_deep_tile_beyond_128():
     assert (r[..., 3] == T).all()
 
 
+def tile_counts(pos, tri, H, W, ranges=None):
+    torch = torch_dev()
+    from diffrast import DiffRast
+    got = host(DiffRast.rasterizeTileCounts(
+        dev(pos), dev(tri), (H, W), ranges=None if ranges is None else torch.as_tensor(ranges)))
+    ref = O.rasterize_tile_counts(pos, tri, (H, W), ranges=ranges)
+    np.testing.assert_array_equal(got, ref)
+    return got
+
+
+def test_tile_counts():
+    # the reference's bins[tile, 0], bit-exact: random (some behind the
+    # camera, some degenerate), a tile past the reference's 128, range mode
+    rng = np.random.default_rng(7)
+    T = 400
+    xyz = rng.uniform(-1.3, 1.3, size=(2, 3 * T, 3)).astype(np.float32)
+    w = rng.uniform(0.4, 1.6, size=(2, 3 * T, 1)).astype(np.float32)
+    w[0, :5] = -0.5
+    xyz[1, 30:33] = xyz[1, 30]       # zero area
+    pos = np.concatenate([xyz * w, w], 2)
+    tri = np.arange(3 * T, dtype=np.int32).reshape(T, 3)
+    c = tile_counts(pos, tri, 61, 45)
+    assert c.shape == (2, 4, 3)
+    T2 = 300
+    p = np.tile(np.array([[-3, 3, 0, 1], [-3, -3, 0, 1], [3, 0, 0, 1]], np.float32), (T2, 1))
+    tri2 = np.arange(3 * T2, dtype=np.int32).reshape(T2, 3)
+    c = tile_counts(p[None], tri2, 40, 40)
+    assert (c == T2).all() and c.max() > 128      # every tile past the reference's limit
+    sc = scenes.range_batch(N=24, T_per=40)
+    tile_counts(sc["pos"], sc["tri"], 48, 40, ranges=sc["ranges"])
+    tile_counts(sc["pos"], sc["tri"], 33, 35,
+                ranges=np.array([[0, 80], [30, 20], [900, 5000], [5, 0]], np.int32))
+    from diffrast import _lib
+    lib = _lib.load()
+    import ctypes
+    torch = torch_dev()
+    pd, td = dev(p[None]), dev(tri2)
+    out = torch.empty((1, 3, 3), dtype=torch.int32, device="cuda")
+    mx = ctypes.c_int64(-1)
+    _lib.check(lib.dr_rasterize_tile_counts(pd.data_ptr(), 3 * T2 * 4, td.data_ptr(), None, 1,
+                                            3 * T2, T2, 40, 40, out.data_ptr(), ctypes.byref(mx),
+                                            torch.cuda.current_stream().cuda_stream))
+    assert mx.value == T2
+
+
 def test_range_mode():
     sc = scenes.range_batch(N=24, T_per=40)
     r = check_fwd(sc["pos"], sc["tri"], 48, 40, ranges=sc["ranges"])

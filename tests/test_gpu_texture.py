@@ -166,3 +166,53 @@ def test_smooth_lod_ramp(filt, bnd):
     assert_grad_close(host(uu.grad), d_uv, "d_uv")
     if mip:
         assert_grad_close(host(d.grad), d_da, "d_uvDA", rtol=1e-3)
+
+
+def test_cached_pyramid():
+    # texture(..., mip=textureConstructMip(tex)) reuses the pyramid: the same
+    # outputs and gradients as a pyramid built in the call, and a copied
+    # (unpacked) list gives the same again
+    torch = torch_dev()
+    from diffrast import DiffRast
+    rng = np.random.default_rng(11)
+    tex, uv, da = inputs(rng, 2, 1, 64, 32, 4, 29, 31)
+    outs = []
+    for mode in ("built", "cached", "copied"):
+        t = dev(tex).requires_grad_(True)
+        u = dev(uv).requires_grad_(True)
+        d = dev(da).requires_grad_(True)
+        mip = None
+        if mode != "built":
+            mip = DiffRast.textureConstructMip(t.detach())
+            if mode == "copied":
+                mip = [lv.clone() for lv in mip]
+        out = DiffRast.texture(t, u, uvDA=d, filterMode="linear-mipmap-linear",
+                               boundaryMode="clamp", mip=mip)
+        g = dev(np.linspace(-1, 1, out.numel(), dtype=np.float32).reshape(out.shape))
+        (out * g).sum().backward()
+        outs.append([host(x) for x in (out, t.grad, u.grad, d.grad)])
+    for k in (1, 2):
+        np.testing.assert_array_equal(outs[k][0], outs[0][0])
+        for a, b in zip(outs[k][1:], outs[0][1:]):
+            assert_grad_close(a, b)
+
+
+def test_cached_pyramid_fewer_levels():
+    # a pyramid of 4 levels caps the LOD at 3: a large footprint samples the
+    # 8x8 box means of level 3 (at texel centres, exactly one texel)
+    torch = torch_dev()
+    from diffrast import DiffRast
+    rng = np.random.default_rng(12)
+    tex = rng.random((1, 32, 32, 3)).astype(np.float32)
+    mip = DiffRast.textureConstructMip(dev(tex), maxLevel=3)
+    assert len(mip) == 4
+    iy, ix = np.meshgrid(np.arange(4), np.arange(4), indexing="ij")
+    uv = np.stack([(ix + 0.5) / 4, (iy + 0.5) / 4], -1).astype(np.float32)[None]
+    da = np.tile(np.array([1.0, 0.0, 0.0, 1.0], np.float32), (1, 4, 4, 1))
+    out = DiffRast.texture(dev(tex), dev(uv), uvDA=dev(da), filterMode="linear-mipmap-linear",
+                           boundaryMode="clamp", mip=mip)
+    want = tex.astype(np.float64).reshape(1, 4, 8, 4, 8, 3).mean(axis=(2, 4))
+    np.testing.assert_allclose(host(out), want, rtol=1e-6, atol=1e-6)
+    with pytest.raises(ValueError):
+        DiffRast.texture(dev(tex), dev(uv), uvDA=dev(da), filterMode="linear-mipmap-linear",
+                         mip=[dev(tex), dev(tex)])

@@ -254,3 +254,21 @@ def test_icosphere_tile_occupancy():
     changed = (r128[..., 3] != rall[..., 3]).sum()
     covered = (rall[..., 3] > 0).sum()
     assert 0 < changed < 0.02 * covered
+
+
+def test_tile_counts_closed_form():
+    # one triangle over the top-left quadrant of a 64x64 image: pixel AABB
+    # x, y in [0, 31] (px = (ndc+1)*W/2 - 0.5), i.e. tiles (0..1, 0..1);
+    # a second one behind the camera (w < 0) and a degenerate one add nothing
+    pos = np.array([[-1, 1, 0, 1], [-1, 0, 0, 1], [0, 1, 0, 1],
+                    [-1, 1, 0, -1], [1, 1, 0, -1], [0, 0, 0, -1],
+                    [0, 0, 0, 1], [0.5, 0.5, 0, 1], [1, 1, 0, 1]], np.float32)[None]
+    tri = np.arange(9, dtype=np.int32).reshape(3, 3)
+    c = O.rasterize_tile_counts(pos, tri, (64, 64))
+    want = np.zeros((1, 4, 4), np.int32)
+    want[0, :2, :2] = 1
+    np.testing.assert_array_equal(c, want)
+    # counts agree with the forward's bin statistics
+    st = {}
+    O.rasterize(pos, tri, (64, 64), stats=st)
+    assert st["max_tile_count"] == c.max() and st["pairs"] == c.sum()
