@@ -67,7 +67,12 @@ enum {
   DR_ERR_MEMORY = 3    /* scratch allocation failed */
 };
 
-enum { DR_ACCUMULATE = 1u };
+enum {
+  DR_ACCUMULATE = 1u,
+  /* dr_texture_bwd of a cube map: the direction gradient (an extension; the
+   * reference returns zeros, Texture.swift:196-198, which is the default) */
+  DR_CUBE_DIR_GRAD = 2u
+};
 
 /* Texture.swift:8-17 (BoundaryMode) */
 enum { DR_BOUNDARY_WRAP = 0, DR_BOUNDARY_CLAMP = 1, DR_BOUNDARY_ZERO = 2, DR_BOUNDARY_CUBE = 3 };
@@ -168,12 +173,17 @@ int dr_texture_build_mip(const float* tex, int Nt, int H, int W, int C, int L, f
 /* Forward of DiffRast.texture (Texture.swift:62-131).
  *   tex: [Nt, Ht, Wt, C], or [Nt, 6, Ht, Wt, C] for DR_BOUNDARY_CUBE; Nt is
  *     1 (shared by every image) or N.
- *   pyramid / L: mip levels 1..L-1 from dr_texture_build_mip (mip filters).
+ *   pyramid / L: mip levels 1..L-1 from dr_texture_build_mip (mip filters;
+ *     for a cube map, built for its Nt*6 faces as textures).
  *   uv: [N,Hi,Wi,2] (cube: direction [N,Hi,Wi,3]).
- *   uv_da: [N,Hi,Wi,4] (mip filters).
+ *   uv_da: [N,Hi,Wi,4] (mip filters; cube: the direction's screen
+ *     derivatives [N,Hi,Wi,6] = (dx/dX, dx/dY, dy/dX, dy/dY, dz/dX, dz/dY)).
  *   bias_map: NULL or [N,Hi,Wi] per-pixel mip level bias; bias: scalar
  *     bias.  Both scale uv_da by 2^bias before the LOD (Texture.swift:104-126).
- */
+ * Cube maps with the mip filters are an extension (the reference samples
+ * cube maps bilinearly only, Texture.swift:75-76): the face's (u, v)
+ * derivatives by the chain rule through the face projection, then the 2D
+ * LOD and trilinear filter on that face. */
 int dr_texture_fwd(const float* tex, const float* pyramid, int Nt, int Ht, int Wt, int C,
                    int L, const float* uv, const float* uv_da, const float* bias_map,
                    float bias, int filter, int boundary, int N, int Hi, int Wi, float* out,
@@ -181,8 +191,10 @@ int dr_texture_fwd(const float* tex, const float* pyramid, int Nt, int Ht, int W
 
 /* VJP of DiffRast.texture.  d_tex has tex's shape ([Nt,...]: a shared
  * texture receives the sum over images).  d_uv may be NULL; it is zero for
- * nearest and cube, as in the reference.  d_uv_da (mip filters) and
- * d_bias_map (when bias_map is given) may be NULL. */
+ * nearest, and for cube unless DR_CUBE_DIR_GRAD is set (then the direction
+ * gradient through the sample position and, for mip filters, the LOD).
+ * d_uv_da (mip filters) and d_bias_map (when bias_map is given) may be
+ * NULL. */
 int dr_texture_bwd(const float* tex, const float* pyramid, int Nt, int Ht, int Wt, int C,
                    int L, const float* uv, const float* uv_da, const float* bias_map,
                    float bias, int filter, int boundary, int N, int Hi, int Wi,

@@ -1181,6 +1181,332 @@ hipError_t launch_tex_bwd(const TexBwdArgs& args, int total_tiles, hipStream_t s
   return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// cube maps with mip filters, and the direction gradient
+// ---------------------------------------------------------------------------
+// An extension of the reference, which samples cube maps bilinearly only
+// (Texture.swift:75-76) and returns a zero direction gradient (:196-198).
+// Faces and face (u, v) as :620-635; the face (u, v) screen derivatives
+// from the direction's (dx/dX, dx/dY, dy/dX, dy/dY, dz/dX, dz/dY) by the
+// chain rule through u = (sc/ma + 1)/2, v = (tc/ma + 1)/2 with the face
+// fixed; then the 2D LOD, clamped bilinear taps and two-rounding trilinear
+// blend of :764-863 on the chosen face of each level.  The backward adds
+// the direction gradient through the sample position and, for mip
+// filters, through the LOD; the pyramid is every face's 2x2 box pyramid.
+
+struct CubeSel {
+  int face, as, at, am;  // axes of sc, tc, ma
+  float ss, ts, ms;      // their signs
+  float sc, tc, ma;
+};
+
+__device__ __forceinline__ CubeSel cube_select(float x, float y, float z) {
+  CubeSel s;
+  const float ax = fabsf(x), ay = fabsf(y), az = fabsf(z);
+  if (ax >= ay && ax >= az) {
+    s.am = 0; s.ms = x > 0.0f ? 1.0f : -1.0f; s.ma = ax;
+    s.at = 1; s.ts = -1.0f; s.tc = -y;
+    s.as = 2;
+    if (x > 0.0f) { s.face = 0; s.ss = -1.0f; s.sc = -z; }
+    else          { s.face = 1; s.ss = 1.0f;  s.sc = z; }
+  } else if (ay >= az) {
+    s.am = 1; s.ms = y > 0.0f ? 1.0f : -1.0f; s.ma = ay;
+    s.as = 0; s.ss = 1.0f; s.sc = x;
+    s.at = 2;
+    if (y > 0.0f) { s.face = 2; s.ts = 1.0f;  s.tc = z; }
+    else          { s.face = 3; s.ts = -1.0f; s.tc = -z; }
+  } else {
+    s.am = 2; s.ms = z > 0.0f ? 1.0f : -1.0f; s.ma = az;
+    s.at = 1; s.ts = -1.0f; s.tc = -y;
+    s.as = 0;
+    if (z > 0.0f) { s.face = 4; s.ss = 1.0f;  s.sc = x; }
+    else          { s.face = 5; s.ss = -1.0f; s.sc = -x; }
+  }
+  return s;
+}
+
+__device__ __forceinline__ float pick3(int a, float v0, float v1, float v2) {
+  return a == 0 ? v0 : (a == 1 ? v1 : v2);
+}
+
+// The direction's screen derivatives as (d/dX, d/dY) per axis.
+struct DirDA {
+  float x[3], y[3];
+};
+
+// Face (u_X, u_Y, v_X, v_Y) from the direction's derivatives.
+__device__ __forceinline__ float4 cube_face_da(const CubeSel& s, const DirDA& d) {
+  const float inv = 0.5f / (s.ma * s.ma);
+  const float sX = s.ss * pick3(s.as, d.x[0], d.x[1], d.x[2]);
+  const float sY = s.ss * pick3(s.as, d.y[0], d.y[1], d.y[2]);
+  const float tX = s.ts * pick3(s.at, d.x[0], d.x[1], d.x[2]);
+  const float tY = s.ts * pick3(s.at, d.y[0], d.y[1], d.y[2]);
+  const float mX = s.ms * pick3(s.am, d.x[0], d.x[1], d.x[2]);
+  const float mY = s.ms * pick3(s.am, d.y[0], d.y[1], d.y[2]);
+  return make_float4((sX * s.ma - s.sc * mX) * inv, (sY * s.ma - s.sc * mY) * inv,
+                     (tX * s.ma - s.tc * mX) * inv, (tY * s.ma - s.tc * mY) * inv);
+}
+
+struct CubeArgs {
+  const float* tex;  // [Nt, 6, Ht, Wt, C]
+  const float* pyr;  // levels 1..L-1 of the Nt*6 faces
+  MipDesc md;        // built for Nt*6 textures
+  int64_t tex_stride;  // 6*Ht*Wt*C, or 0 for one shared cube map
+  int Ht, Wt, C;
+  const float* dir;      // [N, Hi, Wi, 3]
+  const float* dir_da;   // [N, Hi, Wi, 6] (mip modes)
+  const float* bias_map;
+  float scale_bias;
+  int has_bias;
+  int64_t P;
+  int HWi;
+  float* out;  // forward
+  // backward
+  const float* d_out;
+  float* d_tex;
+  float* d_pyr;
+  float* d_dir;     // NULL: not requested
+  int dir_grad;     // 0: d_dir is written as zeros (the reference's value)
+  float* d_dir_da;
+  float* d_bias;
+};
+
+__device__ __forceinline__ const float* cube_level(const CubeArgs& A, int n, int face, int k,
+                                                   int Hk, int Wk) {
+  if (k == 0) return A.tex + n * A.tex_stride + (int64_t)face * A.Ht * A.Wt * A.C;
+  const int64_t nt = A.tex_stride ? n : 0;
+  return A.pyr + mip_off(A.md, k) + (nt * 6 + face) * (int64_t)Hk * Wk * A.C;
+}
+
+__device__ __forceinline__ float* cube_dlevel(const CubeArgs& A, int n, int face, int k, int Hk,
+                                              int Wk) {
+  if (k == 0) return A.d_tex + n * A.tex_stride + (int64_t)face * A.Ht * A.Wt * A.C;
+  const int64_t nt = A.tex_stride ? n : 0;
+  return A.d_pyr + mip_off(A.md, k) + (nt * 6 + face) * (int64_t)Hk * Wk * A.C;
+}
+
+// Per-pixel set-up shared by both passes.
+struct CubePx {
+  CubeSel s;
+  float u, v, inv_ma, bscale;
+  bool scaled;
+  DirDA dd, dd_in;  // folded (dd) and as given (dd_in)
+  float4 da;        // face derivatives
+  Lod ld;
+};
+
+template <int MODE>
+__device__ __forceinline__ CubePx cube_px(const CubeArgs& A, int64_t pix) {
+  CubePx p;
+  const float* dp = A.dir + pix * 3;
+  p.s = cube_select(dp[0], dp[1], dp[2]);
+  p.inv_ma = 1.0f / p.s.ma;
+  p.u = (p.s.sc * p.inv_ma + 1.0f) * 0.5f;
+  p.v = (p.s.tc * p.inv_ma + 1.0f) * 0.5f;
+  p.ld.k0 = p.ld.k1 = 0;
+  p.ld.frac = 0.0f;
+  p.scaled = false;
+  p.bscale = 1.0f;
+  if (MODE > 0) {
+    const float2* q = reinterpret_cast<const float2*>(A.dir_da + pix * 6);
+    const float2 a = q[0], b = q[1], c = q[2];
+    p.dd_in.x[0] = a.x; p.dd_in.y[0] = a.y;
+    p.dd_in.x[1] = b.x; p.dd_in.y[1] = b.y;
+    p.dd_in.x[2] = c.x; p.dd_in.y[2] = c.y;
+    p.dd = p.dd_in;
+    p.scaled = A.bias_map != nullptr || A.has_bias;
+    if (p.scaled) {
+      p.bscale = bias_scale(A.bias_map, pix, A.scale_bias, A.has_bias != 0);
+#pragma unroll
+      for (int i = 0; i < 3; ++i) {
+        p.dd.x[i] = p.dd_in.x[i] * p.bscale;
+        p.dd.y[i] = p.dd_in.y[i] * p.bscale;
+      }
+    }
+    p.da = cube_face_da(p.s, p.dd);
+    p.ld = mip_lod(p.da, A.Ht, A.Wt, A.md.L, MODE == 2);
+  }
+  return p;
+}
+
+// MODE: 1 = mip-nearest, 2 = trilinear (bilinear cube sampling is k_tex_fwd).
+template <int MODE, int CT>
+__global__ void __launch_bounds__(256) k_cube_fwd(CubeArgs A) {
+  const int64_t pix = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (pix >= A.P) return;
+  const int C = dimC<CT>(A.C);
+  const int n = (int)(pix / A.HWi);
+  const CubePx p = cube_px<MODE>(A, pix);
+  float* op = A.out + pix * C;
+  float acc[kMaxC];
+  for (int li = 0; li < 2; ++li) {
+    const int k = li == 0 ? p.ld.k0 : p.ld.k1;
+    const int Hk = mip_h(A.md, k), Wk = mip_w(A.md, k);
+    const float* lv = cube_level(A, n, p.s.face, k, Hk, Wk);
+    const Bilin b = bilin(p.u, p.v, Wk, Hk, DR_BOUNDARY_CLAMP);
+    const float wgt = li == 0 ? (1.0f - p.ld.frac) : p.ld.frac;
+    if constexpr (CT > 0) {
+      float t00[kMaxC], t10[kMaxC], t01[kMaxC], t11[kMaxC];
+      load_texel<CT>(lv + ((int64_t)b.iy0 * Wk + b.ix0) * C, C, t00);
+      load_texel<CT>(lv + ((int64_t)b.iy0 * Wk + b.ix1) * C, C, t10);
+      load_texel<CT>(lv + ((int64_t)b.iy1 * Wk + b.ix0) * C, C, t01);
+      load_texel<CT>(lv + ((int64_t)b.iy1 * Wk + b.ix1) * C, C, t11);
+#pragma unroll
+      for (int c = 0; c < CT; ++c) {
+        const float sample = b.w00 * t00[c] + b.w10 * t10[c] + b.w01 * t01[c] + b.w11 * t11[c];
+        acc[c] = li == 0 ? wgt * sample : acc[c] + wgt * sample;
+      }
+    } else {
+      for (int c = 0; c < C; ++c) {
+        const float t00 = lv[((int64_t)b.iy0 * Wk + b.ix0) * C + c];
+        const float t10 = lv[((int64_t)b.iy0 * Wk + b.ix1) * C + c];
+        const float t01 = lv[((int64_t)b.iy1 * Wk + b.ix0) * C + c];
+        const float t11 = lv[((int64_t)b.iy1 * Wk + b.ix1) * C + c];
+        const float sample = b.w00 * t00 + b.w10 * t10 + b.w01 * t01 + b.w11 * t11;
+        op[c] = li == 0 ? wgt * sample : op[c] + wgt * sample;
+      }
+    }
+  }
+  if constexpr (CT > 0) {
+#pragma unroll
+    for (int c = 0; c < CT; ++c) op[c] = acc[c];
+  }
+}
+
+// MODE: 0 = bilinear (only with the direction gradient), 1 / 2 as above.
+template <int MODE, int CT>
+__global__ void __launch_bounds__(256) k_cube_bwd(CubeArgs A) {
+  const int64_t pix = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (pix >= A.P) return;
+  const int C = dimC<CT>(A.C);
+  const int n = (int)(pix / A.HWi);
+  const CubePx p = cube_px<MODE>(A, pix);
+  const float* g = A.d_out + pix * C;
+  const CubeSel& s = p.s;
+  // sample position gradient (:934-999) and the pyramid scatter (:870-932)
+  float du = 0.0f, dv = 0.0f;
+  for (int li = 0; li < (MODE == 0 ? 1 : 2); ++li) {
+    const int k = li == 0 ? p.ld.k0 : p.ld.k1;
+    const float scale = MODE == 0 ? 1.0f : (li == 0 ? (1.0f - p.ld.frac) : p.ld.frac);
+    const int Hk = mip_h(A.md, k), Wk = mip_w(A.md, k);
+    const float* lv = cube_level(A, n, s.face, k, Hk, Wk);
+    float* dl = cube_dlevel(A, n, s.face, k, Hk, Wk);
+    const Bilin b = bilin(p.u, p.v, Wk, Hk, DR_BOUNDARY_CLAMP);
+    float dfx = 0.0f, dfy = 0.0f;
+    for (int c = 0; c < C; ++c) {
+      const float t00 = lv[((int64_t)b.iy0 * Wk + b.ix0) * C + c];
+      const float t10 = lv[((int64_t)b.iy0 * Wk + b.ix1) * C + c];
+      const float t01 = lv[((int64_t)b.iy1 * Wk + b.ix0) * C + c];
+      const float t11 = lv[((int64_t)b.iy1 * Wk + b.ix1) * C + c];
+      const float gs = g[c] * scale;
+      atomicAdd(dl + ((int64_t)b.iy0 * Wk + b.ix0) * C + c, b.w00 * gs);
+      atomicAdd(dl + ((int64_t)b.iy0 * Wk + b.ix1) * C + c, b.w10 * gs);
+      atomicAdd(dl + ((int64_t)b.iy1 * Wk + b.ix0) * C + c, b.w01 * gs);
+      atomicAdd(dl + ((int64_t)b.iy1 * Wk + b.ix1) * C + c, b.w11 * gs);
+      dfx += gs * ((1.0f - b.fy) * (t10 - t00) + b.fy * (t11 - t01));
+      dfy += gs * ((1.0f - b.fx) * (t01 - t00) + b.fx * (t11 - t10));
+    }
+    du += dfx * (float)Wk;
+    dv += dfy * (float)Hk;
+  }
+  const float inv2 = 0.5f / (s.ma * s.ma);
+  // d u / d dir = inv2 * (ss*ma e_as - sc*ms e_am), likewise v; the axes
+  // are distinct, so each sum below lands in its own component
+  const float g_as = du * (s.ss * s.ma * inv2);
+  const float g_at = dv * (s.ts * s.ma * inv2);
+  const float g_am = -((du * s.sc + dv * s.tc) * s.ms * inv2);
+  float gdd_x[3] = {0.0f, 0.0f, 0.0f}, gdd_y[3] = {0.0f, 0.0f, 0.0f};
+  float l_as = 0.0f, l_at = 0.0f, l_am = 0.0f;
+  if (MODE > 0) {
+    const float sx = p.da.x * (float)A.Wt, sy = p.da.y * (float)A.Wt;
+    const float tx_ = p.da.z * (float)A.Ht, ty_ = p.da.w * (float)A.Ht;
+    const float Asq = sx * sx + tx_ * tx_;
+    const float Bsq = sy * sy + ty_ * ty_;
+    const float rho_sq = fmaxf(Asq, Bsq);
+    const float lod_raw = 0.5f * log2f(fmaxf(rho_sq, 1e-20f));
+    if (lod_raw > 0.0f && lod_raw < (float)(A.md.L - 1)) {
+      const int j0 = f2i(floorf(lod_raw));
+      const int j1 = min(j0 + 1, A.md.L - 1);
+      float d_lod = 0.0f;
+      for (int li = 0; li < 2; ++li) {
+        const int k = li == 0 ? j0 : j1;
+        const float sign = li == 0 ? -1.0f : 1.0f;
+        const int Hk = mip_h(A.md, k), Wk = mip_w(A.md, k);
+        const float* lv = cube_level(A, n, s.face, k, Hk, Wk);
+        const Bilin b = bilin(p.u, p.v, Wk, Hk, DR_BOUNDARY_CLAMP);
+        for (int c = 0; c < C; ++c) {
+          const float t00 = lv[((int64_t)b.iy0 * Wk + b.ix0) * C + c];
+          const float t10 = lv[((int64_t)b.iy0 * Wk + b.ix1) * C + c];
+          const float t01 = lv[((int64_t)b.iy1 * Wk + b.ix0) * C + c];
+          const float t11 = lv[((int64_t)b.iy1 * Wk + b.ix1) * C + c];
+          const float sample = b.w00 * t00 + b.w10 * t10 + b.w01 * t01 + b.w11 * t11;
+          d_lod += sign * sample * g[c];
+        }
+      }
+      const float ln2 = 0.6931471805599453f;
+      const float dlod_drho_sq = 1.0f / (2.0f * rho_sq * ln2);
+      const float A_is_max = (Asq >= Bsq) ? 1.0f : 0.0f;
+      const float B_is_max = 1.0f - A_is_max;
+      const float duX = d_lod * dlod_drho_sq * A_is_max * 2.0f * sx * (float)A.Wt;
+      const float duY = d_lod * dlod_drho_sq * B_is_max * 2.0f * sy * (float)A.Wt;
+      const float dvX = d_lod * dlod_drho_sq * A_is_max * 2.0f * tx_ * (float)A.Ht;
+      const float dvY = d_lod * dlod_drho_sq * B_is_max * 2.0f * ty_ * (float)A.Ht;
+      const DirDA& d6 = p.dd;
+      const float sX = s.ss * pick3(s.as, d6.x[0], d6.x[1], d6.x[2]);
+      const float sY = s.ss * pick3(s.as, d6.y[0], d6.y[1], d6.y[2]);
+      const float tX = s.ts * pick3(s.at, d6.x[0], d6.x[1], d6.x[2]);
+      const float tY = s.ts * pick3(s.at, d6.y[0], d6.y[1], d6.y[2]);
+      const float mX = s.ms * pick3(s.am, d6.x[0], d6.x[1], d6.x[2]);
+      const float mY = s.ms * pick3(s.am, d6.y[0], d6.y[1], d6.y[2]);
+      // through the direction derivatives: u_X = inv2 * (sX*ma - sc*mX), ...
+      const float ex_as = duX * s.ss * s.ma * inv2, ey_as = duY * s.ss * s.ma * inv2;
+      const float ex_at = dvX * s.ts * s.ma * inv2, ey_at = dvY * s.ts * s.ma * inv2;
+      const float ex_am = -((duX * s.sc + dvX * s.tc) * s.ms * inv2);
+      const float ey_am = -((duY * s.sc + dvY * s.tc) * s.ms * inv2);
+#pragma unroll
+      for (int i = 0; i < 3; ++i) {
+        gdd_x[i] = i == s.as ? ex_as : (i == s.at ? ex_at : ex_am);
+        gdd_y[i] = i == s.as ? ey_as : (i == s.at ? ey_at : ey_am);
+      }
+      // through the direction: d u_X / d sc = -inv2*mX,
+      // d u_X / d ma = inv2*sX - 2*u_X/ma, likewise for the others
+      l_as = -((duX * mX + duY * mY) * s.ss * inv2);
+      l_at = -((dvX * mX + dvY * mY) * s.ts * inv2);
+      l_am = s.ms * (duX * (sX * inv2 - 2.0f * p.da.x * p.inv_ma) +
+                     duY * (sY * inv2 - 2.0f * p.da.y * p.inv_ma) +
+                     dvX * (tX * inv2 - 2.0f * p.da.z * p.inv_ma) +
+                     dvY * (tY * inv2 - 2.0f * p.da.w * p.inv_ma));
+    }
+  }
+  if (A.d_dir) {
+    float o[3] = {0.0f, 0.0f, 0.0f};
+    if (A.dir_grad) {
+#pragma unroll
+      for (int i = 0; i < 3; ++i) {
+        const float a = i == s.as ? g_as : (i == s.at ? g_at : g_am);
+        const float l = i == s.as ? l_as : (i == s.at ? l_at : l_am);
+        o[i] = a + l;
+      }
+    }
+    float* dd_o = A.d_dir + pix * 3;
+    dd_o[0] = o[0];
+    dd_o[1] = o[1];
+    dd_o[2] = o[2];
+  }
+  if (MODE > 0 && A.d_dir_da) {
+    float2* q = reinterpret_cast<float2*>(A.d_dir_da + pix * 6);
+    const float sc_ = p.scaled ? p.bscale : 1.0f;
+#pragma unroll
+    for (int i = 0; i < 3; ++i) q[i] = make_float2(gdd_x[i] * sc_, gdd_y[i] * sc_);
+  }
+  if (MODE > 0 && A.d_bias && A.bias_map) {
+    float gm = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 3; ++i) gm = gm + gdd_x[i] * p.dd_in.x[i] + gdd_y[i] * p.dd_in.y[i];
+    A.d_bias[pix] = gm * p.bscale * 0.6931471805599453f;
+  }
+}
+
 }  // namespace dr
 
 using namespace dr;
@@ -1279,15 +1605,17 @@ static int check_tex(const float* tex, const float* pyr, int Nt, int N, int Ht, 
   DR_CHECK_ARG(Nt == 1 || Nt == N, "texture: tex batch dim incompatible with uv batch");
   DR_CHECK_ARG(filter >= 0 && filter <= 3 && boundary >= 0 && boundary <= 3,
                "texture: bad filter / boundary");
-  DR_CHECK_ARG(boundary != DR_BOUNDARY_CUBE || filter == DR_FILTER_LINEAR,
-               "texture: cube textures currently support filterMode .linear only");
-  const bool mip = filter >= DR_FILTER_LINEAR_MIPMAP_NEAREST && boundary != DR_BOUNDARY_CUBE;
+  const bool cube = boundary == DR_BOUNDARY_CUBE;
+  DR_CHECK_ARG(!cube || filter != DR_FILTER_NEAREST,
+               "texture: cube textures support the linear and mipmap filterModes");
+  const int ntex = cube ? Nt * 6 : Nt;  // a cube map is six face textures
+  const bool mip = filter >= DR_FILTER_LINEAR_MIPMAP_NEAREST;
   if (mip) {
     DR_CHECK_ARG(uv_da != nullptr, "texture: mipmap filterModes require uvDA");
     DR_CHECK_ARG(L == 1 || pyr != nullptr, "texture: mip pyramid missing");
-    return build_desc(Ht, Wt, C, Nt, L, md);
+    return build_desc(Ht, Wt, C, ntex, L, md);
   }
-  return build_desc(Ht, Wt, C, Nt, 1, md);
+  return build_desc(Ht, Wt, C, ntex, 1, md);
 }
 
 #define DR_TEX_C_DISPATCH(KERNEL, F, CUBEV, GRID, ...)                                       \
@@ -1310,6 +1638,39 @@ static int check_tex(const float* tex, const float* pyr, int Nt, int N, int Ht, 
     else DR_TEX_C_DISPATCH(KERNEL, DR_FILTER_LINEAR_MIPMAP_LINEAR, false, GRID, __VA_ARGS__);   \
   } while (0)
 
+static CubeArgs cube_args(const float* tex, const float* pyr, const MipDesc& md,
+                          int64_t tex_stride, int Ht, int Wt, int C, const float* dir,
+                          const float* dir_da, const float* bias_map, float scale_bias,
+                          int has_bias, int64_t P, int HWi) {
+  CubeArgs A{};
+  A.tex = tex;
+  A.pyr = pyr;
+  A.md = md;
+  A.tex_stride = tex_stride;
+  A.Ht = Ht;
+  A.Wt = Wt;
+  A.C = C;
+  A.dir = dir;
+  A.dir_da = dir_da;
+  A.bias_map = bias_map;
+  A.scale_bias = scale_bias;
+  A.has_bias = has_bias;
+  A.P = P;
+  A.HWi = HWi;
+  return A;
+}
+
+#define DR_CUBE_DISPATCH(KERNEL, MODE, GRID, ARGS)                                           \
+  do {                                                                                        \
+    switch (C) {                                                                              \
+      case 1: hipLaunchKernelGGL((KERNEL<MODE, 1>), GRID, dim3(256), 0, stream, ARGS); break; \
+      case 2: hipLaunchKernelGGL((KERNEL<MODE, 2>), GRID, dim3(256), 0, stream, ARGS); break; \
+      case 3: hipLaunchKernelGGL((KERNEL<MODE, 3>), GRID, dim3(256), 0, stream, ARGS); break; \
+      case 4: hipLaunchKernelGGL((KERNEL<MODE, 4>), GRID, dim3(256), 0, stream, ARGS); break; \
+      default: hipLaunchKernelGGL((KERNEL<MODE, 0>), GRID, dim3(256), 0, stream, ARGS); break; \
+    }                                                                                         \
+  } while (0)
+
 extern "C" int dr_texture_fwd(const float* tex, const float* pyramid, int Nt, int Ht, int Wt,
                               int C, int L, const float* uv, const float* uv_da,
                               const float* bias_map, float bias, int filter, int boundary, int N,
@@ -1326,10 +1687,65 @@ extern "C" int dr_texture_fwd(const float* tex, const float* pyramid, int Nt, in
   const float scale_bias = exp2f(bias);
   const int has_bias = bias != 0.0f;
   const dim3 grid(grid_for(P, 256));
+  if (cube && filter >= DR_FILTER_LINEAR_MIPMAP_NEAREST) {
+    CubeArgs A = cube_args(tex, pyramid, md, tex_stride, Ht, Wt, C, uv, uv_da, bias_map,
+                           scale_bias, has_bias, P, Hi * Wi);
+    A.out = out;
+    DR_TIMED("k_cube_fwd", stream);
+    if (filter == DR_FILTER_LINEAR_MIPMAP_LINEAR) DR_CUBE_DISPATCH(k_cube_fwd, 2, grid, A);
+    else DR_CUBE_DISPATCH(k_cube_fwd, 1, grid, A);
+    DR_CHECK_LAUNCH();
+    return DR_OK;
+  }
   DR_TIMED("k_tex_fwd", stream);
   DR_TEX_DISPATCH(k_tex_fwd, grid, tex, pyramid, md, tex_stride, Ht, Wt, C, uv, uv_da, bias_map,
                   scale_bias, has_bias, boundary, P, Hi * Wi, out);
   DR_CHECK_LAUNCH();
+  return DR_OK;
+}
+
+// The cube extension's backward: one thread per pixel, d_tex / d_pyramid by
+// global atomics, then the pyramid collapse over the Nt*6 faces.
+static int cube_bwd(const float* tex, const float* pyramid, const MipDesc& md, int64_t tex_stride,
+                    int Nt, int Ht, int Wt, int C, const float* dir, const float* dir_da,
+                    const float* bias_map, float bias, int filter, int N, int Hi, int Wi,
+                    const float* d_out, float* d_tex, float* d_dir, float* d_dir_da,
+                    float* d_bias_map, unsigned flags, hipStream_t stream) {
+  const bool mip = filter >= DR_FILTER_LINEAR_MIPMAP_NEAREST;
+  float* d_pyr = nullptr;
+  if (mip && md.L > 1) {
+    Scratch* sc = scratch_for(stream);
+    if (!sc) return DR_ERR_HIP;
+    const int64_t np = dr_texture_mip_size(Nt * 6, Ht, Wt, C, md.L);
+    d_pyr = (float*)scratch_get(sc, stream, SLOT_DPYR, (size_t)np * sizeof(float));
+    if (!d_pyr) return DR_ERR_MEMORY;
+    DR_CHECK_HIP(fill_async(d_pyr, 0.0f, np, stream));
+  }
+  const int64_t P = (int64_t)N * Hi * Wi;
+  CubeArgs A = cube_args(tex, pyramid, md, tex_stride, Ht, Wt, C, dir, dir_da, bias_map,
+                         exp2f(bias), bias != 0.0f, P, Hi * Wi);
+  A.d_out = d_out;
+  A.d_tex = d_tex;
+  A.d_pyr = d_pyr;
+  A.d_dir = d_dir;
+  A.dir_grad = (flags & DR_CUBE_DIR_GRAD) ? 1 : 0;
+  A.d_dir_da = mip ? d_dir_da : nullptr;
+  A.d_bias = mip ? d_bias_map : nullptr;
+  const dim3 grid(grid_for(P, 256));
+  {
+    DR_TIMED("k_cube_bwd", stream);
+    if (filter == DR_FILTER_LINEAR_MIPMAP_LINEAR) DR_CUBE_DISPATCH(k_cube_bwd, 2, grid, A);
+    else if (filter == DR_FILTER_LINEAR_MIPMAP_NEAREST) DR_CUBE_DISPATCH(k_cube_bwd, 1, grid, A);
+    else DR_CUBE_DISPATCH(k_cube_bwd, 0, grid, A);
+  }
+  DR_CHECK_LAUNCH();
+  if (d_pyr) {
+    const int bpr = (Wt + 255) / 256;
+    DR_TIMED("k_mip_collapse", stream);
+    hipLaunchKernelGGL(k_mip_collapse, dim3((unsigned)((int64_t)Nt * 6 * Ht * bpr)), dim3(256), 0,
+                       stream, d_pyr, md, C, bpr, d_tex);
+    DR_CHECK_LAUNCH();
+  }
   return DR_OK;
 }
 
@@ -1346,10 +1762,13 @@ extern "C" int dr_texture_bwd(const float* tex, const float* pyramid, int Nt, in
   if (st) return st;
   DR_CHECK_ARG(d_out && d_tex && Hi >= 1 && Wi >= 1, "texture_bwd: null tensor");
   const bool cube = boundary == DR_BOUNDARY_CUBE;
-  const bool mip = !cube && filter >= DR_FILTER_LINEAR_MIPMAP_NEAREST;
   const int64_t tex_stride = Nt == 1 ? 0 : (int64_t)(cube ? 6 : 1) * Ht * Wt * C;
   const int64_t ntex = (int64_t)Nt * (cube ? 6 : 1) * Ht * Wt * C;
   if (!(flags & DR_ACCUMULATE)) DR_CHECK_HIP(fill_async(d_tex, 0.0f, ntex, stream));
+  if (cube && (filter >= DR_FILTER_LINEAR_MIPMAP_NEAREST || (flags & DR_CUBE_DIR_GRAD)))
+    return cube_bwd(tex, pyramid, md, tex_stride, Nt, Ht, Wt, C, uv, uv_da, bias_map, bias,
+                    filter, N, Hi, Wi, d_out, d_tex, d_uv, d_uv_da, d_bias_map, flags, stream);
+  const bool mip = !cube && filter >= DR_FILTER_LINEAR_MIPMAP_NEAREST;
   float* d_pyr = nullptr;
   if (mip && md.L > 1) {
     Scratch* sc = scratch_for(stream);

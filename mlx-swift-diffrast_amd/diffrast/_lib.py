@@ -48,6 +48,7 @@ SIGNATURES = {
 
 DR_OK, DR_ERR_ARGUMENT, DR_ERR_HIP, DR_ERR_MEMORY = 0, 1, 2, 3
 DR_ACCUMULATE = 1
+DR_CUBE_DIR_GRAD = 2
 ABI_VERSION = 1
 
 _lib = None

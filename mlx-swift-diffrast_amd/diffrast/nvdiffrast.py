@@ -128,7 +128,7 @@ def texture_construct_mip(tex: torch.Tensor, max_mip_level: Optional[int] = None
     """nvdiffrast.torch.texture_construct_mip: the pyramid as a list
     [tex, level1, ...] (2x2 box means); pass it back as `mip=`."""
     if cube_mode:
-        raise ValueError("texture_construct_mip: cube maps support filter_mode 'linear' only")
+        raise ValueError("texture_construct_mip: a cube map's pyramid is built inside texture()")
     return DiffRast.textureConstructMip(tex, maxLevel=max_mip_level)
 
 

@@ -172,6 +172,17 @@ class _InterpolateFn(torch.autograd.Function):
 # texture (Texture.swift:62-327)
 # ---------------------------------------------------------------------------
 
+def _bias_map(m, uv):
+    """Texture.swift:104-108: [N, H_img, W_img] or [N, H_img, W_img, 1]."""
+    if m is None:
+        return None
+    if tuple(m.shape[:3]) != tuple(uv.shape[:3]) or m.ndim not in (3, 4) or \
+            (m.ndim == 4 and m.shape[3] != 1):
+        raise ValueError("texture: mipLevelBiasMap must be [N, H_img, W_img] or "
+                         f"[N, H_img, W_img, 1] (got {list(m.shape)})")
+    return m.to(torch.float32).contiguous()
+
+
 def _packed_pyramid(levels, tex):
     """(L, packed levels 1..L-1) of a `textureConstructMip` list: its levels
     are views of one buffer in the library's packing, used as they are; any
@@ -209,35 +220,37 @@ def _packed_pyramid(levels, tex):
 
 class _TextureFn(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, tex, uv, uv_da, bias_map, filt, boundary, bias, cached):
+    def forward(ctx, tex, uv, uv_da, bias_map, filt, boundary, bias, cached, dir_grad=False):
         lib = _lib.load()
         cube = boundary == BoundaryMode.cube
         N, Hi, Wi = uv.shape[0], uv.shape[1], uv.shape[2]
         Nt = tex.shape[0]
         Ht, Wt, C = (tex.shape[2], tex.shape[3], tex.shape[4]) if cube else \
             (tex.shape[1], tex.shape[2], tex.shape[3])
-        mip = (not cube) and filt >= FilterMode.linearMipmapNearest
+        mip = filt >= FilterMode.linearMipmapNearest
         L, pyr = 1, None
         if mip and cached is not None:
             L, pyr = cached
         elif mip:
+            nfaces = Nt * 6 if cube else Nt   # a cube map's pyramid: every face's
             L = lib.dr_texture_mip_levels(Ht, Wt, -1, None, None)
-            size = lib.dr_texture_mip_size(Nt, Ht, Wt, C, L)
+            size = lib.dr_texture_mip_size(nfaces, Ht, Wt, C, L)
             pyr = torch.empty(max(size, 1), device=tex.device, dtype=torch.float32)
-            _lib.check(lib.dr_texture_build_mip(_ptr(tex), Nt, Ht, Wt, C, L, _ptr(pyr), _stream()))
+            _lib.check(lib.dr_texture_build_mip(_ptr(tex), nfaces, Ht, Wt, C, L, _ptr(pyr),
+                                                _stream()))
         out = torch.empty((N, Hi, Wi, C), device=uv.device, dtype=torch.float32)
         _lib.check(lib.dr_texture_fwd(
             _ptr(tex), _ptr(pyr), Nt, Ht, Wt, C, L, _ptr(uv), _ptr(uv_da), _ptr(bias_map),
             float(bias), int(filt), int(boundary), N, Hi, Wi, _ptr(out), _stream()))
         ctx.save_for_backward(tex, uv, uv_da, bias_map, pyr)
-        ctx.meta = (int(filt), int(boundary), float(bias), L, Nt, Ht, Wt, C)
+        ctx.meta = (int(filt), int(boundary), float(bias), L, Nt, Ht, Wt, C, bool(dir_grad))
         return out
 
     @staticmethod
     def backward(ctx, d_out):
         lib = _lib.load()
         tex, uv, uv_da, bias_map, pyr = ctx.saved_tensors
-        filt, boundary, bias, L, Nt, Ht, Wt, C = ctx.meta
+        filt, boundary, bias, L, Nt, Ht, Wt, C, dir_grad = ctx.meta
         N, Hi, Wi = uv.shape[0], uv.shape[1], uv.shape[2]
         d_out = d_out.to(torch.float32).contiguous()
         d_tex = torch.empty_like(tex)
@@ -248,10 +261,10 @@ class _TextureFn(torch.autograd.Function):
         _lib.check(lib.dr_texture_bwd(
             _ptr(tex), _ptr(pyr), Nt, Ht, Wt, C, L, _ptr(uv), _ptr(uv_da), _ptr(bias_map),
             float(bias), filt, boundary, N, Hi, Wi, _ptr(d_out), _ptr(d_tex), _ptr(d_uv),
-            _ptr(d_uv_da), _ptr(d_bias), 0, _stream()))
+            _ptr(d_uv_da), _ptr(d_bias), _lib.DR_CUBE_DIR_GRAD if dir_grad else 0, _stream()))
         if d_uv_da is None and uv_da is not None and ctx.needs_input_grad[2]:
             d_uv_da = torch.zeros_like(uv_da)
-        return d_tex, d_uv, d_uv_da, d_bias, None, None, None, None
+        return d_tex, d_uv, d_uv_da, d_bias, None, None, None, None, None
 
 
 # ---------------------------------------------------------------------------
@@ -420,7 +433,8 @@ class DiffRast:
                 filterMode: Union[FilterMode, str] = FilterMode.linear,
                 boundaryMode: Union[BoundaryMode, str] = BoundaryMode.wrap,
                 mipLevelBias: float = 0.0, mipLevelBiasMap: Optional[torch.Tensor] = None,
-                mip: Optional[Sequence[torch.Tensor]] = None) -> torch.Tensor:
+                mip: Optional[Sequence[torch.Tensor]] = None, dirGrad: bool = False
+                ) -> torch.Tensor:
         """Texture.swift:62-131.
 
         `mip` (mip filters only; no counterpart argument in the reference):
@@ -429,7 +443,14 @@ class DiffRast:
         (Texture.swift:141-143 suggests such caching).  Its levels are read
         as given (fewer levels cap the LOD); the gradient still flows to
         `tex` through the 2x2 box backward, as for a pyramid built in the
-        call."""
+        call.
+
+        Cube maps (boundaryMode cube) also take the mip filters, with uvDA
+        the direction's screen derivatives [N, H_img, W_img, 6] (the layout
+        `interpolate(..., diffAttrs=.all)` gives a 3-channel direction), and
+        `dirGrad=True` returns the direction gradient instead of the
+        reference's zeros (Texture.swift:196-198).  Both are extensions; the
+        reference samples cube maps bilinearly only (:75-76)."""
         filt = FilterMode(_FILTER_NAMES[filterMode] if isinstance(filterMode, str) else filterMode)
         bnd = BoundaryMode(_BOUNDARY_NAMES[boundaryMode] if isinstance(boundaryMode, str)
                            else boundaryMode)
@@ -438,8 +459,8 @@ class DiffRast:
         if not texf.is_cuda or not uvf.is_cuda:
             raise ValueError("texture: tensors must be on a ROCm device")
         if bnd == BoundaryMode.cube:
-            if filt != FilterMode.linear:
-                raise ValueError("texture: cube textures currently support filterMode .linear only")
+            if filt == FilterMode.nearest:
+                raise ValueError("texture: cube textures support the linear and mipmap filterModes")
             if texf.ndim != 5 or texf.shape[1] != 6:
                 raise ValueError(f"texture: cube tex must be [N, 6, H, W, C] (got {list(texf.shape)})")
             if uvf.ndim != 4 or uvf.shape[3] != 3:
@@ -447,7 +468,17 @@ class DiffRast:
                                  f"(got {list(uvf.shape)})")
             if texf.shape[0] not in (1, uvf.shape[0]):
                 raise ValueError("texture: tex batch dim incompatible with uv batch")
-            return _TextureFn.apply(texf, uvf, None, None, filt, bnd, 0.0, None)
+            if mip is not None:
+                raise ValueError("texture: a prebuilt `mip` is for 2D textures")
+            if filt == FilterMode.linear:
+                return _TextureFn.apply(texf, uvf, None, None, filt, bnd, 0.0, None,
+                                        bool(dirGrad))
+            if uvDA is None or tuple(uvDA.shape) != tuple(uvf.shape[:3]) + (6,):
+                raise ValueError("texture: cube mipmap filterModes require uvDA "
+                                 "[N, H_img, W_img, 6] (direction derivatives)")
+            bm = _bias_map(mipLevelBiasMap, uvf)
+            return _TextureFn.apply(texf, uvf, uvDA.to(torch.float32).contiguous(), bm, filt, bnd,
+                                    float(mipLevelBias), None, bool(dirGrad))
         if texf.ndim != 4:
             raise ValueError(f"texture: tex must be [N, H_tex, W_tex, C] (got {list(texf.shape)})")
         if uvf.ndim != 4 or uvf.shape[3] != 2:
@@ -461,14 +492,7 @@ class DiffRast:
             raise ValueError("texture: mipmap filterModes require uvDA")
         if tuple(uvDA.shape) != tuple(uvf.shape[:3]) + (4,):
             raise ValueError(f"texture: uvDA must be [N, H_img, W_img, 4] (got {list(uvDA.shape)})")
-        bm = None
-        if mipLevelBiasMap is not None:
-            if tuple(mipLevelBiasMap.shape[:3]) != tuple(uvf.shape[:3]) or \
-                    mipLevelBiasMap.ndim not in (3, 4) or \
-                    (mipLevelBiasMap.ndim == 4 and mipLevelBiasMap.shape[3] != 1):
-                raise ValueError("texture: mipLevelBiasMap must be [N, H_img, W_img] or "
-                                 f"[N, H_img, W_img, 1] (got {list(mipLevelBiasMap.shape)})")
-            bm = mipLevelBiasMap.to(torch.float32).contiguous()
+        bm = _bias_map(mipLevelBiasMap, uvf)
         cached = None if mip is None else _packed_pyramid(mip, texf)
         return _TextureFn.apply(texf, uvf, uvDA.to(torch.float32).contiguous(), bm, filt, bnd,
                                 float(mipLevelBias), cached)

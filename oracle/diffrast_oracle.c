@@ -1460,3 +1460,244 @@ void orc_aa_bwd_pos(const float* color, const float* rast, const float* pos,
     }
   }
 }
+
+/* ===================================================================== */
+/* cube maps with mip filters, and the direction gradient                */
+/* ===================================================================== */
+/* An extension: the reference samples cube maps with the bilinear filter
+ * only (Texture.swift:75-76) and returns a zero direction gradient
+ * (:196-198).  The semantics restated here are this build's definition,
+ * built from the reference's own pieces:
+ *   - face selection and face (u, v) of Texture.swift:620-635;
+ *   - the face (u, v) screen derivatives from the direction's derivatives
+ *     dd = (dx/dX, dx/dY, dy/dX, dy/dY, dz/dX, dz/dY) by the chain rule
+ *     through u = (sc/ma + 1)/2, v = (tc/ma + 1)/2 with the face fixed;
+ *   - then exactly the 2D LOD, level choice, clamped bilinear sampling and
+ *     two-rounding trilinear blend of :764-863 on the chosen face of each
+ *     level (the pyramid is the 2x2 box pyramid of every face);
+ *   - gradients: d_tex through the pyramid as in :870-932; d_dd as
+ *     :1011-1102 (same lod_raw mask, A-vs-B rule and the trilinear
+ *     surrogate for mip-nearest) chained through the face derivatives;
+ *     d_dir through the sample position (:934-999 chained through the
+ *     projection) plus, for mip filters, through the LOD's dependence on
+ *     the direction.
+ * Parity with the reference is unpinned by construction (it has no such
+ * path); the tests pin it by reduction to the reference's 2D trilinear on
+ * a face, to its cube bilinear at L = 1, and by finite differences. */
+
+typedef struct {
+  int face, as, at, am;  /* axes of sc, tc, ma */
+  float ss, ts, ms;      /* their signs */
+  float sc, tc, ma;
+} CubeSel;
+
+static inline CubeSel cube_select(float x, float y, float z) {
+  CubeSel s;
+  float ax = fabsf(x), ay = fabsf(y), az = fabsf(z);
+  if (ax >= ay && ax >= az) {
+    s.am = 0; s.ms = x > 0.0f ? 1.0f : -1.0f; s.ma = ax;
+    s.at = 1; s.ts = -1.0f; s.tc = -y;
+    if (x > 0.0f) { s.face = 0; s.as = 2; s.ss = -1.0f; s.sc = -z; }
+    else          { s.face = 1; s.as = 2; s.ss = 1.0f;  s.sc = z; }
+  } else if (ay >= az) {
+    s.am = 1; s.ms = y > 0.0f ? 1.0f : -1.0f; s.ma = ay;
+    s.as = 0; s.ss = 1.0f; s.sc = x;
+    if (y > 0.0f) { s.face = 2; s.at = 2; s.ts = 1.0f;  s.tc = z; }
+    else          { s.face = 3; s.at = 2; s.ts = -1.0f; s.tc = -z; }
+  } else {
+    s.am = 2; s.ms = z > 0.0f ? 1.0f : -1.0f; s.ma = az;
+    s.at = 1; s.ts = -1.0f; s.tc = -y;
+    if (z > 0.0f) { s.face = 4; s.as = 0; s.ss = 1.0f;  s.sc = x; }
+    else          { s.face = 5; s.as = 0; s.ss = -1.0f; s.sc = -x; }
+  }
+  return s;
+}
+
+/* Face (u, v) screen derivatives (u_X, u_Y, v_X, v_Y) from dd. */
+static inline void cube_face_da(const CubeSel* s, const float* dd, float* da4) {
+  float inv = 0.5f / (s->ma * s->ma);
+  float sX = s->ss * dd[2 * s->as], sY = s->ss * dd[2 * s->as + 1];
+  float tX = s->ts * dd[2 * s->at], tY = s->ts * dd[2 * s->at + 1];
+  float mX = s->ms * dd[2 * s->am], mY = s->ms * dd[2 * s->am + 1];
+  da4[0] = (sX * s->ma - s->sc * mX) * inv;
+  da4[1] = (sY * s->ma - s->sc * mY) * inv;
+  da4[2] = (tX * s->ma - s->tc * mX) * inv;
+  da4[3] = (tY * s->ma - s->tc * mY) * inv;
+}
+
+/* mode: 0 = bilinear (level 0 only), 1 = mip-nearest, 2 = trilinear.
+ * packed: pyramid of the N*6 face textures (level 0 included), offsets per
+ * level; level_batch_mul as in orc_tex_mip_fwd.  dd: [N,Hi,Wi,6] with any
+ * bias already folded in (NULL for mode 0). */
+void orc_tex_cube_mip_fwd(const float* packed, int64_t level_batch_mul, const float* dir,
+                          const float* dd, const int64_t* offsets, const int32_t* level_h,
+                          const int32_t* level_w, int L, int N, int Hi, int Wi, int C, int mode,
+                          float* out) {
+  int64_t total = (int64_t)N * Hi * Wi;
+#pragma omp parallel for schedule(static) if (g_threads > 1) num_threads(g_threads)
+  for (int64_t pix = 0; pix < total; ++pix) {
+    int pn = (int)(pix / ((int64_t)Hi * Wi));
+    CubeSel s = cube_select(dir[pix * 3], dir[pix * 3 + 1], dir[pix * 3 + 2]);
+    float inv_ma = 1.0f / s.ma;
+    float u = (s.sc * inv_ma + 1.0f) * 0.5f;
+    float v = (s.tc * inv_ma + 1.0f) * 0.5f;
+    int k0 = 0, k1 = 0;
+    float frac = 0.0f;
+    if (mode > 0) {
+      float da4[4];
+      cube_face_da(&s, dd + pix * 6, da4);
+      mip_lod(da4, level_h[0], level_w[0], L, mode == 2, &k0, &k1, &frac);
+    }
+    for (int li = 0; li < 2; ++li) {
+      int k = li == 0 ? k0 : k1;
+      int Hk = level_h[k], Wk = level_w[k];
+      const float* lv =
+          packed + offsets[k] + ((int64_t)pn * level_batch_mul * 6 + s.face) * Hk * Wk * C;
+      Bilin b;
+      bilin(u, v, Wk, Hk, 1 /* clamp */, &b);
+      for (int c = 0; c < C; ++c) {
+        float t00 = lv[((int64_t)b.iy0 * Wk + b.ix0) * C + c];
+        float t10 = lv[((int64_t)b.iy0 * Wk + b.ix1) * C + c];
+        float t01 = lv[((int64_t)b.iy1 * Wk + b.ix0) * C + c];
+        float t11 = lv[((int64_t)b.iy1 * Wk + b.ix1) * C + c];
+        float sample = b.w00 * t00 + b.w10 * t10 + b.w01 * t01 + b.w11 * t11;
+        if (mode == 0) {
+          out[pix * C + c] = sample;
+        } else if (li == 0) {
+          out[pix * C + c] = (1.0f - frac) * sample;
+        } else {
+          out[pix * C + c] += frac * sample;
+        }
+      }
+      if (mode == 0) break;
+    }
+  }
+}
+
+/* Backward: d_packed (pyramid of the N*6 faces, zeroed by the caller),
+ * d_dir [N,Hi,Wi,3] (NULL to skip), d_dd [N,Hi,Wi,6] (mip modes; NULL to
+ * skip). */
+void orc_tex_cube_mip_bwd(const float* packed, int64_t level_batch_mul, const float* dir,
+                          const float* dd, const float* d_out, const int64_t* offsets,
+                          const int32_t* level_h, const int32_t* level_w, int L, int N, int Hi,
+                          int Wi, int C, int mode, float* d_packed, float* d_dir, float* d_dd) {
+  int64_t total = (int64_t)N * Hi * Wi;
+  int Ht = level_h[0], Wt = level_w[0];
+#pragma omp parallel for schedule(static) if (g_threads > 1) num_threads(g_threads)
+  for (int64_t pix = 0; pix < total; ++pix) {
+    int pn = (int)(pix / ((int64_t)Hi * Wi));
+    const float* g = d_out + pix * C;
+    CubeSel s = cube_select(dir[pix * 3], dir[pix * 3 + 1], dir[pix * 3 + 2]);
+    float inv_ma = 1.0f / s.ma;
+    float u = (s.sc * inv_ma + 1.0f) * 0.5f;
+    float v = (s.tc * inv_ma + 1.0f) * 0.5f;
+    int k0 = 0, k1 = 0;
+    float frac = 0.0f;
+    float da4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (mode > 0) {
+      cube_face_da(&s, dd + pix * 6, da4);
+      mip_lod(da4, Ht, Wt, L, mode == 2, &k0, &k1, &frac);
+    }
+    /* sample-position gradient (:934-999) and the pyramid scatter (:870-932) */
+    float du = 0.0f, dv = 0.0f;
+    for (int li = 0; li < (mode == 0 ? 1 : 2); ++li) {
+      int k = li == 0 ? k0 : k1;
+      float scale = mode == 0 ? 1.0f : (li == 0 ? (1.0f - frac) : frac);
+      int Hk = level_h[k], Wk = level_w[k];
+      int64_t base = offsets[k] + ((int64_t)pn * level_batch_mul * 6 + s.face) * Hk * Wk * C;
+      const float* lv = packed + base;
+      float* dl = d_packed + base;
+      Bilin b;
+      bilin(u, v, Wk, Hk, 1, &b);
+      float dfx = 0.0f, dfy = 0.0f;
+      for (int c = 0; c < C; ++c) {
+        float t00 = lv[((int64_t)b.iy0 * Wk + b.ix0) * C + c];
+        float t10 = lv[((int64_t)b.iy0 * Wk + b.ix1) * C + c];
+        float t01 = lv[((int64_t)b.iy1 * Wk + b.ix0) * C + c];
+        float t11 = lv[((int64_t)b.iy1 * Wk + b.ix1) * C + c];
+        float gs = g[c] * scale;
+        sadd(&dl[((int64_t)b.iy0 * Wk + b.ix0) * C + c], b.w00 * gs);
+        sadd(&dl[((int64_t)b.iy0 * Wk + b.ix1) * C + c], b.w10 * gs);
+        sadd(&dl[((int64_t)b.iy1 * Wk + b.ix0) * C + c], b.w01 * gs);
+        sadd(&dl[((int64_t)b.iy1 * Wk + b.ix1) * C + c], b.w11 * gs);
+        dfx += gs * ((1.0f - b.fy) * (t10 - t00) + b.fy * (t11 - t01));
+        dfy += gs * ((1.0f - b.fx) * (t01 - t00) + b.fx * (t11 - t10));
+      }
+      du += dfx * (float)Wk;
+      dv += dfy * (float)Hk;
+    }
+    float inv2 = 0.5f / (s.ma * s.ma);
+    float gd[3] = {0.0f, 0.0f, 0.0f};
+    /* d u / d dir = inv2 * (ss*ma e_as - sc*ms e_am), likewise v */
+    gd[s.as] += du * (s.ss * s.ma * inv2);
+    gd[s.at] += dv * (s.ts * s.ma * inv2);
+    gd[s.am] -= (du * s.sc + dv * s.tc) * s.ms * inv2;
+    float gdd[6] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    if (mode > 0) {
+      float sx = da4[0] * (float)Wt, sy = da4[1] * (float)Wt;
+      float tx_ = da4[2] * (float)Ht, ty_ = da4[3] * (float)Ht;
+      float Asq = sx * sx + tx_ * tx_;
+      float Bsq = sy * sy + ty_ * ty_;
+      float rho_sq = fmaxf(Asq, Bsq);
+      float lod_raw = 0.5f * log2f(fmaxf(rho_sq, 1e-20f));
+      if (lod_raw > 0.0f && lod_raw < (float)(L - 1)) {
+        int j0 = f2i(floorf(lod_raw));
+        int j1 = j0 + 1;
+        if (j1 >= L) j1 = L - 1;
+        float d_lod = 0.0f;
+        for (int li = 0; li < 2; ++li) {
+          int k = li == 0 ? j0 : j1;
+          float sign = li == 0 ? -1.0f : 1.0f;
+          int Hk = level_h[k], Wk = level_w[k];
+          const float* lv =
+              packed + offsets[k] + ((int64_t)pn * level_batch_mul * 6 + s.face) * Hk * Wk * C;
+          Bilin b;
+          bilin(u, v, Wk, Hk, 1, &b);
+          for (int c = 0; c < C; ++c) {
+            float t00 = lv[((int64_t)b.iy0 * Wk + b.ix0) * C + c];
+            float t10 = lv[((int64_t)b.iy0 * Wk + b.ix1) * C + c];
+            float t01 = lv[((int64_t)b.iy1 * Wk + b.ix0) * C + c];
+            float t11 = lv[((int64_t)b.iy1 * Wk + b.ix1) * C + c];
+            float sample = b.w00 * t00 + b.w10 * t10 + b.w01 * t01 + b.w11 * t11;
+            d_lod += sign * sample * g[c];
+          }
+        }
+        float ln2 = 0.6931471805599453f;
+        float dlod_drho_sq = 1.0f / (2.0f * rho_sq * ln2);
+        float A_is_max = (Asq >= Bsq) ? 1.0f : 0.0f;
+        float B_is_max = 1.0f - A_is_max;
+        /* gradients of the face derivatives (the 2D d_uvDA) */
+        float duX = d_lod * dlod_drho_sq * A_is_max * 2.0f * sx * (float)Wt;
+        float duY = d_lod * dlod_drho_sq * B_is_max * 2.0f * sy * (float)Wt;
+        float dvX = d_lod * dlod_drho_sq * A_is_max * 2.0f * tx_ * (float)Ht;
+        float dvY = d_lod * dlod_drho_sq * B_is_max * 2.0f * ty_ * (float)Ht;
+        const float* d6 = dd + pix * 6;
+        float sX = s.ss * d6[2 * s.as], sY = s.ss * d6[2 * s.as + 1];
+        float tX = s.ts * d6[2 * s.at], tY = s.ts * d6[2 * s.at + 1];
+        float mX = s.ms * d6[2 * s.am], mY = s.ms * d6[2 * s.am + 1];
+        /* through dd: u_X = inv2 * (sX*ma - sc*mX), ... */
+        gdd[2 * s.as] += duX * s.ss * s.ma * inv2;
+        gdd[2 * s.as + 1] += duY * s.ss * s.ma * inv2;
+        gdd[2 * s.at] += dvX * s.ts * s.ma * inv2;
+        gdd[2 * s.at + 1] += dvY * s.ts * s.ma * inv2;
+        gdd[2 * s.am] -= (duX * s.sc + dvX * s.tc) * s.ms * inv2;
+        gdd[2 * s.am + 1] -= (duY * s.sc + dvY * s.tc) * s.ms * inv2;
+        /* through the direction: d u_X / d sc = -inv2*mX,
+         * d u_X / d ma = inv2*sX - 2*u_X/ma, likewise for the others */
+        gd[s.as] -= (duX * mX + duY * mY) * s.ss * inv2;
+        gd[s.at] -= (dvX * mX + dvY * mY) * s.ts * inv2;
+        gd[s.am] += s.ms * (duX * (sX * inv2 - 2.0f * da4[0] * inv_ma) +
+                            duY * (sY * inv2 - 2.0f * da4[1] * inv_ma) +
+                            dvX * (tX * inv2 - 2.0f * da4[2] * inv_ma) +
+                            dvY * (tY * inv2 - 2.0f * da4[3] * inv_ma));
+      }
+    }
+    if (d_dir) {
+      d_dir[pix * 3 + 0] = gd[0];
+      d_dir[pix * 3 + 1] = gd[1];
+      d_dir[pix * 3 + 2] = gd[2];
+    }
+    if (d_dd && mode > 0)
+      for (int i = 0; i < 6; ++i) d_dd[pix * 6 + i] = gdd[i];
+  }
+}

@@ -149,6 +149,18 @@ void orc_tex_mip_grad_uvda(const float* packed, int64_t level_batch_mul,
                            int L, int N, int Hi, int Wi, int Ht, int Wt,
                            int C, int boundary, float* d_uv_da);
 
+/* Cube maps with mip filters and the direction gradient: an extension
+ * (the reference has bilinear cube sampling only and a zero direction
+ * gradient); mode 0 = bilinear, 1 = mip-nearest, 2 = trilinear. */
+void orc_tex_cube_mip_fwd(const float* packed, int64_t level_batch_mul, const float* dir,
+                          const float* dd, const int64_t* offsets, const int32_t* level_h,
+                          const int32_t* level_w, int L, int N, int Hi, int Wi, int C, int mode,
+                          float* out);
+void orc_tex_cube_mip_bwd(const float* packed, int64_t level_batch_mul, const float* dir,
+                          const float* dd, const float* d_out, const int64_t* offsets,
+                          const int32_t* level_h, const int32_t* level_w, int L, int N, int Hi,
+                          int Wi, int C, int mode, float* d_packed, float* d_dir, float* d_dd);
+
 /* ---- antialias (Sources/MLXDiffRast/Antialias.swift) ---------------- */
 
 void orc_aa_topology(const int32_t* tri, int T, int32_t* topo);

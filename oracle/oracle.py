@@ -77,6 +77,10 @@ def _declare(L):
                                 _i, _i, _i, _i, _i, _i, _i, _f32p],
         "orc_tex_mip_grad_uvda": [_f32p, _i64, _f32p, _f32p, _f32p, _i64p, _i32p, _i32p, _i, _i,
                                   _i, _i, _i, _i, _i, _i, _f32p],
+        "orc_tex_cube_mip_fwd": [_f32p, _i64, _f32p, _f32p, _i64p, _i32p, _i32p, _i, _i, _i, _i,
+                                 _i, _i, _f32p],
+        "orc_tex_cube_mip_bwd": [_f32p, _i64, _f32p, _f32p, _f32p, _i64p, _i32p, _i32p, _i, _i,
+                                 _i, _i, _i, _i, _f32p, _f32p, _f32p],
         "orc_aa_topology": [_i32p, _i, _i32p],
         "orc_aa_fwd": [_f32p, _f32p, _f32p, _i32p, _i32p, _i, _i, _i, _i, _i, _f32p],
         "orc_aa_bwd_color": [_f32p, _f32p, _i32p, _i32p, _f32p, _i, _i, _i, _i, _i, _f32p],
@@ -370,18 +374,79 @@ def texture(tex, uv, uvDA=None, filterMode="linear", boundaryMode="wrap",
 
 
 def texture_vjp(tex, uv, d_out, uvDA=None, filterMode="linear", boundaryMode="wrap",
-                mipLevelBias=0.0, mipLevelBiasMap=None):
-    """-> (d_tex, d_uv, d_uvDA or None, d_biasMap or None)."""
+                mipLevelBias=0.0, mipLevelBiasMap=None, dirGrad=False):
+    """-> (d_tex, d_uv, d_uvDA or None, d_biasMap or None).  dirGrad (cube
+    maps): the direction gradient of the extension instead of the
+    reference's zeros."""
     return _texture(tex, uv, uvDA, filterMode, boundaryMode, mipLevelBias, mipLevelBiasMap,
-                    d_out=d_out)
+                    d_out=d_out, dir_grad=dirGrad)
 
 
-def _texture(tex, uv, uvDA, filterMode, boundaryMode, mipLevelBias, mipLevelBiasMap, d_out):
+def _cube_ext(tex, dirs, dd, mode, mipLevelBias, mipLevelBiasMap, g, dir_grad):
+    """Cube maps with mip filters / the direction gradient (an extension; see
+    orc_tex_cube_mip_fwd): the pyramid of the N-broadcast faces, packed."""
+    L = lib()
+    N, Hi, Wi, _ = dirs.shape
+    Ht, Wt, C = tex.shape[2], tex.shape[3], tex.shape[4]
+    faces = c32(np.broadcast_to(tex, (N,) + tex.shape[1:])).reshape(N * 6, Ht, Wt, C)
+    if mode > 0:
+        lh, lw = texture_mip_levels(Ht, Wt)
+        eff, scale = _bias_fold(dd, mipLevelBias, mipLevelBiasMap)
+    else:
+        lh, lw = texture_mip_levels(Ht, Wt, maxLevel=0)
+        eff, scale = None, None
+    nl = len(lh)
+    offsets, total = _pack_offsets(N * 6, lh, lw, C)
+    packed = np.empty(total, np.float32)
+    L.orc_mip_build(fp(faces), N * 6, Ht, Wt, C, nl, lp(offsets), fp(packed))
+    if g is None:
+        out = np.empty((N, Hi, Wi, C), np.float32)
+        L.orc_tex_cube_mip_fwd(fp(packed), 1, fp(dirs), fp(eff), lp(offsets), ip(lh), ip(lw), nl,
+                               N, Hi, Wi, C, mode, fp(out))
+        return out
+    d_packed = np.zeros(total, np.float32)
+    d_dir = np.zeros((N, Hi, Wi, 3), np.float32)
+    d_eff = np.zeros((N, Hi, Wi, 6), np.float32) if mode > 0 else None
+    L.orc_tex_cube_mip_bwd(fp(packed), 1, fp(dirs), fp(eff), fp(g), lp(offsets), ip(lh), ip(lw),
+                           nl, N, Hi, Wi, C, mode, fp(d_packed), fp(d_dir), fp(d_eff))
+    d_faces = np.empty((N * 6, Ht, Wt, C), np.float32)
+    L.orc_mip_collapse(fp(d_packed), N * 6, Ht, Wt, C, nl, lp(offsets), fp(d_faces))
+    d_tex = d_faces.reshape(N, 6, Ht, Wt, C)
+    if tex.shape[0] == 1 and N > 1:
+        d_tex = d_tex.sum(axis=0, keepdims=True, dtype=np.float32)
+    if not dir_grad:
+        d_dir = np.zeros_like(d_dir)
+    d_dd, d_map = None, None
+    if mode > 0:
+        d_dd = d_eff if scale is None else c32(d_eff * scale)
+        if scale is not None and mipLevelBiasMap is not None:
+            gm = (d_eff * dd).astype(np.float32).sum(axis=3, keepdims=True, dtype=np.float32)
+            d_map = c32(gm * scale * np.float32(np.log(2.0)))
+            if np.ndim(mipLevelBiasMap) == 3:
+                d_map = d_map[..., 0]
+    return d_tex, d_dir, d_dd, d_map
+
+
+def _texture(tex, uv, uvDA, filterMode, boundaryMode, mipLevelBias, mipLevelBiasMap, d_out,
+             dir_grad=False):
     L = lib()
     tex = c32(tex)
     uv = c32(uv)
     g = c32(d_out)
     b = BOUNDARY[boundaryMode]
+    if b == 3 and filterMode in ("linear-mipmap-linear", "linear-mipmap-nearest"):
+        if tex.ndim != 5 or tex.shape[1] != 6:
+            raise ValueError("texture: cube tex must be [N, 6, H, W, C]")
+        if uv.ndim != 4 or uv.shape[3] != 3:
+            raise ValueError("texture: cube uv must be [N, H_img, W_img, 3]")
+        if uvDA is None or c32(uvDA).shape != uv.shape[:3] + (6,):
+            raise ValueError("texture: cube mip filters need uvDA [N, H_img, W_img, 6]")
+        mode = 2 if filterMode == "linear-mipmap-linear" else 1
+        return _cube_ext(tex, uv, c32(uvDA), mode, mipLevelBias, mipLevelBiasMap, g, dir_grad)
+    if b == 3 and g is not None and dir_grad:
+        if filterMode != "linear":
+            raise ValueError("texture: cube textures support linear and mip filters")
+        return _cube_ext(tex, uv, None, 0, 0.0, None, g, True)
     if b == 3:  # Texture.swift:74-82, 174-206
         if filterMode != "linear":
             raise ValueError("texture: cube textures currently support filterMode .linear only")

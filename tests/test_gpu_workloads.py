@@ -232,12 +232,18 @@ def test_displaced_sphere_peel_16x2048():
     assert_grad_close(host(a2.grad), d_attr2, "d_attr (down-scaled)")
 
 
+_hw = (np.arange(256, dtype=np.float32) + 0.5) / 256
+ENV = np.stack([np.ones((256, 256), np.float32), np.repeat(1 - 2 * _hw[:, None], 256, 1),
+                np.repeat(1 - 2 * _hw[None, :], 256, 0)], -1).astype(np.float32)
+
+
 def test_range_batch_cube_4096():
     """Range mode: 4096 meshes of 512 triangles in one [V,4] buffer at
-    256^2, per-pixel directions interpolated and looked up in a shared
-    6x512^2x3 cube map (the cube filter the reference supports is .linear),
-    forward and backward.  Meshes 0..15 against the oracle; the full batch
-    against those meshes rendered alone."""
+    256^2, per-pixel directions and their screen derivatives interpolated and
+    looked up in a shared 6x512^2x3 cube map with the trilinear filter and a
+    per-pixel bias map U[-1,1] (the cube + mip + bias extension), forward and
+    backward to the cube map, the directions and pos.  Meshes 0..15 against
+    the oracle; the full batch against those meshes rendered alone."""
     torch = torch_dev()
     from diffrast import DiffRast
     _threads()
@@ -245,41 +251,51 @@ def test_range_batch_cube_4096():
     pos, tri, ranges, d = sc["pos"], sc["tri"], sc["ranges"], sc["dir"]
     rng = np.random.default_rng(9)
     cube = rng.random((1, 6, 512, 512, 3)).astype(np.float32)
+    bias = rng.uniform(-1, 1, size=(4096, 256, 256)).astype(np.float32)
 
     def run(rows):
         p = dev(pos).requires_grad_(True)
-        attr = dev(d)
+        attr = dev(d).requires_grad_(True)
         tex = dev(cube).requires_grad_(True)
-        rast, _ = DiffRast.rasterize(p, dev(tri), (256, 256), gradDB=False,
-                                     ranges=torch.as_tensor(ranges[rows]))
-        dirs, _ = DiffRast.interpolate(attr, rast, dev(tri))
+        rast, db = DiffRast.rasterize(p, dev(tri), (256, 256), gradDB=True,
+                                      ranges=torch.as_tensor(ranges[rows]))
+        dirs, dirs_da = DiffRast.interpolate(attr, rast, dev(tri), rastDB=db, diffAttrs="all")
         # empty pixels interpolate to the zero vector, which has no cube face
-        # (NaN in the reference too): point them along +x
+        # (NaN in the reference too): they look up the environment through
+        # the +x face, one direction per pixel
         bg = (rast[..., 3:4] == 0).float()
-        dirs = dirs + bg * torch.tensor([1.0, 0.0, 0.0], device=bg.device)
-        col = DiffRast.texture(tex, dirs, boundaryMode="cube")
+        dirs = dirs + bg * torch.as_tensor(ENV, device=bg.device)
+        col = DiffRast.texture(tex, dirs, uvDA=dirs_da, filterMode="linear-mipmap-linear",
+                               boundaryMode="cube", mipLevelBiasMap=dev(bias[rows]),
+                               dirGrad=True)
         g = torch.ones_like(col) * 1e-3
         (col * g).sum().backward()
-        return rast, dirs, col, p, tex
+        return rast, dirs, dirs_da, col, p, attr, tex
 
-    rast, dirs, col, p, tex = run(slice(0, 4096))
+    rast, dirs, dirs_da, col, p, attr, tex = run(slice(0, 4096))
     t = rast[..., 3].reshape(4096, -1).long() - 1
     lo = torch.as_tensor(ranges[:, 0], device=t.device)[:, None]
     assert bool(((t < 0) | ((t >= lo) & (t < lo + 512))).all().item())
-    r16, d16, c16, p16, tex16 = run(slice(0, 16))
+    assert bool(torch.isfinite(tex.grad).all().item()) and bool(torch.isfinite(p.grad).all().item())
+    r16, d16, da16, c16, p16, a16, tex16 = run(slice(0, 16))
     np.testing.assert_array_equal(host(rast[:16]), host(r16))
     np.testing.assert_array_equal(host(dirs[:16]), host(d16))
     np.testing.assert_array_equal(host(col[:16]), host(c16))
-    # meshes 0..15 against the oracle (their triangles and vertices come first)
+    # the first 16 meshes' vertices only receive gradients from their images
     nt, nv = 16 * 512, 16 * 512 * 3
-    rr, _ = O.rasterize(pos[:nv], tri[:nt], (256, 256), gradDB=False, ranges=ranges[:16],
-                        max_per_tile=0)
+    assert_grad_close(host(p.grad[:nv]), host(p16.grad[:nv]), "d_pos (batch independence)")
+    # meshes 0..15 against the oracle (their triangles and vertices come first)
+    rr, rdb = O.rasterize(pos[:nv], tri[:nt], (256, 256), gradDB=True, ranges=ranges[:16],
+                          max_per_tile=0)
     np.testing.assert_array_equal(host(r16), rr)
-    dr, _ = O.interpolate(d[:nv], rr, tri[:nt])
-    dr = dr + (rr[..., 3:4] == 0).astype(np.float32) * np.array([1.0, 0.0, 0.0], np.float32)
+    dr, dda = O.interpolate(d[:nv], rr, tri[:nt], rastDB=rdb, diffAttrs="all")
+    dr = dr + (rr[..., 3:4] == 0).astype(np.float32) * ENV
     np.testing.assert_array_equal(host(d16), dr)
-    cr = O.texture(cube, dr, boundaryMode="cube")
-    np.testing.assert_array_equal(host(c16), cr)
+    np.testing.assert_array_equal(host(da16), dda)
+    cr = O.texture(cube, dr, uvDA=dda, filterMode="linear-mipmap-linear", boundaryMode="cube",
+                   mipLevelBiasMap=bias[:16])
+    assert_fwd_close(host(c16), cr)
     g = np.full(cr.shape, 1e-3, np.float32)
-    d_tex, _, _, _ = O.texture_vjp(cube, dr, g, boundaryMode="cube")
+    d_tex, _, _, _ = O.texture_vjp(cube, dr, g, uvDA=dda, filterMode="linear-mipmap-linear",
+                                   boundaryMode="cube", mipLevelBiasMap=bias[:16], dirGrad=True)
     assert_grad_close(host(tex16.grad), d_tex, "d_cube")
