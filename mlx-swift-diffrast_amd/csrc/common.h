@@ -96,13 +96,14 @@ struct ProfScope {
 
 constexpr int kWave = 64;
 
-// `(int)floor(x)` with the conversion GPUs implement (saturate, NaN -> 0);
-// the oracle uses the same definition.
+// Float -> int32 as the hardware converts (v_cvt_i32_f32: truncation,
+// out-of-range values saturate, NaN -> 0), one instruction; C's cast leaves
+// those cases undefined, and spelling them out costs branches.  The oracle
+// uses the same definition.
 __device__ __forceinline__ int f2i(float x) {
-  if (x != x) return 0;
-  if (x >= 2147483648.0f) return 2147483647;
-  if (x <= -2147483648.0f) return (-2147483647 - 1);
-  return (int)x;
+  int r;
+  asm("v_cvt_i32_f32 %0, %1" : "=v"(r) : "v"(x));
+  return r;
 }
 
 __device__ __forceinline__ int xcd_remap(int b, int B) {
@@ -201,6 +202,17 @@ __device__ __forceinline__ void row_run_scan(const RowRun& r, float (&v)[M]) {
   run_scan_step<2>(r.li, r.s, v);
   run_scan_step<4>(r.li, r.s, v);
   run_scan_step<8>(r.li, r.s, v);
+}
+
+// The same scan with only as many steps as the longest run in the wave
+// needs (`maxlen`, wave-uniform): a run of length r is summed after
+// ceil(log2 r) steps.
+template <int M>
+__device__ __forceinline__ void row_run_scan_n(const RowRun& r, float (&v)[M], int maxlen) {
+  if (maxlen > 1) run_scan_step<1>(r.li, r.s, v);
+  if (maxlen > 2) run_scan_step<2>(r.li, r.s, v);
+  if (maxlen > 4) run_scan_step<4>(r.li, r.s, v);
+  if (maxlen > 8) run_scan_step<8>(r.li, r.s, v);
 }
 
 template <int M>

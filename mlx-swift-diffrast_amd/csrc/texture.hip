@@ -995,6 +995,7 @@ __global__ void __launch_bounds__(256, 5) k_tex_bwd_win(TexBwdArgs A, int total_
                   : ((uint64_t)q[li].k << 60) | ((uint64_t)q[li].ix0 << 45) |
                         ((uint64_t)q[li].ix1 << 30) | ((uint64_t)q[li].iy0 << 15) | (uint64_t)q[li].iy1;
       const RowRun run = row_run(key);
+      const int maxlen = wave_max(run.li - run.s + 1);  // longest run in the wave
       const bool adds = w != -2 && run.tail;
       const bool in_win = w >= 0 && usable[w];
       double* wb = win + (w >= 0 ? wbase[w] : 0);
@@ -1006,15 +1007,14 @@ __global__ void __launch_bounds__(256, 5) k_tex_bwd_win(TexBwdArgs A, int total_
         float v[CT];
 #pragma unroll
         for (int c = 0; c < CT; ++c) v[c] = w == -2 ? 0.0f : wt[t] * (g[c] * sc);
-        row_run_scan(run, v);
+        row_run_scan_n(run, v, maxlen);
         if (!adds) continue;
         const int tx_ = (t & 1) ? q[li].ix1 : q[li].ix0;
         const int ty_ = (t & 2) ? q[li].iy1 : q[li].iy0;
         if (in_win) {
           const int o = ((ty_ - by0[w]) * bw[w] + (tx_ - bx0[w])) * CT;  // < area[w]*CT
 #pragma unroll
-          for (int c = 0; c < CT; ++c)
-            if (v[c] != 0.0f) atomicAdd(wb + o + c, (double)v[c]);
+          for (int c = 0; c < CT; ++c) atomicAdd(wb + o + c, (double)v[c]);
         } else {
           lds_table_add(tab, base + (ty_ * Wk + tx_) * CT, v);
         }
@@ -1141,6 +1141,49 @@ __global__ void __launch_bounds__(256) k_mip_collapse(const float* __restrict__ 
     for (int k = kL - 1; k >= 1; --k) acc = at(k) + acc * 0.25f;
     dt[c] = dt[c] + acc * 0.25f;
   }
+}
+
+// The same collapse for C = 4 in two passes with texel vectors: level 1's
+// totals first, in place (one thread per level-1 texel walks its chain of
+// ancestors, the same sums in the same order), then level 0 adds a quarter
+// of its parent's total.
+__global__ void __launch_bounds__(256) k_mip_collapse1_c4(float* __restrict__ d_pyr, MipDesc md,
+                                                          int64_t n1) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n1) return;
+  const int W1 = md.w[1], H1 = md.h[1];
+  const int64_t r = i % ((int64_t)H1 * W1);
+  const int n = (int)(i / ((int64_t)H1 * W1));
+  const int y = (int)(r / W1), x = (int)(r - (int64_t)(r / W1) * W1);
+  const int kL = md.L - 1;
+  auto at = [&](int k) {
+    const int sh = k - 1;
+    return *reinterpret_cast<const float4*>(
+        d_pyr + md.off[k] + (((int64_t)n * md.h[k] + (y >> sh)) * md.w[k] + (x >> sh)) * 4);
+  };
+  float4 acc = at(kL);
+  for (int k = kL - 1; k >= 1; --k) {
+    const float4 o = at(k);
+    acc = make_float4(o.x + acc.x * 0.25f, o.y + acc.y * 0.25f, o.z + acc.z * 0.25f,
+                      o.w + acc.w * 0.25f);
+  }
+  *reinterpret_cast<float4*>(d_pyr + md.off[1] + i * 4) = acc;
+}
+
+__global__ void __launch_bounds__(256) k_mip_collapse0_c4(const float* __restrict__ d_pyr,
+                                                          MipDesc md, int64_t n0,
+                                                          float* __restrict__ d_tex) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n0) return;
+  const int W = md.w[0], H = md.h[0];
+  const int64_t r = i % ((int64_t)H * W);
+  const int n = (int)(i / ((int64_t)H * W));
+  const int y = (int)(r / W), x = (int)(r - (int64_t)(r / W) * W);
+  const float4 t = *reinterpret_cast<const float4*>(
+      d_pyr + md.off[1] + (((int64_t)n * md.h[1] + (y >> 1)) * md.w[1] + (x >> 1)) * 4);
+  float4* dp = reinterpret_cast<float4*>(d_tex + i * 4);
+  const float4 d = *dp;
+  *dp = make_float4(d.x + t.x * 0.25f, d.y + t.y * 0.25f, d.z + t.z * 0.25f, d.w + t.w * 0.25f);
 }
 
 template <int FILTER, int CT>
@@ -1638,6 +1681,30 @@ static int check_tex(const float* tex, const float* pyr, int Nt, int N, int Ht, 
     else DR_TEX_C_DISPATCH(KERNEL, DR_FILTER_LINEAR_MIPMAP_LINEAR, false, GRID, __VA_ARGS__);   \
   } while (0)
 
+// d_tex += the pyramid's gradient (the backward of the 2x2 means).
+static int mip_collapse(float* d_pyr, const MipDesc& md, int ntex, int Ht, int Wt, int C,
+                        float* d_tex, hipStream_t stream) {
+  DR_TIMED("k_mip_collapse", stream);
+  if (C == 4 && (((uintptr_t)d_pyr | (uintptr_t)d_tex) & 15) == 0) {
+    if (md.L >= 3) {
+      const int64_t n1 = (int64_t)ntex * md.h[1] * md.w[1];
+      hipLaunchKernelGGL(k_mip_collapse1_c4, dim3(grid_for(n1, 256)), dim3(256), 0, stream,
+                         d_pyr, md, n1);
+      DR_CHECK_LAUNCH();
+    }
+    const int64_t n0 = (int64_t)ntex * Ht * Wt;
+    hipLaunchKernelGGL(k_mip_collapse0_c4, dim3(grid_for(n0, 256)), dim3(256), 0, stream, d_pyr,
+                       md, n0, d_tex);
+    DR_CHECK_LAUNCH();
+    return DR_OK;
+  }
+  const int bpr = (Wt + 255) / 256;
+  hipLaunchKernelGGL(k_mip_collapse, dim3((unsigned)((int64_t)ntex * Ht * bpr)), dim3(256), 0,
+                     stream, d_pyr, md, C, bpr, d_tex);
+  DR_CHECK_LAUNCH();
+  return DR_OK;
+}
+
 static CubeArgs cube_args(const float* tex, const float* pyr, const MipDesc& md,
                           int64_t tex_stride, int Ht, int Wt, int C, const float* dir,
                           const float* dir_da, const float* bias_map, float scale_bias,
@@ -1739,13 +1806,7 @@ static int cube_bwd(const float* tex, const float* pyramid, const MipDesc& md, i
     else DR_CUBE_DISPATCH(k_cube_bwd, 0, grid, A);
   }
   DR_CHECK_LAUNCH();
-  if (d_pyr) {
-    const int bpr = (Wt + 255) / 256;
-    DR_TIMED("k_mip_collapse", stream);
-    hipLaunchKernelGGL(k_mip_collapse, dim3((unsigned)((int64_t)Nt * 6 * Ht * bpr)), dim3(256), 0,
-                       stream, d_pyr, md, C, bpr, d_tex);
-    DR_CHECK_LAUNCH();
-  }
+  if (d_pyr) return mip_collapse(d_pyr, md, Nt * 6, Ht, Wt, C, d_tex, stream);
   return DR_OK;
 }
 
@@ -1842,12 +1903,6 @@ extern "C" int dr_texture_bwd(const float* tex, const float* pyramid, int Nt, in
 #undef DR_TB
     DR_CHECK_HIP(e);
   }
-  if (d_pyr) {
-    const int bpr = (Wt + 255) / 256;
-    DR_TIMED("k_mip_collapse", stream);
-    hipLaunchKernelGGL(k_mip_collapse, dim3((unsigned)((int64_t)Nt * Ht * bpr)), dim3(256), 0,
-                       stream, d_pyr, md, C, bpr, d_tex);
-    DR_CHECK_LAUNCH();
-  }
+  if (d_pyr) return mip_collapse(d_pyr, md, Nt, Ht, Wt, C, d_tex, stream);
   return DR_OK;
 }
