@@ -242,6 +242,36 @@ __device__ __forceinline__ void test_tri(const TriRec& R, int t, float x, float 
   }
 }
 
+// True when the triangle provably covers no pixel centre of the box
+// [xw0, xw1] x [yw0, yw1]: some edge function is below -delta on the whole
+// box.  The edge function e(x, y) = (xi - x)(yj - y) - (xj - x)(yi - y) is
+// affine in (x, y) (the xy terms cancel), so its maximum over the box is at
+// the corner picked by its slopes; evaluated in fp64 from the fp32 vertex
+// coordinates it is exact up to one final rounding.  delta bounds the error
+// of test_tri's fp32 evaluation at any centre of the box (4 roundings of
+// products bounded by (|xi| + 1)(|yj| + 1) + (|xj| + 1)(|yi| + 1), doubled),
+// so a culled triangle would fail test_tri's e * area >= 0 at every pixel.
+// Triangles of tiny area (where e * area could underflow) are never culled.
+__device__ __forceinline__ bool box_misses(const TriRec& R, float xw0, float xw1, float yw0,
+                                           float yw1) {
+  const float area = R.r2.y;
+  if (!(fabsf(area) > 1e-20f)) return false;
+  const double sg = area > 0.0f ? 1.0 : -1.0;
+  const double X[3] = {R.r0.x, R.r0.z, R.r1.x}, Y[3] = {R.r0.y, R.r0.w, R.r1.y};
+  const double u = 1.0 / 16777216.0;  // 2^-24
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {  // edge k: vertices k+1 and k+2 (e0, e1, e2 of test_tri)
+    const int a_ = (k + 1) % 3, b_ = (k + 2) % 3;
+    const double xi = X[a_], yi = Y[a_], xj = X[b_], yj = Y[b_];
+    const double c0 = sg * (xi * yj - xj * yi), cx = sg * (yi - yj), cy = sg * (xj - xi);
+    const double emax = c0 + fmax(cx * xw0, cx * xw1) + fmax(cy * yw0, cy * yw1);
+    const double delta = 8.0 * u * ((fabs(xi) + 1.0) * (fabs(yj) + 1.0) +
+                                    (fabs(xj) + 1.0) * (fabs(yi) + 1.0));
+    if (emax < -delta) return true;
+  }
+  return false;
+}
+
 __device__ __forceinline__ TriRec load_rec(const TriRec* __restrict__ rec, int64_t r) {
   const float4* q = reinterpret_cast<const float4*>(rec + r);
   TriRec R;
@@ -252,30 +282,12 @@ __device__ __forceinline__ TriRec load_rec(const TriRec* __restrict__ rec, int64
   return R;
 }
 
-__device__ __forceinline__ float rdl(float v, int j) {
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j));
-}
-
-__device__ __forceinline__ float4 rdl4(float4 v, int j) {
-  return make_float4(rdl(v.x, j), rdl(v.y, j), rdl(v.z, j), rdl(v.w, j));
-}
-
-// Lane j's record, in scalar registers.
-__device__ __forceinline__ TriRec bcast_rec(const TriRec& R, int j) {
-  TriRec o;
-  o.r0 = rdl4(R.r0, j);
-  o.r1 = rdl4(R.r1, j);
-  o.r2 = rdl4(R.r2, j);
-  o.r3 = rdl4(R.r3, j);
-  return o;
-}
-
 // Rasterize.swift:371-599.  One workgroup per (image, 16x16 tile); wave w
-// owns the 8x8 quadrant (w&1, w>>1).  The tile's triangle ids and records
-// are wave-uniform, so they travel through the scalar cache; each triangle
-// is first tested against the quadrant's pixel-centre box (exact: the
-// pixel -> NDC map is monotonic), so most of the list costs a few scalar
-// compares.
+// owns the 8x8 quadrant (w&1, w>>1).  Each triangle of the tile's list is
+// first tested against the quadrant's pixel-centre box (its bounding box,
+// then its edge functions over the box; exact: the pixel -> NDC map is
+// monotonic), 64 triangles at a time, one per lane; only the survivors are
+// tested against the quadrant's 64 pixels.
 template <bool DB, bool PEEL>
 __global__ void __launch_bounds__(256) k_raster(
     const TriRec* __restrict__ rec, const int4* __restrict__ rect, Items it, int64_t rec_stride,
@@ -320,8 +332,11 @@ __global__ void __launch_bounds__(256) k_raster(
     // 64 candidates at a time: each lane loads one candidate's record
     // (vector gathers, one round trip for all 64) and tests it against the
     // quadrant's box; the survivors are then taken one by one, their
-    // records broadcast with readlane.
+    // records read back from the wave's LDS slots at a uniform address (a
+    // broadcast read; cheaper than 17 readlanes and their SGPR hazards).
     const int* ids = list + o;
+    __shared__ TriRec s_rec[4][kWave];
+    __shared__ int s_t[4][kWave];
     for (int c0 = 0; c0 < count; c0 += kWave) {
       const int nb = min(kWave, count - c0);
       int myt = 0;
@@ -330,16 +345,26 @@ __global__ void __launch_bounds__(256) k_raster(
       if (lane < nb) {
         myt = ids[c0 + lane];
         Rl = load_rec(rec, rbase + myt);
-        hit = !(Rl.r3.y < xw0 || Rl.r3.x > xw1 || Rl.r3.w < yw0 || Rl.r3.z > yw1);
+        hit = !(Rl.r3.y < xw0 || Rl.r3.x > xw1 || Rl.r3.w < yw0 || Rl.r3.z > yw1) &&
+              !box_misses(Rl, xw0, xw1, yw0, yw1);
       }
       uint64_t m = __ballot(hit);
+      if (hit) {
+        s_rec[wave][lane] = Rl;
+        s_t[wave][lane] = myt;
+      }
+      // LDS is ordered within a wave; the barrier keeps the compiler from
+      // moving the reads above the writes
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
       while (m) {
         const int j = __ffsll((long long)m) - 1;
         m &= m - 1;
-        const int t = __builtin_amdgcn_readlane(myt, j);
-        const TriRec R = bcast_rec(Rl, j);
+        const int t = s_t[wave][j];
+        const TriRec R = s_rec[wave][j];
         if (valid) test_tri(R, t, x, y, peel_z, best);
       }
+      __builtin_amdgcn_wave_barrier();  // reads done before the next chunk writes
     }
   } else {
     // The tile's list overflowed its capacity (sized from an earlier
