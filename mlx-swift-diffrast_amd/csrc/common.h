@@ -160,6 +160,10 @@ __device__ __forceinline__ void run_scan_step(int li, int s, float (&v)[M]) {
   }
 }
 
+__device__ __forceinline__ int wave_max(int v) {
+  return wave_reduce_i(v, [](int a, int b) { return a > b ? a : b; });
+}
+
 // Runs of equal keys along each 16-lane row (the row of pixels a wave row
 // holds): every lane's v[] becomes the sum of its run's values up to
 // itself (a segmented Hillis-Steele scan over DPP row shifts), and the
@@ -218,7 +222,7 @@ __device__ __forceinline__ void row_run_scan_n(const RowRun& r, float (&v)[M], i
 template <int M>
 __device__ __forceinline__ bool row_run_sum(uint64_t key, float (&v)[M]) {
   const RowRun r = row_run(key);
-  row_run_scan(r, v);
+  row_run_scan_n(r, v, wave_max(r.li - r.s + 1));
   return r.tail;
 }
 
@@ -276,9 +280,6 @@ __device__ __forceinline__ int pack16(int lo, int hi) {
 __device__ __forceinline__ int unpack16_lo(int v) { return (int)(int16_t)(v & 0xffff); }
 __device__ __forceinline__ int unpack16_hi(int v) { return (int)(int16_t)((uint32_t)v >> 16); }
 
-__device__ __forceinline__ int wave_max(int v) {
-  return wave_reduce_i(v, [](int a, int b) { return a > b ? a : b; });
-}
 
 // Scatter-add of M values per lane into addresses that are equal for all
 // lanes with the same (`key`, `key2`).  Up to kProbes candidate groups are
