@@ -35,9 +35,13 @@ __device__ __forceinline__ int mip_w(const MipDesc& m, int k) { return m.w[0] >>
 __device__ __forceinline__ int64_t mip_off(const MipDesc& m, int k) {
   // sum_{j=1}^{k-1} Nt*C*(H*W / 4^j) = Nt*C*(H*W - H_{k-1}*W_{k-1}) / 3
   const int j = k > 0 ? k - 1 : 0;
-  const int64_t a = (int64_t)m.h[0] * m.w[0];
-  const int64_t b = (int64_t)(m.h[0] >> j) * (m.w[0] >> j);
-  return m.nc * ((a - b) / 3);
+  const uint64_t a = (uint64_t)(uint32_t)m.h[0] * (uint32_t)m.w[0];
+  if (a < (1ull << 32)) {  // 32-bit arithmetic (uniform branch)
+    const uint32_t b = ((uint32_t)m.h[0] >> j) * ((uint32_t)m.w[0] >> j);
+    return m.nc * (int64_t)(((uint32_t)a - b) / 3u);
+  }
+  const uint64_t b = (uint64_t)(m.h[0] >> j) * (uint64_t)(m.w[0] >> j);
+  return m.nc * (int64_t)((a - b) / 3);
 }
 
 // Texture.swift:336-354.
@@ -300,14 +304,16 @@ __device__ __forceinline__ void tex_fwd_px(
   }
 }
 
-template <int FILTER, bool CUBE, int CT>
+// BND: the boundary mode as a compile-time constant (DR_BOUNDARY_CUBE for
+// cube maps), so the clamp and wrap footprints carry no out-of-range masks.
+template <int FILTER, int BND, int CT>
 __global__ void __launch_bounds__(256) k_tex_fwd(
     const float* __restrict__ tex, const float* __restrict__ pyr, MipDesc md, int64_t tex_stride,
     int Ht, int Wt, int C_, const float* __restrict__ uv, const float* __restrict__ uv_da,
-    const float* __restrict__ bias_map, float scale_bias, int has_bias, int boundary, int64_t P,
+    const float* __restrict__ bias_map, float scale_bias, int has_bias, int64_t P,
     int HWi, float* __restrict__ out) {
-  tex_fwd_px<FILTER, CUBE, CT>(tex, pyr, md, tex_stride, Ht, Wt, C_, uv, uv_da, bias_map,
-                               scale_bias, has_bias, boundary, P, HWi, out,
+  tex_fwd_px<FILTER, BND == DR_BOUNDARY_CUBE, CT>(tex, pyr, md, tex_stride, Ht, Wt, C_, uv, uv_da,
+                                                  bias_map, scale_bias, has_bias, BND, P, HWi, out,
                                (int64_t)blockIdx.x * blockDim.x + threadIdx.x);
 }
 
@@ -732,7 +738,7 @@ __device__ __forceinline__ void slot_box(const TapSlot& q, int& x0, int& x1, int
 }
 
 
-template <int FILTER, int CT>
+template <int FILTER, int CT, int BND>
 // Five workgroups per CU (the register budget this asks for costs a few
 // spilled values, measured cheaper than four resident workgroups).
 __global__ void __launch_bounds__(256, 5) k_tex_bwd_win(TexBwdArgs A, int total_tiles) {
@@ -802,7 +808,7 @@ __global__ void __launch_bounds__(256, 5) k_tex_bwd_win(TexBwdArgs A, int total_
 #pragma unroll
     for (int li = 0; li < 2; ++li) {
       const int k = q[li].k, Hk = mip_h(md, k), Wk = mip_w(md, k);
-      const Bilin b = bilin(uvp.x, uvp.y, Wk, Hk, A.boundary);
+      const Bilin b = bilin(uvp.x, uvp.y, Wk, Hk, BND);
       float w00 = b.w00, w10 = b.w10, w01 = b.w01, w11 = b.w11;
       if (b.ix1 == b.ix0) { w00 += w10; w01 += w11; w10 = 0.0f; w11 = 0.0f; }
       if (b.iy1 == b.iy0) { w00 += w01; w10 += w11; w01 = 0.0f; w11 = 0.0f; }
@@ -835,9 +841,9 @@ __global__ void __launch_bounds__(256, 5) k_tex_bwd_win(TexBwdArgs A, int total_
           const int k0 = f2i(floorf(lod_raw));
           const int k1 = min(k0 + 1, md.L - 1);
           float s0 = 0.0f, s1 = 0.0f, u0, u1;
-          const Bilin b0 = bilin(uvp.x, uvp.y, mip_w(md, k0), mip_h(md, k0), A.boundary);
+          const Bilin b0 = bilin(uvp.x, uvp.y, mip_w(md, k0), mip_h(md, k0), BND);
           duv_level(level_ptr(k0), mip_w(md, k0), CT, b0, g, 0.0f, u0, u1, s0);
-          const Bilin b1 = bilin(uvp.x, uvp.y, mip_w(md, k1), mip_h(md, k1), A.boundary);
+          const Bilin b1 = bilin(uvp.x, uvp.y, mip_w(md, k1), mip_h(md, k1), BND);
           duv_level(level_ptr(k1), mip_w(md, k1), CT, b1, g, 0.0f, u0, u1, s1);
           d_lod = -s0 + s1;
         }
@@ -1186,12 +1192,12 @@ __global__ void __launch_bounds__(256) k_mip_collapse0_c4(const float* __restric
   *dp = make_float4(d.x + t.x * 0.25f, d.y + t.y * 0.25f, d.z + t.z * 0.25f, d.w + t.w * 0.25f);
 }
 
-template <int FILTER, int CT>
-hipError_t launch_tex_bwd_win(const TexBwdArgs& args, int total_tiles, hipStream_t stream) {
+template <int FILTER, int CT, int BND>
+hipError_t launch_tex_bwd_win_b(const TexBwdArgs& args, int total_tiles, hipStream_t stream) {
   static int per_cu = 0;
   if (per_cu == 0) {
     int b = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, k_tex_bwd_win<FILTER, CT>, 256, 0) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, k_tex_bwd_win<FILTER, CT, BND>, 256, 0) !=
             hipSuccess ||
         b <= 0)
       b = 2;
@@ -1199,9 +1205,20 @@ hipError_t launch_tex_bwd_win(const TexBwdArgs& args, int total_tiles, hipStream
   }
   const int64_t resident = (int64_t)device_cu_count() * per_cu;
   const unsigned grid = (unsigned)(total_tiles < resident ? total_tiles : resident);
-  hipLaunchKernelGGL((k_tex_bwd_win<FILTER, CT>), dim3(grid), dim3(256), 0, stream, args,
+  hipLaunchKernelGGL((k_tex_bwd_win<FILTER, CT, BND>), dim3(grid), dim3(256), 0, stream, args,
                      total_tiles);
   return hipGetLastError();
+}
+
+// The boundary mode is a compile-time constant of the windowed kernel (the
+// clamp and wrap footprints need no out-of-range masks).
+template <int FILTER, int CT>
+hipError_t launch_tex_bwd_win(const TexBwdArgs& args, int total_tiles, hipStream_t stream) {
+  if (args.boundary == DR_BOUNDARY_CLAMP)
+    return launch_tex_bwd_win_b<FILTER, CT, DR_BOUNDARY_CLAMP>(args, total_tiles, stream);
+  if (args.boundary == DR_BOUNDARY_WRAP)
+    return launch_tex_bwd_win_b<FILTER, CT, DR_BOUNDARY_WRAP>(args, total_tiles, stream);
+  return launch_tex_bwd_win_b<FILTER, CT, DR_BOUNDARY_ZERO>(args, total_tiles, stream);
 }
 
 // Launches the persistent backward with as many workgroups as fit on the
@@ -1661,24 +1678,31 @@ static int check_tex(const float* tex, const float* pyr, int Nt, int N, int Ht, 
   return build_desc(Ht, Wt, C, ntex, 1, md);
 }
 
-#define DR_TEX_C_DISPATCH(KERNEL, F, CUBEV, GRID, ...)                                       \
+#define DR_TEX_C_DISPATCH(KERNEL, F, BNDV, GRID, ...)                                        \
   do {                                                                                        \
     switch (C) {                                                                              \
-      case 1: hipLaunchKernelGGL((KERNEL<F, CUBEV, 1>), GRID, dim3(256), 0, stream, __VA_ARGS__); break; \
-      case 2: hipLaunchKernelGGL((KERNEL<F, CUBEV, 2>), GRID, dim3(256), 0, stream, __VA_ARGS__); break; \
-      case 3: hipLaunchKernelGGL((KERNEL<F, CUBEV, 3>), GRID, dim3(256), 0, stream, __VA_ARGS__); break; \
-      case 4: hipLaunchKernelGGL((KERNEL<F, CUBEV, 4>), GRID, dim3(256), 0, stream, __VA_ARGS__); break; \
-      default: hipLaunchKernelGGL((KERNEL<F, CUBEV, 0>), GRID, dim3(256), 0, stream, __VA_ARGS__); break; \
+      case 1: hipLaunchKernelGGL((KERNEL<F, BNDV, 1>), GRID, dim3(256), 0, stream, __VA_ARGS__); break; \
+      case 2: hipLaunchKernelGGL((KERNEL<F, BNDV, 2>), GRID, dim3(256), 0, stream, __VA_ARGS__); break; \
+      case 3: hipLaunchKernelGGL((KERNEL<F, BNDV, 3>), GRID, dim3(256), 0, stream, __VA_ARGS__); break; \
+      case 4: hipLaunchKernelGGL((KERNEL<F, BNDV, 4>), GRID, dim3(256), 0, stream, __VA_ARGS__); break; \
+      default: hipLaunchKernelGGL((KERNEL<F, BNDV, 0>), GRID, dim3(256), 0, stream, __VA_ARGS__); break; \
     }                                                                                         \
+  } while (0)
+
+#define DR_TEX_B_DISPATCH(KERNEL, F, GRID, ...)                                                          \
+  do {                                                                                                  \
+    if (boundary == DR_BOUNDARY_CLAMP) DR_TEX_C_DISPATCH(KERNEL, F, DR_BOUNDARY_CLAMP, GRID, __VA_ARGS__); \
+    else if (boundary == DR_BOUNDARY_WRAP) DR_TEX_C_DISPATCH(KERNEL, F, DR_BOUNDARY_WRAP, GRID, __VA_ARGS__); \
+    else DR_TEX_C_DISPATCH(KERNEL, F, DR_BOUNDARY_ZERO, GRID, __VA_ARGS__);                             \
   } while (0)
 
 #define DR_TEX_DISPATCH(KERNEL, GRID, ...)                                                              \
   do {                                                                                                  \
-    if (boundary == DR_BOUNDARY_CUBE) DR_TEX_C_DISPATCH(KERNEL, DR_FILTER_LINEAR, true, GRID, __VA_ARGS__); \
-    else if (filter == DR_FILTER_NEAREST) DR_TEX_C_DISPATCH(KERNEL, DR_FILTER_NEAREST, false, GRID, __VA_ARGS__); \
-    else if (filter == DR_FILTER_LINEAR) DR_TEX_C_DISPATCH(KERNEL, DR_FILTER_LINEAR, false, GRID, __VA_ARGS__); \
-    else if (filter == DR_FILTER_LINEAR_MIPMAP_NEAREST) DR_TEX_C_DISPATCH(KERNEL, DR_FILTER_LINEAR_MIPMAP_NEAREST, false, GRID, __VA_ARGS__); \
-    else DR_TEX_C_DISPATCH(KERNEL, DR_FILTER_LINEAR_MIPMAP_LINEAR, false, GRID, __VA_ARGS__);   \
+    if (boundary == DR_BOUNDARY_CUBE) DR_TEX_C_DISPATCH(KERNEL, DR_FILTER_LINEAR, DR_BOUNDARY_CUBE, GRID, __VA_ARGS__); \
+    else if (filter == DR_FILTER_NEAREST) DR_TEX_B_DISPATCH(KERNEL, DR_FILTER_NEAREST, GRID, __VA_ARGS__); \
+    else if (filter == DR_FILTER_LINEAR) DR_TEX_B_DISPATCH(KERNEL, DR_FILTER_LINEAR, GRID, __VA_ARGS__); \
+    else if (filter == DR_FILTER_LINEAR_MIPMAP_NEAREST) DR_TEX_B_DISPATCH(KERNEL, DR_FILTER_LINEAR_MIPMAP_NEAREST, GRID, __VA_ARGS__); \
+    else DR_TEX_B_DISPATCH(KERNEL, DR_FILTER_LINEAR_MIPMAP_LINEAR, GRID, __VA_ARGS__);   \
   } while (0)
 
 // d_tex += the pyramid's gradient (the backward of the 2x2 means).
@@ -1766,7 +1790,7 @@ extern "C" int dr_texture_fwd(const float* tex, const float* pyramid, int Nt, in
   }
   DR_TIMED("k_tex_fwd", stream);
   DR_TEX_DISPATCH(k_tex_fwd, grid, tex, pyramid, md, tex_stride, Ht, Wt, C, uv, uv_da, bias_map,
-                  scale_bias, has_bias, boundary, P, Hi * Wi, out);
+                  scale_bias, has_bias, P, Hi * Wi, out);
   DR_CHECK_LAUNCH();
   return DR_OK;
 }
