@@ -738,7 +738,7 @@ __device__ __forceinline__ void slot_box(const TapSlot& q, int& x0, int& x1, int
 }
 
 
-template <int FILTER, int CT, int BND>
+template <int FILTER, int CT, int BND, bool BIAS>
 // Five workgroups per CU (the register budget this asks for costs a few
 // spilled values, measured cheaper than four resident workgroups).
 __global__ void __launch_bounds__(256, 5) k_tex_bwd_win(TexBwdArgs A, int total_tiles) {
@@ -790,8 +790,10 @@ __global__ void __launch_bounds__(256, 5) k_tex_bwd_win(TexBwdArgs A, int total_
     bool scaled = false;
     if (mip) {
       da_in = *reinterpret_cast<const float4*>(A.uv_da + pix * 4);
-      s = bias_scale(A.bias_map, pix, A.scale_bias, A.has_bias != 0);
-      scaled = A.bias_map || A.has_bias;
+      if (BIAS) {
+        s = bias_scale(A.bias_map, pix, A.scale_bias, A.has_bias != 0);
+        scaled = true;
+      }
       da = scaled ? make_float4(da_in.x * s, da_in.y * s, da_in.z * s, da_in.w * s) : da_in;
       const Lod ld = mip_lod(da, A.Ht, A.Wt, md.L, FILTER == DR_FILTER_LINEAR_MIPMAP_LINEAR);
       q[0].k = ld.k0;
@@ -861,7 +863,7 @@ __global__ void __launch_bounds__(256, 5) k_tex_bwd_win(TexBwdArgs A, int total_
         const float4 o = scaled ? make_float4(d_eff.x * s, d_eff.y * s, d_eff.z * s, d_eff.w * s) : d_eff;
         *reinterpret_cast<float4*>(A.d_uv_da + pix * 4) = o;
       }
-      if (A.d_bias && A.bias_map) {
+      if (BIAS && A.d_bias && A.bias_map) {
         const float gm = d_eff.x * da_in.x + d_eff.y * da_in.y + d_eff.z * da_in.z + d_eff.w * da_in.w;
         A.d_bias[pix] = gm * s * 0.6931471805599453f;
       }
@@ -1192,12 +1194,12 @@ __global__ void __launch_bounds__(256) k_mip_collapse0_c4(const float* __restric
   *dp = make_float4(d.x + t.x * 0.25f, d.y + t.y * 0.25f, d.z + t.z * 0.25f, d.w + t.w * 0.25f);
 }
 
-template <int FILTER, int CT, int BND>
-hipError_t launch_tex_bwd_win_b(const TexBwdArgs& args, int total_tiles, hipStream_t stream) {
+template <int FILTER, int CT, int BND, bool BIAS>
+hipError_t launch_tex_bwd_win_bb(const TexBwdArgs& args, int total_tiles, hipStream_t stream) {
   static int per_cu = 0;
   if (per_cu == 0) {
     int b = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, k_tex_bwd_win<FILTER, CT, BND>, 256, 0) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, k_tex_bwd_win<FILTER, CT, BND, BIAS>, 256, 0) !=
             hipSuccess ||
         b <= 0)
       b = 2;
@@ -1205,9 +1207,16 @@ hipError_t launch_tex_bwd_win_b(const TexBwdArgs& args, int total_tiles, hipStre
   }
   const int64_t resident = (int64_t)device_cu_count() * per_cu;
   const unsigned grid = (unsigned)(total_tiles < resident ? total_tiles : resident);
-  hipLaunchKernelGGL((k_tex_bwd_win<FILTER, CT, BND>), dim3(grid), dim3(256), 0, stream, args,
-                     total_tiles);
+  hipLaunchKernelGGL((k_tex_bwd_win<FILTER, CT, BND, BIAS>), dim3(grid), dim3(256), 0, stream,
+                     args, total_tiles);
   return hipGetLastError();
+}
+
+template <int FILTER, int CT, int BND>
+hipError_t launch_tex_bwd_win_b(const TexBwdArgs& args, int total_tiles, hipStream_t stream) {
+  if (args.bias_map || args.has_bias)
+    return launch_tex_bwd_win_bb<FILTER, CT, BND, true>(args, total_tiles, stream);
+  return launch_tex_bwd_win_bb<FILTER, CT, BND, false>(args, total_tiles, stream);
 }
 
 // The boundary mode is a compile-time constant of the windowed kernel (the
