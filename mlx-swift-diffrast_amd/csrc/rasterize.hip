@@ -212,6 +212,73 @@ __global__ void __launch_bounds__(256) k_bin_fill(Items it, int64_t n_items, int
   }
 }
 
+// Binning through LDS (used while an image has at most kBinLdsTiles tiles):
+// one workgroup per (image, chunk of kBinChunk items of that image).  The
+// chunk's per-tile counts are taken with LDS atomics; one global atomic per
+// touched tile then adds them to the tile's count (consecutive lanes on
+// consecutive tiles, so a wave's atomics share few cache lines) and, when
+// filling, returns where the chunk's slots start; a second LDS pass hands
+// the slots out.  Raster results do not depend on list order (ties go to
+// the lower triangle id).
+constexpr int kBinChunk = 1024;
+constexpr int kBinLdsTiles = 16384;
+
+template <bool FILL>
+__global__ void __launch_bounds__(256) k_bin_lds(Items it, int chunks,
+                                                 const int4* __restrict__ rect, int ntx,
+                                                 int tiles, int* __restrict__ cnt,
+                                                 int* __restrict__ list, int cap) {
+  extern __shared__ int s_tile[];
+  const int n = (int)blockIdx.x / chunks;
+  const int c = (int)blockIdx.x - n * chunks;
+  int64_t i0, i1, r0;  // items [i0, i1) of image n; item i uses record r0 + (i - i0)
+  if (it.prefix) {
+    i0 = it.prefix[n];
+    i1 = it.prefix[n + 1];
+    r0 = it.start[n];
+  } else {
+    i0 = (int64_t)n * it.T;
+    i1 = i0 + it.T;
+    r0 = i0;
+  }
+  const int64_t b0 = i0 + (int64_t)c * kBinChunk;
+  const int64_t b1 = min(i1, b0 + kBinChunk);
+  if (b0 >= b1) return;  // uniform over the workgroup
+  const int tid = threadIdx.x;
+  for (int k = tid; k < tiles; k += 256) s_tile[k] = 0;
+  __syncthreads();
+  for (int64_t i = b0 + tid; i < b1; i += 256) {
+    const int4 rc = rect[r0 + (i - i0)];
+    if (rc.x < 0) continue;
+    for (int y = rc.z; y <= rc.w; ++y)
+      for (int x = rc.x; x <= rc.y; ++x) atomicAdd(&s_tile[y * ntx + x], 1);
+  }
+  __syncthreads();
+  int* cimg = cnt + (int64_t)n * tiles;
+  for (int k = tid; k < tiles; k += 256) {
+    const int v = s_tile[k];
+    if (v > 0) {
+      const int at = atomicAdd(&cimg[k], v);
+      if (FILL) s_tile[k] = at;
+    }
+  }
+  if (!FILL) return;
+  __syncthreads();
+  int* limg = list + (int64_t)n * tiles * cap;
+  for (int64_t i = b0 + tid; i < b1; i += 256) {
+    const int64_t r = r0 + (i - i0);
+    const int4 rc = rect[r];
+    if (rc.x < 0) continue;
+    const int t = (int)(it.prefix ? r : i - i0);
+    for (int y = rc.z; y <= rc.w; ++y)
+      for (int x = rc.x; x <= rc.y; ++x) {
+        const int j = y * ntx + x;
+        const int p = atomicAdd(&s_tile[j], 1);
+        if (p < cap) limg[(int64_t)j * cap + p] = t;
+      }
+  }
+}
+
 struct Best {
   float z, u, v;
   int t;
@@ -539,18 +606,21 @@ using namespace dr;
 // in range mode, each image's clamped range, listed through a prefix sum
 // that is copied to the device (synchronously: the host vector is local).
 static int plan_items(Scratch* sc, hipStream_t stream, const int32_t* ranges_host, int N, int T,
-                      Items& it, int64_t& n_items) {
+                      Items& it, int64_t& n_items, int64_t& max_items) {
   it = Items{nullptr, nullptr, T};
   n_items = (int64_t)N * T;
+  max_items = T;
   if (!ranges_host) return DR_OK;
   std::vector<int64_t> h(2 * (size_t)N + 1);
   h[0] = 0;
+  max_items = 0;
   for (int n = 0; n < N; ++n) {
     int64_t s = ranges_host[2 * n], c = ranges_host[2 * n + 1];
     int64_t lo = s < 0 ? 0 : s, hi = s + c > T ? T : s + c;
     if (hi < lo) hi = lo;
     h[n + 1] = h[n] + (hi - lo);
     h[N + 1 + n] = lo;
+    max_items = std::max<int64_t>(max_items, hi - lo);
   }
   n_items = h[N];
   int64_t* d = (int64_t*)scratch_get(sc, stream, SLOT_RAST_ITEMS, h.size() * sizeof(int64_t));
@@ -578,6 +648,42 @@ static int check_raster_args(const float* pos, int64_t pos_batch_stride, const i
   return DR_OK;
 }
 
+// Workgroups per image of k_bin_lds, or 0 when the LDS path does not apply.
+static int bin_lds_chunks(int N, int tiles, int64_t max_items) {
+  const int64_t chunks = (max_items + kBinChunk - 1) / kBinChunk;
+  if (tiles > kBinLdsTiles || chunks == 0 || (int64_t)N * chunks > ((int64_t)1 << 23)) return 0;
+  return (int)chunks;
+}
+
+// Per-tile counts (FILL false) or counts and lists (FILL true) of the items.
+static void launch_binning(bool fill, const Items& it, int64_t n_items, int64_t max_items, int N,
+                           const int4* rect, int ntx, int tiles, int* cnt, int* list, int cap,
+                           hipStream_t stream) {
+  if (n_items == 0) return;
+  const int chunks = bin_lds_chunks(N, tiles, max_items);
+  if (chunks > 0) {
+    const dim3 grid((unsigned)((int64_t)N * chunks));
+    const size_t lds = (size_t)tiles * sizeof(int);
+    if (fill) {
+      DR_TIMED("k_bin_fill", stream);
+      hipLaunchKernelGGL(k_bin_lds<true>, grid, dim3(256), lds, stream, it, chunks, rect, ntx,
+                         tiles, cnt, list, cap);
+    } else {
+      DR_TIMED("k_bin_count", stream);
+      hipLaunchKernelGGL(k_bin_lds<false>, grid, dim3(256), lds, stream, it, chunks, rect, ntx,
+                         tiles, cnt, list, cap);
+    }
+  } else if (fill) {
+    DR_TIMED("k_bin_fill", stream);
+    hipLaunchKernelGGL(k_bin_fill, dim3(grid_for(n_items, 256)), dim3(256), 0, stream, it,
+                       n_items, N, rect, ntx, tiles, cnt, list, cap);
+  } else {
+    DR_TIMED("k_bin_count", stream);
+    hipLaunchKernelGGL(k_bin_count, dim3(grid_for(n_items, 256)), dim3(256), 0, stream, it,
+                       n_items, N, rect, ntx, tiles, cnt);
+  }
+}
+
 extern "C" int dr_rasterize_tile_counts(const float* pos, int64_t pos_batch_stride,
                                         const int32_t* tri, const int32_t* ranges_host, int N,
                                         int V, int T, int H, int W, int32_t* counts,
@@ -592,8 +698,8 @@ extern "C" int dr_rasterize_tile_counts(const float* pos, int64_t pos_batch_stri
   const int tiles = ntx * nty;
   const int64_t n_tiles = (int64_t)N * tiles;
   Items it;
-  int64_t n_items = 0;
-  st = plan_items(sc, stream, ranges_host, N, T, it, n_items);
+  int64_t n_items = 0, max_items = 0;
+  st = plan_items(sc, stream, ranges_host, N, T, it, n_items, max_items);
   if (st) return st;
   const int Npos = ranges_host ? 1 : N;
   const int64_t n_rec = (int64_t)Npos * T;
@@ -608,12 +714,9 @@ extern "C" int dr_rasterize_tile_counts(const float* pos, int64_t pos_batch_stri
     DR_CHECK_LAUNCH();
   }
   DR_CHECK_HIP(fill_async(counts, 0, n_tiles, stream));
-  if (n_items > 0) {
-    DR_TIMED("k_bin_count", stream);
-    hipLaunchKernelGGL(k_bin_count, dim3(grid_for(n_items, 256)), dim3(256), 0, stream, it,
-                       n_items, N, rect, ntx, tiles, (int*)counts);
-    DR_CHECK_LAUNCH();
-  }
+  launch_binning(false, it, n_items, max_items, N, rect, ntx, tiles, (int*)counts, nullptr, 0,
+                 stream);
+  DR_CHECK_LAUNCH();
   if (max_count_host) {
     int* tmax = small + 8;  // apart from the forward's read-back counter
     DR_CHECK_HIP(fill_async(tmax, 0, 1, stream));
@@ -645,8 +748,8 @@ extern "C" int dr_rasterize_fwd(const float* pos, int64_t pos_batch_stride, cons
 
   // Items: which (image, triangle) pairs are drawn.
   Items it;
-  int64_t n_items = 0;
-  st = plan_items(sc, stream, ranges_host, N, T, it, n_items);
+  int64_t n_items = 0, max_items = 0;
+  st = plan_items(sc, stream, ranges_host, N, T, it, n_items, max_items);
   if (st) return st;
   const int Npos = ranges_host ? 1 : N;
   const int64_t n_rec = (int64_t)Npos * T;
@@ -684,12 +787,8 @@ extern "C" int dr_rasterize_fwd(const float* pos, int64_t pos_batch_stride, cons
   if (C == 0) {
     DR_CHECK_HIP(fill_async(cnt, 0, n_tiles, stream));
     DR_CHECK_HIP(fill_async(tmax, 0, 1, stream));
-    if (n_items > 0) {
-      DR_TIMED("k_bin_count", stream);
-      hipLaunchKernelGGL(k_bin_count, dim3(grid_for(n_items, 256)), dim3(256), 0, stream, it,
-                         n_items, N, rect, ntx, tiles, cnt);
-      DR_CHECK_LAUNCH();
-    }
+    launch_binning(false, it, n_items, max_items, N, rect, ntx, tiles, cnt, nullptr, 0, stream);
+    DR_CHECK_LAUNCH();
     hipLaunchKernelGGL(k_tile_max, dim3(grid_for(n_tiles, 256)), dim3(256), 0, stream, cnt,
                        n_tiles, tmax);
     DR_CHECK_LAUNCH();
@@ -706,12 +805,8 @@ extern "C" int dr_rasterize_fwd(const float* pos, int64_t pos_batch_stride, cons
   if (!list) return DR_ERR_MEMORY;
 
   DR_CHECK_HIP(fill_async(fillc, 0, n_tiles, stream));
-  if (n_items > 0) {
-    DR_TIMED("k_bin_fill", stream);
-    hipLaunchKernelGGL(k_bin_fill, dim3(grid_for(n_items, 256)), dim3(256), 0, stream, it,
-                       n_items, N, rect, ntx, tiles, fillc, list, C);
-    DR_CHECK_LAUNCH();
-  }
+  launch_binning(true, it, n_items, max_items, N, rect, ntx, tiles, fillc, list, C, stream);
+  DR_CHECK_LAUNCH();
   const dim3 grid((unsigned)n_tiles), block(256);
 #define DR_RASTER(DBV, PV)                                                                    \
   hipLaunchKernelGGL((k_raster<DBV, PV>), grid, block, 0, stream, rec, rect, it, rec_stride, \
