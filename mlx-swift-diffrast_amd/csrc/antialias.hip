@@ -246,6 +246,16 @@ __device__ __forceinline__ AATile aa_load_tile(const float* __restrict__ rast, i
   return g;
 }
 
+// Blend-mask byte of pixel (n, h, w): 16x16 tiles in row-major order, 256
+// bytes each, a tile's 8x8 quadrants in the order of the waves that own
+// them and pixels row-major within a quadrant, so each wave writes and
+// reads 64 consecutive bytes.
+__device__ __forceinline__ int64_t mask_index(int n, int h, int w, int ntx, int nty) {
+  const int ly = h & 15, lx = w & 15;
+  return (((int64_t)n * nty + (h >> 4)) * ntx + (w >> 4)) * 256 +
+         ((ly >> 3) * 2 + (lx >> 3)) * 64 + (ly & 7) * 8 + (lx & 7);
+}
+
 // Neighbour of tile cell (r, c) (1-based, border included) in direction d:
 // 0 = +w, 1 = +h, 2 = -w, 3 = -h.
 __device__ __forceinline__ int aa_nb(int (*s_tri)[18], int r, int c, int d) {
@@ -298,7 +308,8 @@ __global__ void __launch_bounds__(256) k_aa_fwd(const float* __restrict__ rast,
                                                 const AARec* __restrict__ rec,
                                                 const float* __restrict__ color, int H, int W,
                                                 int T, int C, int ntx, int nty,
-                                                float* __restrict__ out) {
+                                                float* __restrict__ out,
+                                                uint8_t* __restrict__ blend_mask) {
   __shared__ int s_tri[18][18];
   const AATile g = aa_load_tile(rast, H, W, T, ntx, nty, s_tri);
   const int64_t pix = ((int64_t)g.n * H + min(g.ph, H - 1)) * W + min(g.pw, W - 1);
@@ -319,6 +330,7 @@ __global__ void __launch_bounds__(256) k_aa_fwd(const float* __restrict__ rast,
   }
   float alpha[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   bool blend = false;
+  int bits = 0;
   if (any) {
     const AARec* recn = rec + (int64_t)g.n * T;
     AARec rp;
@@ -330,9 +342,11 @@ __global__ void __launch_bounds__(256) k_aa_fwd(const float* __restrict__ rast,
       if (aa_pair(recn, rp, tp, tn[d], g.ph, g.pw, d, s)) {
         alpha[d] = s.alpha;
         blend = true;
+        bits |= 1 << d;
       }
     }
   }
+  if (blend_mask) blend_mask[mask_index(g.n, g.ph, g.pw, ntx, nty)] = (uint8_t)bits;
   if constexpr (CT > 0) {
     if (blend) {
       float acc[CT];
@@ -369,16 +383,10 @@ __global__ void __launch_bounds__(256) k_aa_fwd(const float* __restrict__ rast,
 
 // d_pos terms of one partial blend (Antialias.swift:405-495): the blend
 // weight's gradient d_alpha = sum_c g * (c_neighbour - c_own) through the
-// crossing point into the edge's two clip-space vertices.
-__device__ __forceinline__ bool aa_dpos_terms(const SilDir& s, int d, int ph, int pw, int Cn,
-                                              const float* __restrict__ gp,
-                                              const float* __restrict__ cpp,
-                                              const float* __restrict__ cnp,
-                                              const float* __restrict__ p, float* __restrict__ dp,
-                                              float halfW, float halfH, LdsTable<4, 128>& tab) {
-  float d_alpha = 0.0f;
-  for (int k = 0; k < Cn; ++k) d_alpha += gp[k] * (cnp[k] - cpp[k]);
-  if (d_alpha == 0.0f) return false;
+// crossing point into the edge's two clip-space vertices P0, P1.
+__device__ __forceinline__ void aa_dpos_add(const SilDir& s, int d, int ph, int pw, float d_alpha,
+                                            float4 P0, float4 P1, float* __restrict__ dp,
+                                            float halfW, float halfH, LdsTable<4, 128>& tab) {
   float dade0x, dade0y, dade1x, dade1y;
   const float inv_denom_sq = 1.0f / (s.denom * s.denom);
   if (d == 0 || d == 2) {
@@ -400,7 +408,7 @@ __device__ __forceinline__ bool aa_dpos_terms(const SilDir& s, int d, int ph, in
   const float dex[2] = {dade0x, dade1x}, dey[2] = {dade0y, dade1y};
 #pragma unroll
   for (int e = 0; e < 2; ++e) {
-    const float4 P = *reinterpret_cast<const float4*>(p + (int64_t)iv[e] * 4);
+    const float4 P = e == 0 ? P0 : P1;
     const float inv_w = 1.0f / P.w;
     const float nd_x = P.x * inv_w, nd_y = P.y * inv_w;
     const float dv[4] = {
@@ -408,6 +416,21 @@ __device__ __forceinline__ bool aa_dpos_terms(const SilDir& s, int d, int ph, in
         d_alpha * (dex[e] * (-halfW * nd_x) + dey[e] * (halfH * nd_y)) * inv_w};
     lds_table_add(tab, dp + (int64_t)iv[e] * 4, dv);
   }
+}
+
+// The same with d_alpha and the vertices loaded from global memory.
+__device__ __forceinline__ bool aa_dpos_terms(const SilDir& s, int d, int ph, int pw, int Cn,
+                                              const float* __restrict__ gp,
+                                              const float* __restrict__ cpp,
+                                              const float* __restrict__ cnp,
+                                              const float* __restrict__ p, float* __restrict__ dp,
+                                              float halfW, float halfH, LdsTable<4, 128>& tab) {
+  float d_alpha = 0.0f;
+  for (int k = 0; k < Cn; ++k) d_alpha += gp[k] * (cnp[k] - cpp[k]);
+  if (d_alpha == 0.0f) return false;
+  const float4 P0 = *reinterpret_cast<const float4*>(p + (int64_t)s.ie0 * 4);
+  const float4 P1 = *reinterpret_cast<const float4*>(p + (int64_t)s.ie1 * 4);
+  aa_dpos_add(s, d, ph, pw, d_alpha, P0, P1, dp, halfW, halfH, tab);
   return true;
 }
 
@@ -595,6 +618,187 @@ __global__ void __launch_bounds__(256) k_aa_bwd(const float* __restrict__ rast,
   lds_table_flush(tab);  // contains a barrier
 }
 
+// Backward with the forward's blend mask (bit d of a pixel set when its
+// blend weight toward direction d is nonzero).  Only the masked pairs are
+// evaluated: the tile's own pairs and the border pairs that point into the
+// tile are compacted into an LDS queue (it holds every pair of the tile, so
+// it cannot overflow); each thread takes one, recomputes its edge state
+// with the forward's expressions, leaves the blend weight for the d_color
+// exchange and, for the tile's own pixels, adds the d_pos terms.  Pixels
+// without blends load no record.  With CT > 0 the cotangents of the tile
+// and its border are staged in LDS before the first barrier (colours are
+// loaded only for the queued pairs: staging them measured slower).
+constexpr int kMaskQueue = 256 * 4 + 64;
+
+template <int CT>
+__global__ void __launch_bounds__(256) k_aa_bwd_masked(
+    const float* __restrict__ rast, const AARec* __restrict__ rec, const float* __restrict__ pos,
+    const float* __restrict__ color, const float* __restrict__ d_out,
+    const uint8_t* __restrict__ blend_mask, int H, int W, int V, int T, int C, int ntx, int nty,
+    float* __restrict__ d_color, float* __restrict__ d_pos, int accumulate) {
+  constexpr int CS = CT > 0 ? CT : 1;
+  constexpr int kCells = CT > 0 ? 18 * 18 : 1;
+  __shared__ int s_tri[18][18];
+  __shared__ float s_alpha[4][16][17];
+  __shared__ float s_halo[4][16];
+  __shared__ LdsTable<4, 128> tab;  // d_pos rows touched by this tile
+  __shared__ int s_q[kMaskQueue];   // (cell r * 18 + c) << 2 | direction
+  __shared__ int s_nq;
+  __shared__ float s_g[kCells][CS];  // d_out of the tile and its border (CT > 0)
+  if (d_pos) lds_table_clear(tab);
+  if (threadIdx.x == 0) s_nq = 0;
+  const AATile g = aa_load_tile(rast, H, W, T, ntx, nty, s_tri);
+  const int64_t pix = ((int64_t)g.n * H + min(g.ph, H - 1)) * W + min(g.pw, W - 1);
+  const int lx = g.lx, ly = g.ly;
+  const int own = (ly + 1) * 18 + (lx + 1);
+  if constexpr (CT > 0) {
+    if (g.inside) {
+      float v[CT];
+      ld_px<CT>(d_out + pix * CT, CT, v);
+#pragma unroll
+      for (int k = 0; k < CT; ++k) s_g[own][k] = v[k];
+
+    }
+  }
+  // 1) queue the masked pairs: own pixel (all four directions), and for
+  //    lanes 0..15 of each wave one border pixel's direction into the tile.
+  {
+    const int m = g.inside ? blend_mask[mask_index(g.n, g.ph, g.pw, ntx, nty)] : 0;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) s_alpha[d][ly][lx] = 0.0f;
+    int hm = 0, hcell = 0;
+    if ((threadIdx.x & 63) < 16) {
+      const int side = threadIdx.x >> 6, i = threadIdx.x & 15;
+      int qh, qw, rr, cc, qd;
+      if (side == 0) { qw = g.x0 - 1;  qh = g.y0 + i;  rr = i + 1; cc = 0;     qd = 0; }
+      else if (side == 1) { qw = g.x0 + 16; qh = g.y0 + i;  rr = i + 1; cc = 17;    qd = 2; }
+      else if (side == 2) { qw = g.x0 + i;  qh = g.y0 - 1;  rr = 0;     cc = i + 1; qd = 1; }
+      else { qw = g.x0 + i;  qh = g.y0 + 16; rr = 17;    cc = i + 1; qd = 3; }
+      s_halo[side][i] = 0.0f;
+      const bool in = qh >= 0 && qh < H && qw >= 0 && qw < W;
+      if (in) {
+        const int64_t q = ((int64_t)g.n * H + qh) * W + qw;
+        if constexpr (CT > 0) {
+          const int cell = rr * 18 + cc;
+          float v[CT];
+          ld_px<CT>(d_out + q * CT, CT, v);
+#pragma unroll
+          for (int k = 0; k < CT; ++k) s_g[cell][k] = v[k];
+
+        }
+        if ((blend_mask[mask_index(g.n, qh, qw, ntx, nty)] >> qd) & 1) {
+          hm = 1;
+          hcell = ((rr * 18 + cc) << 2) | qd;
+        }
+      }
+    }
+    const int cnt = __popc(m) + hm;
+    if (cnt) {
+      int slot = atomicAdd(&s_nq, cnt);
+#pragma unroll
+      for (int d = 0; d < 4; ++d)
+        if ((m >> d) & 1) s_q[slot++] = (own << 2) | d;
+      if (hm) s_q[slot] = hcell;
+    }
+  }
+  __syncthreads();
+  // 2) one queued pair per thread: blend weight and the d_pos terms.
+  const AARec* recn = rec + (int64_t)g.n * T;
+  const float* posn = pos + (int64_t)g.n * V * 4;
+  const int nq = s_nq;
+  for (int i = threadIdx.x; i < nq; i += blockDim.x) {
+    const int e = s_q[i];
+    const int d = e & 3, cell = e >> 2;
+    const int rr = cell / 18, cc = cell - rr * 18;
+    const int tq = s_tri[rr][cc];
+    const int tn = aa_nb(s_tri, rr, cc, d);
+    const int qph = g.y0 + rr - 1, qpw = g.x0 + cc - 1;
+    const bool border = rr == 0 || rr == 17 || cc == 0 || cc == 17;
+    // the foreground record (:206-222); a masked pair always has one
+    const AARec R = recn[tq >= 0 ? tq : tn];
+    float4 P[3];
+    if (d_pos && !border) {  // the edge is two of the record's vertices
+      P[0] = *reinterpret_cast<const float4*>(posn + (int64_t)R.tv.y * 4);
+      P[1] = *reinterpret_cast<const float4*>(posn + (int64_t)R.tv.z * 4);
+      P[2] = *reinterpret_cast<const float4*>(posn + (int64_t)R.tv.w * 4);
+    }
+    SilDir s;
+    const bool on = sil_geom(R, tq >= 0 ? tn : -1, qph, qpw, d, s);
+    const float al = on ? s.alpha : 0.0f;
+    if (border) {
+      const int side = cc == 0 ? 0 : cc == 17 ? 1 : rr == 0 ? 2 : 3;
+      s_halo[side][side < 2 ? rr - 1 : cc - 1] = al;
+      continue;
+    }
+    s_alpha[d][rr - 1][cc - 1] = al;
+    if (!d_pos || !on || !(s.alpha < 1.0f)) continue;
+    const int64_t qp = ((int64_t)g.n * H + qph) * W + qpw;
+    const int64_t qn = d == 0 ? qp + 1 : d == 1 ? qp + W : d == 2 ? qp - 1 : qp - W;
+    float d_alpha = 0.0f;
+    if constexpr (CT > 0) {
+      float cp[CT], cn[CT];
+      ld_px<CT>(color + qp * CT, CT, cp);
+      ld_px<CT>(color + qn * CT, CT, cn);
+#pragma unroll
+      for (int k = 0; k < CT; ++k) d_alpha += s_g[cell][k] * (cn[k] - cp[k]);
+    } else {
+      for (int k = 0; k < C; ++k)
+        d_alpha += d_out[qp * C + k] * (color[qn * C + k] - color[qp * C + k]);
+    }
+    if (d_alpha == 0.0f) continue;
+    const float4 P0 = s.ie0 == R.tv.y ? P[0] : s.ie0 == R.tv.z ? P[1] : P[2];
+    const float4 P1 = s.ie1 == R.tv.y ? P[0] : s.ie1 == R.tv.z ? P[1] : P[2];
+    aa_dpos_add(s, d, qph, qpw, d_alpha, P0, P1, d_pos + (int64_t)g.n * V * 4, (float)W * 0.5f,
+                (float)H * 0.5f, tab);
+  }
+  __syncthreads();
+  // 3) d_color: own term + what each neighbour's blend sends here.
+  if (d_color && g.inside) {
+    float asum = 0.0f;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) asum += s_alpha[d][ly][lx];
+    float wn[4];
+    wn[0] = lx < 15 ? s_alpha[2][ly][lx + 1] : s_halo[1][ly];  // right neighbour, its dir 2
+    wn[1] = ly < 15 ? s_alpha[3][ly + 1][lx] : s_halo[3][lx];  // lower neighbour, its dir 3
+    wn[2] = lx > 0 ? s_alpha[0][ly][lx - 1] : s_halo[0][ly];   // left neighbour, its dir 0
+    wn[3] = ly > 0 ? s_alpha[1][ly - 1][lx] : s_halo[2][lx];   // upper neighbour, its dir 1
+    if constexpr (CT > 0) {
+      const int nc[4] = {own + 1, own + 18, own - 1, own - 18};
+      float acc[CT];
+#pragma unroll
+      for (int k = 0; k < CT; ++k) acc[k] = s_g[own][k] * (1.0f - asum);
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        if (wn[d] > 0.0f) {
+#pragma unroll
+          for (int k = 0; k < CT; ++k) acc[k] += s_g[nc[d]][k] * wn[d];
+        }
+      }
+      if (accumulate) {
+        float old[CT];
+        ld_px<CT>(d_color + pix * CT, CT, old);
+#pragma unroll
+        for (int k = 0; k < CT; ++k) acc[k] = old[k] + acc[k];
+      }
+      st_px<CT>(d_color + pix * CT, acc);
+    } else {
+      const int64_t qn[4] = {pix + 1, pix + W, pix - 1, pix - W};
+      const float* gp = d_out + pix * C;
+      float* dc = d_color + pix * C;
+      for (int k = 0; k < C; ++k) {
+        float acc = gp[k] * (1.0f - asum);
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+          if (wn[d] > 0.0f) acc += d_out[qn[d] * C + k] * wn[d];
+        dc[k] = accumulate ? dc[k] + acc : acc;
+      }
+    }
+  }
+  if (!d_pos || nq == 0) return;  // uniform: nq was read after the barrier
+  __syncthreads();
+  lds_table_flush(tab);  // contains a barrier
+}
+
 }  // namespace dr
 
 using namespace dr;
@@ -672,10 +876,9 @@ static int aa_ct(int C, const void* a, const void* b, const void* c) {
     default: hipLaunchKernelGGL((KER<0>), __VA_ARGS__); break;                    \
   }
 
-extern "C" int dr_antialias_fwd(const float* color, const float* rast, const float* pos,
-                                const int32_t* tri, const int32_t* topo, int N, int H, int W,
-                                int C, int V, int T, float* out, dr_stream_t stream_) {
-  hipStream_t stream = (hipStream_t)stream_;
+static int aa_fwd(const float* color, const float* rast, const float* pos, const int32_t* tri,
+                  const int32_t* topo, int N, int H, int W, int C, int V, int T, float* out,
+                  uint8_t* blend_mask, hipStream_t stream) {
   (void)hipGetLastError();
   int st = check_aa(color, rast, pos, tri, topo, N, H, W, C, V, T);
   if (st) return st;
@@ -688,16 +891,15 @@ extern "C" int dr_antialias_fwd(const float* color, const float* rast, const flo
   const int ct = aa_ct(C, color, out, color);
   DR_TIMED("k_aa_fwd", stream);
   DR_AA_DISPATCH(k_aa_fwd, ct, grid, block, 0, stream, rast, rec, color, H, W, T, C, ntx, nty,
-                 out);
+                 out, blend_mask);
   DR_CHECK_LAUNCH();
   return DR_OK;
 }
 
-extern "C" int dr_antialias_bwd(const float* color, const float* rast, const float* pos,
-                                const int32_t* tri, const int32_t* topo, const float* d_out,
-                                int N, int H, int W, int C, int V, int T, float* d_color,
-                                float* d_pos, unsigned flags, dr_stream_t stream_) {
-  hipStream_t stream = (hipStream_t)stream_;
+static int aa_bwd(const float* color, const float* rast, const float* pos, const int32_t* tri,
+                  const int32_t* topo, const float* d_out, const uint8_t* blend_mask, int N,
+                  int H, int W, int C, int V, int T, float* d_color, float* d_pos,
+                  unsigned flags, hipStream_t stream) {
   (void)hipGetLastError();
   int st = check_aa(color, rast, pos, tri, topo, N, H, W, C, V, T);
   if (st) return st;
@@ -712,8 +914,52 @@ extern "C" int dr_antialias_bwd(const float* color, const float* rast, const flo
   const dim3 grid((unsigned)((int64_t)N * ntx * nty)), block(256);
   const int ct = aa_ct(C, color, d_out, d_color);
   DR_TIMED("k_aa_bwd", stream);
-  DR_AA_DISPATCH(k_aa_bwd, ct, grid, block, 0, stream, rast, rec, pos, color, d_out, H, W, V, T,
-                 C, ntx, nty, d_color, d_pos, acc ? 1 : 0);
+  if (blend_mask) {
+    DR_AA_DISPATCH(k_aa_bwd_masked, ct, grid, block, 0, stream, rast, rec, pos, color, d_out,
+                   blend_mask, H, W, V, T, C, ntx, nty, d_color, d_pos, acc ? 1 : 0);
+  } else {
+    DR_AA_DISPATCH(k_aa_bwd, ct, grid, block, 0, stream, rast, rec, pos, color, d_out, H, W, V,
+                   T, C, ntx, nty, d_color, d_pos, acc ? 1 : 0);
+  }
   DR_CHECK_LAUNCH();
   return DR_OK;
+}
+
+extern "C" int dr_antialias_fwd(const float* color, const float* rast, const float* pos,
+                                const int32_t* tri, const int32_t* topo, int N, int H, int W,
+                                int C, int V, int T, float* out, dr_stream_t stream) {
+  return aa_fwd(color, rast, pos, tri, topo, N, H, W, C, V, T, out, nullptr,
+                (hipStream_t)stream);
+}
+
+extern "C" int dr_antialias_bwd(const float* color, const float* rast, const float* pos,
+                                const int32_t* tri, const int32_t* topo, const float* d_out,
+                                int N, int H, int W, int C, int V, int T, float* d_color,
+                                float* d_pos, unsigned flags, dr_stream_t stream) {
+  return aa_bwd(color, rast, pos, tri, topo, d_out, nullptr, N, H, W, C, V, T, d_color, d_pos,
+                flags, (hipStream_t)stream);
+}
+
+extern "C" int64_t dr_antialias_mask_bytes(int N, int H, int W) {
+  if (N < 1 || H < 1 || W < 1) return -1;
+  return (int64_t)N * ((H + 15) / 16) * ((W + 15) / 16) * 256;
+}
+
+extern "C" int dr_antialias_fwd_mask(const float* color, const float* rast, const float* pos,
+                                     const int32_t* tri, const int32_t* topo, int N, int H,
+                                     int W, int C, int V, int T, float* out, uint8_t* blend_mask,
+                                     dr_stream_t stream) {
+  DR_CHECK_ARG(blend_mask != nullptr, "antialias_fwd_mask: null blend_mask");
+  return aa_fwd(color, rast, pos, tri, topo, N, H, W, C, V, T, out, blend_mask,
+                (hipStream_t)stream);
+}
+
+extern "C" int dr_antialias_bwd_mask(const float* color, const float* rast, const float* pos,
+                                     const int32_t* tri, const int32_t* topo,
+                                     const float* d_out, const uint8_t* blend_mask, int N, int H,
+                                     int W, int C, int V, int T, float* d_color, float* d_pos,
+                                     unsigned flags, dr_stream_t stream) {
+  DR_CHECK_ARG(blend_mask != nullptr, "antialias_bwd_mask: null blend_mask");
+  return aa_bwd(color, rast, pos, tri, topo, d_out, blend_mask, N, H, W, C, V, T, d_color, d_pos,
+                flags, (hipStream_t)stream);
 }

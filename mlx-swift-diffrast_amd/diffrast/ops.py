@@ -278,23 +278,37 @@ class _AntialiasFn(torch.autograd.Function):
         N, H, W, C = color.shape
         V, T = pos.shape[1], tri.shape[0]
         out = torch.empty_like(color)
-        _lib.check(lib.dr_antialias_fwd(_ptr(color), _ptr(rast), _ptr(pos), _ptr(tri), _ptr(topo),
-                                        N, H, W, C, V, T, _ptr(out), _stream()))
-        ctx.save_for_backward(color, pos, rast, tri, topo)
+        if ctx.needs_input_grad[0] or ctx.needs_input_grad[1]:
+            # the blend mask lets the backward skip the pixels without blends
+            mask = torch.empty(lib.dr_antialias_mask_bytes(N, H, W), dtype=torch.uint8,
+                               device=color.device)
+            _lib.check(lib.dr_antialias_fwd_mask(_ptr(color), _ptr(rast), _ptr(pos), _ptr(tri),
+                                                 _ptr(topo), N, H, W, C, V, T, _ptr(out),
+                                                 _ptr(mask), _stream()))
+        else:
+            mask = None
+            _lib.check(lib.dr_antialias_fwd(_ptr(color), _ptr(rast), _ptr(pos), _ptr(tri),
+                                            _ptr(topo), N, H, W, C, V, T, _ptr(out), _stream()))
+        ctx.save_for_backward(color, pos, rast, tri, topo, mask)
         return out
 
     @staticmethod
     def backward(ctx, d_out):
         lib = _lib.load()
-        color, pos, rast, tri, topo = ctx.saved_tensors
+        color, pos, rast, tri, topo, mask = ctx.saved_tensors
         N, H, W, C = color.shape
         V, T = pos.shape[1], tri.shape[0]
         d_out = d_out.to(torch.float32).contiguous()
         d_color = torch.empty_like(color) if ctx.needs_input_grad[0] else None
         d_pos = torch.empty_like(pos) if ctx.needs_input_grad[1] else None
-        _lib.check(lib.dr_antialias_bwd(_ptr(color), _ptr(rast), _ptr(pos), _ptr(tri), _ptr(topo),
-                                        _ptr(d_out), N, H, W, C, V, T, _ptr(d_color), _ptr(d_pos),
-                                        0, _stream()))
+        if mask is not None:
+            _lib.check(lib.dr_antialias_bwd_mask(_ptr(color), _ptr(rast), _ptr(pos), _ptr(tri),
+                                                 _ptr(topo), _ptr(d_out), _ptr(mask), N, H, W, C,
+                                                 V, T, _ptr(d_color), _ptr(d_pos), 0, _stream()))
+        else:
+            _lib.check(lib.dr_antialias_bwd(_ptr(color), _ptr(rast), _ptr(pos), _ptr(tri),
+                                            _ptr(topo), _ptr(d_out), N, H, W, C, V, T,
+                                            _ptr(d_color), _ptr(d_pos), 0, _stream()))
         return d_color, d_pos, None, None, None
 
 

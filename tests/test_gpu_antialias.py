@@ -115,3 +115,73 @@ def test_antialias_dense_edges(C):
     d_color, d_pos = O.antialias_vjp(color, rast, pos, tri, g)
     assert_grad_close(host(c.grad), d_color, "d_color")
     assert_grad_close(host(p.grad), d_pos, "d_pos")
+
+
+def aa_abi(color, rast, pos, tri, g, masked):
+    """Forward and backward straight through the C ABI: dr_antialias_fwd /
+    dr_antialias_bwd, or the _mask pair (forward writes the blend mask the
+    backward reads).  Returns out, mask (or None), d_color, d_pos."""
+    torch = torch_dev()
+    import diffrast._lib as L
+    from diffrast import DiffRast
+    from diffrast.ops import _ptr, _stream
+    lib = L.load()
+    N, H, W, C = color.shape
+    V, T = pos.shape[1], tri.shape[0]
+    c, r, p, t = dev(color), dev(rast), dev(pos), dev(tri)
+    topo = DiffRast.antialiasConstructTopologyHash(t)
+    out = torch.empty_like(c)
+    d_color = torch.empty_like(c)
+    d_pos = torch.empty_like(p)
+    gd = dev(g)
+    if masked:
+        mask = torch.full((lib.dr_antialias_mask_bytes(N, H, W),), 0xAA, dtype=torch.uint8,
+                          device="cuda")
+        L.check(lib.dr_antialias_fwd_mask(_ptr(c), _ptr(r), _ptr(p), _ptr(t), _ptr(topo), N, H, W,
+                                          C, V, T, _ptr(out), _ptr(mask), _stream()))
+        L.check(lib.dr_antialias_bwd_mask(_ptr(c), _ptr(r), _ptr(p), _ptr(t), _ptr(topo), _ptr(gd),
+                                          _ptr(mask), N, H, W, C, V, T, _ptr(d_color), _ptr(d_pos),
+                                          0, _stream()))
+    else:
+        mask = None
+        L.check(lib.dr_antialias_fwd(_ptr(c), _ptr(r), _ptr(p), _ptr(t), _ptr(topo), N, H, W, C, V,
+                                     T, _ptr(out), _stream()))
+        L.check(lib.dr_antialias_bwd(_ptr(c), _ptr(r), _ptr(p), _ptr(t), _ptr(topo), _ptr(gd), N, H,
+                                     W, C, V, T, _ptr(d_color), _ptr(d_pos), 0, _stream()))
+    if mask is not None:  # the header's byte order -> [N, H, W]
+        h, w = np.meshgrid(np.arange(H), np.arange(W), indexing="ij")
+        nty, ntx = -(-H // 16), -(-W // 16)
+        idx = ((h // 16) * ntx + w // 16) * 256 + ((h % 16) // 8 * 2 + (w % 16) // 8) * 64 + \
+            (h % 8) * 8 + w % 8
+        m = host(mask)
+        mask = np.stack([m[n * nty * ntx * 256 + idx] for n in range(N)])
+    return host(out), mask, host(d_color), host(d_pos)
+
+
+@pytest.mark.parametrize("scene", ["dense", "icosphere", "hexpie"])
+def test_antialias_mask_abi(scene):
+    """Both backward entry points against the oracle on the same inputs; the
+    forward's blend mask marks exactly the pixels that blend (random
+    colours, so a blend changes the pixel), in a tile-border-heavy scene
+    too.  The unmasked backward's d_pos queue overflows in the dense scene."""
+    torch_dev()
+    rng = np.random.default_rng(5)
+    if scene == "dense":
+        sc = scenes.textured_icosphere(N=2, H=128, W=128, level=5, tex_size=8)
+        pos, tri, H, W = sc["pos"], sc["tri"], 128, 128
+    else:
+        pos, tri, H, W = aa_scene(scene)
+    rast, _ = O.rasterize(pos, tri, (H, W), gradDB=False, max_per_tile=0)
+    N = pos.shape[0]
+    color = rng.random((N, H, W, 4)).astype(np.float32)
+    ref = O.antialias(color, rast, pos, tri)
+    g = rng.normal(size=ref.shape).astype(np.float32)
+    d_color, d_pos = O.antialias_vjp(color, rast, pos, tri, g)
+    for masked in (False, True):
+        out, mask, dc, dp = aa_abi(color, rast, pos, tri, g, masked)
+        assert_fwd_close(out, ref)
+        assert_grad_close(dc, d_color, f"d_color masked={masked}")
+        assert_grad_close(dp, d_pos, f"d_pos masked={masked}")
+        if masked:
+            assert mask.max() < 16
+            np.testing.assert_array_equal(mask != 0, (ref != color).any(-1))
