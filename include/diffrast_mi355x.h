@@ -130,10 +130,12 @@ int dr_rasterize_tile_counts(const float* pos, int64_t pos_batch_stride, const i
 
 /* VJP of DiffRast.rasterize: d_pos (same layout and batch stride as pos;
  * range mode accumulates all images into the shared [V,4]).  d_rast_db may
- * be NULL (gradDB = false). */
+ * be NULL (gradDB = false).  T = rows of tri; pixels whose triangle id is
+ * outside [0, T) contribute nothing. */
 int dr_rasterize_bwd(const float* pos, int64_t pos_batch_stride, const int32_t* tri,
                      const float* rast, const float* d_rast, const float* d_rast_db, int N,
-                     int V, int H, int W, float* d_pos, unsigned flags, dr_stream_t stream);
+                     int V, int T, int H, int W, float* d_pos, unsigned flags,
+                     dr_stream_t stream);
 
 /* ---- interpolate ----------------------------------------------------- */
 
@@ -222,30 +224,32 @@ int dr_antialias_bwd(const float* color, const float* rast, const float* pos,
                      int W, int C, int V, int T, float* d_color, float* d_pos, unsigned flags,
                      dr_stream_t stream);
 
-/* Size in bytes of the blend mask of an [N,H,W] image batch (-1 for bad
- * sizes): one byte per pixel of the image padded to 16x16 tiles. */
-int64_t dr_antialias_mask_bytes(int N, int H, int W);
+/* Size in bytes of the state dr_antialias_fwd_save keeps for the backward
+ * (-1 for bad sizes). */
+int64_t dr_antialias_saved_bytes(int N, int H, int W, int T);
 
-/* dr_antialias_fwd that also writes blend_mask (dr_antialias_mask_bytes
- * bytes).  One byte per pixel: bit d set when the pixel's blend weight
- * toward direction d is nonzero (d = 0 +w, 1 +h, 2 -w, 3 -h).  Byte of
- * pixel (n, h, w): ((n * ceil(H/16) + h/16) * ceil(W/16) + w/16) * 256 +
- * ((h%16)/8 * 2 + (w%16)/8) * 64 + (h%8) * 8 + w%8, so each 8x8 block of
- * pixels is 64 consecutive bytes.  Same `out` as dr_antialias_fwd.  The
- * reference recomputes the blend weights in its VJP
- * (Antialias.swift:118-128); the mask lets the backward skip the pixels
- * that do not blend. */
-int dr_antialias_fwd_mask(const float* color, const float* rast, const float* pos,
+/* dr_antialias_fwd that also fills `saved` (dr_antialias_saved_bytes bytes,
+ * 16-byte aligned) for dr_antialias_bwd_saved.  Same `out` as
+ * dr_antialias_fwd.  The reference recomputes the blend weights and the
+ * edge geometry in its VJP (Antialias.swift:118-128); the saved state lets
+ * the backward skip the pixels that do not blend and the per-triangle
+ * setup.  Its first N * ceil(H/16) * ceil(W/16) * 256 bytes are the blend
+ * mask, one byte per pixel: bit d set when the pixel's blend weight toward
+ * direction d is nonzero (d = 0 +w, 1 +h, 2 -w, 3 -h); the byte of pixel
+ * (n, h, w) is at ((n * ceil(H/16) + h/16) * ceil(W/16) + w/16) * 256 +
+ * ((h%16)/8 * 2 + (w%16)/8) * 64 + (h%8) * 8 + w%8 (each 8x8 block of
+ * pixels is 64 consecutive bytes).  The rest is opaque. */
+int dr_antialias_fwd_save(const float* color, const float* rast, const float* pos,
                           const int32_t* tri, const int32_t* topo, int N, int H, int W, int C,
-                          int V, int T, float* out, uint8_t* blend_mask, dr_stream_t stream);
+                          int V, int T, float* out, void* saved, dr_stream_t stream);
 
-/* dr_antialias_bwd given the blend_mask that dr_antialias_fwd_mask wrote
- * for the same color, rast, pos, tri and topo (other inputs give wrong
- * gradients).  Same results as dr_antialias_bwd. */
-int dr_antialias_bwd_mask(const float* color, const float* rast, const float* pos,
-                          const int32_t* tri, const int32_t* topo, const float* d_out,
-                          const uint8_t* blend_mask, int N, int H, int W, int C, int V, int T,
-                          float* d_color, float* d_pos, unsigned flags, dr_stream_t stream);
+/* dr_antialias_bwd given the state dr_antialias_fwd_save kept for the same
+ * color, rast, pos, tri and topo (other inputs give wrong gradients).  Same
+ * results as dr_antialias_bwd. */
+int dr_antialias_bwd_saved(const float* color, const float* rast, const float* pos,
+                           const int32_t* tri, const int32_t* topo, const float* d_out,
+                           const void* saved, int N, int H, int W, int C, int V, int T,
+                           float* d_color, float* d_pos, unsigned flags, dr_stream_t stream);
 
 /* ---- loss and optimizer of the inverse-rendering samples -------------- */
 

@@ -834,14 +834,16 @@ extern "C" int dr_antialias_topology(const int32_t* tri, int T, int32_t* topo,
   return DR_OK;
 }
 
+// Per-(image, triangle) records into rec (scratch when rec is null).
 static int aa_records(const float* pos, const int32_t* tri, const int32_t* topo, int N, int V,
-                      int T, int H, int W, hipStream_t stream, AARec** out) {
-  Scratch* sc = scratch_for(stream);
-  if (!sc) return DR_ERR_HIP;
+                      int T, int H, int W, hipStream_t stream, AARec* rec, AARec** out) {
   const int64_t nt = (int64_t)N * T;
-  AARec* rec = (AARec*)scratch_get(sc, stream, SLOT_AA_REC,
-                                   (size_t)(nt > 0 ? nt : 1) * sizeof(AARec));
-  if (!rec) return DR_ERR_MEMORY;
+  if (!rec) {
+    Scratch* sc = scratch_for(stream);
+    if (!sc) return DR_ERR_HIP;
+    rec = (AARec*)scratch_get(sc, stream, SLOT_AA_REC, (size_t)(nt > 0 ? nt : 1) * sizeof(AARec));
+    if (!rec) return DR_ERR_MEMORY;
+  }
   if (nt > 0) {
     DR_TIMED("k_aa_rec", stream);
     hipLaunchKernelGGL(k_aa_rec, dim3(grid_for(nt, 256)), dim3(256), 0, stream, pos, tri, topo,
@@ -850,6 +852,13 @@ static int aa_records(const float* pos, const int32_t* tri, const int32_t* topo,
   DR_CHECK_LAUNCH();
   *out = rec;
   return DR_OK;
+}
+
+// Saved state of dr_antialias_fwd_save: the blend mask (one byte per pixel
+// of the image padded to 16x16 tiles, a multiple of 256 bytes), then the
+// per-(image, triangle) records.
+static int64_t aa_mask_bytes(int N, int H, int W) {
+  return (int64_t)N * ((H + 15) / 16) * ((W + 15) / 16) * 256;
 }
 
 static int check_aa(const float* color, const float* rast, const float* pos, const int32_t* tri,
@@ -878,45 +887,55 @@ static int aa_ct(int C, const void* a, const void* b, const void* c) {
 
 static int aa_fwd(const float* color, const float* rast, const float* pos, const int32_t* tri,
                   const int32_t* topo, int N, int H, int W, int C, int V, int T, float* out,
-                  uint8_t* blend_mask, hipStream_t stream) {
+                  uint8_t* saved, hipStream_t stream) {
   (void)hipGetLastError();
   int st = check_aa(color, rast, pos, tri, topo, N, H, W, C, V, T);
   if (st) return st;
   DR_CHECK_ARG(out != nullptr, "antialias: null output");
+  DR_CHECK_ARG(((uintptr_t)saved & 15) == 0, "antialias_fwd_save: saved must be 16-byte aligned");
+  uint8_t* mask = saved;
   AARec* rec = nullptr;
-  int st2 = aa_records(pos, tri, topo, N, V, T, H, W, stream, &rec);
+  int st2 = aa_records(pos, tri, topo, N, V, T, H, W, stream,
+                       saved ? (AARec*)(saved + aa_mask_bytes(N, H, W)) : nullptr, &rec);
   if (st2) return st2;
   const int ntx = (W + 15) / 16, nty = (H + 15) / 16;
   const dim3 grid((unsigned)((int64_t)N * ntx * nty)), block(256);
   const int ct = aa_ct(C, color, out, color);
   DR_TIMED("k_aa_fwd", stream);
   DR_AA_DISPATCH(k_aa_fwd, ct, grid, block, 0, stream, rast, rec, color, H, W, T, C, ntx, nty,
-                 out, blend_mask);
+                 out, mask);
   DR_CHECK_LAUNCH();
   return DR_OK;
 }
 
 static int aa_bwd(const float* color, const float* rast, const float* pos, const int32_t* tri,
-                  const int32_t* topo, const float* d_out, const uint8_t* blend_mask, int N,
-                  int H, int W, int C, int V, int T, float* d_color, float* d_pos,
-                  unsigned flags, hipStream_t stream) {
+                  const int32_t* topo, const float* d_out, const uint8_t* saved, int N, int H,
+                  int W, int C, int V, int T, float* d_color, float* d_pos, unsigned flags,
+                  hipStream_t stream) {
   (void)hipGetLastError();
   int st = check_aa(color, rast, pos, tri, topo, N, H, W, C, V, T);
   if (st) return st;
   DR_CHECK_ARG(d_out != nullptr, "antialias_bwd: null d_out");
+  DR_CHECK_ARG(((uintptr_t)saved & 15) == 0, "antialias_bwd_saved: saved must be 16-byte aligned");
   if (!d_color && !d_pos) return DR_OK;
   const bool acc = (flags & DR_ACCUMULATE) != 0;
   if (d_pos && !acc) DR_CHECK_HIP(fill_async(d_pos, 0.0f, (int64_t)N * V * 4, stream));
-  AARec* rec = nullptr;
-  int st2 = aa_records(pos, tri, topo, N, V, T, H, W, stream, &rec);
-  if (st2) return st2;
+  const AARec* rec = nullptr;
+  if (saved) {  // the forward's records
+    rec = (const AARec*)(saved + aa_mask_bytes(N, H, W));
+  } else {
+    AARec* r = nullptr;
+    int st2 = aa_records(pos, tri, topo, N, V, T, H, W, stream, nullptr, &r);
+    if (st2) return st2;
+    rec = r;
+  }
   const int ntx = (W + 15) / 16, nty = (H + 15) / 16;
   const dim3 grid((unsigned)((int64_t)N * ntx * nty)), block(256);
   const int ct = aa_ct(C, color, d_out, d_color);
   DR_TIMED("k_aa_bwd", stream);
-  if (blend_mask) {
+  if (saved) {
     DR_AA_DISPATCH(k_aa_bwd_masked, ct, grid, block, 0, stream, rast, rec, pos, color, d_out,
-                   blend_mask, H, W, V, T, C, ntx, nty, d_color, d_pos, acc ? 1 : 0);
+                   saved, H, W, V, T, C, ntx, nty, d_color, d_pos, acc ? 1 : 0);
   } else {
     DR_AA_DISPATCH(k_aa_bwd, ct, grid, block, 0, stream, rast, rec, pos, color, d_out, H, W, V,
                    T, C, ntx, nty, d_color, d_pos, acc ? 1 : 0);
@@ -940,26 +959,26 @@ extern "C" int dr_antialias_bwd(const float* color, const float* rast, const flo
                 flags, (hipStream_t)stream);
 }
 
-extern "C" int64_t dr_antialias_mask_bytes(int N, int H, int W) {
-  if (N < 1 || H < 1 || W < 1) return -1;
-  return (int64_t)N * ((H + 15) / 16) * ((W + 15) / 16) * 256;
+extern "C" int64_t dr_antialias_saved_bytes(int N, int H, int W, int T) {
+  if (N < 1 || H < 1 || W < 1 || T < 0) return -1;
+  return aa_mask_bytes(N, H, W) + (int64_t)N * T * (int64_t)sizeof(AARec);
 }
 
-extern "C" int dr_antialias_fwd_mask(const float* color, const float* rast, const float* pos,
+extern "C" int dr_antialias_fwd_save(const float* color, const float* rast, const float* pos,
                                      const int32_t* tri, const int32_t* topo, int N, int H,
-                                     int W, int C, int V, int T, float* out, uint8_t* blend_mask,
+                                     int W, int C, int V, int T, float* out, void* saved,
                                      dr_stream_t stream) {
-  DR_CHECK_ARG(blend_mask != nullptr, "antialias_fwd_mask: null blend_mask");
-  return aa_fwd(color, rast, pos, tri, topo, N, H, W, C, V, T, out, blend_mask,
+  DR_CHECK_ARG(saved != nullptr, "antialias_fwd_save: null saved");
+  return aa_fwd(color, rast, pos, tri, topo, N, H, W, C, V, T, out, (uint8_t*)saved,
                 (hipStream_t)stream);
 }
 
-extern "C" int dr_antialias_bwd_mask(const float* color, const float* rast, const float* pos,
-                                     const int32_t* tri, const int32_t* topo,
-                                     const float* d_out, const uint8_t* blend_mask, int N, int H,
-                                     int W, int C, int V, int T, float* d_color, float* d_pos,
-                                     unsigned flags, dr_stream_t stream) {
-  DR_CHECK_ARG(blend_mask != nullptr, "antialias_bwd_mask: null blend_mask");
-  return aa_bwd(color, rast, pos, tri, topo, d_out, blend_mask, N, H, W, C, V, T, d_color, d_pos,
-                flags, (hipStream_t)stream);
+extern "C" int dr_antialias_bwd_saved(const float* color, const float* rast, const float* pos,
+                                      const int32_t* tri, const int32_t* topo,
+                                      const float* d_out, const void* saved, int N, int H,
+                                      int W, int C, int V, int T, float* d_color, float* d_pos,
+                                      unsigned flags, dr_stream_t stream) {
+  DR_CHECK_ARG(saved != nullptr, "antialias_bwd_saved: null saved");
+  return aa_bwd(color, rast, pos, tri, topo, d_out, (const uint8_t*)saved, N, H, W, C, V, T,
+                d_color, d_pos, flags, (hipStream_t)stream);
 }

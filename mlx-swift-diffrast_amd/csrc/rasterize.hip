@@ -477,7 +477,7 @@ __global__ void __launch_bounds__(256) k_raster(
 __global__ void __launch_bounds__(256) k_raster_bwd(
     const float* __restrict__ pos, int64_t pos_stride, const int32_t* __restrict__ tri,
     const float* __restrict__ rast, const float* __restrict__ d_rast,
-    const float* __restrict__ d_rast_db, int N, int H, int W, int ntx, int nty,
+    const float* __restrict__ d_rast_db, int N, int T, int H, int W, int ntx, int nty,
     float* __restrict__ d_pos) {
   __shared__ LdsTable<4, 256> tab;  // d_pos rows touched by this tile
   lds_table_clear(tab);
@@ -497,7 +497,7 @@ __global__ void __launch_bounds__(256) k_raster_bwd(
   const int64_t pix = ((int64_t)n * H + min(ph, H - 1)) * W + min(pw, W - 1);
   const float4 r = *reinterpret_cast<const float4*>(rast + pix * 4);
   const int t = f2i(r.w) - 1;
-  valid = valid && t >= 0;
+  valid = valid && t >= 0 && t < T;
   float val[12];
   int i0 = 0, i1 = 0, i2 = 0;
 #pragma unroll
@@ -837,10 +837,10 @@ extern "C" int dr_rasterize_fwd(const float* pos, int64_t pos_batch_stride, cons
 
 extern "C" int dr_rasterize_bwd(const float* pos, int64_t pos_batch_stride, const int32_t* tri,
                                 const float* rast, const float* d_rast, const float* d_rast_db,
-                                int N, int V, int H, int W, float* d_pos, unsigned flags,
+                                int N, int V, int T, int H, int W, float* d_pos, unsigned flags,
                                 dr_stream_t stream_) {
   hipStream_t stream = (hipStream_t)stream_;
-  DR_CHECK_ARG(N >= 1 && V >= 0 && H >= 1 && W >= 1, "rasterize_bwd: bad sizes");
+  DR_CHECK_ARG(N >= 1 && V >= 0 && T >= 0 && H >= 1 && W >= 1, "rasterize_bwd: bad sizes");
   DR_CHECK_ARG(pos && tri && rast && d_rast && d_pos, "rasterize_bwd: null tensor");
   DR_CHECK_ARG(pos_batch_stride == 0 || pos_batch_stride == (int64_t)V * 4,
                "rasterize_bwd: pos_batch_stride must be 0 or V*4");
@@ -851,7 +851,8 @@ extern "C" int dr_rasterize_bwd(const float* pos, int64_t pos_batch_stride, cons
   {
     DR_TIMED("k_raster_bwd", stream);
     hipLaunchKernelGGL(k_raster_bwd, dim3((unsigned)blocks), dim3(256), 0, stream, pos,
-                       pos_batch_stride, tri, rast, d_rast, d_rast_db, N, H, W, ntx, nty, d_pos);
+                       pos_batch_stride, tri, rast, d_rast, d_rast_db, N, T, H, W, ntx, nty,
+                       d_pos);
   }
   DR_CHECK_LAUNCH();
   return DR_OK;

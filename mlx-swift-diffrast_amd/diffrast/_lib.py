@@ -28,7 +28,7 @@ SIGNATURES = {
     "dr_profile_report": ([ctypes.c_char_p, _i], _i),
     "dr_rasterize_fwd": ([_p, _i64, _p, _p, _p, _i, _i, _i, _i, _i, _p, _p, _p], _i),
     "dr_rasterize_tile_counts": ([_p, _i64, _p, _p, _i, _i, _i, _i, _i, _p, _p, _p], _i),
-    "dr_rasterize_bwd": ([_p, _i64, _p, _p, _p, _p, _i, _i, _i, _i, _p, _u, _p], _i),
+    "dr_rasterize_bwd": ([_p, _i64, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p, _u, _p], _i),
     "dr_interpolate_fwd": ([_p, _i64, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p, _p, _p], _i),
     "dr_interpolate_bwd": ([_p, _i64, _p, _p, _p, _p, _i, _p, _p, _i, _i, _i, _i, _i, _p, _i64,
                             _p, _p, _u, _p], _i),
@@ -42,10 +42,10 @@ SIGNATURES = {
     "dr_antialias_topology": ([_p, _i, _p, _p], _i),
     "dr_antialias_fwd": ([_p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p, _p], _i),
     "dr_antialias_bwd": ([_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p, _p, _u, _p], _i),
-    "dr_antialias_mask_bytes": ([_i, _i, _i], _i64),
-    "dr_antialias_fwd_mask": ([_p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p, _p, _p], _i),
-    "dr_antialias_bwd_mask": ([_p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p, _p, _u,
-                               _p], _i),
+    "dr_antialias_saved_bytes": ([_i, _i, _i, _i], _i64),
+    "dr_antialias_fwd_save": ([_p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p, _p, _p], _i),
+    "dr_antialias_bwd_saved": ([_p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p, _p, _u,
+                                _p], _i),
     "dr_mse_loss": ([_p, _p, _i64, _p, _p, _p], _i),
     "dr_adam_step": ([_p, _p, _p, _p, _p, _p, _i64, _i, _f, _f, _f, _f, _p], _i),
 }

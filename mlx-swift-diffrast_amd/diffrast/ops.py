@@ -121,7 +121,7 @@ class _RasterizeFn(torch.autograd.Function):
         d_pos = torch.empty_like(pos)
         _lib.check(lib.dr_rasterize_bwd(
             _ptr(pos), 0 if range_mode else V * 4, _ptr(tri), _ptr(rast), _ptr(d_rast), _ptr(db),
-            N, V, H, W, _ptr(d_pos), 0, _stream()))
+            N, V, tri.shape[0], H, W, _ptr(d_pos), 0, _stream()))
         return d_pos, None, None, None, None, None, None
 
 
@@ -279,32 +279,34 @@ class _AntialiasFn(torch.autograd.Function):
         V, T = pos.shape[1], tri.shape[0]
         out = torch.empty_like(color)
         if ctx.needs_input_grad[0] or ctx.needs_input_grad[1]:
-            # the blend mask lets the backward skip the pixels without blends
-            mask = torch.empty(lib.dr_antialias_mask_bytes(N, H, W), dtype=torch.uint8,
-                               device=color.device)
-            _lib.check(lib.dr_antialias_fwd_mask(_ptr(color), _ptr(rast), _ptr(pos), _ptr(tri),
+            # the saved state (blend mask, edge records) spares the backward
+            # the pixels without blends and the per-triangle setup
+            saved = torch.empty(lib.dr_antialias_saved_bytes(N, H, W, T), dtype=torch.uint8,
+                                device=color.device)
+            _lib.check(lib.dr_antialias_fwd_save(_ptr(color), _ptr(rast), _ptr(pos), _ptr(tri),
                                                  _ptr(topo), N, H, W, C, V, T, _ptr(out),
-                                                 _ptr(mask), _stream()))
+                                                 _ptr(saved), _stream()))
         else:
-            mask = None
+            saved = None
             _lib.check(lib.dr_antialias_fwd(_ptr(color), _ptr(rast), _ptr(pos), _ptr(tri),
                                             _ptr(topo), N, H, W, C, V, T, _ptr(out), _stream()))
-        ctx.save_for_backward(color, pos, rast, tri, topo, mask)
+        ctx.save_for_backward(color, pos, rast, tri, topo, saved)
         return out
 
     @staticmethod
     def backward(ctx, d_out):
         lib = _lib.load()
-        color, pos, rast, tri, topo, mask = ctx.saved_tensors
+        color, pos, rast, tri, topo, saved = ctx.saved_tensors
         N, H, W, C = color.shape
         V, T = pos.shape[1], tri.shape[0]
         d_out = d_out.to(torch.float32).contiguous()
         d_color = torch.empty_like(color) if ctx.needs_input_grad[0] else None
         d_pos = torch.empty_like(pos) if ctx.needs_input_grad[1] else None
-        if mask is not None:
-            _lib.check(lib.dr_antialias_bwd_mask(_ptr(color), _ptr(rast), _ptr(pos), _ptr(tri),
-                                                 _ptr(topo), _ptr(d_out), _ptr(mask), N, H, W, C,
-                                                 V, T, _ptr(d_color), _ptr(d_pos), 0, _stream()))
+        if saved is not None:
+            _lib.check(lib.dr_antialias_bwd_saved(_ptr(color), _ptr(rast), _ptr(pos), _ptr(tri),
+                                                  _ptr(topo), _ptr(d_out), _ptr(saved), N, H, W,
+                                                  C, V, T, _ptr(d_color), _ptr(d_pos), 0,
+                                                  _stream()))
         else:
             _lib.check(lib.dr_antialias_bwd(_ptr(color), _ptr(rast), _ptr(pos), _ptr(tri),
                                             _ptr(topo), _ptr(d_out), N, H, W, C, V, T,

@@ -67,8 +67,8 @@ def test_rasterize_bwd_accumulate(chain):
     d_db = dev(rng.normal(size=c["db"].shape).astype(np.float32))
     d_pos = torch.empty_like(c["pos"])
     run = lambda fl: _lib.check(lib.dr_rasterize_bwd(
-        _p(c["pos"]), V * 4, _p(c["tri"]), _p(c["rast"]), _p(d_rast), _p(d_db), N, V, c["H"],
-        c["W"], _p(d_pos), fl, _s(torch)))
+        _p(c["pos"]), V * 4, _p(c["tri"]), _p(c["rast"]), _p(d_rast), _p(d_db), N, V,
+        c["tri"].shape[0], c["H"], c["W"], _p(d_pos), fl, _s(torch)))
     _twice(run, [d_pos], [True], rng)
 
 

@@ -119,8 +119,10 @@ def test_antialias_dense_edges(C):
 
 def aa_abi(color, rast, pos, tri, g, masked):
     """Forward and backward straight through the C ABI: dr_antialias_fwd /
-    dr_antialias_bwd, or the _mask pair (forward writes the blend mask the
-    backward reads).  Returns out, mask (or None), d_color, d_pos."""
+    dr_antialias_bwd, or dr_antialias_fwd_save / dr_antialias_bwd_saved
+    (the forward keeps state, the blend mask first, that the backward
+    reads).  Returns out, the blend mask as [N, H, W] (or None), d_color,
+    d_pos."""
     torch = torch_dev()
     import diffrast._lib as L
     from diffrast import DiffRast
@@ -135,13 +137,13 @@ def aa_abi(color, rast, pos, tri, g, masked):
     d_pos = torch.empty_like(p)
     gd = dev(g)
     if masked:
-        mask = torch.full((lib.dr_antialias_mask_bytes(N, H, W),), 0xAA, dtype=torch.uint8,
+        mask = torch.full((lib.dr_antialias_saved_bytes(N, H, W, T),), 0xAA, dtype=torch.uint8,
                           device="cuda")
-        L.check(lib.dr_antialias_fwd_mask(_ptr(c), _ptr(r), _ptr(p), _ptr(t), _ptr(topo), N, H, W,
+        L.check(lib.dr_antialias_fwd_save(_ptr(c), _ptr(r), _ptr(p), _ptr(t), _ptr(topo), N, H, W,
                                           C, V, T, _ptr(out), _ptr(mask), _stream()))
-        L.check(lib.dr_antialias_bwd_mask(_ptr(c), _ptr(r), _ptr(p), _ptr(t), _ptr(topo), _ptr(gd),
-                                          _ptr(mask), N, H, W, C, V, T, _ptr(d_color), _ptr(d_pos),
-                                          0, _stream()))
+        L.check(lib.dr_antialias_bwd_saved(_ptr(c), _ptr(r), _ptr(p), _ptr(t), _ptr(topo),
+                                           _ptr(gd), _ptr(mask), N, H, W, C, V, T, _ptr(d_color),
+                                           _ptr(d_pos), 0, _stream()))
     else:
         mask = None
         L.check(lib.dr_antialias_fwd(_ptr(c), _ptr(r), _ptr(p), _ptr(t), _ptr(topo), N, H, W, C, V,

@@ -208,3 +208,35 @@ def test_tile_capacity_overflow():
         r = check_fwd(p[None], tri, 32, 32)
         assert (r[..., 3] == T).all()
         torch.cuda.synchronize()
+
+
+def test_backward_ignores_foreign_triangle_ids():
+    """A rast whose triangle ids lie outside [0, T) (not one this mesh's
+    forward wrote) adds nothing at those pixels and reads nothing out of
+    bounds: d_pos equals that of the same rast with those pixels empty."""
+    torch = torch_dev()
+    import diffrast._lib as L
+    from diffrast.ops import _ptr, _stream
+    lib = L.load()
+    rng = np.random.default_rng(17)
+    sc = scenes.hex_pie(N=2, H=64, W=64)
+    pos, tri, H, W = sc["pos"], sc["tri"], 64, 64
+    rast, _ = O.rasterize(pos, tri, (H, W), gradDB=False, max_per_tile=0)
+    N, V, T = pos.shape[0], pos.shape[1], tri.shape[0]
+    bad = rng.random((N, H, W)) < 0.3
+    foreign = rast.copy()
+    foreign[..., 3][bad] = T + 1 + rng.integers(0, 1 << 20, size=int(bad.sum()))
+    emptied = rast.copy()
+    emptied[bad] = 0.0
+    # every device buffer stays referenced until the results are read back
+    pd, td = dev(pos), dev(tri)
+    g = dev(rng.normal(size=rast.shape).astype(np.float32))
+    out = []
+    for r in (foreign, emptied):
+        rd = dev(r)
+        d_pos = torch.empty((N, V, 4), device="cuda")
+        L.check(lib.dr_rasterize_bwd(_ptr(pd), V * 4, _ptr(td), _ptr(rd), _ptr(g), None, N, V, T,
+                                     H, W, _ptr(d_pos), 0, _stream()))
+        out.append(host(d_pos))
+    # same terms; only the order of the cross-tile fp32 atomics may differ
+    assert_grad_close(out[0], out[1], "d_pos with foreign ids")
