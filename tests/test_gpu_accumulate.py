@@ -130,3 +130,39 @@ def test_antialias_bwd_accumulate(chain, C):
         _p(color), _p(c["rast"]), _p(c["pos"]), _p(c["tri"]), _p(c["topo"]), _p(d_out), N, H,
         W, C, V, T, _p(d_color), _p(d_pos), fl, _s(torch)))
     _twice(run, [d_color, d_pos], [True, True], rng)
+
+
+@pytest.mark.parametrize("C", [4, 3, 5])
+def test_antialias_bwd_saved_accumulate(chain, C):
+    """The same through dr_antialias_fwd_save / dr_antialias_bwd_saved (C 3
+    and 5 take the other kernel instantiations), and the saved pair's
+    gradients equal the plain pair's."""
+    from diffrast import _lib
+    lib, c = _lib.load(), chain
+    torch = c["torch"]
+    rng = np.random.default_rng(40 + C)
+    N, V = c["pos"].shape[:2]
+    T = c["tri"].shape[0]
+    H, W = c["H"], c["W"]
+    color = dev(rng.random((N, H, W, C)).astype(np.float32))
+    d_out = dev(rng.normal(size=(N, H, W, C)).astype(np.float32))
+    out = torch.empty_like(color)
+    saved = torch.empty(lib.dr_antialias_saved_bytes(N, H, W, T), dtype=torch.uint8,
+                        device="cuda")
+    _lib.check(lib.dr_antialias_fwd_save(_p(color), _p(c["rast"]), _p(c["pos"]), _p(c["tri"]),
+                                         _p(c["topo"]), N, H, W, C, V, T, _p(out), _p(saved),
+                                         _s(torch)))
+    d_color = torch.empty_like(color)
+    d_pos = torch.empty_like(c["pos"])
+    run = lambda fl: _lib.check(lib.dr_antialias_bwd_saved(
+        _p(color), _p(c["rast"]), _p(c["pos"]), _p(c["tri"]), _p(c["topo"]), _p(d_out),
+        _p(saved), N, H, W, C, V, T, _p(d_color), _p(d_pos), fl, _s(torch)))
+    _twice(run, [d_color, d_pos], [True, True], rng)
+    plain_c = torch.empty_like(color)
+    plain_p = torch.empty_like(c["pos"])
+    _lib.check(lib.dr_antialias_bwd(_p(color), _p(c["rast"]), _p(c["pos"]), _p(c["tri"]),
+                                    _p(c["topo"]), _p(d_out), N, H, W, C, V, T, _p(plain_c),
+                                    _p(plain_p), 0, _s(torch)))
+    run(0)
+    assert_grad_close(host(d_color), host(plain_c), "d_color saved vs plain")
+    assert_grad_close(host(d_pos), host(plain_p), "d_pos saved vs plain")
