@@ -240,3 +240,22 @@ def test_backward_ignores_foreign_triangle_ids():
         out.append(host(d_pos))
     # same terms; only the order of the cross-tile fp32 atomics may differ
     assert_grad_close(out[0], out[1], "d_pos with foreign ids")
+
+
+def test_many_tiles_binning_path():
+    """An image of more than 16,384 tiles (16 x 262,160 pixels, 16,385
+    tiles) takes the binning without LDS counters; the result is the same
+    as the oracle's, including the tile counts."""
+    torch = torch_dev()
+    import diffrast._lib as L
+    from diffrast import DiffRast
+    rng = np.random.default_rng(23)
+    H, W, T = 16, 16 * 16385, 400
+    xyz = rng.uniform(-1.1, 1.1, size=(1, 3 * T, 3)).astype(np.float32)
+    xyz[..., 0] = np.repeat(rng.uniform(-1.0, 1.0, size=(1, T)), 3, axis=1) + \
+        rng.uniform(-2e-3, 2e-3, size=(1, 3 * T))  # narrow triangles across the width
+    pos = np.concatenate([xyz, np.ones((1, 3 * T, 1), np.float32)], 2).astype(np.float32)
+    tri = np.arange(3 * T, dtype=np.int32).reshape(T, 3)
+    check_fwd(pos, tri, H, W, gradDB=True)
+    counts = host(DiffRast.rasterizeTileCounts(dev(pos), dev(tri), (H, W)))
+    np.testing.assert_array_equal(counts, O.rasterize_tile_counts(pos, tri, (H, W)))
