@@ -306,15 +306,24 @@ __device__ __forceinline__ void tex_fwd_px(
 
 // BND: the boundary mode as a compile-time constant (DR_BOUNDARY_CUBE for
 // cube maps), so the clamp and wrap footprints carry no out-of-range masks.
+// One workgroup per 16x16 pixel tile, a 16x4 strip per wave: neighbouring
+// pixels sample neighbouring texels, so a wave's gathers share cache lines
+// (measured 0.105 -> 0.089 ms at 8 x 1024^2 against whole pixel rows).
 template <int FILTER, int BND, int CT>
 __global__ void __launch_bounds__(256) k_tex_fwd(
     const float* __restrict__ tex, const float* __restrict__ pyr, MipDesc md, int64_t tex_stride,
     int Ht, int Wt, int C_, const float* __restrict__ uv, const float* __restrict__ uv_da,
-    const float* __restrict__ bias_map, float scale_bias, int has_bias, int64_t P,
-    int HWi, float* __restrict__ out) {
+    const float* __restrict__ bias_map, float scale_bias, int has_bias, int64_t P, int Hi,
+    int Wi, float* __restrict__ out) {
+  const int ntx = (Wi + 15) >> 4, tiles = ntx * ((Hi + 15) >> 4);
+  const int b = (int)blockIdx.x, n = b / tiles, tile = b - n * tiles;
+  const int ty = tile / ntx, tx = tile - ty * ntx;
+  const int ph = ty * 16 + ((int)threadIdx.x >> 4), pw = tx * 16 + ((int)threadIdx.x & 15);
+  // pixels past the image's right or bottom edge get index P: no work
+  const int64_t pix = ph < Hi && pw < Wi ? ((int64_t)n * Hi + ph) * Wi + pw : P;
   tex_fwd_px<FILTER, BND == DR_BOUNDARY_CUBE, CT>(tex, pyr, md, tex_stride, Ht, Wt, C_, uv, uv_da,
-                                                  bias_map, scale_bias, has_bias, BND, P, HWi, out,
-                               (int64_t)blockIdx.x * blockDim.x + threadIdx.x);
+                                                  bias_map, scale_bias, has_bias, BND, P, Hi * Wi,
+                                                  out, pix);
 }
 
 // ---------------------------------------------------------------------------
@@ -1797,9 +1806,11 @@ extern "C" int dr_texture_fwd(const float* tex, const float* pyramid, int Nt, in
     DR_CHECK_LAUNCH();
     return DR_OK;
   }
+  const int64_t px_tiles = (int64_t)N * ((Hi + 15) / 16) * ((Wi + 15) / 16);
+  DR_CHECK_ARG(px_tiles < ((int64_t)1 << 31), "texture: too many pixels");
   DR_TIMED("k_tex_fwd", stream);
-  DR_TEX_DISPATCH(k_tex_fwd, grid, tex, pyramid, md, tex_stride, Ht, Wt, C, uv, uv_da, bias_map,
-                  scale_bias, has_bias, P, Hi * Wi, out);
+  DR_TEX_DISPATCH(k_tex_fwd, dim3((unsigned)px_tiles), tex, pyramid, md, tex_stride, Ht, Wt, C, uv,
+                  uv_da, bias_map, scale_bias, has_bias, P, Hi, Wi, out);
   DR_CHECK_LAUNCH();
   return DR_OK;
 }
