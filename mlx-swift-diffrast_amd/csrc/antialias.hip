@@ -663,7 +663,7 @@ __global__ void __launch_bounds__(256) k_aa_bwd_masked(
   // 1) queue the masked pairs: own pixel (all four directions), and for
   //    lanes 0..15 of each wave one border pixel's direction into the tile.
   {
-    const int m = g.inside ? blend_mask[mask_index(g.n, g.ph, g.pw, ntx, nty)] : 0;
+    const int m = g.inside ? blend_mask[mask_index(g.n, g.ph, g.pw, ntx, nty)] & 15 : 0;
 #pragma unroll
     for (int d = 0; d < 4; ++d) s_alpha[d][ly][lx] = 0.0f;
     int hm = 0, hcell = 0;
@@ -712,9 +712,12 @@ __global__ void __launch_bounds__(256) k_aa_bwd_masked(
     const int rr = cell / 18, cc = cell - rr * 18;
     const int tq = s_tri[rr][cc];
     const int tn = aa_nb(s_tri, rr, cc, d);
+    // a mask the forward wrote only marks candidate pairs; anything else is
+    // skipped, so no mask content can make the record index go out of range
+    if (!aa_cand(tq, tn)) continue;
     const int qph = g.y0 + rr - 1, qpw = g.x0 + cc - 1;
     const bool border = rr == 0 || rr == 17 || cc == 0 || cc == 17;
-    // the foreground record (:206-222); a masked pair always has one
+    // the foreground record (:206-222): the pixel's own, else the neighbour's
     const AARec R = recn[tq >= 0 ? tq : tn];
     float4 P[3];
     if (d_pos && !border) {  // the edge is two of the record's vertices

@@ -187,3 +187,36 @@ def test_antialias_mask_abi(scene):
         if masked:
             assert mask.max() < 16
             np.testing.assert_array_equal(mask != 0, (ref != color).any(-1))
+
+
+def test_antialias_saved_mask_superset():
+    """The backward re-derives every queued pair's blend weight, so a blend
+    mask with every bit set (also on pixels next to nothing, next to the
+    image border, or on empty pixels) gives the same gradients, and no mask
+    content can send a record or vertex read out of range."""
+    torch = torch_dev()
+    import diffrast._lib as L
+    from diffrast import DiffRast
+    from diffrast.ops import _ptr, _stream
+    lib = L.load()
+    rng = np.random.default_rng(9)
+    pos, tri, H, W = aa_scene("tier1")  # ragged 61 x 47, mostly empty pixels
+    rast, _ = O.rasterize(pos, tri, (H, W), gradDB=False, max_per_tile=0)
+    N, V, T, C = pos.shape[0], pos.shape[1], tri.shape[0], 4
+    color = rng.random((N, H, W, C)).astype(np.float32)
+    g = rng.normal(size=color.shape).astype(np.float32)
+    d_color, d_pos = O.antialias_vjp(color, rast, pos, tri, g)
+    c, r, p, t, gd = dev(color), dev(rast), dev(pos), dev(tri), dev(g)
+    topo = DiffRast.antialiasConstructTopologyHash(t)
+    out = torch.empty_like(c)
+    saved = torch.empty(lib.dr_antialias_saved_bytes(N, H, W, T), dtype=torch.uint8, device="cuda")
+    L.check(lib.dr_antialias_fwd_save(_ptr(c), _ptr(r), _ptr(p), _ptr(t), _ptr(topo), N, H, W, C,
+                                      V, T, _ptr(out), _ptr(saved), _stream()))
+    mask_bytes = N * (-(-H // 16)) * (-(-W // 16)) * 256
+    saved[:mask_bytes].fill_(0xFF)
+    dc, dp = torch.empty_like(c), torch.empty_like(p)
+    L.check(lib.dr_antialias_bwd_saved(_ptr(c), _ptr(r), _ptr(p), _ptr(t), _ptr(topo), _ptr(gd),
+                                       _ptr(saved), N, H, W, C, V, T, _ptr(dc), _ptr(dp), 0,
+                                       _stream()))
+    assert_grad_close(host(dc), d_color, "d_color, full mask")
+    assert_grad_close(host(dp), d_pos, "d_pos, full mask")
