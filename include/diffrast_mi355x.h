@@ -46,6 +46,12 @@
  *     of the last error on the calling thread is dr_get_last_error().
  *   - Host-memory arguments are named *_host; everything else is device
  *     memory.
+ *   - Indices are checked where they are used, so no input makes a kernel
+ *     read or write out of range: a triangle with a vertex id outside
+ *     [0, V) is not drawn and gets no gradient; a rast pixel whose triangle
+ *     id is outside [0, T) is empty for interpolate and the backward passes;
+ *     a diff_idx entry outside [0, A) gives zero derivatives.  (The
+ *     reference reads out of range in these cases.)
  */
 #ifndef DIFFRAST_MI355X_H
 #define DIFFRAST_MI355X_H
@@ -146,8 +152,8 @@ int dr_rasterize_bwd(const float* pos, int64_t pos_batch_stride, const int32_t* 
  *     (then K must equal A); out_da [N,H,W,2K]. */
 int dr_interpolate_fwd(const float* attr, int64_t attr_batch_stride, const float* rast,
                        const float* rast_db, const int32_t* tri, const int32_t* diff_idx,
-                       int K, int N, int H, int W, int V, int A, float* out, float* out_da,
-                       dr_stream_t stream);
+                       int K, int N, int H, int W, int V, int T, int A, float* out,
+                       float* out_da, dr_stream_t stream);
 
 /* VJP of DiffRast.interpolate: d_attr (layout/stride d_attr_batch_stride,
  * 0 = accumulate every image into one [V,A]), d_rast [N,H,W,4] (channels 2,3
@@ -155,8 +161,8 @@ int dr_interpolate_fwd(const float* attr, int64_t attr_batch_stride, const float
 int dr_interpolate_bwd(const float* attr, int64_t attr_batch_stride, const float* rast,
                        const float* rast_db, const int32_t* tri, const int32_t* diff_idx,
                        int K, const float* d_out, const float* d_out_da, int N, int H, int W,
-                       int V, int A, float* d_attr, int64_t d_attr_batch_stride, float* d_rast,
-                       float* d_rast_db, unsigned flags, dr_stream_t stream);
+                       int V, int T, int A, float* d_attr, int64_t d_attr_batch_stride,
+                       float* d_rast, float* d_rast_db, unsigned flags, dr_stream_t stream);
 
 /* ---- texture --------------------------------------------------------- */
 

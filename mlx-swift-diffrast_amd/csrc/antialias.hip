@@ -105,11 +105,23 @@ __global__ void __launch_bounds__(256) k_aa_rec(const float* __restrict__ pos,
   const float* p = pos + n * V * 4;
   const int v0 = tri[(int64_t)t * 3 + 0], v1 = tri[(int64_t)t * 3 + 1],
             v2 = tri[(int64_t)t * 3 + 2];
+  AARec r;
+  if (!verts_ok(v0, v1, v2, V)) {
+    // a vertex id outside [0, V): NaN corners, so no edge of this triangle
+    // separates two pixel centres (it never blends, nothing reads its
+    // vertices)
+    const float q = __int_as_float(0x7fc00000);
+    r.s01 = make_float4(q, q, q, q);
+    r.s2 = make_float4(q, q, __int_as_float(topo[(int64_t)t * 3 + 0]),
+                       __int_as_float(topo[(int64_t)t * 3 + 1]));
+    r.tv = make_int4(topo[(int64_t)t * 3 + 2], -1, -1, -1);
+    rec[i] = r;
+    return;
+  }
   const float4 P0 = *reinterpret_cast<const float4*>(p + (int64_t)v0 * 4);
   const float4 P1 = *reinterpret_cast<const float4*>(p + (int64_t)v1 * 4);
   const float4 P2 = *reinterpret_cast<const float4*>(p + (int64_t)v2 * 4);
   const float hw = (float)W, hh = (float)H;
-  AARec r;
   r.s01 = make_float4((P0.x / P0.w + 1.0f) * hw * 0.5f, (1.0f - P0.y / P0.w) * hh * 0.5f,
                       (P1.x / P1.w + 1.0f) * hw * 0.5f, (1.0f - P1.y / P1.w) * hh * 0.5f);
   r.s2 = make_float4((P2.x / P2.w + 1.0f) * hw * 0.5f, (1.0f - P2.y / P2.w) * hh * 0.5f,
@@ -630,8 +642,10 @@ __global__ void __launch_bounds__(256) k_aa_bwd(const float* __restrict__ rast,
 // loaded only for the queued pairs: staging them measured slower).
 constexpr int kMaskQueue = 256 * 4 + 64;
 
+// Seven workgroups per CU: the register budget this asks for (72) is met
+// without spills, one workgroup more than the compiler's own choice.
 template <int CT>
-__global__ void __launch_bounds__(256) k_aa_bwd_masked(
+__global__ void __launch_bounds__(256, 7) k_aa_bwd_masked(
     const float* __restrict__ rast, const AARec* __restrict__ rec, const float* __restrict__ pos,
     const float* __restrict__ color, const float* __restrict__ d_out,
     const uint8_t* __restrict__ blend_mask, int H, int W, int V, int T, int C, int ntx, int nty,
@@ -720,7 +734,7 @@ __global__ void __launch_bounds__(256) k_aa_bwd_masked(
     // the foreground record (:206-222): the pixel's own, else the neighbour's
     const AARec R = recn[tq >= 0 ? tq : tn];
     float4 P[3];
-    if (d_pos && !border) {  // the edge is two of the record's vertices
+    if (d_pos && !border && R.tv.y >= 0) {  // the edge is two of the record's vertices
       P[0] = *reinterpret_cast<const float4*>(posn + (int64_t)R.tv.y * 4);
       P[1] = *reinterpret_cast<const float4*>(posn + (int64_t)R.tv.z * 4);
       P[2] = *reinterpret_cast<const float4*>(posn + (int64_t)R.tv.w * 4);

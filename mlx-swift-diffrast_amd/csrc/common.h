@@ -106,6 +106,13 @@ __device__ __forceinline__ int f2i(float x) {
   return r;
 }
 
+// Whether a triangle's three vertex ids index rows [0, V) of its vertex
+// buffer.  Triangles that fail are not drawn and get no gradient, so no
+// input can send a vertex read out of range.
+__device__ __forceinline__ bool verts_ok(int i0, int i1, int i2, int V) {
+  return (unsigned)i0 < (unsigned)V && (unsigned)i1 < (unsigned)V && (unsigned)i2 < (unsigned)V;
+}
+
 __device__ __forceinline__ int xcd_remap(int b, int B) {
   // Blocks are dealt round-robin to the 8 XCDs; give each XCD a contiguous
   // run of tiles so neighbouring tiles share that XCD's L2.

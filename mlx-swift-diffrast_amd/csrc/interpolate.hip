@@ -36,7 +36,7 @@ template <int AT, int KT>
 __global__ void __launch_bounds__(256) k_interp_fwd(
     const float* __restrict__ attr, int64_t attr_stride, const float* __restrict__ rast,
     const float* __restrict__ rast_db, const int32_t* __restrict__ tri,
-    const int32_t* __restrict__ diff_idx, int K_, int64_t P, int HW, int A_,
+    const int32_t* __restrict__ diff_idx, int K_, int64_t P, int HW, int V, int T, int A_,
     float* __restrict__ out, float* __restrict__ out_da) {
   constexpr int NA = AT > 0 ? AT : 8;       // register slots for attributes
   constexpr int NK = KT > 0 ? 2 * KT : 8;   // and for derivative outputs
@@ -50,6 +50,7 @@ __global__ void __launch_bounds__(256) k_interp_fwd(
     const int64_t pix = base + q * 256;
     r[q] = pix < P ? *reinterpret_cast<const float4*>(rast + pix * 4) : make_float4(0.f, 0.f, 0.f, 0.f);
     t[q] = pix < P ? f2i(r[q].w) - 1 : -1;
+    if (t[q] >= T) t[q] = -1;  // not a triangle of this mesh: empty
   }
   int iv[kInterpPix][3];
 #pragma unroll
@@ -59,6 +60,7 @@ __global__ void __launch_bounds__(256) k_interp_fwd(
       iv[q][0] = tri[t[q] * 3 + 0];
       iv[q][1] = tri[t[q] * 3 + 1];
       iv[q][2] = tri[t[q] * 3 + 2];
+      if (!verts_ok(iv[q][0], iv[q][1], iv[q][2], V)) t[q] = -1;
     }
   }
 #pragma unroll
@@ -84,6 +86,10 @@ __global__ void __launch_bounds__(256) k_interp_fwd(
         const float4 db = *reinterpret_cast<const float4*>(rast_db + pix * 4);
         for (int k = 0; k < K; ++k) {
           const int a = diff_idx ? diff_idx[k] : k;
+          if ((unsigned)a >= (unsigned)A) {  // not an attribute: zero derivatives
+            od[2 * k + 0] = od[2 * k + 1] = 0.0f;
+            continue;
+          }
           const float d01 = a1p[a] - a0p[a];
           const float d02 = a2p[a] - a0p[a];
           od[2 * k + 0] = d01 * db.x + d02 * db.z;
@@ -135,8 +141,8 @@ __global__ void __launch_bounds__(256) k_interp_bwd(
     const float* __restrict__ attr, int64_t attr_stride, const float* __restrict__ rast,
     const float* __restrict__ rast_db, const int32_t* __restrict__ tri,
     const int32_t* __restrict__ diff_idx, int K_, const float* __restrict__ d_out,
-    const float* __restrict__ d_out_da, int N, int H, int W, int ntx, int nty, int A_,
-    float* __restrict__ d_attr, int64_t d_attr_stride, float* __restrict__ d_rast,
+    const float* __restrict__ d_out_da, int N, int H, int W, int ntx, int nty, int V, int T,
+    int A_, float* __restrict__ d_attr, int64_t d_attr_stride, float* __restrict__ d_rast,
     float* __restrict__ d_rast_db) {
   constexpr int NV = AT > 0 ? AT : 1;
   __shared__ LdsTable<NV, 256> tab;  // d_attr rows (or elements) touched by this tile
@@ -157,7 +163,7 @@ __global__ void __launch_bounds__(256) k_interp_bwd(
 
   const float4 r = *reinterpret_cast<const float4*>(rast + pix * 4);
   const int t = f2i(r.w) - 1;
-  const bool valid = inside && t >= 0;
+  bool valid = inside && t >= 0 && t < T;
   const float u = r.x, v = r.y;
   const float bw = 1.0f - u - v;
   int i0 = 0, i1 = 0, i2 = 0;
@@ -165,6 +171,7 @@ __global__ void __launch_bounds__(256) k_interp_bwd(
     i0 = tri[t * 3 + 0];
     i1 = tri[t * 3 + 1];
     i2 = tri[t * 3 + 2];
+    valid = verts_ok(i0, i1, i2, V);  // pixels of foreign ids are empty
   }
   const float* at = attr + (int64_t)n * attr_stride;
   float* da = d_attr + (int64_t)n * d_attr_stride;
@@ -187,6 +194,7 @@ __global__ void __launch_bounds__(256) k_interp_bwd(
     const float* gd = d_out_da + pix * 2 * K;
     for (int k = 0; k < K; ++k) {
       const int a = diff_idx ? diff_idx[k] : k;
+      if ((unsigned)a >= (unsigned)A) continue;  // not an attribute
       const float a0 = at[(int64_t)i0 * A + a], a1 = at[(int64_t)i1 * A + a],
                   a2 = at[(int64_t)i2 * A + a];
       const float d01 = a1 - a0, d02 = a2 - a0;
@@ -250,6 +258,7 @@ __global__ void __launch_bounds__(256) k_interp_bwd(
       const float* gd = d_out_da + pix * 2 * K;
       for (int k = 0; k < K; ++k) {
         const int a = diff_idx ? diff_idx[k] : k;
+        if ((unsigned)a >= (unsigned)A) continue;  // not an attribute
         const float gx = gd[2 * k + 0], gy = gd[2 * k + 1];
         const float u_term = gx * db.x + gy * db.y;
         const float v_term = gx * db.z + gy * db.w;
@@ -280,9 +289,9 @@ using namespace dr;
   } while (0)
 
 static int check_interp(const float* attr, const float* rast, const int32_t* tri,
-                        const float* rast_db, int K, int N, int H, int W, int V, int A,
+                        const float* rast_db, int K, int N, int H, int W, int V, int T, int A,
                         int64_t attr_stride, const int32_t* diff_idx) {
-  DR_CHECK_ARG(N >= 1 && H >= 1 && W >= 1 && V >= 0 && A >= 1 && K >= 0,
+  DR_CHECK_ARG(N >= 1 && H >= 1 && W >= 1 && V >= 0 && T >= 0 && A >= 1 && K >= 0,
                "interpolate: bad sizes");
   DR_CHECK_ARG(attr && rast && tri, "interpolate: null tensor");
   DR_CHECK_ARG(attr_stride == 0 || attr_stride == (int64_t)V * A,
@@ -295,10 +304,10 @@ static int check_interp(const float* attr, const float* rast, const int32_t* tri
 extern "C" int dr_interpolate_fwd(const float* attr, int64_t attr_batch_stride,
                                   const float* rast, const float* rast_db, const int32_t* tri,
                                   const int32_t* diff_idx, int K, int N, int H, int W, int V,
-                                  int A, float* out, float* out_da, dr_stream_t stream_) {
+                                  int T, int A, float* out, float* out_da, dr_stream_t stream_) {
   hipStream_t stream = (hipStream_t)stream_;
   (void)hipGetLastError();
-  int st = check_interp(attr, rast, tri, rast_db, K, N, H, W, V, A, attr_batch_stride, diff_idx);
+  int st = check_interp(attr, rast, tri, rast_db, K, N, H, W, V, T, A, attr_batch_stride, diff_idx);
   if (st) return st;
   DR_CHECK_ARG(out && (K == 0 || out_da), "interpolate: null output");
   const int64_t P = (int64_t)N * H * W;
@@ -308,10 +317,10 @@ extern "C" int dr_interpolate_fwd(const float* attr, int64_t attr_batch_stride,
   const bool aligned = (((uintptr_t)out | (uintptr_t)(out_da ? out_da : out)) & 15) == 0;
   if (!aligned)
     hipLaunchKernelGGL((k_interp_fwd<0, 0>), grid, dim3(256), 0, stream, attr, attr_batch_stride,
-                       rast, rast_db, tri, diff_idx, K, P, H * W, A, out, out_da);
+                       rast, rast_db, tri, diff_idx, K, P, H * W, V, T, A, out, out_da);
   else
     DR_INTERP_DISPATCH(k_interp_fwd, grid, attr, attr_batch_stride, rast, rast_db, tri, diff_idx,
-                       K, P, H * W, A, out, out_da);
+                       K, P, H * W, V, T, A, out, out_da);
   DR_CHECK_LAUNCH();
   return DR_OK;
 }
@@ -319,12 +328,13 @@ extern "C" int dr_interpolate_fwd(const float* attr, int64_t attr_batch_stride,
 extern "C" int dr_interpolate_bwd(const float* attr, int64_t attr_batch_stride,
                                   const float* rast, const float* rast_db, const int32_t* tri,
                                   const int32_t* diff_idx, int K, const float* d_out,
-                                  const float* d_out_da, int N, int H, int W, int V, int A,
-                                  float* d_attr, int64_t d_attr_batch_stride, float* d_rast,
-                                  float* d_rast_db, unsigned flags, dr_stream_t stream_) {
+                                  const float* d_out_da, int N, int H, int W, int V, int T,
+                                  int A, float* d_attr, int64_t d_attr_batch_stride,
+                                  float* d_rast, float* d_rast_db, unsigned flags,
+                                  dr_stream_t stream_) {
   hipStream_t stream = (hipStream_t)stream_;
   (void)hipGetLastError();
-  int st = check_interp(attr, rast, tri, rast_db, K, N, H, W, V, A, attr_batch_stride, diff_idx);
+  int st = check_interp(attr, rast, tri, rast_db, K, N, H, W, V, T, A, attr_batch_stride, diff_idx);
   if (st) return st;
   DR_CHECK_ARG(d_out && d_attr && d_rast && (K == 0 || d_out_da), "interpolate_bwd: null tensor");
   DR_CHECK_ARG(d_attr_batch_stride == 0 || d_attr_batch_stride == (int64_t)V * A,
@@ -335,8 +345,8 @@ extern "C" int dr_interpolate_bwd(const float* attr, int64_t attr_batch_stride,
   const dim3 grid((unsigned)((int64_t)N * ntx * nty));
   DR_TIMED("k_interp_bwd", stream);
   DR_INTERP_DISPATCH(k_interp_bwd, grid, attr, attr_batch_stride, rast, rast_db, tri, diff_idx, K,
-                     d_out, d_out_da, N, H, W, ntx, nty, A, d_attr, d_attr_batch_stride, d_rast,
-                     d_rast_db);
+                     d_out, d_out_da, N, H, W, ntx, nty, V, T, A, d_attr, d_attr_batch_stride,
+                     d_rast, d_rast_db);
   DR_CHECK_LAUNCH();
   return DR_OK;
 }

@@ -30,8 +30,8 @@ struct alignas(16) TriRec {
 
 // Rasterize.swift:280-328 (+ the AABB and tile range of :191-223).
 __global__ void __launch_bounds__(256) k_setup(const float* __restrict__ pos, int64_t pos_stride,
-                                               const int32_t* __restrict__ tri, int Npos, int T,
-                                               int H, int W, TriRec* __restrict__ rec,
+                                               const int32_t* __restrict__ tri, int Npos, int V,
+                                               int T, int H, int W, TriRec* __restrict__ rec,
                                                int4* __restrict__ rect) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= (int64_t)Npos * T) return;
@@ -39,12 +39,14 @@ __global__ void __launch_bounds__(256) k_setup(const float* __restrict__ pos, in
   const int t = (int)(i - (int64_t)n * T);
   const float* p = pos + (int64_t)n * pos_stride;
   const int i0 = tri[t * 3 + 0], i1 = tri[t * 3 + 1], i2 = tri[t * 3 + 2];
-  const float4 v0 = *reinterpret_cast<const float4*>(p + (int64_t)i0 * 4);
-  const float4 v1 = *reinterpret_cast<const float4*>(p + (int64_t)i1 * 4);
-  const float4 v2 = *reinterpret_cast<const float4*>(p + (int64_t)i2 * 4);
+  const bool ok = verts_ok(i0, i1, i2, V);  // else not drawn
+  const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
+  const float4 v0 = ok ? *reinterpret_cast<const float4*>(p + (int64_t)i0 * 4) : z4;
+  const float4 v1 = ok ? *reinterpret_cast<const float4*>(p + (int64_t)i1 * 4) : z4;
+  const float4 v2 = ok ? *reinterpret_cast<const float4*>(p + (int64_t)i2 * 4) : z4;
   TriRec r;
   int4 rc = make_int4(-1, -1, -1, -1);
-  if (v0.w <= 0.0f || v1.w <= 0.0f || v2.w <= 0.0f) {
+  if (!ok || v0.w <= 0.0f || v1.w <= 0.0f || v2.w <= 0.0f) {
     r.r0 = r.r1 = r.r2 = r.r3 = make_float4(0.f, 0.f, 0.f, 0.f);
   } else {
     const float sx0 = v0.x / v0.w, sy0 = v0.y / v0.w, sz0 = v0.z / v0.w;
@@ -477,7 +479,7 @@ __global__ void __launch_bounds__(256) k_raster(
 __global__ void __launch_bounds__(256) k_raster_bwd(
     const float* __restrict__ pos, int64_t pos_stride, const int32_t* __restrict__ tri,
     const float* __restrict__ rast, const float* __restrict__ d_rast,
-    const float* __restrict__ d_rast_db, int N, int T, int H, int W, int ntx, int nty,
+    const float* __restrict__ d_rast_db, int N, int V, int T, int H, int W, int ntx, int nty,
     float* __restrict__ d_pos) {
   __shared__ LdsTable<4, 256> tab;  // d_pos rows touched by this tile
   lds_table_clear(tab);
@@ -505,6 +507,12 @@ __global__ void __launch_bounds__(256) k_raster_bwd(
   const float* p = pos + (int64_t)n * pos_stride;
   float* dp = d_pos + (int64_t)n * pos_stride;
   if (valid) {
+    i0 = tri[t * 3 + 0];
+    i1 = tri[t * 3 + 1];
+    i2 = tri[t * 3 + 2];
+    valid = verts_ok(i0, i1, i2, V);
+  }
+  if (valid) {
     const float u_val = r.x, v_val = r.y;
     const float bw_val = 1.0f - u_val - v_val;
     const float4 dr = *reinterpret_cast<const float4*>(d_rast + pix * 4);
@@ -514,9 +522,6 @@ __global__ void __launch_bounds__(256) k_raster_bwd(
     const float d_db0 = ddb.x, d_db1 = ddb.y, d_db2 = ddb.z, d_db3 = ddb.w;
     const float Px = 2.0f * ((float)pw + 0.5f) / (float)W - 1.0f;
     const float Py = 1.0f - 2.0f * ((float)ph + 0.5f) / (float)H;
-    i0 = tri[t * 3 + 0];
-    i1 = tri[t * 3 + 1];
-    i2 = tri[t * 3 + 2];
     const float4 P0 = *reinterpret_cast<const float4*>(p + (int64_t)i0 * 4);
     const float4 P1 = *reinterpret_cast<const float4*>(p + (int64_t)i1 * 4);
     const float4 P2 = *reinterpret_cast<const float4*>(p + (int64_t)i2 * 4);
@@ -710,7 +715,8 @@ extern "C" int dr_rasterize_tile_counts(const float* pos, int64_t pos_batch_stri
   if (n_rec > 0) {
     DR_TIMED("k_setup", stream);
     hipLaunchKernelGGL(k_setup, dim3(grid_for(n_rec, 256)), dim3(256), 0, stream, pos,
-                       ranges_host ? (int64_t)0 : pos_batch_stride, tri, Npos, T, H, W, rec, rect);
+                       ranges_host ? (int64_t)0 : pos_batch_stride, tri, Npos, V, T, H, W, rec,
+                       rect);
     DR_CHECK_LAUNCH();
   }
   DR_CHECK_HIP(fill_async(counts, 0, n_tiles, stream));
@@ -768,7 +774,8 @@ extern "C" int dr_rasterize_fwd(const float* pos, int64_t pos_batch_stride, cons
   if (n_rec > 0) {
     DR_TIMED("k_setup", stream);
     hipLaunchKernelGGL(k_setup, dim3(grid_for(n_rec, 256)), dim3(256), 0, stream, pos,
-                       ranges_host ? (int64_t)0 : pos_batch_stride, tri, Npos, T, H, W, rec, rect);
+                       ranges_host ? (int64_t)0 : pos_batch_stride, tri, Npos, V, T, H, W, rec,
+                       rect);
     DR_CHECK_LAUNCH();
   }
 
@@ -851,7 +858,7 @@ extern "C" int dr_rasterize_bwd(const float* pos, int64_t pos_batch_stride, cons
   {
     DR_TIMED("k_raster_bwd", stream);
     hipLaunchKernelGGL(k_raster_bwd, dim3((unsigned)blocks), dim3(256), 0, stream, pos,
-                       pos_batch_stride, tri, rast, d_rast, d_rast_db, N, T, H, W, ntx, nty,
+                       pos_batch_stride, tri, rast, d_rast, d_rast_db, N, V, T, H, W, ntx, nty,
                        d_pos);
   }
   DR_CHECK_LAUNCH();

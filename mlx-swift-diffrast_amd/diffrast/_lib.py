@@ -29,8 +29,9 @@ SIGNATURES = {
     "dr_rasterize_fwd": ([_p, _i64, _p, _p, _p, _i, _i, _i, _i, _i, _p, _p, _p], _i),
     "dr_rasterize_tile_counts": ([_p, _i64, _p, _p, _i, _i, _i, _i, _i, _p, _p, _p], _i),
     "dr_rasterize_bwd": ([_p, _i64, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p, _u, _p], _i),
-    "dr_interpolate_fwd": ([_p, _i64, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p, _p, _p], _i),
-    "dr_interpolate_bwd": ([_p, _i64, _p, _p, _p, _p, _i, _p, _p, _i, _i, _i, _i, _i, _p, _i64,
+    "dr_interpolate_fwd": ([_p, _i64, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i, _p, _p, _p],
+                           _i),
+    "dr_interpolate_bwd": ([_p, _i64, _p, _p, _p, _p, _i, _p, _p, _i, _i, _i, _i, _i, _i, _p, _i64,
                             _p, _p, _u, _p], _i),
     "dr_texture_mip_levels": ([_i, _i, _i, _p, _p], _i),
     "dr_texture_mip_size": ([_i, _i, _i, _i, _i], _i64),

@@ -140,7 +140,8 @@ class _InterpolateFn(torch.autograd.Function):
         out_da = torch.empty((N, H, W, 2 * K), device=rast.device, dtype=torch.float32)
         _lib.check(lib.dr_interpolate_fwd(
             _ptr(attr), stride, _ptr(rast), _ptr(rast_db) if K else None, _ptr(tri),
-            _ptr(diff_idx), K, N, H, W, V, A, _ptr(out), _ptr(out_da) if K else None, _stream()))
+            _ptr(diff_idx), K, N, H, W, V, tri.shape[0], A, _ptr(out), _ptr(out_da) if K else None,
+            _stream()))
         ctx.save_for_backward(attr, rast, rast_db if K else None, tri, diff_idx)
         ctx.meta = (K, shared)
         return out, out_da
@@ -163,7 +164,8 @@ class _InterpolateFn(torch.autograd.Function):
         d_rast_db = torch.empty_like(rast) if K else None
         _lib.check(lib.dr_interpolate_bwd(
             _ptr(attr), stride, _ptr(rast), _ptr(rast_db), _ptr(tri), _ptr(diff_idx), K,
-            _ptr(d_out), _ptr(d_out_da) if K else None, N, H, W, V, A, _ptr(d_attr), stride,
+            _ptr(d_out), _ptr(d_out_da) if K else None, N, H, W, V, tri.shape[0], A, _ptr(d_attr),
+            stride,
             _ptr(d_rast), _ptr(d_rast_db), 0, _stream()))
         return d_attr, d_rast, d_rast_db, None, None, None, None
 

@@ -59,7 +59,7 @@ def test_argument_errors_are_codes():
     rc = lib.dr_rasterize_fwd(None, 0, None, None, None, 1, 3, 1, 4, 4, None, None, None)
     assert rc == L.DR_ERR_ARGUMENT
     assert b"rasterize" in lib.dr_get_last_error()
-    rc = lib.dr_interpolate_fwd(None, 0, None, None, None, None, 0, 1, 2, 2, 3, 2, None, None,
+    rc = lib.dr_interpolate_fwd(None, 0, None, None, None, None, 0, 1, 2, 2, 3, 1, 2, None, None,
                                 None)
     assert rc == L.DR_ERR_ARGUMENT
     with pytest.raises(ValueError):

@@ -86,8 +86,8 @@ def test_interpolate_bwd_accumulate(chain):
     d_db = torch.empty_like(c["db"])
     run = lambda fl: _lib.check(lib.dr_interpolate_bwd(
         _p(c["attr"]), 0, _p(c["rast"]), _p(c["db"]), _p(c["tri"]), None, A, _p(d_out),
-        _p(d_da), N, c["H"], c["W"], V, A, _p(d_attr), 0, _p(d_rast), _p(d_db), fl,
-        _s(torch)))
+        _p(d_da), N, c["H"], c["W"], V, c["tri"].shape[0], A, _p(d_attr), 0, _p(d_rast), _p(d_db),
+        fl, _s(torch)))
     _twice(run, [d_attr, d_rast, d_db], [True, False, False], rng)
 
 
