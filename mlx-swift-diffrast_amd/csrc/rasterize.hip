@@ -311,36 +311,6 @@ __device__ __forceinline__ void test_tri(const TriRec& R, int t, float x, float 
   }
 }
 
-// True when the triangle provably covers no pixel centre of the box
-// [xw0, xw1] x [yw0, yw1]: some edge function is below -delta on the whole
-// box.  The edge function e(x, y) = (xi - x)(yj - y) - (xj - x)(yi - y) is
-// affine in (x, y) (the xy terms cancel), so its maximum over the box is at
-// the corner picked by its slopes; evaluated in fp64 from the fp32 vertex
-// coordinates it is exact up to one final rounding.  delta bounds the error
-// of test_tri's fp32 evaluation at any centre of the box (4 roundings of
-// products bounded by (|xi| + 1)(|yj| + 1) + (|xj| + 1)(|yi| + 1), doubled),
-// so a culled triangle would fail test_tri's e * area >= 0 at every pixel.
-// Triangles of tiny area (where e * area could underflow) are never culled.
-__device__ __forceinline__ bool box_misses(const TriRec& R, float xw0, float xw1, float yw0,
-                                           float yw1) {
-  const float area = R.r2.y;
-  if (!(fabsf(area) > 1e-20f)) return false;
-  const double sg = area > 0.0f ? 1.0 : -1.0;
-  const double X[3] = {R.r0.x, R.r0.z, R.r1.x}, Y[3] = {R.r0.y, R.r0.w, R.r1.y};
-  const double u = 1.0 / 16777216.0;  // 2^-24
-#pragma unroll
-  for (int k = 0; k < 3; ++k) {  // edge k: vertices k+1 and k+2 (e0, e1, e2 of test_tri)
-    const int a_ = (k + 1) % 3, b_ = (k + 2) % 3;
-    const double xi = X[a_], yi = Y[a_], xj = X[b_], yj = Y[b_];
-    const double c0 = sg * (xi * yj - xj * yi), cx = sg * (yi - yj), cy = sg * (xj - xi);
-    const double emax = c0 + fmax(cx * xw0, cx * xw1) + fmax(cy * yw0, cy * yw1);
-    const double delta = 8.0 * u * ((fabs(xi) + 1.0) * (fabs(yj) + 1.0) +
-                                    (fabs(xj) + 1.0) * (fabs(yi) + 1.0));
-    if (emax < -delta) return true;
-  }
-  return false;
-}
-
 __device__ __forceinline__ TriRec load_rec(const TriRec* __restrict__ rec, int64_t r) {
   const float4* q = reinterpret_cast<const float4*>(rec + r);
   TriRec R;
@@ -353,10 +323,11 @@ __device__ __forceinline__ TriRec load_rec(const TriRec* __restrict__ rec, int64
 
 // Rasterize.swift:371-599.  One workgroup per (image, 16x16 tile); wave w
 // owns the 8x8 quadrant (w&1, w>>1).  Each triangle of the tile's list is
-// first tested against the quadrant's pixel-centre box (its bounding box,
-// then its edge functions over the box; exact: the pixel -> NDC map is
-// monotonic), 64 triangles at a time, one per lane; only the survivors are
-// tested against the quadrant's 64 pixels.
+// first tested against the quadrant's pixel-centre box by its bounding box
+// (exact: the pixel -> NDC map is monotonic), 64 triangles at a time, one
+// per lane; only the survivors are tested against the quadrant's 64 pixels.
+// (A conservative edge-function test of the box, in fp64 or fp32, removed
+// more candidates but cost more than the survivor tests it saved.)
 template <bool DB, bool PEEL>
 __global__ void __launch_bounds__(256) k_raster(
     const TriRec* __restrict__ rec, const int4* __restrict__ rect, Items it, int64_t rec_stride,
@@ -414,8 +385,7 @@ __global__ void __launch_bounds__(256) k_raster(
       if (lane < nb) {
         myt = ids[c0 + lane];
         Rl = load_rec(rec, rbase + myt);
-        hit = !(Rl.r3.y < xw0 || Rl.r3.x > xw1 || Rl.r3.w < yw0 || Rl.r3.z > yw1) &&
-              !box_misses(Rl, xw0, xw1, yw0, yw1);
+        hit = !(Rl.r3.y < xw0 || Rl.r3.x > xw1 || Rl.r3.w < yw0 || Rl.r3.z > yw1);
       }
       uint64_t m = __ballot(hit);
       if (hit) {
