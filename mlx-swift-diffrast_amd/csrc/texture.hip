@@ -726,8 +726,10 @@ __global__ void __launch_bounds__(256) k_tex_bwd(TexBwdArgs A, int total_tiles) 
 // or boxes too large for a window, go to the LDS hash table.
 // ---------------------------------------------------------------------------
 
-constexpr int kWinTexels = 768;  // texels of the two windows together (~30 KB of LDS with the table)
-constexpr int kWinFallback = 128;
+constexpr int kWinWaves = 4;                  // waves per workgroup; a tile is 16 x (4 * kWinWaves) pixels
+constexpr int kWinTexels = 192 * kWinWaves;  // texels of the two windows together
+constexpr int kWinFallback = 32 * kWinWaves;  // LDS hash table entries
+constexpr int kWinThreads = 64 * kWinWaves;
 
 struct TapSlot {
   int k;         // level
@@ -748,18 +750,18 @@ __device__ __forceinline__ void slot_box(const TapSlot& q, int& x0, int& x1, int
 
 
 template <int FILTER, int CT, int BND, bool BIAS>
-// Five workgroups per CU (the register budget this asks for costs a few
-// spilled values, measured cheaper than four resident workgroups).
-__global__ void __launch_bounds__(256, 5) k_tex_bwd_win(TexBwdArgs A, int total_tiles) {
+// Five waves per SIMD (the register budget this asks for costs a few
+// spilled values, measured cheaper than four).
+__global__ void __launch_bounds__(kWinThreads, 5) k_tex_bwd_win(TexBwdArgs A, int total_tiles) {
   __shared__ double win[kWinTexels * CT];
-  __shared__ int s_wk[4];          // per wave: lowest level in use
-  __shared__ int s_wbox[4][2][4];  // per wave: boxes on that level and the next
+  __shared__ int s_wk[kWinWaves];          // per wave: lowest level in use
+  __shared__ int s_wbox[kWinWaves][2][4];  // per wave: boxes on that level and the next
   __shared__ int s_tab_used[2];    // per tile parity: the table took entries
   __shared__ LdsTable<CT, kWinFallback> tab;
   FootAcc<CT> acc;
   acc_init(acc);
   const int tid = threadIdx.x;
-  for (int i = tid; i < kWinTexels * CT; i += 256) win[i] = 0.0;
+  for (int i = tid; i < kWinTexels * CT; i += kWinThreads) win[i] = 0.0;
   lds_table_clear(tab);
   if (tid < 2) s_tab_used[tid] = 0;
   __syncthreads();
@@ -776,7 +778,7 @@ __global__ void __launch_bounds__(256, 5) k_tex_bwd_win(TexBwdArgs A, int total_
     const int tile = bt - n * tiles;
     const int ty = tile / A.ntx, tx = tile - ty * A.ntx;
     const int pw = tx * 16 + (lane & 15);  // 16x4 strip per wave, one pixel row per 16 lanes
-    const int ph = ty * 16 + wave * 4 + (lane >> 4);
+    const int ph = ty * (4 * kWinWaves) + wave * 4 + (lane >> 4);
     const bool valid = pw < A.Wi && ph < A.Hi;
     const int64_t pix = ((int64_t)n * A.Hi + min(ph, A.Hi - 1)) * A.Wi + min(pw, A.Wi - 1);
     auto level_ptr = [&](int k) -> const float* {
@@ -964,7 +966,9 @@ __global__ void __launch_bounds__(256, 5) k_tex_bwd_win(TexBwdArgs A, int total_
     }
     __syncthreads();
     if (tid == 0) s_tab_used[par ^ 1] = 0;  // read by every thread before the last barrier
-    const int ka = min(min(s_wk[0], s_wk[1]), min(s_wk[2], s_wk[3]));
+    int ka = s_wk[0];
+#pragma unroll
+    for (int v = 1; v < kWinWaves; ++v) ka = min(ka, s_wk[v]);
     int wsel[2];
 #pragma unroll
     for (int li = 0; li < 2; ++li) {
@@ -978,7 +982,7 @@ __global__ void __launch_bounds__(256, 5) k_tex_bwd_win(TexBwdArgs A, int total_
     for (int w = 0; w < 2; ++w) {
       int x0 = 0x7fffffff, x1 = -1, y0 = 0x7fffffff, y1 = -1;
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
+      for (int v = 0; v < kWinWaves; ++v) {
         const int kv = s_wk[v];
         const int j = w - (kv - ka);  // wave v's box j lies on level ka + w
         if (kv == 0x7fffffff || j < 0 || j > 1) continue;
@@ -1050,7 +1054,7 @@ __global__ void __launch_bounds__(256, 5) k_tex_bwd_win(TexBwdArgs A, int total_
       const int row = bw[w] * CT;
       const int total = row * bh[w];
       double* wb = win + wbase[w];
-      for (int i = tid; i < total; i += 256) {
+      for (int i = tid; i < total; i += kWinThreads) {
         const double v = wb[i];
         if (v != 0.0) {
           const int r = i / row, cpos = i - r * row;
@@ -1208,16 +1212,16 @@ hipError_t launch_tex_bwd_win_bb(const TexBwdArgs& args, int total_tiles, hipStr
   static int per_cu = 0;
   if (per_cu == 0) {
     int b = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, k_tex_bwd_win<FILTER, CT, BND, BIAS>, 256, 0) !=
-            hipSuccess ||
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, k_tex_bwd_win<FILTER, CT, BND, BIAS>,
+                                                     kWinThreads, 0) != hipSuccess ||
         b <= 0)
       b = 2;
     per_cu = b;
   }
   const int64_t resident = (int64_t)device_cu_count() * per_cu;
   const unsigned grid = (unsigned)(total_tiles < resident ? total_tiles : resident);
-  hipLaunchKernelGGL((k_tex_bwd_win<FILTER, CT, BND, BIAS>), dim3(grid), dim3(256), 0, stream,
-                     args, total_tiles);
+  hipLaunchKernelGGL((k_tex_bwd_win<FILTER, CT, BND, BIAS>), dim3(grid), dim3(kWinThreads), 0,
+                     stream, args, total_tiles);
   return hipGetLastError();
 }
 
@@ -1925,12 +1929,16 @@ extern "C" int dr_texture_bwd(const float* tex, const float* pyramid, int Nt, in
     case 4: DR_TB(F, CUBEV, 4); break;     \
     default: DR_TB(F, CUBEV, 0); break;    \
   }
+    // the windowed kernel's tiles are 16 x (4 * kWinWaves) pixels
+    TexBwdArgs wargs = args;
+    wargs.nty = (Hi + 4 * kWinWaves - 1) / (4 * kWinWaves);
+    const int wtiles = (int)((int64_t)N * ntx * wargs.nty);
 #define DR_TW(F)                                                   \
   switch (C) {                                                     \
-    case 1: e = launch_tex_bwd_win<F, 1>(args, (int)total_tiles, stream); break; \
-    case 2: e = launch_tex_bwd_win<F, 2>(args, (int)total_tiles, stream); break; \
-    case 3: e = launch_tex_bwd_win<F, 3>(args, (int)total_tiles, stream); break; \
-    default: e = launch_tex_bwd_win<F, 4>(args, (int)total_tiles, stream); break; \
+    case 1: e = launch_tex_bwd_win<F, 1>(wargs, wtiles, stream); break; \
+    case 2: e = launch_tex_bwd_win<F, 2>(wargs, wtiles, stream); break; \
+    case 3: e = launch_tex_bwd_win<F, 3>(wargs, wtiles, stream); break; \
+    default: e = launch_tex_bwd_win<F, 4>(wargs, wtiles, stream); break; \
   }
     const bool windowed = !cube && filter != DR_FILTER_NEAREST && C >= 1 && C <= 4 &&
                           Wt <= 32767 && Ht <= 32767;  // window boxes use 16-bit texel coordinates
