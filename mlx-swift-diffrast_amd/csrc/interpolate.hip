@@ -144,8 +144,7 @@ __global__ void __launch_bounds__(256) k_interp_bwd(
     const float* __restrict__ d_out_da, int N, int H, int W, int ntx, int nty, int V, int T,
     int A_, float* __restrict__ d_attr, int64_t d_attr_stride, float* __restrict__ d_rast,
     float* __restrict__ d_rast_db) {
-  constexpr int NV = AT > 0 ? AT : 1;
-  __shared__ LdsTable<NV, 256> tab;  // d_attr rows (or elements) touched by this tile
+  __shared__ LdsTable<(AT > 0 ? AT : 1), 256> tab;  // d_attr rows (or elements) touched by this tile
   lds_table_clear(tab);
   __syncthreads();
   const int tiles = ntx * nty;
@@ -158,114 +157,166 @@ __global__ void __launch_bounds__(256) k_interp_bwd(
   const int pw = tx * 16 + (lane & 15), ph = ty * 16 + wave * 4 + (lane >> 4);
   const bool inside = pw < W && ph < H;
   const int64_t pix = ((int64_t)n * H + min(ph, H - 1)) * W + min(pw, W - 1);
-  const int A = dimA<AT>(A_);
-  const int K = KT > 0 ? KT : K_;
 
   const float4 r = *reinterpret_cast<const float4*>(rast + pix * 4);
   const int t = f2i(r.w) - 1;
   bool valid = inside && t >= 0 && t < T;
   const float u = r.x, v = r.y;
   const float bw = 1.0f - u - v;
-  int i0 = 0, i1 = 0, i2 = 0;
-  if (valid) {
-    i0 = tri[t * 3 + 0];
-    i1 = tri[t * 3 + 1];
-    i2 = tri[t * 3 + 2];
-    valid = verts_ok(i0, i1, i2, V);  // pixels of foreign ids are empty
-  }
   const float* at = attr + (int64_t)n * attr_stride;
   float* da = d_attr + (int64_t)n * d_attr_stride;
-  const float* g = d_out + pix * A;
-  float4 db = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (K > 0 && valid) db = *reinterpret_cast<const float4*>(rast_db + pix * 4);
+  int i0 = 0, i1 = 0, i2 = 0;
 
-  // d_rast (Interpolate.swift:327-367) and d_rast_db (:370-417).
-  float du = 0.0f, dv = 0.0f;
-  if (valid) {
-    for (int a = 0; a < A; ++a) {
-      const float a0 = at[(int64_t)i0 * A + a], a1 = at[(int64_t)i1 * A + a],
-                  a2 = at[(int64_t)i2 * A + a];
-      du += (a1 - a0) * g[a];
-      dv += (a2 - a0) * g[a];
-    }
-  }
-  float d_udx = 0.0f, d_udy = 0.0f, d_vdx = 0.0f, d_vdy = 0.0f;
-  if (K > 0 && valid) {
-    const float* gd = d_out_da + pix * 2 * K;
-    for (int k = 0; k < K; ++k) {
-      const int a = diff_idx ? diff_idx[k] : k;
-      if ((unsigned)a >= (unsigned)A) continue;  // not an attribute
-      const float a0 = at[(int64_t)i0 * A + a], a1 = at[(int64_t)i1 * A + a],
-                  a2 = at[(int64_t)i2 * A + a];
-      const float d01 = a1 - a0, d02 = a2 - a0;
-      const float gx = gd[2 * k + 0], gy = gd[2 * k + 1];
-      d_udx += d01 * gx;
-      d_udy += d01 * gy;
-      d_vdx += d02 * gx;
-      d_vdy += d02 * gy;
-    }
-  }
-  if (inside) {
-    *reinterpret_cast<float4*>(d_rast + pix * 4) = make_float4(du, dv, 0.0f, 0.0f);
-    if (K > 0 && d_rast_db)
-      *reinterpret_cast<float4*>(d_rast_db + pix * 4) = make_float4(d_udx, d_udy, d_vdx, d_vdy);
-  }
-
-  // d_attr (Interpolate.swift:231-264, :269-324), summed per vertex row in
-  // LDS before the global atomics.
-  if (AT > 0) {
-    float rv[3 * NV];  // rows of i0, i1, i2
+  if constexpr (AT > 0) {
+    // Compile-time shape (identity diff_idx when KT > 0): every input of the
+    // pixel is loaded once, the cotangents and rast_db together with the
+    // triangle's vertex ids, then the three attribute rows.
+    constexpr int NK = KT > 0 ? KT : 1;
+    float gv[AT], gdv[2 * NK], a0[AT], a1[AT], a2[AT];
+    float4 db = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-    for (int q = 0; q < 3 * NV; ++q) rv[q] = 0.0f;
+    for (int a = 0; a < AT; ++a) gv[a] = a0[a] = a1[a] = a2[a] = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 2 * NK; ++k) gdv[k] = 0.0f;
+    if (valid) {
+      i0 = tri[t * 3 + 0];
+      i1 = tri[t * 3 + 1];
+      i2 = tri[t * 3 + 2];
+#pragma unroll
+      for (int a = 0; a < AT; ++a) gv[a] = d_out[pix * AT + a];
+      if constexpr (KT > 0) {
+#pragma unroll
+        for (int k = 0; k < 2 * KT; ++k) gdv[k] = d_out_da[pix * 2 * KT + k];
+        db = *reinterpret_cast<const float4*>(rast_db + pix * 4);
+      }
+      valid = verts_ok(i0, i1, i2, V);  // pixels of foreign ids are empty
+    }
     if (valid) {
 #pragma unroll
-      for (int a = 0; a < NV; ++a) {
-        const float ga = g[a];
-        rv[a] = bw * ga;
-        rv[NV + a] = u * ga;
-        rv[2 * NV + a] = v * ga;
+      for (int a = 0; a < AT; ++a) {
+        a0[a] = at[(int64_t)i0 * AT + a];
+        a1[a] = at[(int64_t)i1 * AT + a];
+        a2[a] = at[(int64_t)i2 * AT + a];
       }
-      if (KT > 0) {  // identity diff_idx (DiffAttrs.all)
-        const float* gd = d_out_da + pix * 2 * K;
+    }
+    // d_rast (Interpolate.swift:327-367) and d_rast_db (:370-417).
+    float du = 0.0f, dv = 0.0f;
+    float d_udx = 0.0f, d_udy = 0.0f, d_vdx = 0.0f, d_vdy = 0.0f;
+    if (valid) {
 #pragma unroll
-        for (int k = 0; k < (KT > 0 ? KT : 1); ++k) {
-          const float gx = gd[2 * k + 0], gy = gd[2 * k + 1];
-          const float u_term = gx * db.x + gy * db.y;
-          const float v_term = gx * db.z + gy * db.w;
-          rv[k] += -u_term - v_term;
-          rv[NV + k] += u_term;
-          rv[2 * NV + k] += v_term;
-        }
+      for (int a = 0; a < AT; ++a) {
+        du += (a1[a] - a0[a]) * gv[a];
+        dv += (a2[a] - a0[a]) * gv[a];
+      }
+#pragma unroll
+      for (int k = 0; k < (KT > 0 ? KT : 0); ++k) {
+        const float d01 = a1[k] - a0[k], d02 = a2[k] - a0[k];
+        const float gx = gdv[2 * k + 0], gy = gdv[2 * k + 1];
+        d_udx += d01 * gx;
+        d_udy += d01 * gy;
+        d_vdx += d02 * gx;
+        d_vdy += d02 * gy;
+      }
+    }
+    if (inside) {
+      *reinterpret_cast<float4*>(d_rast + pix * 4) = make_float4(du, dv, 0.0f, 0.0f);
+      if (KT > 0 && d_rast_db)
+        *reinterpret_cast<float4*>(d_rast_db + pix * 4) = make_float4(d_udx, d_udy, d_vdx, d_vdy);
+    }
+    // d_attr (Interpolate.swift:231-264, :269-324), summed per vertex row in
+    // LDS before the global atomics.
+    float rv[3 * AT];  // rows of i0, i1, i2
+#pragma unroll
+    for (int q = 0; q < 3 * AT; ++q) rv[q] = 0.0f;
+    if (valid) {
+#pragma unroll
+      for (int a = 0; a < AT; ++a) {
+        rv[a] = bw * gv[a];
+        rv[AT + a] = u * gv[a];
+        rv[2 * AT + a] = v * gv[a];
+      }
+#pragma unroll
+      for (int k = 0; k < (KT > 0 ? KT : 0); ++k) {
+        const float gx = gdv[2 * k + 0], gy = gdv[2 * k + 1];
+        const float u_term = gx * db.x + gy * db.y;
+        const float v_term = gx * db.z + gy * db.w;
+        rv[k] += -u_term - v_term;
+        rv[AT + k] += u_term;
+        rv[2 * AT + k] += v_term;
       }
     }
     // Runs of same-triangle lanes along a pixel row add into the same rows:
     // sum each run first, its last lane adds the total.
     const bool tail = row_run_sum(valid ? (uint64_t)t : (1ull << 63) | (uint64_t)lane, rv);
     if (valid && tail) {
-      lds_table_add(tab, da + (int64_t)i0 * A, &rv[0]);
-      lds_table_add(tab, da + (int64_t)i1 * A, &rv[NV]);
-      lds_table_add(tab, da + (int64_t)i2 * A, &rv[2 * NV]);
+      lds_table_add(tab, da + (int64_t)i0 * AT, &rv[0]);
+      lds_table_add(tab, da + (int64_t)i1 * AT, &rv[AT]);
+      lds_table_add(tab, da + (int64_t)i2 * AT, &rv[2 * AT]);
     }
-  } else if (valid) {
-    for (int a = 0; a < A; ++a) {
-      const float ga = g[a];
-      const float v0[1] = {bw * ga}, v1[1] = {u * ga}, v2[1] = {v * ga};
-      lds_table_add(tab, da + (int64_t)i0 * A + a, v0);
-      lds_table_add(tab, da + (int64_t)i1 * A + a, v1);
-      lds_table_add(tab, da + (int64_t)i2 * A + a, v2);
+  } else {
+    // Any shape: element by element.
+    const int A = A_;
+    const int K = K_;
+    if (valid) {
+      i0 = tri[t * 3 + 0];
+      i1 = tri[t * 3 + 1];
+      i2 = tri[t * 3 + 2];
+      valid = verts_ok(i0, i1, i2, V);  // pixels of foreign ids are empty
     }
-    if (K > 0) {
+    const float* g = d_out + pix * A;
+    float4 db = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (K > 0 && valid) db = *reinterpret_cast<const float4*>(rast_db + pix * 4);
+    float du = 0.0f, dv = 0.0f;
+    if (valid) {
+      for (int a = 0; a < A; ++a) {
+        const float a0 = at[(int64_t)i0 * A + a], a1 = at[(int64_t)i1 * A + a],
+                    a2 = at[(int64_t)i2 * A + a];
+        du += (a1 - a0) * g[a];
+        dv += (a2 - a0) * g[a];
+      }
+    }
+    float d_udx = 0.0f, d_udy = 0.0f, d_vdx = 0.0f, d_vdy = 0.0f;
+    if (K > 0 && valid) {
       const float* gd = d_out_da + pix * 2 * K;
       for (int k = 0; k < K; ++k) {
         const int a = diff_idx ? diff_idx[k] : k;
         if ((unsigned)a >= (unsigned)A) continue;  // not an attribute
+        const float a0 = at[(int64_t)i0 * A + a], a1 = at[(int64_t)i1 * A + a],
+                    a2 = at[(int64_t)i2 * A + a];
+        const float d01 = a1 - a0, d02 = a2 - a0;
         const float gx = gd[2 * k + 0], gy = gd[2 * k + 1];
-        const float u_term = gx * db.x + gy * db.y;
-        const float v_term = gx * db.z + gy * db.w;
-        const float v0[1] = {-u_term - v_term}, v1[1] = {u_term}, v2[1] = {v_term};
+        d_udx += d01 * gx;
+        d_udy += d01 * gy;
+        d_vdx += d02 * gx;
+        d_vdy += d02 * gy;
+      }
+    }
+    if (inside) {
+      *reinterpret_cast<float4*>(d_rast + pix * 4) = make_float4(du, dv, 0.0f, 0.0f);
+      if (K > 0 && d_rast_db)
+        *reinterpret_cast<float4*>(d_rast_db + pix * 4) = make_float4(d_udx, d_udy, d_vdx, d_vdy);
+    }
+    if (valid) {
+      for (int a = 0; a < A; ++a) {
+        const float ga = g[a];
+        const float v0[1] = {bw * ga}, v1[1] = {u * ga}, v2[1] = {v * ga};
         lds_table_add(tab, da + (int64_t)i0 * A + a, v0);
         lds_table_add(tab, da + (int64_t)i1 * A + a, v1);
         lds_table_add(tab, da + (int64_t)i2 * A + a, v2);
+      }
+      if (K > 0) {
+        const float* gd = d_out_da + pix * 2 * K;
+        for (int k = 0; k < K; ++k) {
+          const int a = diff_idx ? diff_idx[k] : k;
+          if ((unsigned)a >= (unsigned)A) continue;  // not an attribute
+          const float gx = gd[2 * k + 0], gy = gd[2 * k + 1];
+          const float u_term = gx * db.x + gy * db.y;
+          const float v_term = gx * db.z + gy * db.w;
+          const float v0[1] = {-u_term - v_term}, v1[1] = {u_term}, v2[1] = {v_term};
+          lds_table_add(tab, da + (int64_t)i0 * A + a, v0);
+          lds_table_add(tab, da + (int64_t)i1 * A + a, v1);
+          lds_table_add(tab, da + (int64_t)i2 * A + a, v2);
+        }
       }
     }
   }
