@@ -222,14 +222,15 @@ struct AATile {
   bool inside;
 };
 
-__device__ __forceinline__ int aa_tri_id(const float* __restrict__ rast, int n, int h, int w,
-                                         int H, int W, int T) {
-  const int id = f2i(rast[((((int64_t)n * H + h) * W + w) << 2) + 3]) - 1;
+// Triangle id of a rast pixel from its fourth channel; ids outside [0, T)
+// read as empty.
+__device__ __forceinline__ int aa_id(float w, int T) {
+  const int id = f2i(w) - 1;
   return (unsigned)id < (unsigned)T ? id : -1;
 }
 
-__device__ __forceinline__ AATile aa_load_tile(const float* __restrict__ rast, int H, int W, int T,
-                                               int ntx, int nty, int (*s_tri)[18]) {
+// The workgroup's tile and this thread's pixel (no memory access).
+__device__ __forceinline__ AATile aa_tile(int H, int W, int ntx, int nty) {
   AATile g;
   const int tiles = ntx * nty;
   const int b = xcd_remap((int)blockIdx.x, (int)gridDim.x);
@@ -244,18 +245,38 @@ __device__ __forceinline__ AATile aa_load_tile(const float* __restrict__ rast, i
   g.pw = g.x0 + g.lx;
   g.ph = g.y0 + g.ly;
   g.inside = g.pw < W && g.ph < H;
-  s_tri[g.ly + 1][g.lx + 1] = g.inside ? aa_tri_id(rast, g.n, g.ph, g.pw, H, W, T) : kOut;
-  if (threadIdx.x < 64) {
-    const int side = threadIdx.x >> 4, i = threadIdx.x & 15;
-    int qh, qw, r, c;
-    if (side == 0) { qw = g.x0 - 1;  qh = g.y0 + i;  r = i + 1; c = 0; }
-    else if (side == 1) { qw = g.x0 + 16; qh = g.y0 + i;  r = i + 1; c = 17; }
-    else if (side == 2) { qw = g.x0 + i;  qh = g.y0 - 1;  r = 0;     c = i + 1; }
-    else { qw = g.x0 + i;  qh = g.y0 + 16; r = 17;    c = i + 1; }
-    const bool in = qh >= 0 && qh < H && qw >= 0 && qw < W;
-    s_tri[r][c] = in ? aa_tri_id(rast, g.n, qh, qw, H, W, T) : kOut;
-  }
   return g;
+}
+
+// The border pixel of lanes 0..15 of each wave (wave 0: left column,
+// 1: right, 2: top row, 3: bottom): its cell in the 18x18 tile array, the
+// direction from it into the tile, and whether it lies in the image.
+struct AABorder {
+  bool lane, in;
+  int qh, qw, r, c, d;
+  int64_t q;  // pixel index (when in)
+};
+
+__device__ __forceinline__ AABorder aa_border(const AATile& g, int H, int W) {
+  AABorder b;
+  const int side = threadIdx.x >> 6, i = threadIdx.x & 15;
+  b.lane = (threadIdx.x & 63) < 16;
+  if (side == 0) { b.qw = g.x0 - 1;  b.qh = g.y0 + i;  b.r = i + 1; b.c = 0;     b.d = 0; }
+  else if (side == 1) { b.qw = g.x0 + 16; b.qh = g.y0 + i;  b.r = i + 1; b.c = 17;    b.d = 2; }
+  else if (side == 2) { b.qw = g.x0 + i;  b.qh = g.y0 - 1;  b.r = 0;     b.c = i + 1; b.d = 1; }
+  else { b.qw = g.x0 + i;  b.qh = g.y0 + 16; b.r = 17;    b.c = i + 1; b.d = 3; }
+  b.in = b.lane && b.qh >= 0 && b.qh < H && b.qw >= 0 && b.qw < W;
+  b.q = ((int64_t)g.n * H + b.qh) * W + b.qw;
+  return b;
+}
+
+// Triangle ids of the tile and its border into s_tri (corners unused): the
+// kernels issue these rast loads together with their other per-pixel loads
+// and store afterwards, so the loads share one round trip.
+__device__ __forceinline__ void aa_store_ids(const AATile& g, const AABorder& bd, float own_w,
+                                             float border_w, int T, int (*s_tri)[18]) {
+  s_tri[g.ly + 1][g.lx + 1] = g.inside ? aa_id(own_w, T) : kOut;
+  if (bd.lane) s_tri[bd.r][bd.c] = bd.in ? aa_id(border_w, T) : kOut;
 }
 
 // Blend-mask byte of pixel (n, h, w): 16x16 tiles in row-major order, 256
@@ -323,12 +344,18 @@ __global__ void __launch_bounds__(256) k_aa_fwd(const float* __restrict__ rast,
                                                 float* __restrict__ out,
                                                 uint8_t* __restrict__ blend_mask) {
   __shared__ int s_tri[18][18];
-  const AATile g = aa_load_tile(rast, H, W, T, ntx, nty, s_tri);
+  const AATile g = aa_tile(H, W, ntx, nty);
+  const AABorder bd = aa_border(g, H, W);
   const int64_t pix = ((int64_t)g.n * H + min(g.ph, H - 1)) * W + min(g.pw, W - 1);
+  // every load before the barrier is issued first: own and border ids, own colour
+  const float own_w = rast[pix * 4 + 3];
+  float border_w = 0.0f;
+  if (bd.in) border_w = rast[bd.q * 4 + 3];
   float cp[CT > 0 ? CT : 1];
-  if constexpr (CT > 0) {  // own colour: needed by every pixel, issued before the barrier
+  if constexpr (CT > 0) {
     if (g.inside) ld_px<CT>(color + pix * CT, CT, cp);
   }
+  aa_store_ids(g, bd, own_w, border_w, T, s_tri);
   __syncthreads();
   if (!g.inside) return;
   const int r = g.ly + 1, c = g.lx + 1;
@@ -478,15 +505,21 @@ __global__ void __launch_bounds__(256) k_aa_bwd(const float* __restrict__ rast,
   __shared__ int s_need;            // the table holds terms
   if (d_pos) lds_table_clear(tab);
   if (threadIdx.x == 0) { s_need = 0; s_nq = 0; }
-  const AATile g = aa_load_tile(rast, H, W, T, ntx, nty, s_tri);
+  const AATile g = aa_tile(H, W, ntx, nty);
+  const AABorder bd = aa_border(g, H, W);
   const int64_t pix = ((int64_t)g.n * H + min(g.ph, H - 1)) * W + min(g.pw, W - 1);
+  // every load before the barrier is issued first: own and border ids, own cotangent
+  const float own_w = rast[pix * 4 + 3];
+  float border_w = 0.0f;
+  if (bd.in) border_w = rast[bd.q * 4 + 3];
   float gv[CT > 0 ? CT : 1], old[CT > 0 ? CT : 1];
-  if constexpr (CT > 0) {  // own cotangent: needed by every pixel, issued before the barrier
+  if constexpr (CT > 0) {
     if (d_color && g.inside) {
       ld_px<CT>(d_out + pix * CT, CT, gv);
       if (accumulate) ld_px<CT>(d_color + pix * CT, CT, old);
     }
   }
+  aa_store_ids(g, bd, own_w, border_w, T, s_tri);
   __syncthreads();
   const AARec* recn = rec + (int64_t)g.n * T;
   const int r = g.ly + 1, c = g.lx + 1;
@@ -532,25 +565,19 @@ __global__ void __launch_bounds__(256) k_aa_bwd(const float* __restrict__ rast,
   if (ovf) s_need = 1;
   // 2) border: the one direction of each outside neighbour that points into
   //    the tile; lanes 0..15 of each wave take one side.
-  if ((threadIdx.x & 63) < 16) {
-    const int side = threadIdx.x >> 6, i = threadIdx.x & 15;
-    int qh, qw, rr, cc, qd;
-    if (side == 0) { qw = g.x0 - 1;  qh = g.y0 + i;  rr = i + 1; cc = 0;     qd = 0; }
-    else if (side == 1) { qw = g.x0 + 16; qh = g.y0 + i;  rr = i + 1; cc = 17;    qd = 2; }
-    else if (side == 2) { qw = g.x0 + i;  qh = g.y0 - 1;  rr = 0;     cc = i + 1; qd = 1; }
-    else { qw = g.x0 + i;  qh = g.y0 + 16; rr = 17;    cc = i + 1; qd = 3; }
+  if (bd.lane) {
     float al = 0.0f;
-    const int tq = s_tri[rr][cc];
+    const int tq = s_tri[bd.r][bd.c];
     if (tq != kOut) {
-      const int tn = aa_nb(s_tri, rr, cc, qd);
+      const int tn = aa_nb(s_tri, bd.r, bd.c, bd.d);
       if (aa_cand(tq, tn)) {
         AARec rq;
         if (tq >= 0) rq = recn[tq];
         SilDir s;
-        if (aa_pair(recn, rq, tq, tn, qh, qw, qd, s)) al = s.alpha;
+        if (aa_pair(recn, rq, tq, tn, bd.qh, bd.qw, bd.d, s)) al = s.alpha;
       }
     }
-    s_halo[side][i] = al;
+    s_halo[threadIdx.x >> 6][threadIdx.x & 15] = al;
   }
   __syncthreads();
 
@@ -661,58 +688,49 @@ __global__ void __launch_bounds__(256, 7) k_aa_bwd_masked(
   __shared__ float s_g[kCells][CS];  // d_out of the tile and its border (CT > 0)
   if (d_pos) lds_table_clear(tab);
   if (threadIdx.x == 0) s_nq = 0;
-  const AATile g = aa_load_tile(rast, H, W, T, ntx, nty, s_tri);
+  const AATile g = aa_tile(H, W, ntx, nty);
+  const AABorder bd = aa_border(g, H, W);
   const int64_t pix = ((int64_t)g.n * H + min(g.ph, H - 1)) * W + min(g.pw, W - 1);
   const int lx = g.lx, ly = g.ly;
   const int own = (ly + 1) * 18 + (lx + 1);
+  // every load before the barrier is issued first: the ids, blend-mask bytes
+  // and cotangents of the own pixel and (lanes 0..15 of each wave) one
+  // border pixel
+  const float own_w = rast[pix * 4 + 3];
+  const int own_m = blend_mask[mask_index(g.n, min(g.ph, H - 1), min(g.pw, W - 1), ntx, nty)];
+  float border_w = 0.0f;
+  int border_m = 0;
+  float gown[CS], gbor[CS];
+  if constexpr (CT > 0) ld_px<CT>(d_out + pix * CT, CT, gown);
+  if (bd.in) {
+    border_w = rast[bd.q * 4 + 3];
+    border_m = blend_mask[mask_index(g.n, bd.qh, bd.qw, ntx, nty)];
+    if constexpr (CT > 0) ld_px<CT>(d_out + bd.q * CT, CT, gbor);
+  }
+  aa_store_ids(g, bd, own_w, border_w, T, s_tri);
   if constexpr (CT > 0) {
-    if (g.inside) {
-      float v[CT];
-      ld_px<CT>(d_out + pix * CT, CT, v);
 #pragma unroll
-      for (int k = 0; k < CT; ++k) s_g[own][k] = v[k];
-
+    for (int k = 0; k < CT; ++k) s_g[own][k] = gown[k];
+    if (bd.in) {
+#pragma unroll
+      for (int k = 0; k < CT; ++k) s_g[bd.r * 18 + bd.c][k] = gbor[k];
     }
   }
-  // 1) queue the masked pairs: own pixel (all four directions), and for
-  //    lanes 0..15 of each wave one border pixel's direction into the tile.
+  // 1) queue the masked pairs: own pixel (all four directions), and the
+  //    border pixel's direction into the tile.
   {
-    const int m = g.inside ? blend_mask[mask_index(g.n, g.ph, g.pw, ntx, nty)] & 15 : 0;
+    const int m = g.inside ? own_m & 15 : 0;
 #pragma unroll
     for (int d = 0; d < 4; ++d) s_alpha[d][ly][lx] = 0.0f;
-    int hm = 0, hcell = 0;
-    if ((threadIdx.x & 63) < 16) {
-      const int side = threadIdx.x >> 6, i = threadIdx.x & 15;
-      int qh, qw, rr, cc, qd;
-      if (side == 0) { qw = g.x0 - 1;  qh = g.y0 + i;  rr = i + 1; cc = 0;     qd = 0; }
-      else if (side == 1) { qw = g.x0 + 16; qh = g.y0 + i;  rr = i + 1; cc = 17;    qd = 2; }
-      else if (side == 2) { qw = g.x0 + i;  qh = g.y0 - 1;  rr = 0;     cc = i + 1; qd = 1; }
-      else { qw = g.x0 + i;  qh = g.y0 + 16; rr = 17;    cc = i + 1; qd = 3; }
-      s_halo[side][i] = 0.0f;
-      const bool in = qh >= 0 && qh < H && qw >= 0 && qw < W;
-      if (in) {
-        const int64_t q = ((int64_t)g.n * H + qh) * W + qw;
-        if constexpr (CT > 0) {
-          const int cell = rr * 18 + cc;
-          float v[CT];
-          ld_px<CT>(d_out + q * CT, CT, v);
-#pragma unroll
-          for (int k = 0; k < CT; ++k) s_g[cell][k] = v[k];
-
-        }
-        if ((blend_mask[mask_index(g.n, qh, qw, ntx, nty)] >> qd) & 1) {
-          hm = 1;
-          hcell = ((rr * 18 + cc) << 2) | qd;
-        }
-      }
-    }
+    if (bd.lane) s_halo[threadIdx.x >> 6][threadIdx.x & 15] = 0.0f;
+    const int hm = bd.in && ((border_m >> bd.d) & 1);
     const int cnt = __popc(m) + hm;
     if (cnt) {
       int slot = atomicAdd(&s_nq, cnt);
 #pragma unroll
       for (int d = 0; d < 4; ++d)
         if ((m >> d) & 1) s_q[slot++] = (own << 2) | d;
-      if (hm) s_q[slot] = hcell;
+      if (hm) s_q[slot] = ((bd.r * 18 + bd.c) << 2) | bd.d;
     }
   }
   __syncthreads();
