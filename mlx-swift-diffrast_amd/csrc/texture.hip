@@ -792,8 +792,9 @@ __global__ void __launch_bounds__(kWinThreads, 5) k_tex_bwd_win(TexBwdArgs A, in
 
     // -- per pixel: footprints, gradients of uv / uvDA ------------------------
     float g[CT];
+    load_texel<CT>(A.d_out + pix * CT, CT, g);  // one vector load for CT = 4
 #pragma unroll
-    for (int c = 0; c < CT; ++c) g[c] = valid ? A.d_out[pix * CT + c] : 0.0f;
+    for (int c = 0; c < CT; ++c) g[c] = valid ? g[c] : 0.0f;
     const float2 uvp = *reinterpret_cast<const float2*>(A.uv + pix * 2);
     TapSlot q[2];
     float4 da_in = make_float4(0.f, 0.f, 0.f, 0.f), da = da_in;
