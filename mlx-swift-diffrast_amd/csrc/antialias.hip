@@ -665,14 +665,13 @@ __global__ void __launch_bounds__(256) k_aa_bwd(const float* __restrict__ rast,
 // with the forward's expressions, leaves the blend weight for the d_color
 // exchange and, for the tile's own pixels, adds the d_pos terms.  Pixels
 // without blends load no record.  With CT > 0 the cotangents of the tile
-// and its border are staged in LDS before the first barrier (colours are
-// loaded only for the queued pairs: staging them measured slower).
+// are staged in LDS before the first barrier (the few border neighbours
+// that blend into the tile are read from memory; colours are loaded only
+// for the queued pairs: staging them measured slower).
 constexpr int kMaskQueue = 256 * 4 + 64;
 
-// Seven workgroups per CU: the register budget this asks for (72) is met
-// without spills, one workgroup more than the compiler's own choice.
 template <int CT>
-__global__ void __launch_bounds__(256, 7) k_aa_bwd_masked(
+__global__ void __launch_bounds__(256) k_aa_bwd_masked(
     const float* __restrict__ rast, const AARec* __restrict__ rec, const float* __restrict__ pos,
     const float* __restrict__ color, const float* __restrict__ d_out,
     const uint8_t* __restrict__ blend_mask, int H, int W, int V, int T, int C, int ntx, int nty,
@@ -685,7 +684,7 @@ __global__ void __launch_bounds__(256, 7) k_aa_bwd_masked(
   __shared__ LdsTable<4, 128> tab;  // d_pos rows touched by this tile
   __shared__ int s_q[kMaskQueue];   // (cell r * 18 + c) << 2 | direction
   __shared__ int s_nq;
-  __shared__ float s_g[kCells][CS];  // d_out of the tile and its border (CT > 0)
+  __shared__ float s_g[kCells][CS];  // d_out of the tile (CT > 0; border cells unused)
   if (d_pos) lds_table_clear(tab);
   if (threadIdx.x == 0) s_nq = 0;
   const AATile g = aa_tile(H, W, ntx, nty);
@@ -700,21 +699,16 @@ __global__ void __launch_bounds__(256, 7) k_aa_bwd_masked(
   const int own_m = blend_mask[mask_index(g.n, min(g.ph, H - 1), min(g.pw, W - 1), ntx, nty)];
   float border_w = 0.0f;
   int border_m = 0;
-  float gown[CS], gbor[CS];
+  float gown[CS];
   if constexpr (CT > 0) ld_px<CT>(d_out + pix * CT, CT, gown);
   if (bd.in) {
     border_w = rast[bd.q * 4 + 3];
     border_m = blend_mask[mask_index(g.n, bd.qh, bd.qw, ntx, nty)];
-    if constexpr (CT > 0) ld_px<CT>(d_out + bd.q * CT, CT, gbor);
   }
   aa_store_ids(g, bd, own_w, border_w, T, s_tri);
   if constexpr (CT > 0) {
 #pragma unroll
     for (int k = 0; k < CT; ++k) s_g[own][k] = gown[k];
-    if (bd.in) {
-#pragma unroll
-      for (int k = 0; k < CT; ++k) s_g[bd.r * 18 + bd.c][k] = gbor[k];
-    }
   }
   // 1) queue the masked pairs: own pixel (all four directions), and the
   //    border pixel's direction into the tile.
@@ -799,14 +793,23 @@ __global__ void __launch_bounds__(256, 7) k_aa_bwd_masked(
     wn[3] = ly > 0 ? s_alpha[1][ly - 1][lx] : s_halo[2][lx];   // upper neighbour, its dir 1
     if constexpr (CT > 0) {
       const int nc[4] = {own + 1, own + 18, own - 1, own - 18};
+      const int64_t qn[4] = {pix + 1, pix + W, pix - 1, pix - W};
+      const bool edge[4] = {lx == 15, ly == 15, lx == 0, ly == 0};  // neighbour outside the tile
       float acc[CT];
 #pragma unroll
       for (int k = 0; k < CT; ++k) acc[k] = s_g[own][k] * (1.0f - asum);
 #pragma unroll
       for (int d = 0; d < 4; ++d) {
         if (wn[d] > 0.0f) {
+          float gq[CT];
+          if (edge[d]) {
+            ld_px<CT>(d_out + qn[d] * CT, CT, gq);
+          } else {
 #pragma unroll
-          for (int k = 0; k < CT; ++k) acc[k] += s_g[nc[d]][k] * wn[d];
+            for (int k = 0; k < CT; ++k) gq[k] = s_g[nc[d]][k];
+          }
+#pragma unroll
+          for (int k = 0; k < CT; ++k) acc[k] += gq[k] * wn[d];
         }
       }
       if (accumulate) {
