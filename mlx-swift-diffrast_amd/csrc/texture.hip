@@ -800,6 +800,11 @@ __global__ void __launch_bounds__(kWinThreads, 5) k_tex_bwd_win(TexBwdArgs A, in
     float4 da_in = make_float4(0.f, 0.f, 0.f, 0.f), da = da_in;
     float s = 1.0f;
     bool scaled = false;
+    // The second level's texels are read only when they count: a nonzero
+    // weight, or (trilinear) a LOD inside (0, L-1) at an integer, where
+    // d_lod needs its sample.  Magnified and background pixels (LOD clamped
+    // to 0) skip them.
+    bool need1 = false;
     if (mip) {
       da_in = *reinterpret_cast<const float4*>(A.uv_da + pix * 4);
       if (BIAS) {
@@ -812,6 +817,7 @@ __global__ void __launch_bounds__(kWinThreads, 5) k_tex_bwd_win(TexBwdArgs A, in
       q[0].scale = 1.0f - ld.frac;
       q[1].k = ld.k1;
       q[1].scale = ld.frac;
+      need1 = ld.frac != 0.0f || (FILTER == DR_FILTER_LINEAR_MIPMAP_LINEAR && ld.k0 != 0);
     } else {
       q[0].k = 0;
       q[0].scale = 1.0f;
@@ -830,7 +836,7 @@ __global__ void __launch_bounds__(kWinThreads, 5) k_tex_bwd_win(TexBwdArgs A, in
       const bool on = valid && q[li].scale != 0.0f;
       q[li].w00 = on ? w00 : 0.0f; q[li].w10 = on ? w10 : 0.0f;
       q[li].w01 = on ? w01 : 0.0f; q[li].w11 = on ? w11 : 0.0f;
-      if (valid && (mip || li == 0)) {
+      if (valid && (li == 0 || need1)) {
         float dfx, dfy;
         duv_level(level_ptr(k), Wk, CT, b, g, mip ? q[li].scale : 1.0f, dfx, dfy, samp[li]);
         dfx_total += dfx * (float)Wk;
