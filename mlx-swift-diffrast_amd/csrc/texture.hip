@@ -260,6 +260,9 @@ __device__ __forceinline__ void tex_fwd_px(
     float acc[CT];
 #pragma unroll
     for (int li = 0; li < 2; ++li) {
+      // a zero weight adds +0 to every channel: the second level is not read
+      // (the result differs only for non-finite texels, where 0 * inf is NaN)
+      if (li == 1 && ld.frac == 0.0f) break;
       const int k = li == 0 ? ld.k0 : ld.k1;
       const int Hk = mip_h(md, k), Wk = mip_w(md, k);
       const float* lv = k == 0 ? tex + n * tex_stride
