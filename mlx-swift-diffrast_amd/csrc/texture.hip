@@ -1017,6 +1017,7 @@ __global__ void __launch_bounds__(kWinThreads, 5) k_tex_bwd_win(TexBwdArgs A, in
 #pragma unroll
     for (int li = 0; li < 2; ++li) {
       const int w = wsel[li];
+      if (__ballot(w != -2) == 0) continue;  // no lane uses this slot (uniform)
       const float wt[4] = {q[li].w00, q[li].w10, q[li].w01, q[li].w11};
       const float sc = mip ? q[li].scale : 1.0f;
       // level and the four texel coordinates (each < 32767 on the window
