@@ -754,7 +754,7 @@ __device__ __forceinline__ void slot_box(const TapSlot& q, int& x0, int& x1, int
 
 template <int FILTER, int CT, int BND, bool BIAS>
 // Five waves per SIMD (the register budget this asks for costs a few
-// spilled values, measured cheaper than four).
+// spilled values; measured cheaper than four or six).
 __global__ void __launch_bounds__(kWinThreads, 5) k_tex_bwd_win(TexBwdArgs A, int total_tiles) {
   __shared__ double win[kWinTexels * CT];
   __shared__ int s_wk[kWinWaves];          // per wave: lowest level in use
