@@ -1151,6 +1151,49 @@ __global__ void __launch_bounds__(256) k_mip_block(const float* __restrict__ src
   }
 }
 
+// k_mip_block for four channels: one output texel per thread, 16-byte
+// loads and stores, the same sums in the same order.
+__global__ void __launch_bounds__(256) k_mip_block_c4(const float* __restrict__ src,
+                                                      float* __restrict__ pyr, MipDesc md, int s,
+                                                      int m) {
+  __shared__ float4 buf[2][256];
+  const int bs = 1 << m;  // source block edge
+  const int Ws = md.w[s];
+  const int nbx = Ws / bs;
+  const int bx = (int)blockIdx.x % nbx, by = (int)blockIdx.x / nbx;
+  const int n = (int)blockIdx.y;
+  const float4* lvl = reinterpret_cast<const float4*>(src) + (int64_t)n * md.h[s] * Ws;
+  auto mean4 = [](float4 a, float4 b, float4 d, float4 f) {
+    return make_float4((((a.x + b.x) + d.x) + f.x) * 0.25f, (((a.y + b.y) + d.y) + f.y) * 0.25f,
+                       (((a.z + b.z) + d.z) + f.z) * 0.25f, (((a.w + b.w) + d.w) + f.w) * 0.25f);
+  };
+  int cur = 0;
+  for (int j = 1; j <= m; ++j) {
+    const int e = bs >> j;  // output edge at this step
+    const int k = s + j;
+    const int Wk = md.w[k];
+    float4* dst = reinterpret_cast<float4*>(pyr + md.off[k]) + (int64_t)n * md.h[k] * Wk;
+    for (int t = threadIdx.x; t < e * e; t += blockDim.x) {
+      const int x = t % e, y = t / e;
+      float4 v;
+      if (j == 1) {
+        const int sx = bx * bs + 2 * x, sy = by * bs + 2 * y;
+        v = mean4(lvl[(int64_t)sy * Ws + sx], lvl[(int64_t)sy * Ws + sx + 1],
+                  lvl[(int64_t)(sy + 1) * Ws + sx], lvl[(int64_t)(sy + 1) * Ws + sx + 1]);
+      } else {
+        const int pe = 2 * e;
+        const float4* pb = buf[cur ^ 1];
+        v = mean4(pb[(2 * y) * pe + 2 * x], pb[(2 * y) * pe + 2 * x + 1],
+                  pb[(2 * y + 1) * pe + 2 * x], pb[(2 * y + 1) * pe + 2 * x + 1]);
+      }
+      buf[cur][y * e + x] = v;
+      dst[(int64_t)(by * e + y) * Wk + bx * e + x] = v;
+    }
+    __syncthreads();
+    cur ^= 1;
+  }
+}
+
 // Backward of the pyramid (MLX autodiff of concatenate + mean): level k's
 // total cotangent is its own gradient plus 1/4 of level k+1's total,
 // accumulated from the coarsest level down; level 0's total is added to
@@ -1673,7 +1716,11 @@ extern "C" int dr_texture_build_mip(const float* tex, int Nt, int H, int W, int 
       const dim3 grid((unsigned)((md.h[sl] / bs) * (md.w[sl] / bs)), (unsigned)Nt);
       {
         DR_TIMED("k_mip_block", stream);
-        hipLaunchKernelGGL(k_mip_block, grid, dim3(256), 0, stream, src, pyramid, md, sl, m, Nt, C);
+        if (C == 4 && (((uintptr_t)src | (uintptr_t)pyramid) & 15) == 0)
+          hipLaunchKernelGGL(k_mip_block_c4, grid, dim3(256), 0, stream, src, pyramid, md, sl, m);
+        else
+          hipLaunchKernelGGL(k_mip_block, grid, dim3(256), 0, stream, src, pyramid, md, sl, m, Nt,
+                             C);
       }
       DR_CHECK_LAUNCH();
       sl += m;
