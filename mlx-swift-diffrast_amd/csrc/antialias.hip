@@ -692,9 +692,9 @@ __global__ void __launch_bounds__(256) k_aa_bwd_masked(
   const int64_t pix = ((int64_t)g.n * H + min(g.ph, H - 1)) * W + min(g.pw, W - 1);
   const int lx = g.lx, ly = g.ly;
   const int own = (ly + 1) * 18 + (lx + 1);
-  // every load before the barrier is issued first: the ids, blend-mask bytes
-  // and cotangents of the own pixel and (lanes 0..15 of each wave) one
-  // border pixel
+  // every load before the barrier is issued first: the own pixel's id, mask
+  // byte and cotangent, and (lanes 0..15 of each wave) one border pixel's id
+  // and mask byte
   const float own_w = rast[pix * 4 + 3];
   const int own_m = blend_mask[mask_index(g.n, min(g.ph, H - 1), min(g.pw, W - 1), ntx, nty)];
   float border_w = 0.0f;
