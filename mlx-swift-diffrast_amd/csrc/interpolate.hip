@@ -145,8 +145,7 @@ __global__ void __launch_bounds__(256) k_interp_bwd(
     int A_, float* __restrict__ d_attr, int64_t d_attr_stride, float* __restrict__ d_rast,
     float* __restrict__ d_rast_db) {
   __shared__ LdsTable<(AT > 0 ? AT : 1), 256> tab;  // d_attr rows (or elements) touched by this tile
-  lds_table_clear(tab);
-  __syncthreads();
+  __shared__ int s_any[4];  // per wave: a covered pixel
   const int tiles = ntx * nty;
   const int b = (int)blockIdx.x;
   const int n = b / tiles;
@@ -161,6 +160,21 @@ __global__ void __launch_bounds__(256) k_interp_bwd(
   const float4 r = *reinterpret_cast<const float4*>(rast + pix * 4);
   const int t = f2i(r.w) - 1;
   bool valid = inside && t >= 0 && t < T;
+  {
+    const uint64_t any = __ballot(valid);
+    if (lane == 0) s_any[wave] = any != 0ull;
+  }
+  __syncthreads();
+  if (!(s_any[0] | s_any[1] | s_any[2] | s_any[3])) {  // uniform: an empty tile
+    if (inside) {
+      *reinterpret_cast<float4*>(d_rast + pix * 4) = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (K_ > 0 && d_rast_db)
+        *reinterpret_cast<float4*>(d_rast_db + pix * 4) = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    return;
+  }
+  lds_table_clear(tab);
+  __syncthreads();
   const float u = r.x, v = r.y;
   const float bw = 1.0f - u - v;
   const float* at = attr + (int64_t)n * attr_stride;

@@ -452,8 +452,7 @@ __global__ void __launch_bounds__(256) k_raster_bwd(
     const float* __restrict__ d_rast_db, int N, int V, int T, int H, int W, int ntx, int nty,
     float* __restrict__ d_pos) {
   __shared__ LdsTable<4, 256> tab;  // d_pos rows touched by this tile
-  lds_table_clear(tab);
-  __syncthreads();
+  __shared__ int s_any[4];          // per wave: a covered pixel
   const int tiles = ntx * nty;
   const int b = xcd_remap((int)blockIdx.x, tiles * N);
   const int n = b / tiles;
@@ -470,6 +469,14 @@ __global__ void __launch_bounds__(256) k_raster_bwd(
   const float4 r = *reinterpret_cast<const float4*>(rast + pix * 4);
   const int t = f2i(r.w) - 1;
   valid = valid && t >= 0 && t < T;
+  {
+    const uint64_t any = __ballot(valid);
+    if (lane == 0) s_any[wave] = any != 0ull;
+  }
+  __syncthreads();
+  if (!(s_any[0] | s_any[1] | s_any[2] | s_any[3])) return;  // uniform: nothing to add
+  lds_table_clear(tab);
+  __syncthreads();
   float val[12];
   int i0 = 0, i1 = 0, i2 = 0;
 #pragma unroll
