@@ -808,6 +808,7 @@ __global__ void __launch_bounds__(kWinThreads, 5) k_tex_bwd_win(TexBwdArgs A, in
     // d_lod needs its sample.  Magnified and background pixels (LOD clamped
     // to 0) skip them.
     bool need1 = false;
+    bool lod0 = true;  // LOD clamped to 0: no d_lod sample is needed
     if (mip) {
       da_in = *reinterpret_cast<const float4*>(A.uv_da + pix * 4);
       if (BIAS) {
@@ -821,6 +822,7 @@ __global__ void __launch_bounds__(kWinThreads, 5) k_tex_bwd_win(TexBwdArgs A, in
       q[1].k = ld.k1;
       q[1].scale = ld.frac;
       need1 = ld.frac != 0.0f || (FILTER == DR_FILTER_LINEAR_MIPMAP_LINEAR && ld.k0 != 0);
+      lod0 = FILTER != DR_FILTER_LINEAR_MIPMAP_LINEAR || (ld.k0 == 0 && ld.frac == 0.0f);
     } else {
       q[0].k = 0;
       q[0].scale = 1.0f;
@@ -839,7 +841,11 @@ __global__ void __launch_bounds__(kWinThreads, 5) k_tex_bwd_win(TexBwdArgs A, in
       const bool on = valid && q[li].scale != 0.0f;
       q[li].w00 = on ? w00 : 0.0f; q[li].w10 = on ? w10 : 0.0f;
       q[li].w01 = on ? w01 : 0.0f; q[li].w11 = on ? w11 : 0.0f;
-      if (valid && (li == 0 || need1)) {
+      // A footprint collapsed onto one texel (clamped at a corner; every
+      // background pixel) has zero texel differences: its uv gradient is
+      // zero and, at LOD 0, its sample is not needed.
+      const bool flat = BND != DR_BOUNDARY_ZERO && b.ix0 == b.ix1 && b.iy0 == b.iy1 && lod0;
+      if (valid && (li == 0 || need1) && !flat) {
         float dfx, dfy;
         duv_level(level_ptr(k), Wk, CT, b, g, mip ? q[li].scale : 1.0f, dfx, dfy, samp[li]);
         dfx_total += dfx * (float)Wk;
