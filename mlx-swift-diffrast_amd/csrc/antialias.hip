@@ -100,8 +100,9 @@ __global__ void __launch_bounds__(256) k_aa_rec(const float* __restrict__ pos,
                                                 AARec* __restrict__ rec) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= NT) return;
-  const int64_t n = i / T;
-  const int t = (int)(i - n * T);
+  int64_t n;
+  int t;
+  divmod64(i, T, n, t);
   const float* p = pos + n * V * 4;
   const int v0 = tri[(int64_t)t * 3 + 0], v1 = tri[(int64_t)t * 3 + 1],
             v2 = tri[(int64_t)t * 3 + 2];

@@ -106,6 +106,19 @@ __device__ __forceinline__ int f2i(float x) {
   return r;
 }
 
+// q = i / d, r = i % d for 0 <= i and 0 < d: a 32-bit division while i fits
+// in 31 bits (several times cheaper than the 64-bit one).
+__device__ __forceinline__ void divmod64(int64_t i, int d, int64_t& q, int& r) {
+  if (i <= 0x7fffffff) {
+    const int ii = (int)i, qq = ii / d;
+    q = qq;
+    r = ii - qq * d;
+  } else {
+    q = i / d;
+    r = (int)(i - q * d);
+  }
+}
+
 // Whether a triangle's three vertex ids index rows [0, V) of its vertex
 // buffer.  Triangles that fail are not drawn and get no gradient, so no
 // input can send a vertex read out of range.

@@ -35,15 +35,18 @@ __global__ void __launch_bounds__(256) k_setup(const float* __restrict__ pos, in
                                                int4* __restrict__ rect) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= (int64_t)Npos * T) return;
-  const int n = (int)(i / T);
-  const int t = (int)(i - (int64_t)n * T);
-  const float* p = pos + (int64_t)n * pos_stride;
+  int64_t n;
+  int t;
+  divmod64(i, T, n, t);
+  const float* p = pos + n * pos_stride;
   const int i0 = tri[t * 3 + 0], i1 = tri[t * 3 + 1], i2 = tri[t * 3 + 2];
   const bool ok = verts_ok(i0, i1, i2, V);  // else not drawn
-  const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
-  const float4 v0 = ok ? *reinterpret_cast<const float4*>(p + (int64_t)i0 * 4) : z4;
-  const float4 v1 = ok ? *reinterpret_cast<const float4*>(p + (int64_t)i1 * 4) : z4;
-  const float4 v2 = ok ? *reinterpret_cast<const float4*>(p + (int64_t)i2 * 4) : z4;
+  float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f), v1 = v0, v2 = v0;
+  if (ok) {
+    v0 = *reinterpret_cast<const float4*>(p + (int64_t)i0 * 4);
+    v1 = *reinterpret_cast<const float4*>(p + (int64_t)i1 * 4);
+    v2 = *reinterpret_cast<const float4*>(p + (int64_t)i2 * 4);
+  }
   TriRec r;
   int4 rc = make_int4(-1, -1, -1, -1);
   if (!ok || v0.w <= 0.0f || v1.w <= 0.0f || v2.w <= 0.0f) {
