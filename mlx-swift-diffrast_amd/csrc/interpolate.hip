@@ -105,7 +105,9 @@ __global__ void __launch_bounds__(256) k_interp_fwd(
 #pragma unroll
     for (int k = 0; k < NK; ++k) odv[k] = 0.0f;
     if (t[q] >= 0) {
-      const float* at = attr + (int64_t)(pix / HW) * attr_stride;
+      // image index: 32-bit division while the pixel index fits
+      const int64_t img = pix <= 0x7fffffff ? (int64_t)((int)pix / HW) : pix / HW;
+      const float* at = attr + img * attr_stride;
       float a0[NA], a1[NA], a2[NA];
 #pragma unroll
       for (int a = 0; a < NA; ++a) {

@@ -196,10 +196,9 @@ __device__ __forceinline__ void tex_fwd_px(
     const float* __restrict__ tex, const float* __restrict__ pyr, const MipDesc& md,
     int64_t tex_stride, int Ht, int Wt, int C_, const float* __restrict__ uv,
     const float* __restrict__ uv_da, const float* __restrict__ bias_map, float scale_bias,
-    int has_bias, int boundary, int64_t P, int HWi, float* __restrict__ out, int64_t pix) {
+    int has_bias, int boundary, int64_t P, int n, float* __restrict__ out, int64_t pix) {
   if (pix >= P) return;
   const int C = dimC<CT>(C_);
-  const int n = (int)(pix / HWi);
   float* o = out + pix * C;
   if (CUBE) {  // Texture.swift:638-684
     const float x = uv[pix * 3 + 0], y = uv[pix * 3 + 1], z = uv[pix * 3 + 2];
@@ -325,8 +324,8 @@ __global__ void __launch_bounds__(256) k_tex_fwd(
   // pixels past the image's right or bottom edge get index P: no work
   const int64_t pix = ph < Hi && pw < Wi ? ((int64_t)n * Hi + ph) * Wi + pw : P;
   tex_fwd_px<FILTER, BND == DR_BOUNDARY_CUBE, CT>(tex, pyr, md, tex_stride, Ht, Wt, C_, uv, uv_da,
-                                                  bias_map, scale_bias, has_bias, BND, P, Hi * Wi,
-                                                  out, pix);
+                                                  bias_map, scale_bias, has_bias, BND, P, n, out,
+                                                  pix);
 }
 
 // ---------------------------------------------------------------------------
