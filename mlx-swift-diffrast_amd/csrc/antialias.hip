@@ -345,18 +345,27 @@ __global__ void __launch_bounds__(256) k_aa_fwd(const float* __restrict__ rast,
                                                 float* __restrict__ out,
                                                 uint8_t* __restrict__ blend_mask) {
   __shared__ int s_tri[18][18];
+  // colours of the tile and its border (CT > 0), so a blend reads its
+  // neighbour from LDS rather than in a third global round trip
+  __shared__ __align__(16) float s_col[18][18][CT > 0 ? CT : 1];
   const AATile g = aa_tile(H, W, ntx, nty);
   const AABorder bd = aa_border(g, H, W);
   const int64_t pix = ((int64_t)g.n * H + min(g.ph, H - 1)) * W + min(g.pw, W - 1);
-  // every load before the barrier is issued first: own and border ids, own colour
+  // every load before the barrier is issued first: own and border ids and colours
   const float own_w = rast[pix * 4 + 3];
   float border_w = 0.0f;
   if (bd.in) border_w = rast[bd.q * 4 + 3];
   float cp[CT > 0 ? CT : 1];
+  float cb[CT > 0 ? CT : 1];
   if constexpr (CT > 0) {
     if (g.inside) ld_px<CT>(color + pix * CT, CT, cp);
+    if (bd.in) ld_px<CT>(color + bd.q * CT, CT, cb);
   }
   aa_store_ids(g, bd, own_w, border_w, T, s_tri);
+  if constexpr (CT > 0) {
+    if (g.inside) st_px<CT>(&s_col[g.ly + 1][g.lx + 1][0], cp);
+    if (bd.in) st_px<CT>(&s_col[bd.r][bd.c][0], cb);
+  }
   __syncthreads();
   if (!g.inside) return;
   const int r = g.ly + 1, c = g.lx + 1;
@@ -392,12 +401,14 @@ __global__ void __launch_bounds__(256) k_aa_fwd(const float* __restrict__ rast,
       float acc[CT];
 #pragma unroll
       for (int k = 0; k < CT; ++k) acc[k] = cp[k];
-      const int64_t nb[4] = {pix + 1, pix + W, pix - 1, pix - W};
+      // a blending neighbour is a candidate, so it lies in the image and
+      // its colour is in s_col
+      const int nr[4] = {r, r + 1, r, r - 1}, nc[4] = {c + 1, c, c - 1, c};
 #pragma unroll
       for (int d = 0; d < 4; ++d) {
         if (alpha[d] > 0.0f) {
           float cn[CT];
-          ld_px<CT>(color + nb[d] * CT, CT, cn);
+          ld_px<CT>(&s_col[nr[d]][nc[d]][0], CT, cn);
 #pragma unroll
           for (int k = 0; k < CT; ++k) acc[k] += alpha[d] * (cn[k] - cp[k]);
         }
