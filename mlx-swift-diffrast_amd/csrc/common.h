@@ -465,6 +465,44 @@ inline hipError_t fill_async(T* p, T v, int64_t n, hipStream_t s) {
   return hipGetLastError();
 }
 
+// Two 16-byte aligned runs of 4-byte values in one launch.
+template <typename T>
+__global__ void fill4x2_kernel(T* __restrict__ p0, int64_t n0, T* __restrict__ p1, int64_t n1,
+                               T v) {
+  static_assert(sizeof(T) == 4, "4-byte values");
+  const int64_t a = n0 >> 2, n4 = a + (n1 >> 2);
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  const uint32_t b = __builtin_bit_cast(uint32_t, v);
+  uint4* q0 = reinterpret_cast<uint4*>(p0);
+  uint4* q1 = reinterpret_cast<uint4*>(p1);
+  for (int64_t j = i; j < n4; j += stride) {
+    if (j < a) q0[j] = make_uint4(b, b, b, b);
+    else q1[j - a] = make_uint4(b, b, b, b);
+  }
+  if (i < (n0 & 3)) p0[a * 4 + i] = v;
+  if (i < (n1 & 3)) p1[(n1 >> 2) * 4 + i] = v;
+}
+
+// Fills two buffers with v: one launch when both are 16-byte aligned.
+template <typename T>
+inline hipError_t fill2_async(T* p0, int64_t n0, T* p1, int64_t n1, T v, hipStream_t s) {
+  if constexpr (sizeof(T) == 4) {
+    if (n0 > 0 && n1 > 0 && ((uintptr_t)p0 & 15) == 0 && ((uintptr_t)p1 & 15) == 0) {
+      DR_TIMED("fill", s);
+      int64_t blocks = (n0 / 4 + n1 / 4 + 255) / 256;
+      if (blocks < 1) blocks = 1;
+      if (blocks > 8192) blocks = 8192;
+      hipLaunchKernelGGL(fill4x2_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, s, p0, n0, p1,
+                         n1, v);
+      return hipGetLastError();
+    }
+  }
+  hipError_t e = fill_async(p0, v, n0, s);
+  if (e != hipSuccess) return e;
+  return fill_async(p1, v, n1, s);
+}
+
 inline unsigned grid_for(int64_t n, int block) {
   return (unsigned)((n + block - 1) / block);
 }

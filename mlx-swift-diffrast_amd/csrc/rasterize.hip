@@ -791,7 +791,9 @@ extern "C" int dr_rasterize_fwd(const float* pos, int64_t pos_batch_stride, cons
   int* list = (int*)scratch_get(sc, stream, SLOT_RAST_LIST, (size_t)n_tiles * C * 4);
   if (!list) return DR_ERR_MEMORY;
 
-  DR_CHECK_HIP(fill_async(fillc, 0, n_tiles, stream));
+  // fillc and the largest-count cell after it (cbuf holds 4 ints per tile)
+  int* fmax = fillc + n_tiles;
+  DR_CHECK_HIP(fill_async(fillc, 0, n_tiles + 1, stream));
   launch_binning(true, it, n_items, max_items, N, rect, ntx, tiles, fillc, list, C, stream);
   DR_CHECK_LAUNCH();
   const dim3 grid((unsigned)n_tiles), block(256);
@@ -809,12 +811,11 @@ extern "C" int dr_rasterize_fwd(const float* pos, int64_t pos_batch_stride, cons
 #undef DR_RASTER
   DR_CHECK_LAUNCH();
   if (!sc->total_pending) {  // largest count of this call, for the next one
-    DR_CHECK_HIP(fill_async(tmax, 0, 1, stream));
     hipLaunchKernelGGL(k_tile_max, dim3(grid_for(n_tiles, 256)), dim3(256), 0, stream, fillc,
-                       n_tiles, tmax);
+                       n_tiles, fmax);
     DR_CHECK_LAUNCH();
     *sc->pinned_total = 0;
-    DR_CHECK_HIP(hipMemcpyAsync(sc->pinned_total, tmax, sizeof(int), hipMemcpyDeviceToHost,
+    DR_CHECK_HIP(hipMemcpyAsync(sc->pinned_total, fmax, sizeof(int), hipMemcpyDeviceToHost,
                                 stream));
     DR_CHECK_HIP(hipEventRecord(sc->total_event, stream));
     sc->total_pending = true;

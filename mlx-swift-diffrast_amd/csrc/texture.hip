@@ -1936,10 +1936,12 @@ extern "C" int dr_texture_bwd(const float* tex, const float* pyramid, int Nt, in
   const bool cube = boundary == DR_BOUNDARY_CUBE;
   const int64_t tex_stride = Nt == 1 ? 0 : (int64_t)(cube ? 6 : 1) * Ht * Wt * C;
   const int64_t ntex = (int64_t)Nt * (cube ? 6 : 1) * Ht * Wt * C;
-  if (!(flags & DR_ACCUMULATE)) DR_CHECK_HIP(fill_async(d_tex, 0.0f, ntex, stream));
-  if (cube && (filter >= DR_FILTER_LINEAR_MIPMAP_NEAREST || (flags & DR_CUBE_DIR_GRAD)))
+  const bool zero_tex = !(flags & DR_ACCUMULATE);
+  if (cube && (filter >= DR_FILTER_LINEAR_MIPMAP_NEAREST || (flags & DR_CUBE_DIR_GRAD))) {
+    if (zero_tex) DR_CHECK_HIP(fill_async(d_tex, 0.0f, ntex, stream));
     return cube_bwd(tex, pyramid, md, tex_stride, Nt, Ht, Wt, C, uv, uv_da, bias_map, bias,
                     filter, N, Hi, Wi, d_out, d_tex, d_uv, d_uv_da, d_bias_map, flags, stream);
+  }
   const bool mip = !cube && filter >= DR_FILTER_LINEAR_MIPMAP_NEAREST;
   float* d_pyr = nullptr;
   if (mip && md.L > 1) {
@@ -1948,7 +1950,11 @@ extern "C" int dr_texture_bwd(const float* tex, const float* pyramid, int Nt, in
     const int64_t np = dr_texture_mip_size(Nt, Ht, Wt, C, md.L);
     d_pyr = (float*)scratch_get(sc, stream, SLOT_DPYR, (size_t)np * sizeof(float));
     if (!d_pyr) return DR_ERR_MEMORY;
-    DR_CHECK_HIP(fill_async(d_pyr, 0.0f, np, stream));
+    // d_tex and the coarser levels' accumulator are zeroed in one launch
+    if (zero_tex) DR_CHECK_HIP(fill2_async(d_tex, ntex, d_pyr, np, 0.0f, stream));
+    else DR_CHECK_HIP(fill_async(d_pyr, 0.0f, np, stream));
+  } else if (zero_tex) {
+    DR_CHECK_HIP(fill_async(d_tex, 0.0f, ntex, stream));
   }
   const int ntx = (Wi + 15) / 16, nty = (Hi + 15) / 16;
   TexBwdArgs args;
