@@ -185,10 +185,30 @@ def _bias_map(m, uv):
     return m.to(torch.float32).contiguous()
 
 
-def _packed_pyramid(levels, tex):
+class MipPyramid(list):
+    """What `textureConstructMip` returns: the list [tex, level1, ...] plus
+    the identity and in-place version of `tex` when the levels were built,
+    so that `texture(mip=...)` can refuse a pyramid whose texture has been
+    changed since (an optimizer step updates it in place)."""
+
+    def __init__(self, levels, tex):
+        super().__init__(levels)
+        self.source_ptr = tex.data_ptr()
+        self.source_version = tex._version
+
+
+def _packed_pyramid(levels, tex, tex_arg):
     """(L, packed levels 1..L-1) of a `textureConstructMip` list: its levels
     are views of one buffer in the library's packing, used as they are; any
-    other list of [Nt, Hk, Wk, C] levels is packed by a copy."""
+    other list of [Nt, Hk, Wk, C] levels is packed by a copy.  A
+    `MipPyramid` must still describe `tex_arg` as it is now."""
+    if isinstance(levels, MipPyramid):
+        if tex_arg.data_ptr() != levels.source_ptr:
+            raise ValueError("texture: mip was built from another texture tensor "
+                             "(textureConstructMip(tex) of the tex passed here)")
+        if tex_arg._version != levels.source_version:
+            raise ValueError("texture: tex was modified in place after textureConstructMip; "
+                             "rebuild mip from the current texture")
     levels = list(levels)
     if not levels:
         raise ValueError("texture: mip must hold at least level 0")
@@ -461,7 +481,9 @@ class DiffRast:
         (Texture.swift:141-143 suggests such caching).  Its levels are read
         as given (fewer levels cap the LOD); the gradient still flows to
         `tex` through the 2x2 box backward, as for a pyramid built in the
-        call.
+        call.  A pyramid from `textureConstructMip` raises ValueError once
+        `tex` has been changed in place (or when another tensor is passed);
+        a plain list of levels is taken as it is.
 
         Cube maps (boundaryMode cube) also take the mip filters, with uvDA
         the direction's screen derivatives [N, H_img, W_img, 6] (the layout
@@ -511,13 +533,14 @@ class DiffRast:
         if tuple(uvDA.shape) != tuple(uvf.shape[:3]) + (4,):
             raise ValueError(f"texture: uvDA must be [N, H_img, W_img, 4] (got {list(uvDA.shape)})")
         bm = _bias_map(mipLevelBiasMap, uvf)
-        cached = None if mip is None else _packed_pyramid(mip, texf)
+        cached = None if mip is None else _packed_pyramid(mip, texf, tex)
         return _TextureFn.apply(texf, uvf, uvDA.to(torch.float32).contiguous(), bm, filt, bnd,
                                 float(mipLevelBias), cached)
 
     @staticmethod
     def textureConstructMip(tex: torch.Tensor, maxLevel: Optional[int] = None) -> List[torch.Tensor]:
-        """Texture.swift:144-161: [level0 = tex, level1, ...], 2x2 box means."""
+        """Texture.swift:144-161: [level0 = tex, level1, ...], 2x2 box means
+        (a `MipPyramid`, which also records tex's in-place version)."""
         if tex.ndim != 4:
             raise ValueError(f"textureConstructMip: tex must be [N, H, W, C] (got {list(tex.shape)})")
         lib = _lib.load()
@@ -533,7 +556,7 @@ class DiffRast:
             n = Nt * h * w * C
             levels.append(pyr[off:off + n].view(Nt, h, w, C))
             off += n
-        return levels
+        return MipPyramid(levels, tex)
 
     @staticmethod
     def antialiasConstructTopologyHash(tri) -> torch.Tensor:

@@ -69,8 +69,9 @@ def test_texture(fixtures):
     out = dr.texture(dev(TEX8), dev(fixtures["uv"]), uv_da=dev(fixtures["uv_da"]),
                      filter_mode="auto", boundary_mode="clamp")
     assert np.abs(host(out) - fixtures["tex_trilinear"]).max() <= 1e-4
-    mip = dr.texture_construct_mip(dev(TEX8))
-    out2 = dr.texture(dev(TEX8), dev(fixtures["uv"]), uv_da=dev(fixtures["uv_da"]), mip=mip,
+    t8 = dev(TEX8)
+    mip = dr.texture_construct_mip(t8)
+    out2 = dr.texture(t8, dev(fixtures["uv"]), uv_da=dev(fixtures["uv_da"]), mip=mip,
                       filter_mode="linear-mipmap-linear", boundary_mode="clamp")
     np.testing.assert_array_equal(host(out2), host(out))
 

@@ -135,11 +135,30 @@ def test_range_mode():
     check_fwd(sc["pos"], sc["tri"], 33, 35, ranges=ranges)
 
 
-def test_peel_layers():
-    sc = scenes.textured_icosphere(N=1, H=96, W=96, level=3, tex_size=8)
+@pytest.mark.parametrize("gradDB", [False, True])
+def test_peel_layers(gradDB):
+    """Three depth-peeling layers, with and without rast_db (the reference's
+    default is gradDB = true, Rasterize.swift:48), forward bit-exact and each
+    layer's d_pos against the oracle."""
+    torch = torch_dev()
+    sc = scenes.textured_icosphere(N=2, H=96, W=96, level=3, tex_size=8)
+    pos, tri = sc["pos"], sc["tri"]
+    rng = np.random.default_rng(21)
     prev = None
-    for _ in range(3):
-        prev = check_fwd(sc["pos"], sc["tri"], 96, 96, gradDB=False, peel=prev)
+    for layer in range(3):
+        cur = check_fwd(pos, tri, 96, 96, gradDB=gradDB, peel=prev)
+        # a closed sphere has two layers (front and back); the third is empty
+        assert (cur[..., 3] > 0).any() == (layer < 2), layer
+        p, r, db = run(pos, tri, 96, 96, gradDB, peel=prev)
+        g = rng.normal(size=tuple(r.shape)).astype(np.float32)
+        gdb = rng.normal(size=tuple(r.shape)).astype(np.float32) if gradDB else None
+        loss = (r * dev(g)).sum()
+        if gradDB:
+            loss = loss + (db * dev(gdb)).sum()
+        loss.backward()
+        ref = O.rasterize_vjp(pos, tri, cur, g, gdb)
+        assert_grad_close(host(p.grad), ref, f"d_pos layer {layer}")
+        prev = cur
 
 
 @pytest.mark.parametrize("name", ["tier1", "hexpie", "icosphere"])

@@ -2,13 +2,15 @@
 shared and per-image textures, C in {1,2,3,4,5}, mip bias (scalar and
 per-pixel), cube maps.  Forward within the forward tolerance (the LOD's
 log2 may differ by an ulp between CPU and GPU, so mip modes are compared
-with tolerance); d_uv / d_uvDA / d_biasMap and the scatter-added d_tex
-within the gradient tolerance."""
+with tolerance); d_uv and the scatter-added d_tex within the gradient
+tolerance; d_uvDA / d_biasMap within it off the pixels on a mip-level
+switch (parity.lod_switch_mask), which must be under 1% of all."""
 import numpy as np
 import pytest
 
 import oracle as O
-from parity import assert_fwd_close, assert_grad_close, dev, host, torch_dev
+from parity import (LOD_DELTA, assert_fwd_close, assert_grad_close, assert_grad_close_lod, dev, host,
+                    lod_switch_mask, torch_dev)
 
 pytestmark = pytest.mark.gpu
 
@@ -53,7 +55,9 @@ def test_texture(filt, bnd, C, Nt):
     assert_grad_close(host(t.grad), d_tex, "d_tex")
     assert_grad_close(host(u.grad), d_uv, "d_uv")
     if mip:
-        assert_grad_close(host(d.grad), d_da, "d_uvDA", rtol=1e-3)
+        lo, hi = (O.texture_vjp(tex, uv, g, uvDA=da, filterMode=filt, boundaryMode=bnd,
+                                mipLevelBias=b)[2] for b in (-LOD_DELTA, LOD_DELTA))
+        assert_grad_close_lod(host(d.grad), d_da, lod_switch_mask(d_da, lo, hi), "d_uvDA")
 
 
 @pytest.mark.parametrize("filt", ["linear-mipmap-linear", "linear-mipmap-nearest"])
@@ -79,8 +83,11 @@ def test_mip_bias(filt):
                                             mipLevelBiasMap=bm)
     assert_grad_close(host(t.grad), d_tex, "d_tex")
     assert_grad_close(host(u.grad), d_uv, "d_uv")
-    assert_grad_close(host(d.grad), d_da, "d_uvDA", rtol=1e-3)
-    assert_grad_close(host(b.grad), d_bm, "d_biasMap", rtol=1e-3)
+    lo, hi = (O.texture_vjp(tex, uv, g, uvDA=da, filterMode=filt, boundaryMode="clamp",
+                            mipLevelBias=0.5 + b, mipLevelBiasMap=bm) for b in (-LOD_DELTA, LOD_DELTA))
+    sw = lod_switch_mask(d_da, lo[2], hi[2]) | lod_switch_mask(d_bm, lo[3], hi[3])
+    assert_grad_close_lod(host(d.grad), d_da, sw, "d_uvDA")
+    assert_grad_close_lod(host(b.grad), d_bm, sw, "d_biasMap")
 
 
 @pytest.mark.parametrize("C,Nt", [(3, 1), (1, 2), (4, 2)])
@@ -165,7 +172,9 @@ def test_smooth_lod_ramp(filt, bnd):
     assert_grad_close(host(t.grad), d_tex, "d_tex")
     assert_grad_close(host(uu.grad), d_uv, "d_uv")
     if mip:
-        assert_grad_close(host(d.grad), d_da, "d_uvDA", rtol=1e-3)
+        lo, hi = (O.texture_vjp(tex, uv, g, uvDA=da, filterMode=filt, boundaryMode=bnd,
+                                mipLevelBias=b)[2] for b in (-LOD_DELTA, LOD_DELTA))
+        assert_grad_close_lod(host(d.grad), d_da, lod_switch_mask(d_da, lo, hi), "d_uvDA")
 
 
 def test_cached_pyramid():
@@ -204,15 +213,40 @@ def test_cached_pyramid_fewer_levels():
     from diffrast import DiffRast
     rng = np.random.default_rng(12)
     tex = rng.random((1, 32, 32, 3)).astype(np.float32)
-    mip = DiffRast.textureConstructMip(dev(tex), maxLevel=3)
+    td = dev(tex)
+    mip = DiffRast.textureConstructMip(td, maxLevel=3)
     assert len(mip) == 4
     iy, ix = np.meshgrid(np.arange(4), np.arange(4), indexing="ij")
     uv = np.stack([(ix + 0.5) / 4, (iy + 0.5) / 4], -1).astype(np.float32)[None]
     da = np.tile(np.array([1.0, 0.0, 0.0, 1.0], np.float32), (1, 4, 4, 1))
-    out = DiffRast.texture(dev(tex), dev(uv), uvDA=dev(da), filterMode="linear-mipmap-linear",
+    out = DiffRast.texture(td, dev(uv), uvDA=dev(da), filterMode="linear-mipmap-linear",
                            boundaryMode="clamp", mip=mip)
     want = tex.astype(np.float64).reshape(1, 4, 8, 4, 8, 3).mean(axis=(2, 4))
     np.testing.assert_allclose(host(out), want, rtol=1e-6, atol=1e-6)
     with pytest.raises(ValueError):
         DiffRast.texture(dev(tex), dev(uv), uvDA=dev(da), filterMode="linear-mipmap-linear",
                          mip=[dev(tex), dev(tex)])
+
+
+def test_cached_pyramid_stale():
+    # a pyramid whose texture was changed in place (an optimizer step) or
+    # that belongs to another tensor is refused; a rebuilt one is accepted
+    torch = torch_dev()
+    from diffrast import DiffRast
+    rng = np.random.default_rng(13)
+    tex, uv, da = inputs(rng, 1, 1, 32, 32, 4, 9, 11)
+    t = dev(tex).requires_grad_(True)
+    kw = dict(uvDA=dev(da), filterMode="linear-mipmap-linear", boundaryMode="clamp")
+    mip = DiffRast.textureConstructMip(t.detach())
+    DiffRast.texture(t, dev(uv), mip=mip, **kw)
+    with torch.no_grad():
+        t.add_(0.5)
+    with pytest.raises(ValueError, match="modified in place"):
+        DiffRast.texture(t, dev(uv), mip=mip, **kw)
+    with pytest.raises(ValueError, match="another texture"):
+        DiffRast.texture(dev(tex), dev(uv), mip=DiffRast.textureConstructMip(t.detach()), **kw)
+    mip = DiffRast.textureConstructMip(t.detach())
+    out = DiffRast.texture(t, dev(uv), mip=mip, **kw)
+    ref = O.texture(tex + np.float32(0.5), uv, uvDA=da, filterMode="linear-mipmap-linear",
+                    boundaryMode="clamp")
+    assert_fwd_close(host(out), ref)
