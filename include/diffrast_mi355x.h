@@ -116,11 +116,34 @@ int dr_profile_report(char* buf, int len);
  *     only depths greater than that layer's are kept).
  *   rast_db: NULL for gradDB = false.
  * Unlike the reference, the per-tile triangle lists never overflow (the
- * reference drops triangles beyond 128 per 16x16 tile), and equal depths
- * resolve to the lowest triangle index. */
+ * reference drops triangles beyond 128 per 16x16 tile; see
+ * dr_rasterize_fwd_ex), and equal depths resolve to the lowest triangle
+ * index.
+ * Host synchronisation: the first call on a stream counts every tile's
+ * candidates exactly and waits for that count (it sizes the per-tile
+ * lists); later calls only read back, asynchronously, the largest count
+ * of an earlier call.  A call whose scratch memory must grow waits for the
+ * stream before freeing the smaller buffer.  Range mode stages ranges_host
+ * through pinned memory and does not wait (unless it runs four calls ahead
+ * of the device).  Calls otherwise return before their work has run. */
 int dr_rasterize_fwd(const float* pos, int64_t pos_batch_stride, const int32_t* tri,
                      const int32_t* ranges_host, const float* peel, int N, int V, int T,
                      int H, int W, float* rast, float* rast_db, dr_stream_t stream);
+
+/* dr_rasterize_fwd with the reference's per-tile limit as an option
+ * (MAX_PER_TILE, Rasterize.swift:164-171, 227-239, 410: a 16x16 tile keeps
+ * at most 128 triangles and drops the rest in atomic append order).
+ *   max_per_tile: 0 keeps every triangle (dr_rasterize_fwd); 1..1024 keeps
+ *     at most that many triangles per tile: the lowest triangle indices
+ *     among the tile's candidates (drawn triangles of nonzero area whose
+ *     clamped pixel bounding box touches the tile), i.e. what a sequential
+ *     execution of the reference's appends keeps.  max_per_tile = 128 gives
+ *     the reference's result whenever its appends land in triangle order.
+ * Other arguments, and the backward (dr_rasterize_bwd), as dr_rasterize_fwd. */
+int dr_rasterize_fwd_ex(const float* pos, int64_t pos_batch_stride, const int32_t* tri,
+                        const int32_t* ranges_host, const float* peel, int N, int V, int T,
+                        int H, int W, float* rast, float* rast_db, int max_per_tile,
+                        dr_stream_t stream);
 
 /* Binning report (no counterpart call in the reference; it exposes the
  * reference's bin counts, Rasterize.swift:227-239).  counts [N, ceil(H/16),

@@ -63,7 +63,23 @@ struct Scratch {
   hipEvent_t total_event = nullptr;
   bool total_pending = false;
   int bin_cap = 0;  // slots per tile list, 0 = not known yet
+  // Range-mode item prefix, staged through a ring of pinned host buffers:
+  // a buffer is reused once the copy that read it has run (its event), so
+  // a call waits only when it is kStageRing calls ahead of the device.
+  static constexpr int kStageRing = 4;
+  int64_t* stage[kStageRing] = {};
+  size_t stage_cap[kStageRing] = {};
+  hipEvent_t stage_event[kStageRing] = {};
+  bool stage_pending[kStageRing] = {};
+  int stage_next = 0;
 };
+
+// A pinned host buffer of the range-mode staging ring holding at least
+// `n` int64 values, free to overwrite (waits for the copy that last read
+// it, if it has not run yet); nullptr on error.
+int64_t* stage_acquire(Scratch* sc, size_t n, int& slot);
+// Records that the copy just enqueued on `stream` reads ring buffer `slot`.
+int stage_release(Scratch* sc, int slot, hipStream_t stream);
 
 // Compute units of the current device (cached per device).
 int device_cu_count();

@@ -7,8 +7,10 @@
 //   forward  :371-477 / :487-599 (inclusive edges, first-hit on equal z)
 //   backward :637-812
 // Differences by design: tile lists never overflow (the reference drops
-// triangles beyond 128 per tile), and equal depths pick the lowest triangle
-// index (the reference picks the first in its atomic bin order).
+// triangles beyond 128 per tile; dr_rasterize_fwd_ex with max_per_tile =
+// 128 reproduces that, keeping each tile's lowest triangle indices), and
+// equal depths pick the lowest triangle index (the reference picks the
+// first in its atomic bin order).
 //
 // All float expressions are evaluated exactly as the reference writes them
 // (this file is compiled with -ffp-contract=off), so the tri_id channel and
@@ -324,6 +326,11 @@ __device__ __forceinline__ TriRec load_rec(const TriRec* __restrict__ rec, int64
   return R;
 }
 
+// Largest per-tile cap of the reference-compatible mode, and the largest
+// list that mode ranks in LDS (longer lists take the ordered full scan).
+constexpr int kMaxPerTileCap = 1024;
+constexpr int kRankMax = 4096;
+
 // Rasterize.swift:371-599.  One workgroup per (image, 16x16 tile); wave w
 // owns the 8x8 quadrant (w&1, w>>1).  Each triangle of the tile's list is
 // first tested against the quadrant's pixel-centre box by its bounding box
@@ -331,12 +338,22 @@ __device__ __forceinline__ TriRec load_rec(const TriRec* __restrict__ rec, int64
 // per lane; only the survivors are tested against the quadrant's 64 pixels.
 // (A conservative edge-function test of the box, in fp64 or fp32, removed
 // more candidates but cost more than the survivor tests it saved.)
-template <bool DB, bool PEEL>
+//
+// CAPPED (max_per_tile > 0): the reference's per-tile limit
+// (Rasterize.swift:164-171, 227-239, 410) with its appends in triangle
+// order, i.e. a tile keeps its max_per_tile lowest triangle indices.  A
+// complete list above the limit is ranked in LDS and only the kept ids are
+// rasterized; a list that overflowed its capacity takes the full scan in
+// triangle order and stops at the limit.
+template <bool DB, bool PEEL, bool CAPPED>
 __global__ void __launch_bounds__(256) k_raster(
     const TriRec* __restrict__ rec, const int4* __restrict__ rect, Items it, int64_t rec_stride,
     const int* __restrict__ cnt, const int* __restrict__ list, int cap,
-    const float* __restrict__ peel, int N, int H, int W, int ntx, int nty,
+    const float* __restrict__ peel, int N, int H, int W, int ntx, int nty, int max_per_tile,
     float* __restrict__ rast, float* __restrict__ rast_db) {
+  __shared__ TriRec s_rec[4][kWave];
+  __shared__ int s_t[4][kWave];
+  __shared__ int s_keep[CAPPED ? kMaxPerTileCap : 1];
   const int tiles = ntx * nty;
   const int B = tiles * N;
   const int b = xcd_remap((int)blockIdx.x, B);
@@ -345,6 +362,31 @@ __global__ void __launch_bounds__(256) k_raster(
   const int ty = tile / ntx, tx = tile - ty * ntx;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
+  const int64_t j = (int64_t)n * tiles + tile;
+  int count = cnt[j];
+  const int* ids = list + j * (int64_t)cap;
+  int scan_limit = 0x7fffffff;  // full scan: stop after this many tile candidates
+  if (CAPPED && count > max_per_tile) {  // uniform over the workgroup
+    if (count <= cap && count <= kRankMax) {
+      // rank every id of the complete list (ids of one tile are distinct);
+      // the max_per_tile lowest land in s_keep in ascending order
+      int* s_all = reinterpret_cast<int*>(&s_rec[0][0]);  // kRankMax ints
+      for (int i = threadIdx.x; i < count; i += blockDim.x) s_all[i] = ids[i];
+      __syncthreads();
+      for (int i = threadIdx.x; i < count; i += blockDim.x) {
+        const int v = s_all[i];
+        int r = 0;
+        for (int k = 0; k < count; ++k) r += s_all[k] < v;
+        if (r < max_per_tile) s_keep[r] = v;
+      }
+      __syncthreads();  // s_all (the record slots) is free again after this
+      ids = s_keep;
+      count = max_per_tile;
+    } else {
+      count = cap + 1;  // take the ordered full scan
+      scan_limit = max_per_tile;
+    }
+  }
   const int qx0 = tx * kTile + (wave & 1) * 8;
   const int qy0 = ty * kTile + (wave >> 1) * 8;
   if (qx0 >= W || qy0 >= H) return;  // whole quadrant outside the image
@@ -368,18 +410,12 @@ __global__ void __launch_bounds__(256) k_raster(
   }
   Best best = {1e30f, 0.0f, 0.0f, -1};
   const int64_t rbase = (int64_t)n * rec_stride;
-  const int64_t j = (int64_t)n * tiles + tile;
-  const int count = cnt[j];
-  const int64_t o = j * (int64_t)cap;
   if (count <= cap) {
     // 64 candidates at a time: each lane loads one candidate's record
     // (vector gathers, one round trip for all 64) and tests it against the
     // quadrant's box; the survivors are then taken one by one, their
     // records read back from the wave's LDS slots at a uniform address (a
     // broadcast read; cheaper than 17 readlanes and their SGPR hazards).
-    const int* ids = list + o;
-    __shared__ TriRec s_rec[4][kWave];
-    __shared__ int s_t[4][kWave];
     for (int c0 = 0; c0 < count; c0 += kWave) {
       const int nb = min(kWave, count - c0);
       int myt = 0;
@@ -417,9 +453,11 @@ __global__ void __launch_bounds__(256) k_raster(
       t0 = (int)it.start[n];
       t1 = t0 + (int)(it.prefix[n + 1] - it.prefix[n]);
     }
+    int taken = 0;  // tile candidates so far, in triangle order
     for (int t = t0; t < t1; ++t) {
       const int4 rc = rect[rbase + t];
       if (rc.x < 0 || tx < rc.x || tx > rc.y || ty < rc.z || ty > rc.w) continue;
+      if (CAPPED && ++taken > scan_limit) break;  // uniform: the same tile test everywhere
       const TriRec R = load_rec(rec, rbase + t);
       if (R.r3.y < xw0 || R.r3.x > xw1 || R.r3.w < yw0 || R.r3.z > yw1) continue;
       if (valid) test_tri(R, t, x, y, peel_z, best);
@@ -589,14 +627,18 @@ using namespace dr;
 
 // The (image, triangle) items a call draws: every (n, t) in instanced mode;
 // in range mode, each image's clamped range, listed through a prefix sum
-// that is copied to the device (synchronously: the host vector is local).
+// that is written into a pinned staging buffer and copied to the device
+// asynchronously (no wait for the stream).
 static int plan_items(Scratch* sc, hipStream_t stream, const int32_t* ranges_host, int N, int T,
                       Items& it, int64_t& n_items, int64_t& max_items) {
   it = Items{nullptr, nullptr, T};
   n_items = (int64_t)N * T;
   max_items = T;
   if (!ranges_host) return DR_OK;
-  std::vector<int64_t> h(2 * (size_t)N + 1);
+  const size_t nh = 2 * (size_t)N + 1;
+  int slot = 0;
+  int64_t* h = stage_acquire(sc, nh, slot);
+  if (!h) return DR_ERR_HIP;
   h[0] = 0;
   max_items = 0;
   for (int n = 0; n < N; ++n) {
@@ -608,11 +650,11 @@ static int plan_items(Scratch* sc, hipStream_t stream, const int32_t* ranges_hos
     max_items = std::max<int64_t>(max_items, hi - lo);
   }
   n_items = h[N];
-  int64_t* d = (int64_t*)scratch_get(sc, stream, SLOT_RAST_ITEMS, h.size() * sizeof(int64_t));
+  int64_t* d = (int64_t*)scratch_get(sc, stream, SLOT_RAST_ITEMS, nh * sizeof(int64_t));
   if (!d) return DR_ERR_MEMORY;
-  DR_CHECK_HIP(hipMemcpyAsync(d, h.data(), h.size() * sizeof(int64_t), hipMemcpyHostToDevice,
-                              stream));
-  DR_CHECK_HIP(hipStreamSynchronize(stream));
+  DR_CHECK_HIP(hipMemcpyAsync(d, h, nh * sizeof(int64_t), hipMemcpyHostToDevice, stream));
+  const int st = stage_release(sc, slot, stream);
+  if (st) return st;
   it.prefix = d;
   it.start = d + N + 1;
   return DR_OK;
@@ -721,10 +763,20 @@ extern "C" int dr_rasterize_fwd(const float* pos, int64_t pos_batch_stride, cons
                                 const int32_t* ranges_host, const float* peel, int N, int V,
                                 int T, int H, int W, float* rast, float* rast_db,
                                 dr_stream_t stream_) {
+  return dr_rasterize_fwd_ex(pos, pos_batch_stride, tri, ranges_host, peel, N, V, T, H, W, rast,
+                             rast_db, 0, stream_);
+}
+
+extern "C" int dr_rasterize_fwd_ex(const float* pos, int64_t pos_batch_stride, const int32_t* tri,
+                                   const int32_t* ranges_host, const float* peel, int N, int V,
+                                   int T, int H, int W, float* rast, float* rast_db,
+                                   int max_per_tile, dr_stream_t stream_) {
   hipStream_t stream = (hipStream_t)stream_;
   int st = check_raster_args(pos, pos_batch_stride, tri, ranges_host, N, V, T, H, W);
   if (st) return st;
   DR_CHECK_ARG(rast, "rasterize: null tensor");
+  DR_CHECK_ARG(max_per_tile >= 0 && max_per_tile <= kMaxPerTileCap,
+               "rasterize: max_per_tile must be in [0, 1024] (0: no limit)");
   Scratch* sc = scratch_for(stream);
   if (!sc) return DR_ERR_HIP;
 
@@ -797,17 +849,23 @@ extern "C" int dr_rasterize_fwd(const float* pos, int64_t pos_batch_stride, cons
   launch_binning(true, it, n_items, max_items, N, rect, ntx, tiles, fillc, list, C, stream);
   DR_CHECK_LAUNCH();
   const dim3 grid((unsigned)n_tiles), block(256);
-#define DR_RASTER(DBV, PV)                                                                    \
-  hipLaunchKernelGGL((k_raster<DBV, PV>), grid, block, 0, stream, rec, rect, it, rec_stride, \
-                     fillc, list, C, peel, N, H, W, ntx, nty, rast, rast_db)
+#define DR_RASTER(DBV, PV, CV)                                                                    \
+  hipLaunchKernelGGL((k_raster<DBV, PV, CV>), grid, block, 0, stream, rec, rect, it, rec_stride, \
+                     fillc, list, C, peel, N, H, W, ntx, nty, max_per_tile, rast, rast_db)
+#define DR_RASTER_C(DBV, PV)                                 \
+  do {                                                       \
+    if (max_per_tile > 0) DR_RASTER(DBV, PV, true);          \
+    else DR_RASTER(DBV, PV, false);                          \
+  } while (0)
   {
     DR_TIMED("k_raster", stream);
     if (rast_db) {
-      if (peel) DR_RASTER(true, true); else DR_RASTER(true, false);
+      if (peel) DR_RASTER_C(true, true); else DR_RASTER_C(true, false);
     } else {
-      if (peel) DR_RASTER(false, true); else DR_RASTER(false, false);
+      if (peel) DR_RASTER_C(false, true); else DR_RASTER_C(false, false);
     }
   }
+#undef DR_RASTER_C
 #undef DR_RASTER
   DR_CHECK_LAUNCH();
   if (!sc->total_pending) {  // largest count of this call, for the next one

@@ -67,6 +67,46 @@ void* scratch_get(Scratch* sc, hipStream_t stream, int s, size_t bytes) {
   return p;
 }
 
+int64_t* stage_acquire(Scratch* sc, size_t n, int& slot) {
+  slot = sc->stage_next;
+  sc->stage_next = (sc->stage_next + 1) % Scratch::kStageRing;
+  if (sc->stage_pending[slot]) {
+    if (hipEventSynchronize(sc->stage_event[slot]) != hipSuccess) {
+      set_error("range staging: event synchronize failed");
+      return nullptr;
+    }
+    sc->stage_pending[slot] = false;
+  }
+  if (!sc->stage_event[slot] &&
+      hipEventCreateWithFlags(&sc->stage_event[slot], hipEventDisableTiming) != hipSuccess) {
+    set_error("range staging: event creation failed");
+    return nullptr;
+  }
+  if (sc->stage_cap[slot] < n) {
+    if (sc->stage[slot]) (void)hipHostFree(sc->stage[slot]);
+    sc->stage[slot] = nullptr;
+    sc->stage_cap[slot] = 0;
+    const size_t want = n + n / 4 + 64;
+    if (hipHostMalloc((void**)&sc->stage[slot], want * sizeof(int64_t), hipHostMallocDefault) !=
+        hipSuccess) {
+      (void)hipGetLastError();
+      set_error("range staging: pinned allocation failed");
+      return nullptr;
+    }
+    sc->stage_cap[slot] = want;
+  }
+  return sc->stage[slot];
+}
+
+int stage_release(Scratch* sc, int slot, hipStream_t stream) {
+  if (hipEventRecord(sc->stage_event[slot], stream) != hipSuccess) {
+    set_error("range staging: event record failed");
+    return DR_ERR_HIP;
+  }
+  sc->stage_pending[slot] = true;
+  return DR_OK;
+}
+
 int device_cu_count() {
   static int cached[64] = {0};
   int dev = 0;
@@ -191,6 +231,10 @@ int dr_release_scratch(void) {
       if (sc->ptr[s]) (void)hipFree(sc->ptr[s]);
     if (sc->pinned_total) (void)hipHostFree(sc->pinned_total);
     if (sc->total_event) (void)hipEventDestroy(sc->total_event);
+    for (int r = 0; r < dr::Scratch::kStageRing; ++r) {
+      if (sc->stage_event[r]) (void)hipEventDestroy(sc->stage_event[r]);
+      if (sc->stage[r]) (void)hipHostFree(sc->stage[r]);
+    }
     delete sc;
     it = dr::g_scratch.erase(it);
   }

@@ -89,7 +89,7 @@ def _dev_i32(t, name: str, device) -> torch.Tensor:
 
 class _RasterizeFn(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, pos, tri, ranges_host, peel, H, W, grad_db):
+    def forward(ctx, pos, tri, ranges_host, peel, H, W, grad_db, max_per_tile=0):
         lib = _lib.load()
         range_mode = ranges_host is not None
         N = ranges_host.shape[0] if range_mode else pos.shape[0]
@@ -100,9 +100,9 @@ class _RasterizeFn(torch.autograd.Function):
         rast_db = torch.empty((N, H, W, 4), device=pos.device, dtype=torch.float32) \
             if grad_db else torch.empty((N, H, W, 0), device=pos.device, dtype=torch.float32)
         rng = ranges_host.ctypes.data_as(ctypes.c_void_p) if range_mode else None
-        _lib.check(lib.dr_rasterize_fwd(
+        _lib.check(lib.dr_rasterize_fwd_ex(
             _ptr(posc), 0 if range_mode else V * 4, _ptr(tri), rng, _ptr(peel), N, V, T, H, W,
-            _ptr(rast), _ptr(rast_db) if grad_db else None, _stream()))
+            _ptr(rast), _ptr(rast_db) if grad_db else None, int(max_per_tile), _stream()))
         ctx.save_for_backward(posc, tri, rast)
         ctx.meta = (range_mode, N, V, H, W, grad_db)
         return rast, rast_db
@@ -122,7 +122,7 @@ class _RasterizeFn(torch.autograd.Function):
         _lib.check(lib.dr_rasterize_bwd(
             _ptr(pos), 0 if range_mode else V * 4, _ptr(tri), _ptr(rast), _ptr(d_rast), _ptr(db),
             N, V, tri.shape[0], H, W, _ptr(d_pos), 0, _stream()))
-        return d_pos, None, None, None, None, None, None
+        return d_pos, None, None, None, None, None, None, None
 
 
 # ---------------------------------------------------------------------------
@@ -349,11 +349,18 @@ class DiffRast:
 
     @staticmethod
     def rasterize(pos: torch.Tensor, tri, resolution: Tuple[int, int], gradDB: bool = True,
-                  ranges=None, peelLayer: Optional[torch.Tensor] = None
+                  ranges=None, peelLayer: Optional[torch.Tensor] = None, maxPerTile: int = 0
                   ) -> Tuple[torch.Tensor, torch.Tensor]:
         """Rasterize.swift:44-144.  Instanced pos [N,V,4], or range mode: pos
         [V,4] with ranges [N,2] (start, count) per image.  Returns (rast,
-        rastDB); rastDB is [N,H,W,0] when gradDB is False."""
+        rastDB); rastDB is [N,H,W,0] when gradDB is False.
+
+        `ranges` is read on the host (a device tensor is copied back first,
+        which waits for it).  `maxPerTile` (no counterpart argument in the
+        reference): 0 keeps every triangle; 128 reproduces the reference's
+        per-tile limit (MAX_PER_TILE, Rasterize.swift:164-171), each 16x16
+        tile keeping its 128 lowest triangle indices (the reference keeps
+        the first 128 of its atomic appends)."""
         H, W = int(resolution[0]), int(resolution[1])
         posf = _dev_f32(pos, "rasterize: pos") if not pos.requires_grad else pos.to(torch.float32)
         if not posf.is_cuda:
@@ -380,7 +387,10 @@ class DiffRast:
             if tuple(peel.shape) != (N, H, W, 4):
                 raise ValueError("rasterize: peelLayer must match rast shape [N, H, W, 4] "
                                  f"(got {list(peel.shape)})")
-        return _RasterizeFn.apply(posf.contiguous(), tri32, ranges_host, peel, H, W, bool(gradDB))
+        if not 0 <= int(maxPerTile) <= 1024:
+            raise ValueError("rasterize: maxPerTile must be in [0, 1024] (0: no limit)")
+        return _RasterizeFn.apply(posf.contiguous(), tri32, ranges_host, peel, H, W, bool(gradDB),
+                                  int(maxPerTile))
 
     @staticmethod
     def rasterizeTileCounts(pos: torch.Tensor, tri, resolution: Tuple[int, int],

@@ -278,3 +278,96 @@ def test_many_tiles_binning_path():
     check_fwd(pos, tri, H, W, gradDB=True)
     counts = host(DiffRast.rasterizeTileCounts(dev(pos), dev(tri), (H, W)))
     np.testing.assert_array_equal(counts, O.rasterize_tile_counts(pos, tri, (H, W)))
+
+
+def check_capped(pos, tri, H, W, cap, gradDB=True, ranges=None, peel=None):
+    """maxPerTile = cap against the oracle's max_per_tile = cap (the
+    reference's truncation with its appends in triangle order)."""
+    torch = torch_dev()
+    from diffrast import DiffRast
+    r, db = DiffRast.rasterize(dev(pos), dev(tri), (H, W), gradDB=gradDB,
+                               ranges=None if ranges is None else torch.as_tensor(ranges),
+                               peelLayer=None if peel is None else dev(peel), maxPerTile=cap)
+    rr, rdb = O.rasterize(pos, tri, (H, W), gradDB=gradDB, ranges=ranges, peelLayer=peel,
+                          max_per_tile=cap)
+    r = host(r)
+    np.testing.assert_array_equal(r, rr)
+    if gradDB:
+        np.testing.assert_array_equal(host(db), rdb)
+    return r
+
+
+def test_capped_tile_overflow():
+    """300 full-screen triangles per tile, nearest last: with a per-tile cap
+    every pixel shows the cap's last triangle.  The first call after a
+    sparse scene has list capacity below 300 (ordered full scan stopping at
+    the cap); later calls rank the complete list in LDS."""
+    torch = torch_dev()
+    from diffrast import _lib
+    torch.cuda.synchronize()
+    assert _lib.load().dr_release_scratch() == 0
+    sc = scenes.tier1_triangle(H=32, W=32)
+    check_fwd(sc["pos"], sc["tri"], 32, 32)
+    T = 300
+    p = np.tile(np.array([[-3, 3, 0, 1], [-3, -3, 0, 1], [3, 0, 0, 1]], np.float32), (T, 1))
+    p[:, 2] = np.repeat(np.linspace(0.9, -0.9, T), 3)
+    tri = np.arange(3 * T, dtype=np.int32).reshape(T, 3)
+    for cap in (128, 128, 5, 1, 299, 300, 1024):
+        r = check_capped(p[None], tri, 32, 32, cap)
+        assert (r[..., 3] == min(cap, T)).all(), cap
+        torch.cuda.synchronize()
+    # range mode: image 1 draws triangles [100, 300) and keeps [100, 228)
+    ranges = np.array([[0, 300], [100, 200], [250, 10]], np.int32)
+    r = check_capped(p, tri, 32, 32, 128, ranges=ranges)
+    assert (r[0, ..., 3] == 128).all() and (r[1, ..., 3] == 228).all() and (r[2, ..., 3] == 260).all()
+
+
+def test_capped_icosphere_1024():
+    """The benchmark scene (level-6 icosphere, 1024^2) with the reference's
+    128 per tile: tri_id, barycentrics, z and rast_db bit-exact against the
+    oracle's truncating mode; the truncation changes some pixels."""
+    torch = torch_dev()
+    from diffrast import DiffRast
+    O.set_threads(16)
+    sc = scenes.textured_icosphere(N=2, H=1024, W=1024, tex_size=8)
+    r = check_capped(sc["pos"], sc["tri"], 1024, 1024, 128)
+    full, _ = DiffRast.rasterize(dev(sc["pos"]), dev(sc["tri"]), (1024, 1024))
+    assert (host(full)[..., 3] != r[..., 3]).any()
+
+
+@pytest.mark.parametrize("gradDB", [False, True])
+def test_capped_peel(gradDB):
+    sc = scenes.textured_icosphere(N=1, H=128, W=128, level=5, tex_size=8)
+    prev = None
+    for _ in range(2):
+        prev = check_capped(sc["pos"], sc["tri"], 128, 128, 16, gradDB=gradDB, peel=prev)
+
+
+def test_range_mode_does_not_wait():
+    """A range-mode call returns while work queued before it still runs:
+    its ranges go through pinned staging, not a host-waited copy."""
+    torch = torch_dev()
+    from diffrast import DiffRast
+    sc = scenes.range_batch(N=64, T_per=40)
+    pos, tri = dev(sc["pos"]), dev(sc["tri"])
+    ranges = torch.as_tensor(sc["ranges"])
+    stream = torch.cuda.current_stream()
+
+    def calls(sleep):
+        waited = 0
+        for _ in range(3):
+            if sleep:
+                torch.cuda._sleep(200_000_000)  # ~0.1 s of spinning on the stream
+            r, _ = DiffRast.rasterize(pos, tri, (48, 40), ranges=ranges)
+            waited += stream.query()  # True: the stream drained before the call returned
+        return r, waited
+
+    # the same calls once first: the library sizes its scratch, and torch's
+    # allocator caches the output blocks (a fresh device allocation may wait)
+    calls(False)
+    torch.cuda.synchronize()
+    r, waited = calls(True)
+    torch.cuda.synchronize()
+    assert waited == 0
+    rr, _ = O.rasterize(sc["pos"], sc["tri"], (48, 40), ranges=sc["ranges"], max_per_tile=0)
+    np.testing.assert_array_equal(host(r), rr)
