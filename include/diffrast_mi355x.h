@@ -232,6 +232,25 @@ int dr_texture_bwd(const float* tex, const float* pyramid, int Nt, int Ht, int W
                    const float* d_out, float* d_tex, float* d_uv, float* d_uv_da,
                    float* d_bias_map, unsigned flags, dr_stream_t stream);
 
+/* dr_texture_bwd that allocates nothing.  No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops).  The mip filters' pyramid gradient,
+ * the only memory dr_texture_bwd takes beyond its arguments, is kept in a
+ * fixed device array of DR_TEXTURE_BWD_NOALLOC_FLOATS floats (32 MiB per
+ * GPU, held until the process ends) instead of the library's scratch; a
+ * texture whose pyramid needs more (dr_texture_mip_size of its levels, for
+ * a cube map of its Nt*6 faces) is rejected with DR_ERR_ARGUMENT.  Every
+ * call on one GPU shares that array, so calls that overlap on one GPU
+ * (other streams, other threads) race.  Arguments and results as
+ * dr_texture_bwd. */
+#define DR_TEXTURE_BWD_NOALLOC_FLOATS (8 * 1024 * 1024)
+int dr_texture_bwd_noalloc(const float* tex, const float* pyramid, int Nt, int Ht, int Wt,
+                           int C, int L, const float* uv, const float* uv_da,
+                           const float* bias_map, float bias, int filter, int boundary, int N,
+                           int Hi, int Wi, const float* d_out, float* d_tex, float* d_uv,
+                           float* d_uv_da, float* d_bias_map, unsigned flags,
+                           dr_stream_t stream);
+
 /* ---- antialias ------------------------------------------------------- */
 
 /* antialiasConstructTopologyHash (Antialias.swift:19-66), on the GPU:

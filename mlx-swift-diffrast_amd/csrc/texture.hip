@@ -11,6 +11,9 @@
 // The pyramid is built once per distinct texture (Nt = 1 serves every
 // image), not once per broadcast copy; d_tex of a shared texture is the sum
 // over images, as MLX's broadcast backward gives.
+#include <mutex>
+#include <string>
+
 #include "common.h"
 
 namespace dr {
@@ -1882,21 +1885,41 @@ extern "C" int dr_texture_fwd(const float* tex, const float* pyramid, int Nt, in
   return DR_OK;
 }
 
+// Where the backward keeps the mip pyramid's gradient: the library's
+// per-stream scratch (grown with hipMalloc as needed), or a fixed buffer of
+// `cap` floats (dr_texture_bwd_noalloc).
+struct DPyrBuf {
+  float* fixed;
+  int64_t cap;
+};
+
+static int dpyr_get(const DPyrBuf& buf, int64_t np, hipStream_t stream, float*& d_pyr) {
+  if (buf.fixed) {
+    DR_CHECK_ARG(np <= buf.cap, "texture_bwd_noalloc: the mip pyramid gradient needs " +
+                                    std::to_string(np) + " floats, above the fixed " +
+                                    std::to_string(buf.cap) + " (use dr_texture_bwd)");
+    d_pyr = buf.fixed;
+    return DR_OK;
+  }
+  Scratch* sc = scratch_for(stream);
+  if (!sc) return DR_ERR_HIP;
+  d_pyr = (float*)scratch_get(sc, stream, SLOT_DPYR, (size_t)np * sizeof(float));
+  return d_pyr ? DR_OK : DR_ERR_MEMORY;
+}
+
 // The cube extension's backward: one thread per pixel, d_tex / d_pyramid by
 // global atomics, then the pyramid collapse over the Nt*6 faces.
 static int cube_bwd(const float* tex, const float* pyramid, const MipDesc& md, int64_t tex_stride,
                     int Nt, int Ht, int Wt, int C, const float* dir, const float* dir_da,
                     const float* bias_map, float bias, int filter, int N, int Hi, int Wi,
                     const float* d_out, float* d_tex, float* d_dir, float* d_dir_da,
-                    float* d_bias_map, unsigned flags, hipStream_t stream) {
+                    float* d_bias_map, unsigned flags, const DPyrBuf& pbuf, hipStream_t stream) {
   const bool mip = filter >= DR_FILTER_LINEAR_MIPMAP_NEAREST;
   float* d_pyr = nullptr;
   if (mip && md.L > 1) {
-    Scratch* sc = scratch_for(stream);
-    if (!sc) return DR_ERR_HIP;
     const int64_t np = dr_texture_mip_size(Nt * 6, Ht, Wt, C, md.L);
-    d_pyr = (float*)scratch_get(sc, stream, SLOT_DPYR, (size_t)np * sizeof(float));
-    if (!d_pyr) return DR_ERR_MEMORY;
+    const int st = dpyr_get(pbuf, np, stream, d_pyr);
+    if (st) return st;
     DR_CHECK_HIP(fill_async(d_pyr, 0.0f, np, stream));
   }
   const int64_t P = (int64_t)N * Hi * Wi;
@@ -1921,13 +1944,12 @@ static int cube_bwd(const float* tex, const float* pyramid, const MipDesc& md, i
   return DR_OK;
 }
 
-extern "C" int dr_texture_bwd(const float* tex, const float* pyramid, int Nt, int Ht, int Wt,
-                              int C, int L, const float* uv, const float* uv_da,
-                              const float* bias_map, float bias, int filter, int boundary, int N,
-                              int Hi, int Wi, const float* d_out, float* d_tex, float* d_uv,
-                              float* d_uv_da, float* d_bias_map, unsigned flags,
-                              dr_stream_t stream_) {
-  hipStream_t stream = (hipStream_t)stream_;
+static int texture_bwd(const float* tex, const float* pyramid, int Nt, int Ht, int Wt, int C,
+                       int L, const float* uv, const float* uv_da, const float* bias_map,
+                       float bias, int filter, int boundary, int N, int Hi, int Wi,
+                       const float* d_out, float* d_tex, float* d_uv, float* d_uv_da,
+                       float* d_bias_map, unsigned flags, const DPyrBuf& pbuf,
+                       hipStream_t stream) {
   (void)hipGetLastError();
   MipDesc md;
   int st = check_tex(tex, pyramid, Nt, N, Ht, Wt, C, L, uv, uv_da, filter, boundary, md);
@@ -1940,16 +1962,15 @@ extern "C" int dr_texture_bwd(const float* tex, const float* pyramid, int Nt, in
   if (cube && (filter >= DR_FILTER_LINEAR_MIPMAP_NEAREST || (flags & DR_CUBE_DIR_GRAD))) {
     if (zero_tex) DR_CHECK_HIP(fill_async(d_tex, 0.0f, ntex, stream));
     return cube_bwd(tex, pyramid, md, tex_stride, Nt, Ht, Wt, C, uv, uv_da, bias_map, bias,
-                    filter, N, Hi, Wi, d_out, d_tex, d_uv, d_uv_da, d_bias_map, flags, stream);
+                    filter, N, Hi, Wi, d_out, d_tex, d_uv, d_uv_da, d_bias_map, flags, pbuf,
+                    stream);
   }
   const bool mip = !cube && filter >= DR_FILTER_LINEAR_MIPMAP_NEAREST;
   float* d_pyr = nullptr;
   if (mip && md.L > 1) {
-    Scratch* sc = scratch_for(stream);
-    if (!sc) return DR_ERR_HIP;
     const int64_t np = dr_texture_mip_size(Nt, Ht, Wt, C, md.L);
-    d_pyr = (float*)scratch_get(sc, stream, SLOT_DPYR, (size_t)np * sizeof(float));
-    if (!d_pyr) return DR_ERR_MEMORY;
+    st = dpyr_get(pbuf, np, stream, d_pyr);
+    if (st) return st;
     // d_tex and the coarser levels' accumulator are zeroed in one launch
     if (zero_tex) DR_CHECK_HIP(fill2_async(d_tex, ntex, d_pyr, np, 0.0f, stream));
     else DR_CHECK_HIP(fill_async(d_pyr, 0.0f, np, stream));
@@ -2026,4 +2047,55 @@ extern "C" int dr_texture_bwd(const float* tex, const float* pyramid, int Nt, in
   }
   if (d_pyr) return mip_collapse(d_pyr, md, Nt, Ht, Wt, C, d_tex, stream);
   return DR_OK;
+}
+
+extern "C" int dr_texture_bwd(const float* tex, const float* pyramid, int Nt, int Ht, int Wt,
+                              int C, int L, const float* uv, const float* uv_da,
+                              const float* bias_map, float bias, int filter, int boundary, int N,
+                              int Hi, int Wi, const float* d_out, float* d_tex, float* d_uv,
+                              float* d_uv_da, float* d_bias_map, unsigned flags,
+                              dr_stream_t stream_) {
+  return texture_bwd(tex, pyramid, Nt, Ht, Wt, C, L, uv, uv_da, bias_map, bias, filter, boundary,
+                     N, Hi, Wi, d_out, d_tex, d_uv, d_uv_da, d_bias_map, flags,
+                     DPyrBuf{nullptr, 0}, (hipStream_t)stream_);
+}
+
+// ---- dr_texture_bwd without allocation --------------------------------------
+// The pyramid gradient lives in one fixed device array instead of the
+// library's per-stream scratch.  In host code `scratch` names a host-side
+// stand-in: its device address on each GPU comes from hipGetSymbolAddress
+// (with that GPU current), kept per device, and only that address is used.
+
+static __device__ __align__(256) float scratch[DR_TEXTURE_BWD_NOALLOC_FLOATS];
+
+static std::mutex g_noalloc_mu;
+static float* g_noalloc_ptr[64] = {};
+
+static int noalloc_scratch(float*& ptr) {
+  int dev = 0;
+  DR_CHECK_HIP(hipGetDevice(&dev));
+  DR_CHECK_ARG(dev >= 0 && dev < 64, "texture_bwd_noalloc: device index above 63");
+  std::lock_guard<std::mutex> lk(g_noalloc_mu);
+  if (!g_noalloc_ptr[dev]) {
+    void* p = nullptr;
+    DR_CHECK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    DR_CHECK_ARG(p != nullptr, "texture_bwd_noalloc: no device address for the scratch array");
+    g_noalloc_ptr[dev] = (float*)p;
+  }
+  ptr = g_noalloc_ptr[dev];
+  return DR_OK;
+}
+
+extern "C" int dr_texture_bwd_noalloc(const float* tex, const float* pyramid, int Nt, int Ht,
+                                      int Wt, int C, int L, const float* uv, const float* uv_da,
+                                      const float* bias_map, float bias, int filter, int boundary,
+                                      int N, int Hi, int Wi, const float* d_out, float* d_tex,
+                                      float* d_uv, float* d_uv_da, float* d_bias_map,
+                                      unsigned flags, dr_stream_t stream_) {
+  float* ptr = nullptr;
+  const int st = noalloc_scratch(ptr);
+  if (st) return st;
+  return texture_bwd(tex, pyramid, Nt, Ht, Wt, C, L, uv, uv_da, bias_map, bias, filter, boundary,
+                     N, Hi, Wi, d_out, d_tex, d_uv, d_uv_da, d_bias_map, flags,
+                     DPyrBuf{ptr, (int64_t)DR_TEXTURE_BWD_NOALLOC_FLOATS}, (hipStream_t)stream_);
 }

@@ -41,6 +41,8 @@ SIGNATURES = {
                        _i),
     "dr_texture_bwd": ([_p, _p, _i, _i, _i, _i, _i, _p, _p, _p, _f, _i, _i, _i, _i, _i, _p, _p,
                         _p, _p, _p, _u, _p], _i),
+    "dr_texture_bwd_noalloc": ([_p, _p, _i, _i, _i, _i, _i, _p, _p, _p, _f, _i, _i, _i, _i, _i,
+                                _p, _p, _p, _p, _p, _u, _p], _i),
     "dr_antialias_topology": ([_p, _i, _p, _p], _i),
     "dr_antialias_fwd": ([_p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p, _p], _i),
     "dr_antialias_bwd": ([_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p, _p, _u, _p], _i),
@@ -55,6 +57,7 @@ SIGNATURES = {
 DR_OK, DR_ERR_ARGUMENT, DR_ERR_HIP, DR_ERR_MEMORY = 0, 1, 2, 3
 DR_ACCUMULATE = 1
 DR_CUBE_DIR_GRAD = 2
+DR_TEXTURE_BWD_NOALLOC_FLOATS = 8 * 1024 * 1024
 ABI_VERSION = 1
 
 _lib = None
