@@ -436,7 +436,7 @@ __global__ void __launch_bounds__(256) k_aa_fwd(const float* __restrict__ rast,
 // weight's gradient d_alpha = sum_c g * (c_neighbour - c_own) through the
 // crossing point into the edge's two clip-space vertices P0, P1.
 __device__ __forceinline__ void aa_dpos_add(const SilDir& s, int d, int ph, int pw, float d_alpha,
-                                            float4 P0, float4 P1, float* __restrict__ dp,
+                                            float4 P0, float4 P1, double* __restrict__ dp,
                                             float halfW, float halfH, LdsTable<4, 128>& tab) {
   float dade0x, dade0y, dade1x, dade1y;
   const float inv_denom_sq = 1.0f / (s.denom * s.denom);
@@ -474,7 +474,7 @@ __device__ __forceinline__ bool aa_dpos_terms(const SilDir& s, int d, int ph, in
                                               const float* __restrict__ gp,
                                               const float* __restrict__ cpp,
                                               const float* __restrict__ cnp,
-                                              const float* __restrict__ p, float* __restrict__ dp,
+                                              const float* __restrict__ p, double* __restrict__ dp,
                                               float halfW, float halfH, LdsTable<4, 128>& tab) {
   float d_alpha = 0.0f;
   for (int k = 0; k < Cn; ++k) d_alpha += gp[k] * (cnp[k] - cpp[k]);
@@ -507,7 +507,7 @@ __global__ void __launch_bounds__(256) k_aa_bwd(const float* __restrict__ rast,
                                                 const float* __restrict__ d_out, int H, int W,
                                                 int V, int T, int C, int ntx, int nty,
                                                 float* __restrict__ d_color,
-                                                float* __restrict__ d_pos, int accumulate) {
+                                                double* __restrict__ d_pos, int accumulate) {
   __shared__ int s_tri[18][18];
   __shared__ float s_alpha[4][16][17];
   __shared__ float s_halo[4][16];
@@ -666,7 +666,7 @@ __global__ void __launch_bounds__(256) k_aa_bwd(const float* __restrict__ rast,
     }
   }
   __syncthreads();
-  lds_table_flush(tab);  // contains a barrier
+  lds_table_flush<4, 128, double>(tab);  // contains a barrier
 }
 
 // Backward with the forward's blend mask (bit d of a pixel set when its
@@ -687,7 +687,7 @@ __global__ void __launch_bounds__(256) k_aa_bwd_masked(
     const float* __restrict__ rast, const AARec* __restrict__ rec, const float* __restrict__ pos,
     const float* __restrict__ color, const float* __restrict__ d_out,
     const uint8_t* __restrict__ blend_mask, int H, int W, int V, int T, int C, int ntx, int nty,
-    float* __restrict__ d_color, float* __restrict__ d_pos, int accumulate) {
+    float* __restrict__ d_color, double* __restrict__ d_pos, int accumulate) {
   constexpr int CS = CT > 0 ? CT : 1;
   constexpr int kCells = CT > 0 ? 18 * 18 : 1;
   __shared__ int s_tri[18][18];
@@ -846,7 +846,7 @@ __global__ void __launch_bounds__(256) k_aa_bwd_masked(
   }
   if (!d_pos || nq == 0) return;  // uniform: nq was read after the barrier
   __syncthreads();
-  lds_table_flush(tab);  // contains a barrier
+  lds_table_flush<4, 128, double>(tab);  // contains a barrier
 }
 
 }  // namespace dr
@@ -969,7 +969,13 @@ static int aa_bwd(const float* color, const float* rast, const float* pos, const
   DR_CHECK_ARG(((uintptr_t)saved & 15) == 0, "antialias_bwd_saved: saved must be 16-byte aligned");
   if (!d_color && !d_pos) return DR_OK;
   const bool acc = (flags & DR_ACCUMULATE) != 0;
-  if (d_pos && !acc) DR_CHECK_HIP(fill_async(d_pos, 0.0f, (int64_t)N * V * 4, stream));
+  // d_pos is summed in fp64 across workgroups and rounded once, so it does
+  // not depend on the order in which their additions land
+  double* dpos64 = nullptr;
+  if (d_pos) {
+    dpos64 = acc64_begin(stream, (int64_t)N * V * 4);
+    if (!dpos64) return DR_ERR_MEMORY;
+  }
   const AARec* rec = nullptr;
   if (saved) {  // the forward's records
     rec = (const AARec*)(saved + aa_mask_bytes(N, H, W));
@@ -982,15 +988,18 @@ static int aa_bwd(const float* color, const float* rast, const float* pos, const
   const int ntx = (W + 15) / 16, nty = (H + 15) / 16;
   const dim3 grid((unsigned)((int64_t)N * ntx * nty)), block(256);
   const int ct = aa_ct(C, color, d_out, d_color);
-  DR_TIMED("k_aa_bwd", stream);
-  if (saved) {
-    DR_AA_DISPATCH(k_aa_bwd_masked, ct, grid, block, 0, stream, rast, rec, pos, color, d_out,
-                   saved, H, W, V, T, C, ntx, nty, d_color, d_pos, acc ? 1 : 0);
-  } else {
-    DR_AA_DISPATCH(k_aa_bwd, ct, grid, block, 0, stream, rast, rec, pos, color, d_out, H, W, V,
-                   T, C, ntx, nty, d_color, d_pos, acc ? 1 : 0);
+  {
+    DR_TIMED("k_aa_bwd", stream);
+    if (saved) {
+      DR_AA_DISPATCH(k_aa_bwd_masked, ct, grid, block, 0, stream, rast, rec, pos, color, d_out,
+                     saved, H, W, V, T, C, ntx, nty, d_color, dpos64, acc ? 1 : 0);
+    } else {
+      DR_AA_DISPATCH(k_aa_bwd, ct, grid, block, 0, stream, rast, rec, pos, color, d_out, H, W,
+                     V, T, C, ntx, nty, d_color, dpos64, acc ? 1 : 0);
+    }
   }
   DR_CHECK_LAUNCH();
+  if (d_pos) return acc64_end(dpos64, d_pos, (int64_t)N * V * 4, acc, stream);
   return DR_OK;
 }
 

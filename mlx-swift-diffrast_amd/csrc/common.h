@@ -50,6 +50,7 @@ enum Slot {
   SLOT_SMALL,         // small device-side counters
   SLOT_LOSS,          // partial sums of the loss
   SLOT_AA_REC,        // per (image, triangle) silhouette records (antialias)
+  SLOT_DPOS64,        // fp64 accumulator of d_pos (rasterize and antialias backward)
   SLOT_COUNT
 };
 
@@ -397,9 +398,10 @@ __device__ __forceinline__ void lds_table_clear(LdsTable<NV, CAP>& t) {
   }
 }
 
-// Adds v[0..NV) to dst[0..NV).
-template <int NV, int CAP>
-__device__ __forceinline__ void lds_table_add(LdsTable<NV, CAP>& t, float* dst, const float* v) {
+// Adds v[0..NV) to dst[0..NV) (D: float, or double for an fp64
+// accumulator in global memory).
+template <int NV, int CAP, typename D>
+__device__ __forceinline__ void lds_table_add(LdsTable<NV, CAP>& t, D* dst, const float* v) {
   bool any = false;
 #pragma unroll
   for (int j = 0; j < NV; ++j) any = any || v[j] != 0.0f;
@@ -420,26 +422,33 @@ __device__ __forceinline__ void lds_table_add(LdsTable<NV, CAP>& t, float* dst, 
   }
 #pragma unroll
   for (int j = 0; j < NV; ++j)
-    if (v[j] != 0.0f) unsafeAtomicAdd(dst + j, v[j]);
+    if (v[j] != 0.0f) unsafeAtomicAdd(dst + j, (D)v[j]);
 }
 
-// Writes the table out (call after a barrier) and leaves it cleared.
+// Writes the table out (call after a barrier) and leaves it cleared; the
+// keys are addresses of D values (what lds_table_add was given).
 // Consecutive lanes take consecutive values of one entry, so the atomics of
 // an entry share a cache line request.
-template <int NV, int CAP>
+template <int NV, int CAP, typename D = float>
 __device__ __forceinline__ void lds_table_flush(LdsTable<NV, CAP>& t) {
   for (int i = threadIdx.x; i < CAP * NV; i += blockDim.x) {
     const int e = i / NV, j = i - e * NV;
     const unsigned long long k = t.key[e];
     if (k != kEmptyKey) {
       const double v = t.val[e][j];
-      if (v != 0.0) unsafeAtomicAdd((float*)k + j, (float)v);
+      if (v != 0.0) unsafeAtomicAdd((D*)k + j, (D)v);
       t.val[e][j] = 0.0;
     }
   }
   __syncthreads();
   for (int i = threadIdx.x; i < CAP; i += blockDim.x) t.key[i] = kEmptyKey;
 }
+
+// dst = (float)acc, or dst += (float)acc: the one rounding of a gradient
+// summed in fp64 across workgroups (so the result does not depend on the
+// order in which the workgroups' atomics land).
+__global__ void k_acc_to_f32(const double* __restrict__ acc, float* __restrict__ dst, int64_t n,
+                             int accumulate);
 
 template <typename T>
 __global__ void fill_kernel(T* __restrict__ p, T v, int64_t n) {
@@ -522,5 +531,10 @@ inline hipError_t fill2_async(T* p0, int64_t n0, T* p1, int64_t n1, T v, hipStre
 inline unsigned grid_for(int64_t n, int block) {
   return (unsigned)((n + block - 1) / block);
 }
+
+// An fp64 accumulator of n values (library scratch, zeroed on the stream).
+double* acc64_begin(hipStream_t stream, int64_t n);
+// Rounds the accumulator into dst (overwrite, or add when accumulate).
+int acc64_end(const double* acc, float* dst, int64_t n, bool accumulate, hipStream_t stream);
 
 }  // namespace dr

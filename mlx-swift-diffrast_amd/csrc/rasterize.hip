@@ -486,12 +486,13 @@ __global__ void __launch_bounds__(256) k_raster(
 
 // Rasterize.swift:637-812.  16x16 tiles, a 16x4 strip per wave; runs of
 // same-triangle lanes along a pixel row are summed before the LDS table
-// adds the 12 d_pos terms.
+// adds the 12 d_pos terms; the table is written out into an fp64
+// accumulator laid out as pos.
 __global__ void __launch_bounds__(256) k_raster_bwd(
     const float* __restrict__ pos, int64_t pos_stride, const int32_t* __restrict__ tri,
     const float* __restrict__ rast, const float* __restrict__ d_rast,
     const float* __restrict__ d_rast_db, int N, int V, int T, int H, int W, int ntx, int nty,
-    float* __restrict__ d_pos) {
+    double* __restrict__ d_pos) {
   __shared__ LdsTable<4, 256> tab;  // d_pos rows touched by this tile
   __shared__ int s_any[4];          // per wave: a covered pixel
   const int tiles = ntx * nty;
@@ -523,7 +524,7 @@ __global__ void __launch_bounds__(256) k_raster_bwd(
 #pragma unroll
   for (int q = 0; q < 12; ++q) val[q] = 0.0f;
   const float* p = pos + (int64_t)n * pos_stride;
-  float* dp = d_pos + (int64_t)n * pos_stride;
+  double* dp = d_pos + (int64_t)n * pos_stride;
   if (valid) {
     i0 = tri[t * 3 + 0];
     i1 = tri[t * 3 + 1];
@@ -618,7 +619,37 @@ __global__ void __launch_bounds__(256) k_raster_bwd(
     lds_table_add(tab, dp + (int64_t)i2 * 4, &val[8]);
   }
   __syncthreads();
-  lds_table_flush(tab);
+  lds_table_flush<4, 256, double>(tab);
+}
+
+__global__ void __launch_bounds__(256) k_acc_to_f32(const double* __restrict__ acc,
+                                                    float* __restrict__ dst, int64_t n,
+                                                    int accumulate) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float v = (float)acc[i];
+  dst[i] = accumulate ? dst[i] + v : v;
+}
+
+double* acc64_begin(hipStream_t stream, int64_t n) {
+  Scratch* sc = scratch_for(stream);
+  if (!sc) return nullptr;
+  double* a = (double*)scratch_get(sc, stream, SLOT_DPOS64, (size_t)std::max<int64_t>(n, 1) * 8);
+  if (!a) return nullptr;
+  if (fill_async(a, 0.0, n, stream) != hipSuccess) {
+    set_error("fp64 accumulator: fill launch failed");
+    return nullptr;
+  }
+  return a;
+}
+
+int acc64_end(const double* acc, float* dst, int64_t n, bool accumulate, hipStream_t stream) {
+  if (n <= 0) return DR_OK;
+  DR_TIMED("k_acc_to_f32", stream);
+  hipLaunchKernelGGL(k_acc_to_f32, dim3(grid_for(n, 256)), dim3(256), 0, stream, acc, dst, n,
+                     accumulate ? 1 : 0);
+  DR_CHECK_LAUNCH();
+  return DR_OK;
 }
 
 }  // namespace dr
@@ -836,8 +867,10 @@ extern "C" int dr_rasterize_fwd_ex(const float* pos, int64_t pos_batch_stride, c
     DR_CHECK_HIP(hipStreamSynchronize(stream));
     C = grow(*sc->pinned_total);
   }
-  // at most 1 GiB of lists; a tile above the capacity takes the full scan
-  const int64_t c_budget = std::max<int64_t>(32, ((int64_t)256 << 20) / std::max<int64_t>(n_tiles, 1));
+  // at most 4 GiB of lists (a 16 x 2048^2 batch of a 1.3M-triangle mesh
+  // needs ~1,500 slots per tile); a tile above the capacity takes the full
+  // scan
+  const int64_t c_budget = std::max<int64_t>(32, ((int64_t)1 << 30) / std::max<int64_t>(n_tiles, 1));
   C = (int)std::min<int64_t>(C, c_budget);
   if (C > sc->bin_cap) sc->bin_cap = C;
   int* list = (int*)scratch_get(sc, stream, SLOT_RAST_LIST, (size_t)n_tiles * C * 4);
@@ -891,15 +924,18 @@ extern "C" int dr_rasterize_bwd(const float* pos, int64_t pos_batch_stride, cons
   DR_CHECK_ARG(pos_batch_stride == 0 || pos_batch_stride == (int64_t)V * 4,
                "rasterize_bwd: pos_batch_stride must be 0 or V*4");
   const int64_t npos = (pos_batch_stride ? (int64_t)N : 1) * V * 4;
-  if (!(flags & DR_ACCUMULATE)) DR_CHECK_HIP(fill_async(d_pos, 0.0f, npos, stream));
+  // d_pos is summed in fp64 across workgroups and rounded once, so it does
+  // not depend on the order in which their additions land
+  double* acc = acc64_begin(stream, npos);
+  if (!acc) return DR_ERR_MEMORY;
   const int ntx = (W + kTile - 1) / kTile, nty = (H + kTile - 1) / kTile;
   const int64_t blocks = (int64_t)N * ntx * nty;
   {
     DR_TIMED("k_raster_bwd", stream);
     hipLaunchKernelGGL(k_raster_bwd, dim3((unsigned)blocks), dim3(256), 0, stream, pos,
                        pos_batch_stride, tri, rast, d_rast, d_rast_db, N, V, T, H, W, ntx, nty,
-                       d_pos);
+                       acc);
   }
   DR_CHECK_LAUNCH();
-  return DR_OK;
+  return acc64_end(acc, d_pos, npos, (flags & DR_ACCUMULATE) != 0, stream);
 }

@@ -1518,41 +1518,53 @@ __global__ void __launch_bounds__(256) k_cube_fwd(CubeArgs A) {
 }
 
 // MODE: 0 = bilinear (only with the direction gradient), 1 / 2 as above.
+// One pixel of the backward; every lane of the wave calls it (the scatter
+// groups lanes across the wave), `valid` marks the lanes with a pixel.
 template <int MODE, int CT>
-__global__ void __launch_bounds__(256) k_cube_bwd(CubeArgs A) {
-  const int64_t pix = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (pix >= A.P) return;
+__device__ __forceinline__ void cube_bwd_px(const CubeArgs& A, int64_t pix, bool valid, int n,
+                                            FootAcc<(CT > 0 ? CT : 1)>& acc0, TexTable<CT>& tab) {
   const int C = dimC<CT>(A.C);
-  const int n = (int)(pix / A.HWi);
   const CubePx p = cube_px<MODE>(A, pix);
-  const float* g = A.d_out + pix * C;
+  const float* gp = A.d_out + pix * C;
+  float g[CT > 0 ? CT : 1];
+  if (CT > 0) {
+#pragma unroll
+    for (int c = 0; c < (CT > 0 ? CT : 1); ++c) g[c] = valid ? gp[c] : 0.0f;
+  }
+  const float* gsrc = CT > 0 ? g : gp;  // run-time C reads d_out directly
   const CubeSel& s = p.s;
-  // sample position gradient (:934-999) and the pyramid scatter (:870-932)
+  // sample position gradient (:934-999) and the pyramid scatter (:870-932);
+  // a level of zero weight adds nothing and is skipped (uniformly per wave)
   float du = 0.0f, dv = 0.0f;
   for (int li = 0; li < (MODE == 0 ? 1 : 2); ++li) {
     const int k = li == 0 ? p.ld.k0 : p.ld.k1;
     const float scale = MODE == 0 ? 1.0f : (li == 0 ? (1.0f - p.ld.frac) : p.ld.frac);
+    const bool on = valid && scale != 0.0f;
+    if (__ballot(on) == 0ull) continue;
     const int Hk = mip_h(A.md, k), Wk = mip_w(A.md, k);
     const float* lv = cube_level(A, n, s.face, k, Hk, Wk);
     float* dl = cube_dlevel(A, n, s.face, k, Hk, Wk);
     const Bilin b = bilin(p.u, p.v, Wk, Hk, DR_BOUNDARY_CLAMP);
+    if (li == 0)
+      scatter_footprint<CT, true>(on, dl, Wk, C, b, gsrc, scale, acc0, tab);
+    else
+      scatter_footprint<CT, false>(on, dl, Wk, C, b, gsrc, scale, acc0, tab);
+    if (!on) continue;
     float dfx = 0.0f, dfy = 0.0f;
     for (int c = 0; c < C; ++c) {
       const float t00 = lv[((int64_t)b.iy0 * Wk + b.ix0) * C + c];
       const float t10 = lv[((int64_t)b.iy0 * Wk + b.ix1) * C + c];
       const float t01 = lv[((int64_t)b.iy1 * Wk + b.ix0) * C + c];
       const float t11 = lv[((int64_t)b.iy1 * Wk + b.ix1) * C + c];
-      const float gs = g[c] * scale;
-      atomicAdd(dl + ((int64_t)b.iy0 * Wk + b.ix0) * C + c, b.w00 * gs);
-      atomicAdd(dl + ((int64_t)b.iy0 * Wk + b.ix1) * C + c, b.w10 * gs);
-      atomicAdd(dl + ((int64_t)b.iy1 * Wk + b.ix0) * C + c, b.w01 * gs);
-      atomicAdd(dl + ((int64_t)b.iy1 * Wk + b.ix1) * C + c, b.w11 * gs);
+      const float gs = gsrc[c] * scale;
       dfx += gs * ((1.0f - b.fy) * (t10 - t00) + b.fy * (t11 - t01));
       dfy += gs * ((1.0f - b.fx) * (t01 - t00) + b.fx * (t11 - t10));
     }
     du += dfx * (float)Wk;
     dv += dfy * (float)Hk;
   }
+  if (!valid) return;
+  const float* g_ = gsrc;
   const float inv2 = 0.5f / (s.ma * s.ma);
   // d u / d dir = inv2 * (ss*ma e_as - sc*ms e_am), likewise v; the axes
   // are distinct, so each sum below lands in its own component
@@ -1584,7 +1596,7 @@ __global__ void __launch_bounds__(256) k_cube_bwd(CubeArgs A) {
           const float t01 = lv[((int64_t)b.iy1 * Wk + b.ix0) * C + c];
           const float t11 = lv[((int64_t)b.iy1 * Wk + b.ix1) * C + c];
           const float sample = b.w00 * t00 + b.w10 * t10 + b.w01 * t01 + b.w11 * t11;
-          d_lod += sign * sample * g[c];
+          d_lod += sign * sample * g_[c];
         }
       }
       const float ln2 = 0.6931471805599453f;
@@ -1649,6 +1661,33 @@ __global__ void __launch_bounds__(256) k_cube_bwd(CubeArgs A) {
     for (int i = 0; i < 3; ++i) gm = gm + gdd_x[i] * p.dd_in.x[i] + gdd_y[i] * p.dd_in.y[i];
     A.d_bias[pix] = gm * p.bscale * 0.6931471805599453f;
   }
+}
+
+// Persistent 16x16 pixel tiles, one pixel per thread: each tile's d_tex /
+// d_pyramid contributions are summed in the LDS table (large groups of
+// lanes on one footprint across the wave first, the most frequent one in a
+// per-wave accumulator kept across tiles), then written out.
+template <int MODE, int CT>
+__global__ void __launch_bounds__(256) k_cube_bwd(CubeArgs A, int Hi, int Wi, int ntx,
+                                                  int total_tiles) {
+  __shared__ TexTable<CT> tab;
+  FootAcc<(CT > 0 ? CT : 1)> acc0;
+  acc_init(acc0);
+  lds_table_clear(tab);
+  __syncthreads();
+  const int tiles = ntx * ((Hi + 15) >> 4);
+  for (int t = (int)blockIdx.x; t < total_tiles; t += (int)gridDim.x) {
+    const int n = t / tiles, tile = t - n * tiles;
+    const int ty = tile / ntx, tx = tile - ty * ntx;
+    const int ph = ty * 16 + ((int)threadIdx.x >> 4), pw = tx * 16 + ((int)threadIdx.x & 15);
+    const bool valid = ph < Hi && pw < Wi;
+    const int64_t pix = ((int64_t)n * Hi + min(ph, Hi - 1)) * Wi + min(pw, Wi - 1);
+    cube_bwd_px<MODE, CT>(A, pix, valid, n, acc0, tab);
+    __syncthreads();
+    lds_table_flush(tab);
+    __syncthreads();
+  }
+  acc_flush(acc0);
 }
 
 }  // namespace dr
@@ -1885,6 +1924,26 @@ extern "C" int dr_texture_fwd(const float* tex, const float* pyramid, int Nt, in
   return DR_OK;
 }
 
+// The cube backward's persistent tiles: as many workgroups as fit at once.
+template <int MODE, int CT>
+static hipError_t launch_cube_bwd(const CubeArgs& A, int Hi, int Wi, int ntx, int total_tiles,
+                                  hipStream_t stream) {
+  static int per_cu = 0;
+  if (per_cu == 0) {
+    int b = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, k_cube_bwd<MODE, CT>, 256, 0) !=
+            hipSuccess ||
+        b <= 0)
+      b = 2;
+    per_cu = b;
+  }
+  const int64_t resident = (int64_t)device_cu_count() * per_cu;
+  const unsigned grid = (unsigned)(total_tiles < resident ? total_tiles : resident);
+  hipLaunchKernelGGL((k_cube_bwd<MODE, CT>), dim3(grid), dim3(256), 0, stream, A, Hi, Wi, ntx,
+                     total_tiles);
+  return hipGetLastError();
+}
+
 // Where the backward keeps the mip pyramid's gradient: the library's
 // per-stream scratch (grown with hipMalloc as needed), or a fixed buffer of
 // `cap` floats (dr_texture_bwd_noalloc).
@@ -1932,12 +1991,27 @@ static int cube_bwd(const float* tex, const float* pyramid, const MipDesc& md, i
   A.dir_grad = (flags & DR_CUBE_DIR_GRAD) ? 1 : 0;
   A.d_dir_da = mip ? d_dir_da : nullptr;
   A.d_bias = mip ? d_bias_map : nullptr;
-  const dim3 grid(grid_for(P, 256));
+  const int ntx = (Wi + 15) / 16;
+  const int64_t total_tiles = (int64_t)N * ntx * ((Hi + 15) / 16);
+  DR_CHECK_ARG(total_tiles < ((int64_t)1 << 31), "texture_bwd: too many pixels");
   {
     DR_TIMED("k_cube_bwd", stream);
-    if (filter == DR_FILTER_LINEAR_MIPMAP_LINEAR) DR_CUBE_DISPATCH(k_cube_bwd, 2, grid, A);
-    else if (filter == DR_FILTER_LINEAR_MIPMAP_NEAREST) DR_CUBE_DISPATCH(k_cube_bwd, 1, grid, A);
-    else DR_CUBE_DISPATCH(k_cube_bwd, 0, grid, A);
+    hipError_t e = hipSuccess;
+#define DR_CB(MODEV, CTV) e = launch_cube_bwd<MODEV, CTV>(A, Hi, Wi, ntx, (int)total_tiles, stream)
+#define DR_CB_C(MODEV)                 \
+  switch (C) {                         \
+    case 1: DR_CB(MODEV, 1); break;    \
+    case 2: DR_CB(MODEV, 2); break;    \
+    case 3: DR_CB(MODEV, 3); break;    \
+    case 4: DR_CB(MODEV, 4); break;    \
+    default: DR_CB(MODEV, 0); break;   \
+  }
+    if (filter == DR_FILTER_LINEAR_MIPMAP_LINEAR) DR_CB_C(2)
+    else if (filter == DR_FILTER_LINEAR_MIPMAP_NEAREST) DR_CB_C(1)
+    else DR_CB_C(0)
+#undef DR_CB_C
+#undef DR_CB
+    DR_CHECK_HIP(e);
   }
   DR_CHECK_LAUNCH();
   if (d_pyr) return mip_collapse(d_pyr, md, Nt * 6, Ht, Wt, C, d_tex, stream);
