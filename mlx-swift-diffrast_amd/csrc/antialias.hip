@@ -93,43 +93,78 @@ struct alignas(16) AARec {
   int4 tv;
 };
 
+// The d_pos factors of a triangle's three corners (Antialias.swift:462-465):
+// c[k] = (inv_w, x * inv_w, y * inv_w, 0) of corner k's clip position, with
+// inv_w = 1 / w, so the backward loads them beside the record instead of
+// gathering the vertices after it.
+struct alignas(16) AAPersp {
+  float4 c[3];
+};
+
+__device__ __forceinline__ float4 persp_of(float4 P) {
+  const float inv_w = 1.0f / P.w;
+  return make_float4(inv_w, P.x * inv_w, P.y * inv_w, 0.0f);
+}
+
+// One thread per record; the records of a workgroup (and their corner
+// factors) are assembled in LDS and written out as contiguous 16-byte
+// stores.
 __global__ void __launch_bounds__(256) k_aa_rec(const float* __restrict__ pos,
                                                 const int32_t* __restrict__ tri,
                                                 const int32_t* __restrict__ topo, int64_t NT,
                                                 int T, int V, int H, int W,
-                                                AARec* __restrict__ rec) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= NT) return;
-  int64_t n;
-  int t;
-  divmod64(i, T, n, t);
-  const float* p = pos + n * V * 4;
-  const int v0 = tri[(int64_t)t * 3 + 0], v1 = tri[(int64_t)t * 3 + 1],
-            v2 = tri[(int64_t)t * 3 + 2];
-  AARec r;
-  if (!verts_ok(v0, v1, v2, V)) {
-    // a vertex id outside [0, V): NaN corners, so no edge of this triangle
-    // separates two pixel centres (it never blends, nothing reads its
-    // vertices)
-    const float q = __int_as_float(0x7fc00000);
-    r.s01 = make_float4(q, q, q, q);
-    r.s2 = make_float4(q, q, __int_as_float(topo[(int64_t)t * 3 + 0]),
-                       __int_as_float(topo[(int64_t)t * 3 + 1]));
-    r.tv = make_int4(topo[(int64_t)t * 3 + 2], -1, -1, -1);
-    rec[i] = r;
-    return;
+                                                AARec* __restrict__ rec,
+                                                AAPersp* __restrict__ persp) {
+  __shared__ float4 s_rec[256 * 3];
+  __shared__ float4 s_persp[256 * 3];
+  const int64_t base = (int64_t)blockIdx.x * 256;
+  const int64_t i = base + threadIdx.x;
+  if (i < NT) {
+    int64_t n;
+    int t;
+    divmod64(i, T, n, t);
+    const float* p = pos + n * V * 4;
+    const int v0 = tri[(int64_t)t * 3 + 0], v1 = tri[(int64_t)t * 3 + 1],
+              v2 = tri[(int64_t)t * 3 + 2];
+    const int k0 = topo[(int64_t)t * 3 + 0], k1 = topo[(int64_t)t * 3 + 1],
+              k2 = topo[(int64_t)t * 3 + 2];
+    float4* r = s_rec + threadIdx.x * 3;
+    float4* q = s_persp + threadIdx.x * 3;
+    if (!verts_ok(v0, v1, v2, V)) {
+      // a vertex id outside [0, V): NaN corners, so no edge of this triangle
+      // separates two pixel centres (it never blends, nothing reads its
+      // vertices)
+      const float nan = __int_as_float(0x7fc00000);
+      r[0] = make_float4(nan, nan, nan, nan);
+      r[1] = make_float4(nan, nan, __int_as_float(k0), __int_as_float(k1));
+      r[2] = make_float4(__int_as_float(k2), __int_as_float(-1), __int_as_float(-1),
+                         __int_as_float(-1));
+      const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+      q[0] = z; q[1] = z; q[2] = z;
+    } else {
+      const float4 P0 = *reinterpret_cast<const float4*>(p + (int64_t)v0 * 4);
+      const float4 P1 = *reinterpret_cast<const float4*>(p + (int64_t)v1 * 4);
+      const float4 P2 = *reinterpret_cast<const float4*>(p + (int64_t)v2 * 4);
+      const float hw = (float)W, hh = (float)H;
+      r[0] = make_float4((P0.x / P0.w + 1.0f) * hw * 0.5f, (1.0f - P0.y / P0.w) * hh * 0.5f,
+                         (P1.x / P1.w + 1.0f) * hw * 0.5f, (1.0f - P1.y / P1.w) * hh * 0.5f);
+      r[1] = make_float4((P2.x / P2.w + 1.0f) * hw * 0.5f, (1.0f - P2.y / P2.w) * hh * 0.5f,
+                         __int_as_float(k0), __int_as_float(k1));
+      r[2] = make_float4(__int_as_float(k2), __int_as_float(v0), __int_as_float(v1),
+                         __int_as_float(v2));
+      q[0] = persp_of(P0);
+      q[1] = persp_of(P1);
+      q[2] = persp_of(P2);
+    }
   }
-  const float4 P0 = *reinterpret_cast<const float4*>(p + (int64_t)v0 * 4);
-  const float4 P1 = *reinterpret_cast<const float4*>(p + (int64_t)v1 * 4);
-  const float4 P2 = *reinterpret_cast<const float4*>(p + (int64_t)v2 * 4);
-  const float hw = (float)W, hh = (float)H;
-  r.s01 = make_float4((P0.x / P0.w + 1.0f) * hw * 0.5f, (1.0f - P0.y / P0.w) * hh * 0.5f,
-                      (P1.x / P1.w + 1.0f) * hw * 0.5f, (1.0f - P1.y / P1.w) * hh * 0.5f);
-  r.s2 = make_float4((P2.x / P2.w + 1.0f) * hw * 0.5f, (1.0f - P2.y / P2.w) * hh * 0.5f,
-                     __int_as_float(topo[(int64_t)t * 3 + 0]),
-                     __int_as_float(topo[(int64_t)t * 3 + 1]));
-  r.tv = make_int4(topo[(int64_t)t * 3 + 2], v0, v1, v2);
-  rec[i] = r;
+  __syncthreads();
+  const int nrec = (int)min((int64_t)256, NT - base);
+  float4* dr = reinterpret_cast<float4*>(rec + base);
+  for (int j = threadIdx.x; j < nrec * 3; j += 256) dr[j] = s_rec[j];
+  if (persp) {
+    float4* dq = reinterpret_cast<float4*>(persp + base);
+    for (int j = threadIdx.x; j < nrec * 3; j += 256) dq[j] = s_persp[j];
+  }
 }
 
 struct SilDir {
@@ -435,8 +470,9 @@ __global__ void __launch_bounds__(256) k_aa_fwd(const float* __restrict__ rast,
 // d_pos terms of one partial blend (Antialias.swift:405-495): the blend
 // weight's gradient d_alpha = sum_c g * (c_neighbour - c_own) through the
 // crossing point into the edge's two clip-space vertices P0, P1.
+// Q0, Q1: the edge vertices' (inv_w, x * inv_w, y * inv_w) (persp_of).
 __device__ __forceinline__ void aa_dpos_add(const SilDir& s, int d, int ph, int pw, float d_alpha,
-                                            float4 P0, float4 P1, double* __restrict__ dp,
+                                            float4 Q0, float4 Q1, double* __restrict__ dp,
                                             float halfW, float halfH, LdsTable<4, 128>& tab) {
   float dade0x, dade0y, dade1x, dade1y;
   const float inv_denom_sq = 1.0f / (s.denom * s.denom);
@@ -459,9 +495,8 @@ __device__ __forceinline__ void aa_dpos_add(const SilDir& s, int d, int ph, int 
   const float dex[2] = {dade0x, dade1x}, dey[2] = {dade0y, dade1y};
 #pragma unroll
   for (int e = 0; e < 2; ++e) {
-    const float4 P = e == 0 ? P0 : P1;
-    const float inv_w = 1.0f / P.w;
-    const float nd_x = P.x * inv_w, nd_y = P.y * inv_w;
+    const float4 Q = e == 0 ? Q0 : Q1;
+    const float inv_w = Q.x, nd_x = Q.y, nd_y = Q.z;
     const float dv[4] = {
         d_alpha * dex[e] * halfW * inv_w, d_alpha * dey[e] * (-halfH) * inv_w, 0.0f,
         d_alpha * (dex[e] * (-halfW * nd_x) + dey[e] * (halfH * nd_y)) * inv_w};
@@ -481,7 +516,7 @@ __device__ __forceinline__ bool aa_dpos_terms(const SilDir& s, int d, int ph, in
   if (d_alpha == 0.0f) return false;
   const float4 P0 = *reinterpret_cast<const float4*>(p + (int64_t)s.ie0 * 4);
   const float4 P1 = *reinterpret_cast<const float4*>(p + (int64_t)s.ie1 * 4);
-  aa_dpos_add(s, d, ph, pw, d_alpha, P0, P1, dp, halfW, halfH, tab);
+  aa_dpos_add(s, d, ph, pw, d_alpha, persp_of(P0), persp_of(P1), dp, halfW, halfH, tab);
   return true;
 }
 
@@ -669,6 +704,95 @@ __global__ void __launch_bounds__(256) k_aa_bwd(const float* __restrict__ rast,
   lds_table_flush<4, 128, double>(tab);  // contains a barrier
 }
 
+constexpr int kMaskQueue = 256 * 4 + 64;
+
+// A queued pair with its loads in flight: cell and direction, the
+// foreground record, and (d_pos, inside the tile) its corners' d_pos
+// factors and the two pixels' colours (CT > 0), all issued together.
+template <int CT>
+struct AAPairIn {
+  int cell, d, tq, tn;
+  bool ok, border;
+  AARec R;
+  float4 Q[3];
+  float cp[CT > 0 ? CT : 1], cn[CT > 0 ? CT : 1];
+};
+
+template <int CT>
+__device__ __forceinline__ void aa_pair_load(int e, int (*s_tri)[18], const AATile& g, int H,
+                                             int W, const AARec* __restrict__ recn,
+                                             const AAPersp* __restrict__ perspn,
+                                             const float* __restrict__ color, bool want_pos,
+                                             AAPairIn<CT>& P) {
+  P.d = e & 3;
+  P.cell = e >> 2;
+  const int rr = P.cell / 18, cc = P.cell - rr * 18;
+  P.tq = s_tri[rr][cc];
+  P.tn = aa_nb(s_tri, rr, cc, P.d);
+  // a mask the forward wrote only marks candidate pairs; anything else is
+  // skipped, so no mask content can make the record index go out of range
+  P.ok = aa_cand(P.tq, P.tn);
+  if (!P.ok) return;
+  P.border = rr == 0 || rr == 17 || cc == 0 || cc == 17;
+  // the foreground record (:206-222): the pixel's own, else the neighbour's
+  const int fg = P.tq >= 0 ? P.tq : P.tn;
+  P.R = recn[fg];
+  if (want_pos && !P.border) {
+    P.Q[0] = perspn[fg].c[0];
+    P.Q[1] = perspn[fg].c[1];
+    P.Q[2] = perspn[fg].c[2];
+    if constexpr (CT > 0) {
+      // a masked pair of the tile blends (alpha in (0, 0.5]), so with d_pos
+      // its colours are needed: load them now rather than after the record
+      const int qph = g.y0 + rr - 1, qpw = g.x0 + cc - 1;
+      const int64_t qp = ((int64_t)g.n * H + qph) * W + qpw;
+      const int64_t qn = P.d == 0 ? qp + 1 : P.d == 1 ? qp + W : P.d == 2 ? qp - 1 : qp - W;
+      ld_px<CT>(color + qp * CT, CT, P.cp);
+      ld_px<CT>(color + qn * CT, CT, P.cn);
+    }
+  }
+}
+
+// The pair's blend weight (into s_alpha, or s_halo for a border pixel) and,
+// for the tile's own pixels, its d_pos terms.
+template <int CT>
+__device__ __forceinline__ void aa_pair_eval(const AAPairIn<CT>& P, const AATile& g, int H, int W,
+                                             int C, float (*s_alpha)[16][17],
+                                             float (*s_halo)[16],
+                                             const float (*s_g)[CT > 0 ? CT : 1],
+                                             const float* __restrict__ color,
+                                             const float* __restrict__ d_out,
+                                             double* __restrict__ dpn, LdsTable<4, 128>& tab) {
+  if (!P.ok) return;
+  const int rr = P.cell / 18, cc = P.cell - rr * 18, d = P.d;
+  const int qph = g.y0 + rr - 1, qpw = g.x0 + cc - 1;
+  SilDir s;
+  const bool on = sil_geom(P.R, P.tq >= 0 ? P.tn : -1, qph, qpw, d, s);
+  const float al = on ? s.alpha : 0.0f;
+  if (P.border) {
+    const int side = cc == 0 ? 0 : cc == 17 ? 1 : rr == 0 ? 2 : 3;
+    s_halo[side][side < 2 ? rr - 1 : cc - 1] = al;
+    return;
+  }
+  s_alpha[d][rr - 1][cc - 1] = al;
+  if (!dpn || !on || !(s.alpha < 1.0f)) return;
+  float d_alpha = 0.0f;
+  if constexpr (CT > 0) {
+#pragma unroll
+    for (int k = 0; k < CT; ++k) d_alpha += s_g[P.cell][k] * (P.cn[k] - P.cp[k]);
+  } else {
+    const int64_t qp = ((int64_t)g.n * H + qph) * W + qpw;
+    const int64_t qn = d == 0 ? qp + 1 : d == 1 ? qp + W : d == 2 ? qp - 1 : qp - W;
+    for (int k = 0; k < C; ++k)
+      d_alpha += d_out[qp * C + k] * (color[qn * C + k] - color[qp * C + k]);
+  }
+  if (d_alpha == 0.0f) return;
+  const int4 tv = P.R.tv;
+  const float4 Q0 = s.ie0 == tv.y ? P.Q[0] : s.ie0 == tv.z ? P.Q[1] : P.Q[2];
+  const float4 Q1 = s.ie1 == tv.y ? P.Q[0] : s.ie1 == tv.z ? P.Q[1] : P.Q[2];
+  aa_dpos_add(s, d, qph, qpw, d_alpha, Q0, Q1, dpn, (float)W * 0.5f, (float)H * 0.5f, tab);
+}
+
 // Backward with the forward's blend mask (bit d of a pixel set when its
 // blend weight toward direction d is nonzero).  Only the masked pairs are
 // evaluated: the tile's own pairs and the border pairs that point into the
@@ -676,27 +800,25 @@ __global__ void __launch_bounds__(256) k_aa_bwd(const float* __restrict__ rast,
 // it cannot overflow); each thread takes one, recomputes its edge state
 // with the forward's expressions, leaves the blend weight for the d_color
 // exchange and, for the tile's own pixels, adds the d_pos terms.  Pixels
-// without blends load no record.  With CT > 0 the cotangents of the tile
-// are staged in LDS before the first barrier (the few border neighbours
-// that blend into the tile are read from memory; colours are loaded only
-// for the queued pairs: staging them measured slower).
-constexpr int kMaskQueue = 256 * 4 + 64;
-
+// without blends load no record.  A tile costs two memory round trips:
+// its ids, mask bytes and cotangents (with CT > 0 those of the border too,
+// staged in LDS), then each pair's record, corner factors and colours.
 template <int CT>
 __global__ void __launch_bounds__(256) k_aa_bwd_masked(
-    const float* __restrict__ rast, const AARec* __restrict__ rec, const float* __restrict__ pos,
-    const float* __restrict__ color, const float* __restrict__ d_out,
-    const uint8_t* __restrict__ blend_mask, int H, int W, int V, int T, int C, int ntx, int nty,
-    float* __restrict__ d_color, double* __restrict__ d_pos, int accumulate) {
+    const float* __restrict__ rast, const AARec* __restrict__ rec,
+    const AAPersp* __restrict__ persp, const float* __restrict__ color,
+    const float* __restrict__ d_out, const uint8_t* __restrict__ blend_mask, int H, int W, int V,
+    int T, int C, int ntx, int nty, float* __restrict__ d_color, double* __restrict__ d_pos,
+    int accumulate) {
   constexpr int CS = CT > 0 ? CT : 1;
   constexpr int kCells = CT > 0 ? 18 * 18 : 1;
   __shared__ int s_tri[18][18];
   __shared__ float s_alpha[4][16][17];
   __shared__ float s_halo[4][16];
-  __shared__ LdsTable<4, 128> tab;  // d_pos rows touched by this tile
-  __shared__ int s_q[kMaskQueue];   // (cell r * 18 + c) << 2 | direction
+  __shared__ LdsTable<4, 128> tab;       // d_pos rows touched by this tile
+  __shared__ uint16_t s_q[kMaskQueue];   // (cell r * 18 + c) << 2 | direction
   __shared__ int s_nq;
-  __shared__ float s_g[kCells][CS];  // d_out of the tile (CT > 0; border cells unused)
+  __shared__ float s_g[kCells][CS];  // d_out of the tile and its border (CT > 0)
   if (d_pos) lds_table_clear(tab);
   if (threadIdx.x == 0) s_nq = 0;
   const AATile g = aa_tile(H, W, ntx, nty);
@@ -704,23 +826,31 @@ __global__ void __launch_bounds__(256) k_aa_bwd_masked(
   const int64_t pix = ((int64_t)g.n * H + min(g.ph, H - 1)) * W + min(g.pw, W - 1);
   const int lx = g.lx, ly = g.ly;
   const int own = (ly + 1) * 18 + (lx + 1);
-  // every load before the barrier is issued first: the own pixel's id, mask
-  // byte and cotangent, and (lanes 0..15 of each wave) one border pixel's id
-  // and mask byte
+  // every load before the barriers is issued first: the own pixel's id, mask
+  // byte and cotangent, and (lanes 0..15 of each wave) one border pixel's
+  // id, mask byte and cotangent
   const float own_w = rast[pix * 4 + 3];
   const int own_m = blend_mask[mask_index(g.n, min(g.ph, H - 1), min(g.pw, W - 1), ntx, nty)];
   float border_w = 0.0f;
   int border_m = 0;
-  float gown[CS];
+  float gown[CS], gbd[CS];
   if constexpr (CT > 0) ld_px<CT>(d_out + pix * CT, CT, gown);
   if (bd.in) {
     border_w = rast[bd.q * 4 + 3];
     border_m = blend_mask[mask_index(g.n, bd.qh, bd.qw, ntx, nty)];
+    if constexpr (CT > 0) ld_px<CT>(d_out + bd.q * CT, CT, gbd);
   }
+  // s_nq = 0 is seen by every wave before its first queue slot is taken
+  // (the loads above are in flight meanwhile)
+  __syncthreads();
   aa_store_ids(g, bd, own_w, border_w, T, s_tri);
   if constexpr (CT > 0) {
 #pragma unroll
     for (int k = 0; k < CT; ++k) s_g[own][k] = gown[k];
+    if (bd.in) {
+#pragma unroll
+      for (int k = 0; k < CT; ++k) s_g[bd.r * 18 + bd.c][k] = gbd[k];
+    }
   }
   // 1) queue the masked pairs: own pixel (all four directions), and the
   //    border pixel's direction into the tile.
@@ -735,62 +865,20 @@ __global__ void __launch_bounds__(256) k_aa_bwd_masked(
       int slot = atomicAdd(&s_nq, cnt);
 #pragma unroll
       for (int d = 0; d < 4; ++d)
-        if ((m >> d) & 1) s_q[slot++] = (own << 2) | d;
-      if (hm) s_q[slot] = ((bd.r * 18 + bd.c) << 2) | bd.d;
+        if ((m >> d) & 1) s_q[slot++] = (uint16_t)((own << 2) | d);
+      if (hm) s_q[slot] = (uint16_t)(((bd.r * 18 + bd.c) << 2) | bd.d);
     }
   }
   __syncthreads();
   // 2) one queued pair per thread: blend weight and the d_pos terms.
   const AARec* recn = rec + (int64_t)g.n * T;
-  const float* posn = pos + (int64_t)g.n * V * 4;
+  const AAPersp* perspn = persp + (int64_t)g.n * T;
+  double* dpn = d_pos ? d_pos + (int64_t)g.n * V * 4 : nullptr;
   const int nq = s_nq;
   for (int i = threadIdx.x; i < nq; i += blockDim.x) {
-    const int e = s_q[i];
-    const int d = e & 3, cell = e >> 2;
-    const int rr = cell / 18, cc = cell - rr * 18;
-    const int tq = s_tri[rr][cc];
-    const int tn = aa_nb(s_tri, rr, cc, d);
-    // a mask the forward wrote only marks candidate pairs; anything else is
-    // skipped, so no mask content can make the record index go out of range
-    if (!aa_cand(tq, tn)) continue;
-    const int qph = g.y0 + rr - 1, qpw = g.x0 + cc - 1;
-    const bool border = rr == 0 || rr == 17 || cc == 0 || cc == 17;
-    // the foreground record (:206-222): the pixel's own, else the neighbour's
-    const AARec R = recn[tq >= 0 ? tq : tn];
-    float4 P[3];
-    if (d_pos && !border && R.tv.y >= 0) {  // the edge is two of the record's vertices
-      P[0] = *reinterpret_cast<const float4*>(posn + (int64_t)R.tv.y * 4);
-      P[1] = *reinterpret_cast<const float4*>(posn + (int64_t)R.tv.z * 4);
-      P[2] = *reinterpret_cast<const float4*>(posn + (int64_t)R.tv.w * 4);
-    }
-    SilDir s;
-    const bool on = sil_geom(R, tq >= 0 ? tn : -1, qph, qpw, d, s);
-    const float al = on ? s.alpha : 0.0f;
-    if (border) {
-      const int side = cc == 0 ? 0 : cc == 17 ? 1 : rr == 0 ? 2 : 3;
-      s_halo[side][side < 2 ? rr - 1 : cc - 1] = al;
-      continue;
-    }
-    s_alpha[d][rr - 1][cc - 1] = al;
-    if (!d_pos || !on || !(s.alpha < 1.0f)) continue;
-    const int64_t qp = ((int64_t)g.n * H + qph) * W + qpw;
-    const int64_t qn = d == 0 ? qp + 1 : d == 1 ? qp + W : d == 2 ? qp - 1 : qp - W;
-    float d_alpha = 0.0f;
-    if constexpr (CT > 0) {
-      float cp[CT], cn[CT];
-      ld_px<CT>(color + qp * CT, CT, cp);
-      ld_px<CT>(color + qn * CT, CT, cn);
-#pragma unroll
-      for (int k = 0; k < CT; ++k) d_alpha += s_g[cell][k] * (cn[k] - cp[k]);
-    } else {
-      for (int k = 0; k < C; ++k)
-        d_alpha += d_out[qp * C + k] * (color[qn * C + k] - color[qp * C + k]);
-    }
-    if (d_alpha == 0.0f) continue;
-    const float4 P0 = s.ie0 == R.tv.y ? P[0] : s.ie0 == R.tv.z ? P[1] : P[2];
-    const float4 P1 = s.ie1 == R.tv.y ? P[0] : s.ie1 == R.tv.z ? P[1] : P[2];
-    aa_dpos_add(s, d, qph, qpw, d_alpha, P0, P1, d_pos + (int64_t)g.n * V * 4, (float)W * 0.5f,
-                (float)H * 0.5f, tab);
+    AAPairIn<CT> P;
+    aa_pair_load<CT>(s_q[i], s_tri, g, H, W, recn, perspn, color, dpn != nullptr, P);
+    aa_pair_eval<CT>(P, g, H, W, C, s_alpha, s_halo, s_g, color, d_out, dpn, tab);
   }
   __syncthreads();
   // 3) d_color: own term + what each neighbour's blend sends here.
@@ -804,24 +892,17 @@ __global__ void __launch_bounds__(256) k_aa_bwd_masked(
     wn[2] = lx > 0 ? s_alpha[0][ly][lx - 1] : s_halo[0][ly];   // left neighbour, its dir 0
     wn[3] = ly > 0 ? s_alpha[1][ly - 1][lx] : s_halo[2][lx];   // upper neighbour, its dir 1
     if constexpr (CT > 0) {
+      // a neighbour with a nonzero weight lies in the image, so its
+      // cotangent is in s_g (a border cell when outside the tile)
       const int nc[4] = {own + 1, own + 18, own - 1, own - 18};
-      const int64_t qn[4] = {pix + 1, pix + W, pix - 1, pix - W};
-      const bool edge[4] = {lx == 15, ly == 15, lx == 0, ly == 0};  // neighbour outside the tile
       float acc[CT];
 #pragma unroll
       for (int k = 0; k < CT; ++k) acc[k] = s_g[own][k] * (1.0f - asum);
 #pragma unroll
       for (int d = 0; d < 4; ++d) {
         if (wn[d] > 0.0f) {
-          float gq[CT];
-          if (edge[d]) {
-            ld_px<CT>(d_out + qn[d] * CT, CT, gq);
-          } else {
 #pragma unroll
-            for (int k = 0; k < CT; ++k) gq[k] = s_g[nc[d]][k];
-          }
-#pragma unroll
-          for (int k = 0; k < CT; ++k) acc[k] += gq[k] * wn[d];
+          for (int k = 0; k < CT; ++k) acc[k] += s_g[nc[d]][k] * wn[d];
         }
       }
       if (accumulate) {
@@ -884,9 +965,11 @@ extern "C" int dr_antialias_topology(const int32_t* tri, int T, int32_t* topo,
   return DR_OK;
 }
 
-// Per-(image, triangle) records into rec (scratch when rec is null).
+// Per-(image, triangle) records into rec (scratch when rec is null), and
+// their corners' d_pos factors into persp when it is not null.
 static int aa_records(const float* pos, const int32_t* tri, const int32_t* topo, int N, int V,
-                      int T, int H, int W, hipStream_t stream, AARec* rec, AARec** out) {
+                      int T, int H, int W, hipStream_t stream, AARec* rec, AAPersp* persp,
+                      AARec** out) {
   const int64_t nt = (int64_t)N * T;
   if (!rec) {
     Scratch* sc = scratch_for(stream);
@@ -897,7 +980,7 @@ static int aa_records(const float* pos, const int32_t* tri, const int32_t* topo,
   if (nt > 0) {
     DR_TIMED("k_aa_rec", stream);
     hipLaunchKernelGGL(k_aa_rec, dim3(grid_for(nt, 256)), dim3(256), 0, stream, pos, tri, topo,
-                       nt, T, V, H, W, rec);
+                       nt, T, V, H, W, rec, persp);
   }
   DR_CHECK_LAUNCH();
   *out = rec;
@@ -906,7 +989,7 @@ static int aa_records(const float* pos, const int32_t* tri, const int32_t* topo,
 
 // Saved state of dr_antialias_fwd_save: the blend mask (one byte per pixel
 // of the image padded to 16x16 tiles, a multiple of 256 bytes), then the
-// per-(image, triangle) records.
+// per-(image, triangle) records, then their corners' d_pos factors.
 static int64_t aa_mask_bytes(int N, int H, int W) {
   return (int64_t)N * ((H + 15) / 16) * ((W + 15) / 16) * 256;
 }
@@ -945,12 +1028,15 @@ static int aa_fwd(const float* color, const float* rast, const float* pos, const
   DR_CHECK_ARG(((uintptr_t)saved & 15) == 0, "antialias_fwd_save: saved must be 16-byte aligned");
   uint8_t* mask = saved;
   AARec* rec = nullptr;
-  int st2 = aa_records(pos, tri, topo, N, V, T, H, W, stream,
-                       saved ? (AARec*)(saved + aa_mask_bytes(N, H, W)) : nullptr, &rec);
+  AARec* saved_rec = saved ? (AARec*)(saved + aa_mask_bytes(N, H, W)) : nullptr;
+  AAPersp* saved_persp = saved ? (AAPersp*)(saved_rec + (int64_t)N * T) : nullptr;
+  int st2 = aa_records(pos, tri, topo, N, V, T, H, W, stream, saved_rec, saved_persp, &rec);
   if (st2) return st2;
   const int ntx = (W + 15) / 16, nty = (H + 15) / 16;
-  const dim3 grid((unsigned)((int64_t)N * ntx * nty)), block(256);
+  const int64_t total = (int64_t)N * ntx * nty;
+  DR_CHECK_ARG(total <= INT32_MAX - 4096, "antialias: too many tiles");
   const int ct = aa_ct(C, color, out, color);
+  const dim3 grid((unsigned)total), block(256);
   DR_TIMED("k_aa_fwd", stream);
   DR_AA_DISPATCH(k_aa_fwd, ct, grid, block, 0, stream, rast, rec, color, H, W, T, C, ntx, nty,
                  out, mask);
@@ -977,21 +1063,25 @@ static int aa_bwd(const float* color, const float* rast, const float* pos, const
     if (!dpos64) return DR_ERR_MEMORY;
   }
   const AARec* rec = nullptr;
+  const AAPersp* persp = nullptr;
   if (saved) {  // the forward's records
     rec = (const AARec*)(saved + aa_mask_bytes(N, H, W));
+    persp = (const AAPersp*)(rec + (int64_t)N * T);
   } else {
     AARec* r = nullptr;
-    int st2 = aa_records(pos, tri, topo, N, V, T, H, W, stream, nullptr, &r);
+    int st2 = aa_records(pos, tri, topo, N, V, T, H, W, stream, nullptr, nullptr, &r);
     if (st2) return st2;
     rec = r;
   }
   const int ntx = (W + 15) / 16, nty = (H + 15) / 16;
-  const dim3 grid((unsigned)((int64_t)N * ntx * nty)), block(256);
+  const int64_t total = (int64_t)N * ntx * nty;
+  DR_CHECK_ARG(total <= INT32_MAX - 4096, "antialias: too many tiles");
+  const dim3 grid((unsigned)total), block(256);
   const int ct = aa_ct(C, color, d_out, d_color);
   {
     DR_TIMED("k_aa_bwd", stream);
     if (saved) {
-      DR_AA_DISPATCH(k_aa_bwd_masked, ct, grid, block, 0, stream, rast, rec, pos, color, d_out,
+      DR_AA_DISPATCH(k_aa_bwd_masked, ct, grid, block, 0, stream, rast, rec, persp, color, d_out,
                      saved, H, W, V, T, C, ntx, nty, d_color, dpos64, acc ? 1 : 0);
     } else {
       DR_AA_DISPATCH(k_aa_bwd, ct, grid, block, 0, stream, rast, rec, pos, color, d_out, H, W,
@@ -1020,7 +1110,7 @@ extern "C" int dr_antialias_bwd(const float* color, const float* rast, const flo
 
 extern "C" int64_t dr_antialias_saved_bytes(int N, int H, int W, int T) {
   if (N < 1 || H < 1 || W < 1 || T < 0) return -1;
-  return aa_mask_bytes(N, H, W) + (int64_t)N * T * (int64_t)sizeof(AARec);
+  return aa_mask_bytes(N, H, W) + (int64_t)N * T * (int64_t)(sizeof(AARec) + sizeof(AAPersp));
 }
 
 extern "C" int dr_antialias_fwd_save(const float* color, const float* rast, const float* pos,

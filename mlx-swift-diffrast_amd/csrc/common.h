@@ -379,10 +379,13 @@ __device__ __forceinline__ void group_atomic_add(bool valid, uint64_t key, float
 constexpr unsigned long long kEmptyKey = ~0ull;
 constexpr int kLdsProbes = 8;
 
+// Values are stored component-major (val[j][entry]): an entry's NV values
+// 8 * NV bytes apart would put the entries of a wave's atomics on a few
+// banks only (entry * 2 * NV mod 32); 8 bytes apart they spread over 16.
 template <int NV, int CAP>
 struct LdsTable {
   unsigned long long key[CAP];
-  double val[CAP][NV];
+  double val[NV][CAP];
 };
 
 __device__ __forceinline__ uint32_t addr_hash(uint64_t k) {
@@ -394,7 +397,7 @@ __device__ __forceinline__ void lds_table_clear(LdsTable<NV, CAP>& t) {
   for (int i = threadIdx.x; i < CAP; i += blockDim.x) {
     t.key[i] = kEmptyKey;
 #pragma unroll
-    for (int j = 0; j < NV; ++j) t.val[i][j] = 0.0;
+    for (int j = 0; j < NV; ++j) t.val[j][i] = 0.0;
   }
 }
 
@@ -415,7 +418,7 @@ __device__ __forceinline__ void lds_table_add(LdsTable<NV, CAP>& t, D* dst, cons
     if (cur == kEmptyKey || cur == key) {
 #pragma unroll
       for (int j = 0; j < NV; ++j)
-        if (v[j] != 0.0f) atomicAdd(&t.val[h][j], (double)v[j]);
+        if (v[j] != 0.0f) atomicAdd(&t.val[j][h], (double)v[j]);
       return;
     }
     h = (h + 1) & (CAP - 1);
@@ -435,9 +438,9 @@ __device__ __forceinline__ void lds_table_flush(LdsTable<NV, CAP>& t) {
     const int e = i / NV, j = i - e * NV;
     const unsigned long long k = t.key[e];
     if (k != kEmptyKey) {
-      const double v = t.val[e][j];
+      const double v = t.val[j][e];
       if (v != 0.0) unsafeAtomicAdd((D*)k + j, (D)v);
-      t.val[e][j] = 0.0;
+      t.val[j][e] = 0.0;
     }
   }
   __syncthreads();
