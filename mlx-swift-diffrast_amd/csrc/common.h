@@ -51,6 +51,7 @@ enum Slot {
   SLOT_LOSS,          // partial sums of the loss
   SLOT_AA_REC,        // per (image, triangle) silhouette records (antialias)
   SLOT_DPOS64,        // fp64 accumulator of d_pos (rasterize and antialias backward)
+  SLOT_RBWD_REC,      // per (image, triangle) records of the rasterize backward
   SLOT_COUNT
 };
 

@@ -484,14 +484,63 @@ __global__ void __launch_bounds__(256) k_raster(
   if (DB) *reinterpret_cast<float4*>(rast_db + pix * 4) = d4;
 }
 
+// Per (image, triangle) values of the rasterize backward that do not
+// depend on the pixel (Rasterize.swift:665-690, 790-797), computed once per
+// triangle with the same expressions instead of once per covered pixel:
+//   q0 = (sx0, sy0, sx1, sy1), q1 = (sx2, sy2, sz0, sz1),
+//   q2 = (sz2, 1 / area, 1 / w0, 1 / w1), q3 = (1 / w2, i0, i1, i2)
+// (the vertex ids as int bits; i0 = -1 when an id lies outside [0, V)).
+struct alignas(16) RBwdRec {
+  float4 q0, q1, q2, q3;
+};
+
+__global__ void __launch_bounds__(256) k_rbwd_rec(const float* __restrict__ pos, int64_t pos_stride,
+                                                  const int32_t* __restrict__ tri, int64_t NT,
+                                                  int V, int T, RBwdRec* __restrict__ out) {
+  __shared__ float4 s_r[256 * 4];
+  const int64_t base = (int64_t)blockIdx.x * 256;
+  const int64_t i = base + threadIdx.x;
+  if (i < NT) {
+    int64_t n;
+    int t;
+    divmod64(i, T, n, t);
+    const int i0 = tri[t * 3 + 0], i1 = tri[t * 3 + 1], i2 = tri[t * 3 + 2];
+    float4* r = s_r + threadIdx.x * 4;
+    if (!verts_ok(i0, i1, i2, V)) {
+      const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+      r[0] = z; r[1] = z; r[2] = z;
+      r[3] = make_float4(0.f, __int_as_float(-1), 0.f, 0.f);
+    } else {
+      const float* p = pos + n * pos_stride;
+      const float4 P0 = *reinterpret_cast<const float4*>(p + (int64_t)i0 * 4);
+      const float4 P1 = *reinterpret_cast<const float4*>(p + (int64_t)i1 * 4);
+      const float4 P2 = *reinterpret_cast<const float4*>(p + (int64_t)i2 * 4);
+      const float sx0 = P0.x / P0.w, sy0 = P0.y / P0.w, sz0 = P0.z / P0.w;
+      const float sx1 = P1.x / P1.w, sy1 = P1.y / P1.w, sz1 = P1.z / P1.w;
+      const float sx2 = P2.x / P2.w, sy2 = P2.y / P2.w, sz2 = P2.z / P2.w;
+      const float area = (sx1 - sx0) * (sy2 - sy0) - (sx2 - sx0) * (sy1 - sy0);
+      r[0] = make_float4(sx0, sy0, sx1, sy1);
+      r[1] = make_float4(sx2, sy2, sz0, sz1);
+      r[2] = make_float4(sz2, 1.0f / area, 1.0f / P0.w, 1.0f / P1.w);
+      r[3] = make_float4(1.0f / P2.w, __int_as_float(i0), __int_as_float(i1), __int_as_float(i2));
+    }
+  }
+  __syncthreads();
+  const int nrec = (int)min((int64_t)256, NT - base);
+  float4* d = reinterpret_cast<float4*>(out + base);
+  for (int j = threadIdx.x; j < nrec * 4; j += 256) d[j] = s_r[j];
+}
+
 // Rasterize.swift:637-812.  16x16 tiles, a 16x4 strip per wave; runs of
 // same-triangle lanes along a pixel row are summed before the LDS table
 // adds the 12 d_pos terms; the table is written out into an fp64
-// accumulator laid out as pos.
+// accumulator laid out as pos.  A covered pixel loads its triangle's
+// record (k_rbwd_rec) together with its cotangents, one round trip after
+// its rast value.
 __global__ void __launch_bounds__(256) k_raster_bwd(
-    const float* __restrict__ pos, int64_t pos_stride, const int32_t* __restrict__ tri,
+    const RBwdRec* __restrict__ trec, int64_t rec_stride, int64_t pos_stride,
     const float* __restrict__ rast, const float* __restrict__ d_rast,
-    const float* __restrict__ d_rast_db, int N, int V, int T, int H, int W, int ntx, int nty,
+    const float* __restrict__ d_rast_db, int N, int T, int H, int W, int ntx, int nty,
     double* __restrict__ d_pos) {
   __shared__ LdsTable<4, 256> tab;  // d_pos rows touched by this tile
   __shared__ int s_any[4];          // per wave: a covered pixel
@@ -511,6 +560,13 @@ __global__ void __launch_bounds__(256) k_raster_bwd(
   const float4 r = *reinterpret_cast<const float4*>(rast + pix * 4);
   const int t = f2i(r.w) - 1;
   valid = valid && t >= 0 && t < T;
+  RBwdRec R;
+  float4 dr = make_float4(0.f, 0.f, 0.f, 0.f), ddb = dr;
+  if (valid) {
+    R = trec[(int64_t)n * rec_stride + t];
+    dr = *reinterpret_cast<const float4*>(d_rast + pix * 4);
+    if (d_rast_db) ddb = *reinterpret_cast<const float4*>(d_rast_db + pix * 4);
+  }
   {
     const uint64_t any = __ballot(valid);
     if (lane == 0) s_any[wave] = any != 0ull;
@@ -523,32 +579,23 @@ __global__ void __launch_bounds__(256) k_raster_bwd(
   int i0 = 0, i1 = 0, i2 = 0;
 #pragma unroll
   for (int q = 0; q < 12; ++q) val[q] = 0.0f;
-  const float* p = pos + (int64_t)n * pos_stride;
   double* dp = d_pos + (int64_t)n * pos_stride;
   if (valid) {
-    i0 = tri[t * 3 + 0];
-    i1 = tri[t * 3 + 1];
-    i2 = tri[t * 3 + 2];
-    valid = verts_ok(i0, i1, i2, V);
+    i0 = __float_as_int(R.q3.y);
+    i1 = __float_as_int(R.q3.z);
+    i2 = __float_as_int(R.q3.w);
+    valid = i0 >= 0;  // the triangle's vertex ids lie in [0, V)
   }
   if (valid) {
     const float u_val = r.x, v_val = r.y;
     const float bw_val = 1.0f - u_val - v_val;
-    const float4 dr = *reinterpret_cast<const float4*>(d_rast + pix * 4);
     const float d_u = dr.x, d_v = dr.y, d_z = dr.z;
-    float4 ddb = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (d_rast_db) ddb = *reinterpret_cast<const float4*>(d_rast_db + pix * 4);
     const float d_db0 = ddb.x, d_db1 = ddb.y, d_db2 = ddb.z, d_db3 = ddb.w;
     const float Px = 2.0f * ((float)pw + 0.5f) / (float)W - 1.0f;
     const float Py = 1.0f - 2.0f * ((float)ph + 0.5f) / (float)H;
-    const float4 P0 = *reinterpret_cast<const float4*>(p + (int64_t)i0 * 4);
-    const float4 P1 = *reinterpret_cast<const float4*>(p + (int64_t)i1 * 4);
-    const float4 P2 = *reinterpret_cast<const float4*>(p + (int64_t)i2 * 4);
-    const float sx0 = P0.x / P0.w, sy0 = P0.y / P0.w, sz0 = P0.z / P0.w;
-    const float sx1 = P1.x / P1.w, sy1 = P1.y / P1.w, sz1 = P1.z / P1.w;
-    const float sx2 = P2.x / P2.w, sy2 = P2.y / P2.w, sz2 = P2.z / P2.w;
-    const float area = (sx1 - sx0) * (sy2 - sy0) - (sx2 - sx0) * (sy1 - sy0);
-    const float inv_area = 1.0f / area;
+    const float sx0 = R.q0.x, sy0 = R.q0.y, sx1 = R.q0.z, sy1 = R.q0.w;
+    const float sx2 = R.q1.x, sy2 = R.q1.y, sz0 = R.q1.z, sz1 = R.q1.w;
+    const float sz2 = R.q2.x, inv_area = R.q2.y;
     const float dadsx0 = sy1 - sy2, dadsx1 = sy2 - sy0, dadsx2 = sy0 - sy1;
     const float dadsy0 = sx2 - sx1, dadsy1 = sx0 - sx2, dadsy2 = sx1 - sx0;
     const float de1dsx0 = Py - sy2, de1dsx2 = sy0 - Py;
@@ -596,7 +643,7 @@ __global__ void __launch_bounds__(256) k_raster_bwd(
     dsy1 += d_db2 * (-Kx) * inv_area;
     dsx0 += d_db3 * (-Ky) * inv_area;
     dsx1 += d_db3 * (Ky) * inv_area;
-    const float inv_w0 = 1.0f / P0.w, inv_w1 = 1.0f / P1.w, inv_w2 = 1.0f / P2.w;
+    const float inv_w0 = R.q2.z, inv_w1 = R.q2.w, inv_w2 = R.q3.x;
     val[0] = dsx0 * inv_w0;
     val[1] = dsy0 * inv_w0;
     val[2] = dsz0_s * inv_w0;
@@ -930,11 +977,24 @@ extern "C" int dr_rasterize_bwd(const float* pos, int64_t pos_batch_stride, cons
   if (!acc) return DR_ERR_MEMORY;
   const int ntx = (W + kTile - 1) / kTile, nty = (H + kTile - 1) / kTile;
   const int64_t blocks = (int64_t)N * ntx * nty;
+  // per (image, triangle) records; one set for all images when pos is shared
+  const int64_t nrec = (pos_batch_stride ? (int64_t)N : 1) * T;
+  Scratch* sc = scratch_for(stream);
+  if (!sc) return DR_ERR_HIP;
+  RBwdRec* trec = (RBwdRec*)scratch_get(sc, stream, SLOT_RBWD_REC,
+                                        (size_t)std::max<int64_t>(nrec, 1) * sizeof(RBwdRec));
+  if (!trec) return DR_ERR_MEMORY;
+  if (nrec > 0) {
+    DR_TIMED("k_rbwd_rec", stream);
+    hipLaunchKernelGGL(k_rbwd_rec, dim3((unsigned)((nrec + 255) / 256)), dim3(256), 0, stream,
+                       pos, pos_batch_stride, tri, nrec, V, T, trec);
+  }
+  DR_CHECK_LAUNCH();
   {
     DR_TIMED("k_raster_bwd", stream);
-    hipLaunchKernelGGL(k_raster_bwd, dim3((unsigned)blocks), dim3(256), 0, stream, pos,
-                       pos_batch_stride, tri, rast, d_rast, d_rast_db, N, V, T, H, W, ntx, nty,
-                       acc);
+    hipLaunchKernelGGL(k_raster_bwd, dim3((unsigned)blocks), dim3(256), 0, stream, trec,
+                       pos_batch_stride ? (int64_t)T : (int64_t)0, pos_batch_stride, rast, d_rast,
+                       d_rast_db, N, T, H, W, ntx, nty, acc);
   }
   DR_CHECK_LAUNCH();
   return acc64_end(acc, d_pos, npos, (flags & DR_ACCUMULATE) != 0, stream);

@@ -758,6 +758,9 @@ template <int FILTER, int CT, int BND, bool BIAS>
 // Five waves per SIMD (the register budget this asks for costs a few
 // spilled values; measured cheaper than four or six).
 __global__ void __launch_bounds__(kWinThreads, 5) k_tex_bwd_win(TexBwdArgs A, int total_tiles) {
+  // channel-major (win[c * kWinTexels + texel]): a wave's run tails on
+  // neighbouring texels then add 8 bytes apart, spread over the banks,
+  // rather than 8 * CT bytes apart on a few of them
   __shared__ double win[kWinTexels * CT];
   __shared__ int s_wk[kWinWaves];          // per wave: lowest level in use
   __shared__ int s_wbox[kWinWaves][2][4];  // per wave: boxes on that level and the next
@@ -1017,7 +1020,7 @@ __global__ void __launch_bounds__(kWinThreads, 5) k_tex_bwd_win(TexBwdArgs A, in
     usable[0] = usable[0] && area[0] <= kWinTexels;
     wbase[0] = 0;
     usable[1] = usable[1] && (usable[0] ? area[0] : 0) + area[1] <= kWinTexels;
-    wbase[1] = usable[0] ? (int)area[0] * CT : 0;
+    wbase[1] = usable[0] ? (int)area[0] : 0;  // in texels
 
     // -- accumulate: runs of one footprint along a pixel row are summed
     //    first (lanes of one LDS atomic on one address are serialised), the
@@ -1052,9 +1055,9 @@ __global__ void __launch_bounds__(kWinThreads, 5) k_tex_bwd_win(TexBwdArgs A, in
         const int tx_ = (t & 1) ? q[li].ix1 : q[li].ix0;
         const int ty_ = (t & 2) ? q[li].iy1 : q[li].iy0;
         if (in_win) {
-          const int o = ((ty_ - by0[w]) * bw[w] + (tx_ - bx0[w])) * CT;  // < area[w]*CT
+          const int o = (ty_ - by0[w]) * bw[w] + (tx_ - bx0[w]);  // < area[w]
 #pragma unroll
-          for (int c = 0; c < CT; ++c) atomicAdd(wb + o + c, (double)v[c]);
+          for (int c = 0; c < CT; ++c) atomicAdd(wb + c * kWinTexels + o, (double)v[c]);
         } else {
           lds_table_add(tab, base + (ty_ * Wk + tx_) * CT, v);
         }
@@ -1073,12 +1076,16 @@ __global__ void __launch_bounds__(kWinThreads, 5) k_tex_bwd_win(TexBwdArgs A, in
       const int row = bw[w] * CT;
       const int total = row * bh[w];
       double* wb = win + wbase[w];
+      // consecutive lanes take consecutive channels of a texel, so the
+      // device atomics of a row share cache lines
       for (int i = tid; i < total; i += kWinThreads) {
-        const double v = wb[i];
+        const int r = i / row, cpos = i - r * row;
+        const int tx = cpos / CT, c = cpos - tx * CT;
+        double* e = wb + c * kWinTexels + r * bw[w] + tx;
+        const double v = *e;
         if (v != 0.0) {
-          const int r = i / row, cpos = i - r * row;
           unsafeAtomicAdd(base + ((by0[w] + r) * Wk + bx0[w]) * CT + cpos, (float)v);
-          wb[i] = 0.0;
+          *e = 0.0;
         }
       }
     }
