@@ -59,9 +59,11 @@ struct Scratch {
   void* ptr[SLOT_COUNT] = {};
   size_t cap[SLOT_COUNT] = {};
   // Tile-list capacity protocol (rasterize): the largest per-tile count of
-  // a call is copied to pinned host memory after the call; a later call
-  // reads it (once its copy has landed) and raises the capacity if needed.
+  // a call is written into pinned host memory by a kernel after the call; a
+  // later call reads it (once that kernel has run) and raises the capacity
+  // if needed.
   int64_t* pinned_total = nullptr;
+  int64_t* pinned_total_dev = nullptr;  // the same memory as a kernel writes it
   hipEvent_t total_event = nullptr;
   bool total_pending = false;
   int bin_cap = 0;  // slots per tile list, 0 = not known yet
@@ -74,6 +76,11 @@ struct Scratch {
   hipEvent_t stage_event[kStageRing] = {};
   bool stage_pending[kStageRing] = {};
   int stage_next = 0;
+  // fp64 d_pos accumulator (SLOT_DPOS64): k_acc_to_f32 leaves the elements
+  // it converts zero, so the next call need not clear them; acc64_zero
+  // counts the leading elements of buffer acc64_buf known to be zero.
+  const void* acc64_buf = nullptr;
+  int64_t acc64_zero = 0;
 };
 
 // A pinned host buffer of the range-mode staging ring holding at least
@@ -451,7 +458,7 @@ __device__ __forceinline__ void lds_table_flush(LdsTable<NV, CAP>& t) {
 // dst = (float)acc, or dst += (float)acc: the one rounding of a gradient
 // summed in fp64 across workgroups (so the result does not depend on the
 // order in which the workgroups' atomics land).
-__global__ void k_acc_to_f32(const double* __restrict__ acc, float* __restrict__ dst, int64_t n,
+__global__ void k_acc_to_f32(double* __restrict__ acc, float* __restrict__ dst, int64_t n,
                              int accumulate);
 
 template <typename T>
@@ -536,9 +543,11 @@ inline unsigned grid_for(int64_t n, int block) {
   return (unsigned)((n + block - 1) / block);
 }
 
-// An fp64 accumulator of n values (library scratch, zeroed on the stream).
+// An fp64 accumulator of n values (library scratch, zero on the stream:
+// cleared here unless the last acc64_end on this stream left it zero).
 double* acc64_begin(hipStream_t stream, int64_t n);
-// Rounds the accumulator into dst (overwrite, or add when accumulate).
-int acc64_end(const double* acc, float* dst, int64_t n, bool accumulate, hipStream_t stream);
+// Rounds the accumulator into dst (overwrite, or add when accumulate) and
+// zeroes it for the next acc64_begin.
+int acc64_end(double* acc, float* dst, int64_t n, bool accumulate, hipStream_t stream);
 
 }  // namespace dr

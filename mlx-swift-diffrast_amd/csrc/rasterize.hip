@@ -161,11 +161,25 @@ __global__ void __launch_bounds__(256) k_bin_count(Items it, int64_t n_items, in
 }
 
 // Largest per-tile count (sizes the next call's per-tile list capacity).
+// The largest of c[0..n) (counts, >= 0) into *out, by one workgroup: out is
+// the pinned host cell of the capacity protocol, written directly (no
+// device atomics, no copy).
 __global__ void __launch_bounds__(256) k_tile_max(const int* __restrict__ c, int64_t n,
-                                                  int* __restrict__ out) {
-  const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int m = wave_max(j < n ? c[j] : 0);
-  if (lane_id() == 0) atomicMax(out, m);
+                                                  int64_t* __restrict__ out) {
+  __shared__ int s_m[4];
+  int m0 = 0, m1 = 0, m2 = 0, m3 = 0;
+  int64_t j = threadIdx.x;
+  for (; j + 768 < n; j += 1024) {
+    m0 = max(m0, c[j]);
+    m1 = max(m1, c[j + 256]);
+    m2 = max(m2, c[j + 512]);
+    m3 = max(m3, c[j + 768]);
+  }
+  for (; j < n; j += 256) m0 = max(m0, c[j]);
+  const int m = wave_max(max(max(m0, m1), max(m2, m3)));
+  if (lane_id() == 0) s_m[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) *out = max(max(s_m[0], s_m[1]), max(s_m[2], s_m[3]));
 }
 
 // Rasterize.swift:227-239, second half: append t to each touched tile's
@@ -669,12 +683,15 @@ __global__ void __launch_bounds__(256) k_raster_bwd(
   lds_table_flush<4, 256, double>(tab);
 }
 
-__global__ void __launch_bounds__(256) k_acc_to_f32(const double* __restrict__ acc,
+// The one rounding of the fp64 sums; the accumulator is left zero for the
+// next call.
+__global__ void __launch_bounds__(256) k_acc_to_f32(double* __restrict__ acc,
                                                     float* __restrict__ dst, int64_t n,
                                                     int accumulate) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
   const float v = (float)acc[i];
+  acc[i] = 0.0;
   dst[i] = accumulate ? dst[i] + v : v;
 }
 
@@ -683,19 +700,28 @@ double* acc64_begin(hipStream_t stream, int64_t n) {
   if (!sc) return nullptr;
   double* a = (double*)scratch_get(sc, stream, SLOT_DPOS64, (size_t)std::max<int64_t>(n, 1) * 8);
   if (!a) return nullptr;
-  if (fill_async(a, 0.0, n, stream) != hipSuccess) {
+  if (sc->acc64_buf != a) {  // a new buffer: its contents are unknown
+    sc->acc64_buf = a;
+    sc->acc64_zero = 0;
+  }
+  if (sc->acc64_zero < n && fill_async(a, 0.0, n, stream) != hipSuccess) {
     set_error("fp64 accumulator: fill launch failed");
     return nullptr;
   }
+  sc->acc64_zero = 0;  // in use until acc64_end has queued its conversion
   return a;
 }
 
-int acc64_end(const double* acc, float* dst, int64_t n, bool accumulate, hipStream_t stream) {
+int acc64_end(double* acc, float* dst, int64_t n, bool accumulate, hipStream_t stream) {
   if (n <= 0) return DR_OK;
-  DR_TIMED("k_acc_to_f32", stream);
-  hipLaunchKernelGGL(k_acc_to_f32, dim3(grid_for(n, 256)), dim3(256), 0, stream, acc, dst, n,
-                     accumulate ? 1 : 0);
+  {
+    DR_TIMED("k_acc_to_f32", stream);
+    hipLaunchKernelGGL(k_acc_to_f32, dim3(grid_for(n, 256)), dim3(256), 0, stream, acc, dst, n,
+                       accumulate ? 1 : 0);
+  }
   DR_CHECK_LAUNCH();
+  Scratch* sc = scratch_for(stream);
+  if (sc && sc->acc64_buf == acc) sc->acc64_zero = n;
   return DR_OK;
 }
 
@@ -824,15 +850,14 @@ extern "C" int dr_rasterize_tile_counts(const float* pos, int64_t pos_batch_stri
                  stream);
   DR_CHECK_LAUNCH();
   if (max_count_host) {
-    int* tmax = small + 8;  // apart from the forward's read-back counter
-    DR_CHECK_HIP(fill_async(tmax, 0, 1, stream));
-    hipLaunchKernelGGL(k_tile_max, dim3(grid_for(n_tiles, 256)), dim3(256), 0, stream,
-                       (const int*)counts, n_tiles, tmax);
+    int64_t* tmax = reinterpret_cast<int64_t*>(small + 8);
+    hipLaunchKernelGGL(k_tile_max, dim3(1), dim3(256), 0, stream, (const int*)counts, n_tiles,
+                       tmax);
     DR_CHECK_LAUNCH();
-    int mx = 0;
-    DR_CHECK_HIP(hipMemcpyAsync(&mx, tmax, sizeof(int), hipMemcpyDeviceToHost, stream));
+    int64_t mx = 0;
+    DR_CHECK_HIP(hipMemcpyAsync(&mx, tmax, sizeof(int64_t), hipMemcpyDeviceToHost, stream));
     DR_CHECK_HIP(hipStreamSynchronize(stream));
-    *max_count_host = mx;
+    *max_count_host = (int)mx;
   }
   return DR_OK;
 }
@@ -874,12 +899,9 @@ extern "C" int dr_rasterize_fwd_ex(const float* pos, int64_t pos_batch_stride, c
   TriRec* rec = (TriRec*)scratch_get(sc, stream, SLOT_RAST_REC, (size_t)n_rec * sizeof(TriRec));
   int4* rect = (int4*)scratch_get(sc, stream, SLOT_RAST_RECT, (size_t)n_rec * sizeof(int4));
   char* cbuf = (char*)scratch_get(sc, stream, SLOT_RAST_CNT, (size_t)n_tiles * 16);
-  unsigned long long* total =
-      (unsigned long long*)scratch_get(sc, stream, SLOT_SMALL, 64);
-  if (!rec || !rect || !cbuf || !total) return DR_ERR_MEMORY;
+  if (!rec || !rect || !cbuf) return DR_ERR_MEMORY;
   int* cnt = (int*)cbuf;
   int* fillc = cnt + n_tiles;
-  int* tmax = (int*)total;
 
   if (n_rec > 0) {
     DR_TIMED("k_setup", stream);
@@ -903,14 +925,11 @@ extern "C" int dr_rasterize_fwd_ex(const float* pos, int64_t pos_batch_stride, c
   }
   if (C == 0) {
     DR_CHECK_HIP(fill_async(cnt, 0, n_tiles, stream));
-    DR_CHECK_HIP(fill_async(tmax, 0, 1, stream));
     launch_binning(false, it, n_items, max_items, N, rect, ntx, tiles, cnt, nullptr, 0, stream);
     DR_CHECK_LAUNCH();
-    hipLaunchKernelGGL(k_tile_max, dim3(grid_for(n_tiles, 256)), dim3(256), 0, stream, cnt,
-                       n_tiles, tmax);
+    hipLaunchKernelGGL(k_tile_max, dim3(1), dim3(256), 0, stream, cnt, n_tiles,
+                       sc->pinned_total_dev);
     DR_CHECK_LAUNCH();
-    *sc->pinned_total = 0;
-    DR_CHECK_HIP(hipMemcpyAsync(sc->pinned_total, tmax, sizeof(int), hipMemcpyDeviceToHost, stream));
     DR_CHECK_HIP(hipStreamSynchronize(stream));
     C = grow(*sc->pinned_total);
   }
@@ -923,9 +942,7 @@ extern "C" int dr_rasterize_fwd_ex(const float* pos, int64_t pos_batch_stride, c
   int* list = (int*)scratch_get(sc, stream, SLOT_RAST_LIST, (size_t)n_tiles * C * 4);
   if (!list) return DR_ERR_MEMORY;
 
-  // fillc and the largest-count cell after it (cbuf holds 4 ints per tile)
-  int* fmax = fillc + n_tiles;
-  DR_CHECK_HIP(fill_async(fillc, 0, n_tiles + 1, stream));
+  DR_CHECK_HIP(fill_async(fillc, 0, n_tiles, stream));
   launch_binning(true, it, n_items, max_items, N, rect, ntx, tiles, fillc, list, C, stream);
   DR_CHECK_LAUNCH();
   const dim3 grid((unsigned)n_tiles), block(256);
@@ -949,12 +966,9 @@ extern "C" int dr_rasterize_fwd_ex(const float* pos, int64_t pos_batch_stride, c
 #undef DR_RASTER
   DR_CHECK_LAUNCH();
   if (!sc->total_pending) {  // largest count of this call, for the next one
-    hipLaunchKernelGGL(k_tile_max, dim3(grid_for(n_tiles, 256)), dim3(256), 0, stream, fillc,
-                       n_tiles, fmax);
+    hipLaunchKernelGGL(k_tile_max, dim3(1), dim3(256), 0, stream, fillc, n_tiles,
+                       sc->pinned_total_dev);
     DR_CHECK_LAUNCH();
-    *sc->pinned_total = 0;
-    DR_CHECK_HIP(hipMemcpyAsync(sc->pinned_total, fmax, sizeof(int), hipMemcpyDeviceToHost,
-                                stream));
     DR_CHECK_HIP(hipEventRecord(sc->total_event, stream));
     sc->total_pending = true;
   }

@@ -31,8 +31,10 @@ Scratch* scratch_for(hipStream_t stream) {
   if (it != g_scratch.end()) return it->second;
   Scratch* sc = new Scratch();
   if (hipHostMalloc((void**)&sc->pinned_total, sizeof(int64_t), hipHostMallocDefault) != hipSuccess ||
+      hipHostGetDevicePointer((void**)&sc->pinned_total_dev, sc->pinned_total, 0) != hipSuccess ||
       hipEventCreateWithFlags(&sc->total_event, hipEventDisableTiming) != hipSuccess) {
     set_error("scratch: pinned counter / event allocation failed");
+    if (sc->pinned_total) (void)hipHostFree(sc->pinned_total);
     delete sc;
     return nullptr;
   }
@@ -83,17 +85,29 @@ int64_t* stage_acquire(Scratch* sc, size_t n, int& slot) {
     return nullptr;
   }
   if (sc->stage_cap[slot] < n) {
-    if (sc->stage[slot]) (void)hipHostFree(sc->stage[slot]);
-    sc->stage[slot] = nullptr;
-    sc->stage_cap[slot] = 0;
+    // Pinned allocations may wait for the device: grow this buffer and every
+    // idle one that is also too small now, so that later calls of the same
+    // size allocate nothing (a buffer a queued copy may still read keeps
+    // its size until it is acquired).
     const size_t want = n + n / 4 + 64;
-    if (hipHostMalloc((void**)&sc->stage[slot], want * sizeof(int64_t), hipHostMallocDefault) !=
-        hipSuccess) {
-      (void)hipGetLastError();
-      set_error("range staging: pinned allocation failed");
-      return nullptr;
+    for (int r = 0; r < Scratch::kStageRing; ++r)  // copies that have run free their buffers
+      if (sc->stage_pending[r] && hipEventQuery(sc->stage_event[r]) == hipSuccess)
+        sc->stage_pending[r] = false;
+    (void)hipGetLastError();  // hipErrorNotReady of the queries
+    for (int r = 0; r < Scratch::kStageRing; ++r) {
+      if (r != slot && (sc->stage_pending[r] || sc->stage_cap[r] >= n)) continue;
+      if (sc->stage[r]) (void)hipHostFree(sc->stage[r]);
+      sc->stage[r] = nullptr;
+      sc->stage_cap[r] = 0;
+      if (hipHostMalloc((void**)&sc->stage[r], want * sizeof(int64_t), hipHostMallocDefault) !=
+          hipSuccess) {
+        (void)hipGetLastError();
+        if (r != slot) continue;  // only the acquired buffer must exist now
+        set_error("range staging: pinned allocation failed");
+        return nullptr;
+      }
+      sc->stage_cap[r] = want;
     }
-    sc->stage_cap[slot] = want;
   }
   return sc->stage[slot];
 }
