@@ -508,6 +508,21 @@ struct alignas(16) RBwdRec {
   float4 q0, q1, q2, q3;
 };
 
+// The record of one triangle from its clip-space vertices (ids valid).
+__device__ __forceinline__ RBwdRec rbwd_rec_of(float4 P0, float4 P1, float4 P2, int i0, int i1,
+                                               int i2) {
+  const float sx0 = P0.x / P0.w, sy0 = P0.y / P0.w, sz0 = P0.z / P0.w;
+  const float sx1 = P1.x / P1.w, sy1 = P1.y / P1.w, sz1 = P1.z / P1.w;
+  const float sx2 = P2.x / P2.w, sy2 = P2.y / P2.w, sz2 = P2.z / P2.w;
+  const float area = (sx1 - sx0) * (sy2 - sy0) - (sx2 - sx0) * (sy1 - sy0);
+  RBwdRec r;
+  r.q0 = make_float4(sx0, sy0, sx1, sy1);
+  r.q1 = make_float4(sx2, sy2, sz0, sz1);
+  r.q2 = make_float4(sz2, 1.0f / area, 1.0f / P0.w, 1.0f / P1.w);
+  r.q3 = make_float4(1.0f / P2.w, __int_as_float(i0), __int_as_float(i1), __int_as_float(i2));
+  return r;
+}
+
 __global__ void __launch_bounds__(256) k_rbwd_rec(const float* __restrict__ pos, int64_t pos_stride,
                                                   const int32_t* __restrict__ tri, int64_t NT,
                                                   int V, int T, RBwdRec* __restrict__ out) {
@@ -526,17 +541,11 @@ __global__ void __launch_bounds__(256) k_rbwd_rec(const float* __restrict__ pos,
       r[3] = make_float4(0.f, __int_as_float(-1), 0.f, 0.f);
     } else {
       const float* p = pos + n * pos_stride;
-      const float4 P0 = *reinterpret_cast<const float4*>(p + (int64_t)i0 * 4);
-      const float4 P1 = *reinterpret_cast<const float4*>(p + (int64_t)i1 * 4);
-      const float4 P2 = *reinterpret_cast<const float4*>(p + (int64_t)i2 * 4);
-      const float sx0 = P0.x / P0.w, sy0 = P0.y / P0.w, sz0 = P0.z / P0.w;
-      const float sx1 = P1.x / P1.w, sy1 = P1.y / P1.w, sz1 = P1.z / P1.w;
-      const float sx2 = P2.x / P2.w, sy2 = P2.y / P2.w, sz2 = P2.z / P2.w;
-      const float area = (sx1 - sx0) * (sy2 - sy0) - (sx2 - sx0) * (sy1 - sy0);
-      r[0] = make_float4(sx0, sy0, sx1, sy1);
-      r[1] = make_float4(sx2, sy2, sz0, sz1);
-      r[2] = make_float4(sz2, 1.0f / area, 1.0f / P0.w, 1.0f / P1.w);
-      r[3] = make_float4(1.0f / P2.w, __int_as_float(i0), __int_as_float(i1), __int_as_float(i2));
+      const RBwdRec q = rbwd_rec_of(*reinterpret_cast<const float4*>(p + (int64_t)i0 * 4),
+                                    *reinterpret_cast<const float4*>(p + (int64_t)i1 * 4),
+                                    *reinterpret_cast<const float4*>(p + (int64_t)i2 * 4), i0, i1,
+                                    i2);
+      r[0] = q.q0; r[1] = q.q1; r[2] = q.q2; r[3] = q.q3;
     }
   }
   __syncthreads();
@@ -548,14 +557,17 @@ __global__ void __launch_bounds__(256) k_rbwd_rec(const float* __restrict__ pos,
 // Rasterize.swift:637-812.  16x16 tiles, a 16x4 strip per wave; runs of
 // same-triangle lanes along a pixel row are summed before the LDS table
 // adds the 12 d_pos terms; the table is written out into an fp64
-// accumulator laid out as pos.  A covered pixel loads its triangle's
+// accumulator laid out as pos.  REC: a covered pixel loads its triangle's
 // record (k_rbwd_rec) together with its cotangents, one round trip after
-// its rast value.
+// its rast value; else it gathers tri -> pos and builds the same record
+// itself (cheaper when triangles cover few pixels each: the records of
+// every (image, triangle) then cost more to write than they save).
+template <bool REC>
 __global__ void __launch_bounds__(256) k_raster_bwd(
-    const RBwdRec* __restrict__ trec, int64_t rec_stride, int64_t pos_stride,
-    const float* __restrict__ rast, const float* __restrict__ d_rast,
-    const float* __restrict__ d_rast_db, int N, int T, int H, int W, int ntx, int nty,
-    double* __restrict__ d_pos) {
+    const RBwdRec* __restrict__ trec, int64_t rec_stride, const float* __restrict__ pos,
+    int64_t pos_stride, const int32_t* __restrict__ tri, int V, const float* __restrict__ rast,
+    const float* __restrict__ d_rast, const float* __restrict__ d_rast_db, int N, int T, int H,
+    int W, int ntx, int nty, double* __restrict__ d_pos) {
   __shared__ LdsTable<4, 256> tab;  // d_pos rows touched by this tile
   __shared__ int s_any[4];          // per wave: a covered pixel
   const int tiles = ntx * nty;
@@ -577,7 +589,7 @@ __global__ void __launch_bounds__(256) k_raster_bwd(
   RBwdRec R;
   float4 dr = make_float4(0.f, 0.f, 0.f, 0.f), ddb = dr;
   if (valid) {
-    R = trec[(int64_t)n * rec_stride + t];
+    if (REC) R = trec[(int64_t)n * rec_stride + t];
     dr = *reinterpret_cast<const float4*>(d_rast + pix * 4);
     if (d_rast_db) ddb = *reinterpret_cast<const float4*>(d_rast_db + pix * 4);
   }
@@ -594,6 +606,17 @@ __global__ void __launch_bounds__(256) k_raster_bwd(
 #pragma unroll
   for (int q = 0; q < 12; ++q) val[q] = 0.0f;
   double* dp = d_pos + (int64_t)n * pos_stride;
+  if (valid && !REC) {
+    const int j0 = tri[t * 3 + 0], j1 = tri[t * 3 + 1], j2 = tri[t * 3 + 2];
+    if (verts_ok(j0, j1, j2, V)) {
+      const float* p = pos + (int64_t)n * pos_stride;
+      R = rbwd_rec_of(*reinterpret_cast<const float4*>(p + (int64_t)j0 * 4),
+                      *reinterpret_cast<const float4*>(p + (int64_t)j1 * 4),
+                      *reinterpret_cast<const float4*>(p + (int64_t)j2 * 4), j0, j1, j2);
+    } else {
+      R.q3.y = __int_as_float(-1);
+    }
+  }
   if (valid) {
     i0 = __float_as_int(R.q3.y);
     i1 = __float_as_int(R.q3.z);
@@ -991,14 +1014,16 @@ extern "C" int dr_rasterize_bwd(const float* pos, int64_t pos_batch_stride, cons
   if (!acc) return DR_ERR_MEMORY;
   const int ntx = (W + kTile - 1) / kTile, nty = (H + kTile - 1) / kTile;
   const int64_t blocks = (int64_t)N * ntx * nty;
-  // per (image, triangle) records; one set for all images when pos is shared
+  // per (image, triangle) records (one set for all images when pos is
+  // shared), when the triangles average at least 8 pixels of the images
   const int64_t nrec = (pos_batch_stride ? (int64_t)N : 1) * T;
-  Scratch* sc = scratch_for(stream);
-  if (!sc) return DR_ERR_HIP;
-  RBwdRec* trec = (RBwdRec*)scratch_get(sc, stream, SLOT_RBWD_REC,
-                                        (size_t)std::max<int64_t>(nrec, 1) * sizeof(RBwdRec));
-  if (!trec) return DR_ERR_MEMORY;
-  if (nrec > 0) {
+  const bool use_rec = nrec > 0 && nrec * 8 <= (int64_t)N * H * W;
+  RBwdRec* trec = nullptr;
+  if (use_rec) {
+    Scratch* sc = scratch_for(stream);
+    if (!sc) return DR_ERR_HIP;
+    trec = (RBwdRec*)scratch_get(sc, stream, SLOT_RBWD_REC, (size_t)nrec * sizeof(RBwdRec));
+    if (!trec) return DR_ERR_MEMORY;
     DR_TIMED("k_rbwd_rec", stream);
     hipLaunchKernelGGL(k_rbwd_rec, dim3((unsigned)((nrec + 255) / 256)), dim3(256), 0, stream,
                        pos, pos_batch_stride, tri, nrec, V, T, trec);
@@ -1006,9 +1031,15 @@ extern "C" int dr_rasterize_bwd(const float* pos, int64_t pos_batch_stride, cons
   DR_CHECK_LAUNCH();
   {
     DR_TIMED("k_raster_bwd", stream);
-    hipLaunchKernelGGL(k_raster_bwd, dim3((unsigned)blocks), dim3(256), 0, stream, trec,
-                       pos_batch_stride ? (int64_t)T : (int64_t)0, pos_batch_stride, rast, d_rast,
-                       d_rast_db, N, T, H, W, ntx, nty, acc);
+    const int64_t rs = pos_batch_stride ? (int64_t)T : (int64_t)0;
+    if (use_rec)
+      hipLaunchKernelGGL(k_raster_bwd<true>, dim3((unsigned)blocks), dim3(256), 0, stream, trec,
+                         rs, pos, pos_batch_stride, tri, V, rast, d_rast, d_rast_db, N, T, H, W,
+                         ntx, nty, acc);
+    else
+      hipLaunchKernelGGL(k_raster_bwd<false>, dim3((unsigned)blocks), dim3(256), 0, stream, trec,
+                         rs, pos, pos_batch_stride, tri, V, rast, d_rast, d_rast_db, N, T, H, W,
+                         ntx, nty, acc);
   }
   DR_CHECK_LAUNCH();
   return acc64_end(acc, d_pos, npos, (flags & DR_ACCUMULATE) != 0, stream);
