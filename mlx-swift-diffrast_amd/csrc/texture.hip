@@ -781,10 +781,27 @@ __global__ void __launch_bounds__(kWinThreads, 5) k_tex_bwd_win(TexBwdArgs A, in
   const int tiles = A.ntx * A.nty;
 
   int it = 0;
-  for (int bt = (int)blockIdx.x; bt < total_tiles; bt += (int)gridDim.x, ++it) {
-    const int n = bt / tiles;
-    const int tile = bt - n * tiles;
-    const int ty = tile / A.ntx, tx = tile - ty * A.ntx;
+  // the tile's (n, ty, tx), advanced by the grid stride each step (scalar
+  // adds; a division only when the stride crosses an image)
+  const int G = (int)gridDim.x;
+  const int Gy = G / A.ntx, Gx = G - Gy * A.ntx;
+  int n = (int)blockIdx.x / tiles;
+  int ty = ((int)blockIdx.x - n * tiles) / A.ntx;
+  int tx = (int)blockIdx.x - n * tiles - ty * A.ntx;
+  for (int bt = (int)blockIdx.x; bt < total_tiles; bt += G, ++it) {
+    if (it > 0) {
+      tx += Gx;
+      ty += Gy;
+      if (tx >= A.ntx) {
+        tx -= A.ntx;
+        ++ty;
+      }
+      if (ty >= A.nty) {
+        const int q = ty / A.nty;
+        n += q;
+        ty -= q * A.nty;
+      }
+    }
     const int pw = tx * 16 + (lane & 15);  // 16x4 strip per wave, one pixel row per 16 lanes
     const int ph = ty * (4 * kWinWaves) + wave * 4 + (lane >> 4);
     const bool valid = pw < A.Wi && ph < A.Hi;
@@ -987,9 +1004,14 @@ __global__ void __launch_bounds__(kWinThreads, 5) k_tex_bwd_win(TexBwdArgs A, in
     }
     __syncthreads();
     if (tid == 0) s_tab_used[par ^ 1] = 0;  // read by every thread before the last barrier
-    int ka = s_wk[0];
+    // the window selection is uniform: its LDS inputs go to scalar registers
+    auto su = [](int x) { return __builtin_amdgcn_readfirstlane(x); };
+    int wk[kWinWaves];
 #pragma unroll
-    for (int v = 1; v < kWinWaves; ++v) ka = min(ka, s_wk[v]);
+    for (int v = 0; v < kWinWaves; ++v) wk[v] = su(s_wk[v]);
+    int ka = wk[0];
+#pragma unroll
+    for (int v = 1; v < kWinWaves; ++v) ka = min(ka, wk[v]);
     int wsel[2];
 #pragma unroll
     for (int li = 0; li < 2; ++li) {
@@ -1004,11 +1026,11 @@ __global__ void __launch_bounds__(kWinThreads, 5) k_tex_bwd_win(TexBwdArgs A, in
       int x0 = 0x7fffffff, x1 = -1, y0 = 0x7fffffff, y1 = -1;
 #pragma unroll
       for (int v = 0; v < kWinWaves; ++v) {
-        const int kv = s_wk[v];
+        const int kv = wk[v];
         const int j = w - (kv - ka);  // wave v's box j lies on level ka + w
         if (kv == 0x7fffffff || j < 0 || j > 1) continue;
-        x0 = min(x0, s_wbox[v][j][0]); x1 = max(x1, s_wbox[v][j][1]);
-        y0 = min(y0, s_wbox[v][j][2]); y1 = max(y1, s_wbox[v][j][3]);
+        x0 = min(x0, su(s_wbox[v][j][0])); x1 = max(x1, su(s_wbox[v][j][1]));
+        y0 = min(y0, su(s_wbox[v][j][2])); y1 = max(y1, su(s_wbox[v][j][3]));
       }
       bx0[w] = x0;
       by0[w] = y0;
@@ -1029,7 +1051,6 @@ __global__ void __launch_bounds__(kWinThreads, 5) k_tex_bwd_win(TexBwdArgs A, in
     for (int li = 0; li < 2; ++li) {
       const int w = wsel[li];
       if (__ballot(w != -2) == 0) continue;  // no lane uses this slot (uniform)
-      const float wt[4] = {q[li].w00, q[li].w10, q[li].w01, q[li].w11};
       const float sc = mip ? q[li].scale : 1.0f;
       // level and the four texel coordinates (each < 32767 on the window
       // path) fix the taps; an unused slot gets a key no footprint has
@@ -1041,25 +1062,47 @@ __global__ void __launch_bounds__(kWinThreads, 5) k_tex_bwd_win(TexBwdArgs A, in
       const int maxlen = wave_max(run.li - run.s + 1);  // longest run in the wave
       const bool adds = w != -2 && run.tail;
       const bool in_win = w >= 0 && usable[w];
-      double* wb = win + (w >= 0 ? wbase[w] : 0);
-      float* base = dlevel_ptr(q[li].k);
-      const int Wk = mip_w(md, q[li].k);
-      if (adds && !in_win) s_tab_used[par] = 1;
+      // the 16 values (tap-major) of the footprint, then one segmented scan
+      // over all of them
+      const float wt[4] = {q[li].w00, q[li].w10, q[li].w01, q[li].w11};
+      float gs[CT];
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        float v[CT];
+      for (int c = 0; c < CT; ++c) gs[c] = w == -2 ? 0.0f : g[c] * sc;
+      float v[4 * CT];
 #pragma unroll
-        for (int c = 0; c < CT; ++c) v[c] = w == -2 ? 0.0f : wt[t] * (g[c] * sc);
-        row_run_scan_n(run, v, maxlen);
-        if (!adds) continue;
-        const int tx_ = (t & 1) ? q[li].ix1 : q[li].ix0;
-        const int ty_ = (t & 2) ? q[li].iy1 : q[li].iy0;
-        if (in_win) {
-          const int o = (ty_ - by0[w]) * bw[w] + (tx_ - bx0[w]);  // < area[w]
+      for (int t = 0; t < 4; ++t)
 #pragma unroll
-          for (int c = 0; c < CT; ++c) atomicAdd(wb + c * kWinTexels + o, (double)v[c]);
-        } else {
-          lds_table_add(tab, base + (ty_ * Wk + tx_) * CT, v);
+        for (int c = 0; c < CT; ++c) v[t * CT + c] = wt[t] * gs[c];
+      row_run_scan_n(run, v, maxlen);
+      if (adds && in_win) {
+        // window indices of the four taps.  The box holds every tap with a
+        // nonzero weight in some lane of the run; a tap whose weight is zero
+        // in all of them (a texel column or row with zero weight, outside
+        // the image for the zero boundary) may lie outside it, and its
+        // coordinates are clamped into the box, where it adds 0.
+        const int wx = w == 0 ? bx0[0] : bx0[1], wy = w == 0 ? by0[0] : by0[1];
+        const int ww = w == 0 ? bw[0] : bw[1], wh = w == 0 ? bh[0] : bh[1];
+        const int wo = w == 0 ? wbase[0] : wbase[1];
+        const int cx0 = min(max(q[li].ix0 - wx, 0), ww - 1);
+        const int cx1 = min(max(q[li].ix1 - wx, 0), ww - 1);
+        const int r0 = wo + min(max(q[li].iy0 - wy, 0), wh - 1) * ww;
+        const int r1 = wo + min(max(q[li].iy1 - wy, 0), wh - 1) * ww;
+        const int o[4] = {r0 + cx0, r0 + cx1, r1 + cx0, r1 + cx1};  // < wo + area[w]
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int c = 0; c < CT; ++c)
+            atomicAdd(win + c * kWinTexels + o[t], (double)v[t * CT + c]);
+      }
+      if (adds && !in_win) {  // other levels, or boxes too large for a window
+        s_tab_used[par] = 1;
+        float* base = dlevel_ptr(q[li].k);
+        const int Wk = mip_w(md, q[li].k);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const int tx_ = (t & 1) ? q[li].ix1 : q[li].ix0;
+          const int ty_ = (t & 2) ? q[li].iy1 : q[li].iy0;
+          lds_table_add(tab, base + (ty_ * Wk + tx_) * CT, &v[t * CT]);
         }
       }
     }
@@ -1077,15 +1120,23 @@ __global__ void __launch_bounds__(kWinThreads, 5) k_tex_bwd_win(TexBwdArgs A, in
       const int total = row * bh[w];
       double* wb = win + wbase[w];
       // consecutive lanes take consecutive channels of a texel, so the
-      // device atomics of a row share cache lines
+      // device atomics of a row share cache lines; (r, cpos) of element i
+      // advance by a uniform step instead of a division per element
+      const int dr = kWinThreads / row, dc = kWinThreads - dr * row;
+      int r = tid / row, cpos = tid - r * row;
       for (int i = tid; i < total; i += kWinThreads) {
-        const int r = i / row, cpos = i - r * row;
         const int tx = cpos / CT, c = cpos - tx * CT;
         double* e = wb + c * kWinTexels + r * bw[w] + tx;
         const double v = *e;
         if (v != 0.0) {
           unsafeAtomicAdd(base + ((by0[w] + r) * Wk + bx0[w]) * CT + cpos, (float)v);
           *e = 0.0;
+        }
+        r += dr;
+        cpos += dc;
+        if (cpos >= row) {
+          cpos -= row;
+          ++r;
         }
       }
     }
