@@ -854,6 +854,13 @@ __global__ void __launch_bounds__(kWinThreads, 5) k_tex_bwd_win(TexBwdArgs A, in
     float dfx_total = 0.0f, dfy_total = 0.0f, samp[2] = {0.0f, 0.0f};
 #pragma unroll
     for (int li = 0; li < 2; ++li) {
+      if (li == 1 && !__ballot(valid && (q[1].scale != 0.0f || need1))) {
+        // no lane weights or samples the second level (magnified and
+        // background waves): its footprint would only be discarded
+        q[1].ix0 = q[1].ix1 = q[1].iy0 = q[1].iy1 = 0;
+        q[1].w00 = q[1].w10 = q[1].w01 = q[1].w11 = 0.0f;
+        continue;
+      }
       const int k = q[li].k, Hk = mip_h(md, k), Wk = mip_w(md, k);
       const Bilin b = bilin(uvp.x, uvp.y, Wk, Hk, BND);
       float w00 = b.w00, w10 = b.w10, w01 = b.w01, w11 = b.w11;
