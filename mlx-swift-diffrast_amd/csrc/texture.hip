@@ -987,8 +987,9 @@ __global__ void __launch_bounds__(kWinThreads, 5) k_tex_bwd_win(TexBwdArgs A, in
       if (use0) kmin = q[0].k;
       if (use1) kmin = min(kmin, q[1].k);
       const int kw = wave_min(kmin);
+      // (a wave with no slot in use, kw = INT_MAX, leaves its boxes unread)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
+      for (int j = 0; j < 2 && kw != 0x7fffffff; ++j) {
         // texel coordinates fit in 16 bits (window path needs sizes <= 32767):
         // (x0, -x1) and (y0, -y1) are reduced as packed 16-bit minima
         int x0 = 32767, x1 = -32767, y0 = 32767, y1 = -32767;
@@ -1000,7 +1001,11 @@ __global__ void __launch_bounds__(kWinThreads, 5) k_tex_bwd_win(TexBwdArgs A, in
           slot_box(q[li], a0, a1, b0, b1);
           x0 = min(x0, a0); x1 = max(x1, a1); y0 = min(y0, b0); y1 = max(y1, b1);
         }
-        const int px = wave_min_pk16(pack16(x0, -x1)), py = wave_min_pk16(pack16(y0, -y1));
+        int px = pack16(32767, 32767), py = px;  // an empty box
+        if (__ballot(x1 >= 0)) {  // some lane has a slot on this level
+          px = wave_min_pk16(pack16(x0, -x1));
+          py = wave_min_pk16(pack16(y0, -y1));
+        }
         if (lane == 0) {
           const int X1 = -unpack16_hi(px), Y1 = -unpack16_hi(py);
           s_wbox[wave][j][0] = unpack16_lo(px); s_wbox[wave][j][1] = X1 < 0 ? -1 : X1;
