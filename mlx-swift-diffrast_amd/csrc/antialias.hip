@@ -249,6 +249,12 @@ __device__ __forceinline__ bool sil_geom(const AARec& R, int target, int ph, int
   return true;
 }
 
+// LDS row strides of the tile arrays: a wave's 8x8 quadrant reaches LDS 32
+// lanes (four rows of eight) at a time, and a row stride of 8 mod 32 words
+// puts those four rows on disjoint banks.
+constexpr int kTriRow = 40;    // s_tri[18][kTriRow]: 18 used
+constexpr int kAlphaRow = 24;  // s_alpha[4][16][kAlphaRow]: 16 used
+
 // Triangle ids of a 16x16 tile and its 1-pixel border (corners unused).
 // kOut marks a neighbour outside the image; ids outside [0, T) read as empty.
 constexpr int kOut = -2;
@@ -310,7 +316,7 @@ __device__ __forceinline__ AABorder aa_border(const AATile& g, int H, int W) {
 // kernels issue these rast loads together with their other per-pixel loads
 // and store afterwards, so the loads share one round trip.
 __device__ __forceinline__ void aa_store_ids(const AATile& g, const AABorder& bd, float own_w,
-                                             float border_w, int T, int (*s_tri)[18]) {
+                                             float border_w, int T, int (*s_tri)[kTriRow]) {
   s_tri[g.ly + 1][g.lx + 1] = g.inside ? aa_id(own_w, T) : kOut;
   if (bd.lane) s_tri[bd.r][bd.c] = bd.in ? aa_id(border_w, T) : kOut;
 }
@@ -327,7 +333,7 @@ __device__ __forceinline__ int64_t mask_index(int n, int h, int w, int ntx, int 
 
 // Neighbour of tile cell (r, c) (1-based, border included) in direction d:
 // 0 = +w, 1 = +h, 2 = -w, 3 = -h.
-__device__ __forceinline__ int aa_nb(int (*s_tri)[18], int r, int c, int d) {
+__device__ __forceinline__ int aa_nb(int (*s_tri)[kTriRow], int r, int c, int d) {
   return d == 0 ? s_tri[r][c + 1] : d == 1 ? s_tri[r + 1][c] : d == 2 ? s_tri[r][c - 1]
                                                                       : s_tri[r - 1][c];
 }
@@ -379,7 +385,7 @@ __global__ void __launch_bounds__(256) k_aa_fwd(const float* __restrict__ rast,
                                                 int T, int C, int ntx, int nty,
                                                 float* __restrict__ out,
                                                 uint8_t* __restrict__ blend_mask) {
-  __shared__ int s_tri[18][18];
+  __shared__ int s_tri[18][kTriRow];
   // colours of the tile and its border (CT > 0), so a blend reads its
   // neighbour from LDS rather than in a third global round trip
   __shared__ __align__(16) float s_col[18][18][CT > 0 ? CT : 1];
@@ -543,8 +549,8 @@ __global__ void __launch_bounds__(256) k_aa_bwd(const float* __restrict__ rast,
                                                 int V, int T, int C, int ntx, int nty,
                                                 float* __restrict__ d_color,
                                                 double* __restrict__ d_pos, int accumulate) {
-  __shared__ int s_tri[18][18];
-  __shared__ float s_alpha[4][16][17];
+  __shared__ int s_tri[18][kTriRow];
+  __shared__ float s_alpha[4][16][kAlphaRow];
   __shared__ float s_halo[4][16];
   __shared__ LdsTable<4, 128> tab;  // d_pos rows touched by this tile
   __shared__ PosItem s_q[kPosQueue];
@@ -719,7 +725,7 @@ struct AAPairIn {
 };
 
 template <int CT>
-__device__ __forceinline__ void aa_pair_load(int e, int (*s_tri)[18], const AATile& g, int H,
+__device__ __forceinline__ void aa_pair_load(int e, int (*s_tri)[kTriRow], const AATile& g, int H,
                                              int W, const AARec* __restrict__ recn,
                                              const AAPersp* __restrict__ perspn,
                                              const float* __restrict__ color, bool want_pos,
@@ -757,7 +763,7 @@ __device__ __forceinline__ void aa_pair_load(int e, int (*s_tri)[18], const AATi
 // for the tile's own pixels, its d_pos terms.
 template <int CT>
 __device__ __forceinline__ void aa_pair_eval(const AAPairIn<CT>& P, const AATile& g, int H, int W,
-                                             int C, float (*s_alpha)[16][17],
+                                             int C, float (*s_alpha)[16][kAlphaRow],
                                              float (*s_halo)[16],
                                              const float (*s_g)[CT > 0 ? CT : 1],
                                              const float* __restrict__ color,
@@ -812,8 +818,8 @@ __global__ void __launch_bounds__(256) k_aa_bwd_masked(
     int accumulate) {
   constexpr int CS = CT > 0 ? CT : 1;
   constexpr int kCells = CT > 0 ? 18 * 18 : 1;
-  __shared__ int s_tri[18][18];
-  __shared__ float s_alpha[4][16][17];
+  __shared__ int s_tri[18][kTriRow];
+  __shared__ float s_alpha[4][16][kAlphaRow];
   __shared__ float s_halo[4][16];
   __shared__ LdsTable<4, 128> tab;       // d_pos rows touched by this tile
   __shared__ uint16_t s_q[kMaskQueue];   // (cell r * 18 + c) << 2 | direction
