@@ -145,6 +145,22 @@ int dr_rasterize_fwd_ex(const float* pos, int64_t pos_batch_stride, const int32_
                         int H, int W, float* rast, float* rast_db, int max_per_tile,
                         dr_stream_t stream);
 
+/* dr_rasterize_fwd_ex for the next layer of a depth peel, or any call that
+ * rasterizes the same triangles again (no counterpart call in the
+ * reference, whose chained peel calls repeat their triangle setup and tile
+ * binning, Rasterize.swift:36-38, 90-135).  When pos, pos_batch_stride,
+ * tri, the contents of ranges_host, N, V, T, H, W and max_per_tile equal
+ * those of the previous dr_rasterize_fwd / _ex / _again call on this
+ * stream, that call's setup and tile lists are reused and only the
+ * coverage pass runs; otherwise, or after a dr_rasterize_tile_counts call
+ * on the stream, it does the full work of dr_rasterize_fwd_ex.  The caller
+ * guarantees that the contents of pos and tri have not changed since that
+ * call.  Results equal dr_rasterize_fwd_ex's. */
+int dr_rasterize_fwd_again(const float* pos, int64_t pos_batch_stride, const int32_t* tri,
+                           const int32_t* ranges_host, const float* peel, int N, int V, int T,
+                           int H, int W, float* rast, float* rast_db, int max_per_tile,
+                           dr_stream_t stream);
+
 /* Binning report (no counterpart call in the reference; it exposes the
  * reference's bin counts, Rasterize.swift:227-239).  counts [N, ceil(H/16),
  * ceil(W/16)] (device int32) receives, per 16x16 tile, the number of drawn

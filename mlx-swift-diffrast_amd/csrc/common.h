@@ -2,6 +2,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <vector>
 #include <stdint.h>
 
 #include <string>
@@ -81,6 +82,18 @@ struct Scratch {
   // counts the leading elements of buffer acc64_buf known to be zero.
   const void* acc64_buf = nullptr;
   int64_t acc64_zero = 0;
+  // The previous dr_rasterize_fwd* call on this stream, whose triangle
+  // setup and tile lists (SLOT_RAST_*) dr_rasterize_fwd_again may reuse.
+  struct {
+    bool valid = false;
+    const float* pos = nullptr;
+    const int32_t* tri = nullptr;
+    int64_t pos_stride = 0;
+    int N = 0, V = 0, T = 0, H = 0, W = 0, max_per_tile = 0, C = 0;
+    bool range = false;
+    std::vector<int32_t> ranges;
+    int64_t n_items = 0, max_items = 0;
+  } last_raster;
 };
 
 // A pinned host buffer of the range-mode staging ring holding at least

@@ -848,6 +848,7 @@ extern "C" int dr_rasterize_tile_counts(const float* pos, int64_t pos_batch_stri
   DR_CHECK_ARG(counts, "rasterize_tile_counts: null counts");
   Scratch* sc = scratch_for(stream);
   if (!sc) return DR_ERR_HIP;
+  sc->last_raster.valid = false;  // its setup and item buffers are rewritten here
   const int ntx = (W + kTile - 1) / kTile, nty = (H + kTile - 1) / kTile;
   const int tiles = ntx * nty;
   const int64_t n_tiles = (int64_t)N * tiles;
@@ -893,11 +894,12 @@ extern "C" int dr_rasterize_fwd(const float* pos, int64_t pos_batch_stride, cons
                              rast_db, 0, stream_);
 }
 
-extern "C" int dr_rasterize_fwd_ex(const float* pos, int64_t pos_batch_stride, const int32_t* tri,
-                                   const int32_t* ranges_host, const float* peel, int N, int V,
-                                   int T, int H, int W, float* rast, float* rast_db,
-                                   int max_per_tile, dr_stream_t stream_) {
-  hipStream_t stream = (hipStream_t)stream_;
+// The forward; `again`: reuse the previous call's triangle setup and tile
+// lists when its arguments match (dr_rasterize_fwd_again).
+static int raster_fwd(const float* pos, int64_t pos_batch_stride, const int32_t* tri,
+                      const int32_t* ranges_host, const float* peel, int N, int V, int T, int H,
+                      int W, float* rast, float* rast_db, int max_per_tile, bool again,
+                      hipStream_t stream) {
   int st = check_raster_args(pos, pos_batch_stride, tri, ranges_host, N, V, T, H, W);
   if (st) return st;
   DR_CHECK_ARG(rast, "rasterize: null tensor");
@@ -910,21 +912,47 @@ extern "C" int dr_rasterize_fwd_ex(const float* pos, int64_t pos_batch_stride, c
   const int tiles = ntx * nty;
   const int64_t n_tiles = (int64_t)N * tiles;
 
-  // Items: which (image, triangle) pairs are drawn.
-  Items it;
-  int64_t n_items = 0, max_items = 0;
-  st = plan_items(sc, stream, ranges_host, N, T, it, n_items, max_items);
-  if (st) return st;
   const int Npos = ranges_host ? 1 : N;
   const int64_t n_rec = (int64_t)Npos * T;
   const int64_t rec_stride = ranges_host ? 0 : T;
+  auto& L = sc->last_raster;
+  const bool reuse =
+      again && L.valid && L.pos == pos && L.tri == tri && L.pos_stride == pos_batch_stride &&
+      L.N == N && L.V == V && L.T == T && L.H == H && L.W == W &&
+      L.max_per_tile == max_per_tile && L.range == (ranges_host != nullptr) &&
+      (!ranges_host || std::equal(L.ranges.begin(), L.ranges.end(), ranges_host));
 
-  TriRec* rec = (TriRec*)scratch_get(sc, stream, SLOT_RAST_REC, (size_t)n_rec * sizeof(TriRec));
-  int4* rect = (int4*)scratch_get(sc, stream, SLOT_RAST_RECT, (size_t)n_rec * sizeof(int4));
+  // Items: which (image, triangle) pairs are drawn.
+  Items it{nullptr, nullptr, T};
+  int64_t n_items = 0, max_items = 0;
+  TriRec* rec;
+  int4* rect;
+  int* fillc;
+  int* list;
+  int C;
+  if (reuse) {  // the previous call's setup and lists, untouched since
+    if (ranges_host) {
+      int64_t* d = (int64_t*)sc->ptr[SLOT_RAST_ITEMS];
+      it.prefix = d;
+      it.start = d + N + 1;
+    }
+    n_items = L.n_items;
+    max_items = L.max_items;
+    C = L.C;
+    rec = (TriRec*)sc->ptr[SLOT_RAST_REC];
+    rect = (int4*)sc->ptr[SLOT_RAST_RECT];
+    fillc = (int*)sc->ptr[SLOT_RAST_CNT] + n_tiles;
+    list = (int*)sc->ptr[SLOT_RAST_LIST];
+  } else {
+  L.valid = false;
+  st = plan_items(sc, stream, ranges_host, N, T, it, n_items, max_items);
+  if (st) return st;
+  rec = (TriRec*)scratch_get(sc, stream, SLOT_RAST_REC, (size_t)n_rec * sizeof(TriRec));
+  rect = (int4*)scratch_get(sc, stream, SLOT_RAST_RECT, (size_t)n_rec * sizeof(int4));
   char* cbuf = (char*)scratch_get(sc, stream, SLOT_RAST_CNT, (size_t)n_tiles * 16);
   if (!rec || !rect || !cbuf) return DR_ERR_MEMORY;
   int* cnt = (int*)cbuf;
-  int* fillc = cnt + n_tiles;
+  fillc = cnt + n_tiles;
 
   if (n_rec > 0) {
     DR_TIMED("k_setup", stream);
@@ -940,7 +968,7 @@ extern "C" int dr_rasterize_fwd_ex(const float* pos, int64_t pos_batch_stride, c
   // memory, only ever raises it, and a tile that overflows is rasterized by
   // a full scan, so results never depend on the capacity.
   auto grow = [](int64_t m) { return (int)std::min<int64_t>(((m + m / 4) + 31) / 32 * 32 + 32, 1 << 30); };
-  int C = sc->bin_cap;
+  C = sc->bin_cap;
   if (sc->total_pending && hipEventQuery(sc->total_event) == hipSuccess) {
     const int64_t mx = *sc->pinned_total;
     sc->total_pending = false;
@@ -962,12 +990,13 @@ extern "C" int dr_rasterize_fwd_ex(const float* pos, int64_t pos_batch_stride, c
   const int64_t c_budget = std::max<int64_t>(32, ((int64_t)1 << 30) / std::max<int64_t>(n_tiles, 1));
   C = (int)std::min<int64_t>(C, c_budget);
   if (C > sc->bin_cap) sc->bin_cap = C;
-  int* list = (int*)scratch_get(sc, stream, SLOT_RAST_LIST, (size_t)n_tiles * C * 4);
+  list = (int*)scratch_get(sc, stream, SLOT_RAST_LIST, (size_t)n_tiles * C * 4);
   if (!list) return DR_ERR_MEMORY;
 
   DR_CHECK_HIP(fill_async(fillc, 0, n_tiles, stream));
   launch_binning(true, it, n_items, max_items, N, rect, ntx, tiles, fillc, list, C, stream);
   DR_CHECK_LAUNCH();
+  }
   const dim3 grid((unsigned)n_tiles), block(256);
 #define DR_RASTER(DBV, PV, CV)                                                                    \
   hipLaunchKernelGGL((k_raster<DBV, PV, CV>), grid, block, 0, stream, rec, rect, it, rec_stride, \
@@ -988,6 +1017,7 @@ extern "C" int dr_rasterize_fwd_ex(const float* pos, int64_t pos_batch_stride, c
 #undef DR_RASTER_C
 #undef DR_RASTER
   DR_CHECK_LAUNCH();
+  if (reuse) return DR_OK;
   if (!sc->total_pending) {  // largest count of this call, for the next one
     hipLaunchKernelGGL(k_tile_max, dim3(1), dim3(256), 0, stream, fillc, n_tiles,
                        sc->pinned_total_dev);
@@ -995,8 +1025,37 @@ extern "C" int dr_rasterize_fwd_ex(const float* pos, int64_t pos_batch_stride, c
     DR_CHECK_HIP(hipEventRecord(sc->total_event, stream));
     sc->total_pending = true;
   }
+  L.pos = pos;
+  L.tri = tri;
+  L.pos_stride = pos_batch_stride;
+  L.N = N; L.V = V; L.T = T; L.H = H; L.W = W;
+  L.max_per_tile = max_per_tile;
+  L.range = ranges_host != nullptr;
+  L.ranges.assign(ranges_host ? ranges_host : nullptr, ranges_host ? ranges_host + 2 * N : nullptr);
+  L.n_items = n_items;
+  L.max_items = max_items;
+  L.C = C;
+  L.valid = true;
   return DR_OK;
 }
+
+extern "C" int dr_rasterize_fwd_ex(const float* pos, int64_t pos_batch_stride, const int32_t* tri,
+                                   const int32_t* ranges_host, const float* peel, int N, int V,
+                                   int T, int H, int W, float* rast, float* rast_db,
+                                   int max_per_tile, dr_stream_t stream) {
+  return raster_fwd(pos, pos_batch_stride, tri, ranges_host, peel, N, V, T, H, W, rast, rast_db,
+                    max_per_tile, false, (hipStream_t)stream);
+}
+
+extern "C" int dr_rasterize_fwd_again(const float* pos, int64_t pos_batch_stride,
+                                      const int32_t* tri, const int32_t* ranges_host,
+                                      const float* peel, int N, int V, int T, int H, int W,
+                                      float* rast, float* rast_db, int max_per_tile,
+                                      dr_stream_t stream) {
+  return raster_fwd(pos, pos_batch_stride, tri, ranges_host, peel, N, V, T, H, W, rast, rast_db,
+                    max_per_tile, true, (hipStream_t)stream);
+}
+
 
 extern "C" int dr_rasterize_bwd(const float* pos, int64_t pos_batch_stride, const int32_t* tri,
                                 const float* rast, const float* d_rast, const float* d_rast_db,

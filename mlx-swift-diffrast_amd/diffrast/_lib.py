@@ -28,6 +28,7 @@ SIGNATURES = {
     "dr_profile_report": ([ctypes.c_char_p, _i], _i),
     "dr_rasterize_fwd": ([_p, _i64, _p, _p, _p, _i, _i, _i, _i, _i, _p, _p, _p], _i),
     "dr_rasterize_fwd_ex": ([_p, _i64, _p, _p, _p, _i, _i, _i, _i, _i, _p, _p, _i, _p], _i),
+    "dr_rasterize_fwd_again": ([_p, _i64, _p, _p, _p, _i, _i, _i, _i, _i, _p, _p, _i, _p], _i),
     "dr_rasterize_tile_counts": ([_p, _i64, _p, _p, _i, _i, _i, _i, _i, _p, _p, _p], _i),
     "dr_rasterize_bwd": ([_p, _i64, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p, _u, _p], _i),
     "dr_interpolate_fwd": ([_p, _i64, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i, _p, _p, _p],

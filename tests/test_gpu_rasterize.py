@@ -371,3 +371,111 @@ def test_range_mode_does_not_wait():
     assert waited == 0
     rr, _ = O.rasterize(sc["pos"], sc["tri"], (48, 40), ranges=sc["ranges"], max_per_tile=0)
     np.testing.assert_array_equal(host(r), rr)
+
+
+def _setup_launches(fn):
+    """fn() with the library's launch timing on: how many triangle-setup
+    passes (k_setup) it ran."""
+    import diffrast._lib as L
+    import torch
+    lib = L.load()
+    torch.cuda.synchronize()
+    lib.dr_profile_reset()
+    lib.dr_profile_enable(1)
+    try:
+        fn()
+        torch.cuda.synchronize()
+    finally:
+        lib.dr_profile_enable(0)
+    return L.profile_report().get("k_setup", {}).get("count", 0)
+
+
+@pytest.mark.parametrize("gradDB", [False, True])
+def test_peel_reuses_setup(gradDB):
+    """Peel layers of one pos tensor: the layers after the first reuse the
+    triangle setup and tile lists of the call before (one k_setup for three
+    layers); every layer bit-exact against the oracle, and d_pos of the
+    three layers against the oracle's."""
+    torch = torch_dev()
+    from diffrast import DiffRast
+    sc = scenes.textured_icosphere(N=2, H=96, W=96, level=3, tex_size=8)
+    pos, tri = sc["pos"], sc["tri"]
+    p, t = dev(pos).requires_grad_(True), dev(tri)
+    rng = np.random.default_rng(5)
+    out = {}
+
+    def layers():
+        prev, prev_host, loss, ref = None, None, 0, np.zeros_like(pos)
+        for _ in range(3):
+            r, db = DiffRast.rasterize(p, t, (96, 96), gradDB=gradDB, peelLayer=prev)
+            rr, rdb = O.rasterize(pos, tri, (96, 96), gradDB=gradDB, peelLayer=prev_host,
+                                  max_per_tile=0)
+            np.testing.assert_array_equal(host(r), rr)
+            if gradDB:
+                np.testing.assert_array_equal(host(db), rdb)
+            g = rng.normal(size=rr.shape).astype(np.float32)
+            loss = loss + (r * dev(g)).sum()
+            ref += O.rasterize_vjp(pos, tri, rr, g, None)
+            prev, prev_host = r.detach(), rr
+        out["loss"], out["ref"] = loss, ref
+
+    assert _setup_launches(layers) == 1
+    out["loss"].backward()
+    assert_grad_close(host(p.grad), out["ref"], "d_pos of the peel layers")
+
+
+def test_peel_after_in_place_update_recomputes():
+    """pos changed in place between two layers (a new autograd version): the
+    second layer does its own setup and matches the oracle on the new pos."""
+    torch = torch_dev()
+    from diffrast import DiffRast
+    sc = scenes.textured_icosphere(N=2, H=96, W=96, level=3, tex_size=8)
+    pos, tri = sc["pos"], sc["tri"]
+    p, t = dev(pos), dev(tri)
+    r1, _ = DiffRast.rasterize(p, t, (96, 96), gradDB=False)
+    p[..., 0] += 0.05
+    moved = pos.copy()
+    moved[..., 0] += np.float32(0.05)
+    np.testing.assert_array_equal(host(p), moved)
+    n = _setup_launches(lambda: DiffRast.rasterize(p, t, (96, 96), gradDB=False, peelLayer=r1))
+    assert n == 1
+    r2, _ = DiffRast.rasterize(p, t, (96, 96), gradDB=False, peelLayer=r1)
+    rr, _ = O.rasterize(moved, tri, (96, 96), gradDB=False, peelLayer=host(r1), max_per_tile=0)
+    np.testing.assert_array_equal(host(r2), rr)
+
+
+def test_rasterize_again_abi():
+    """dr_rasterize_fwd_again through the C-ABI: after a call with the same
+    arguments it reuses that call's setup (one k_setup for both calls); with
+    other arguments (here another resolution) it does the full work; every
+    result bit-exact against the oracle."""
+    import ctypes
+    torch = torch_dev()
+    import diffrast._lib as L
+    lib = L.load()
+    sc = scenes.textured_icosphere(N=2, H=64, W=80, level=3, tex_size=8)
+    pos, tri = dev(sc["pos"]), dev(sc["tri"])
+    N, V, T = pos.shape[0], pos.shape[1], tri.shape[0]
+    P = lambda x: None if x is None else ctypes.c_void_p(x.data_ptr())
+    S = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    res = []
+
+    def fwd(fn, H, W, peel=None):
+        r = torch.empty((N, H, W, 4), device="cuda")
+        db = torch.empty((N, H, W, 4), device="cuda")
+        L.check(fn(P(pos), V * 4, P(tri), None, P(peel), N, V, T, H, W, P(r), P(db), 0, S))
+        res.append((H, W, peel, r, db))
+        return r
+
+    def calls():
+        r1 = fwd(lib.dr_rasterize_fwd_ex, 64, 80)
+        fwd(lib.dr_rasterize_fwd_again, 64, 80, peel=r1)    # reuses the first call
+        r3 = fwd(lib.dr_rasterize_fwd_again, 48, 40)        # another size: full work
+        fwd(lib.dr_rasterize_fwd_again, 48, 40, peel=r3)    # reuses the third
+
+    assert _setup_launches(calls) == 2
+    for H, W, peel, r, db in res:
+        rr, rdb = O.rasterize(sc["pos"], sc["tri"], (H, W), gradDB=True,
+                              peelLayer=None if peel is None else host(peel), max_per_tile=0)
+        np.testing.assert_array_equal(host(r), rr)
+        np.testing.assert_array_equal(host(db), rdb)
