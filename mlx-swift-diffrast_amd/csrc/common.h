@@ -209,13 +209,21 @@ __device__ __forceinline__ int dpp_shift(int v) {
   return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, true);
 }
 
+// Step D of the scan, masked on the sending side: lane l's value reaches
+// lane l + D when both lie in one run (run start of l + D <= l); any other
+// lane sends +0.  The receiver then adds unconditionally, so the shift
+// fuses into the add (one DPP instruction per value) and the sums equal a
+// conditional add's.
 template <int D, int M>
 __device__ __forceinline__ void run_scan_step(int li, int s, float (&v)[M]) {
+  const int s_to = dpp_shift<0x100 + D>(s);  // run start of lane l + D
+  const bool send = li + D <= 15 && s_to <= li;
+  float w[M];  // all masks first: a DPP read right after the VALU write of its
+               // source waits two cycles
 #pragma unroll
-  for (int i = 0; i < M; ++i) {
-    const float o = __int_as_float(dpp_shift<0x110 + D>(__float_as_int(v[i])));
-    if (li - D >= s) v[i] += o;
-  }
+  for (int i = 0; i < M; ++i) w[i] = send ? v[i] : 0.0f;
+#pragma unroll
+  for (int i = 0; i < M; ++i) v[i] += __int_as_float(dpp_shift<0x110 + D>(__float_as_int(w[i])));
 }
 
 __device__ __forceinline__ int wave_max(int v) {
