@@ -302,6 +302,21 @@ __device__ __forceinline__ float dpp_movf(float v) {
   return __int_as_float(dpp_mov<CTRL>(__float_as_int(v)));
 }
 
+// v + (v of lane l ^ 32) and v + (v of lane l ^ 16), with the gfx950 lane
+// swaps (one VALU instruction each, no LDS round trip).  permlane32_swap
+// exchanges lanes 32..63 of its first operand with lanes 0..31 of its
+// second; permlane16_swap exchanges the odd 16-lane rows of the first with
+// the even rows of the second.  Given v twice, the two results hold v and
+// its partner's value in every lane.
+__device__ __forceinline__ float add_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float add_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // Sixteen wave sums at once.  A transposing butterfly (row mirror, half-row
 // mirror, then the two quad swaps; each step keeps half of the values and
 // adds the partner's half) leaves lane l with value (l & 15) summed over
@@ -322,9 +337,24 @@ __device__ __forceinline__ float wave_sum16(const float (&a)[16]) {
   for (int i = 0; i < 2; ++i)  // quad_perm [2,3,0,1]
     v2[i] = (b1 ? v4[i + 2] : v4[i]) + dpp_movf<0x4E>(b1 ? v4[i] : v4[i + 2]);
   float v = (b0 ? v2[1] : v2[0]) + dpp_movf<0xB1>(b0 ? v2[0] : v2[1]);  // quad_perm [1,0,3,2]
-  v += __shfl_xor(v, 16, kWave);
-  v += __shfl_xor(v, 32, kWave);
-  return v;
+  return add_xor32(add_xor16(v));
+}
+
+// Four wave sums at once, the same way: the two quad swaps leave lane l
+// with value (l & 3) summed over its quad, row rotations by 4 and 8 add the
+// row's four quads, and the lane swaps the four rows.  Every lane returns
+// the total of value (lane & 3).  All 64 lanes must execute this.
+__device__ __forceinline__ float wave_sum4(const float (&a)[4]) {
+  const int l = lane_id();
+  const bool b1 = (l >> 1) & 1, b0 = l & 1;
+  float v2[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)  // quad_perm [2,3,0,1]
+    v2[i] = (b1 ? a[i + 2] : a[i]) + dpp_movf<0x4E>(b1 ? a[i] : a[i + 2]);
+  float v = (b0 ? v2[1] : v2[0]) + dpp_movf<0xB1>(b0 ? v2[0] : v2[1]);  // quad_perm [1,0,3,2]
+  v += dpp_movf<0x124>(v);  // row_ror:4
+  v += dpp_movf<0x128>(v);  // row_ror:8
+  return add_xor32(add_xor16(v));
 }
 
 __device__ __forceinline__ int wave_min(int v) {

@@ -925,21 +925,26 @@ __global__ void __launch_bounds__(kWinThreads, 5) k_tex_bwd_win(TexBwdArgs A, in
       }
     }
 
-    // -- hot footprint of slot 0: big wave groups go to the accumulator ------
+    // -- hot footprint of slot 0: big groups on one texel go to the accumulator
     bool hot = false;
     {
       const bool on0 = q[0].w00 != 0.0f || q[0].w10 != 0.0f || q[0].w01 != 0.0f || q[0].w11 != 0.0f;
       const int Wk = mip_w(md, q[0].k);
       const uint64_t key = ((uint64_t)q[0].k << 48) | (uint64_t)((int64_t)q[0].iy0 * Wk + q[0].ix0);
       const uint32_t key2 = ((uint32_t)(q[0].ix1 - q[0].ix0) << 16) ^ (uint32_t)(q[0].iy1 - q[0].iy0);
-      uint64_t pending = __ballot(on0);
+      // flat footprints only (all the weight on one texel: every background
+      // pixel); other footprints, however many lanes share them, take the
+      // windows' run sums
+      const bool flat = on0 && q[0].ix0 == q[0].ix1 && q[0].iy0 == q[0].iy1;
+      uint64_t pending = __ballot(flat);
+      if (__popcll(pending) < kGroupMin) pending = 0;
 #pragma unroll 1
       for (int probe = 0; probe < 2 && pending; ++probe) {
         const int leader = probe_leader(pending, probe);  // wave-uniform: readlane
         const uint64_t lkey = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(key >> 32), leader) << 32) |
                               (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)key, leader);
         const uint32_t lkey2 = (uint32_t)__builtin_amdgcn_readlane((int)key2, leader);
-        const bool same = on0 && !hot && key == lkey && key2 == lkey2;
+        const bool same = flat && !hot && key == lkey && key2 == lkey2;
         const uint64_t members = __ballot(same);
         pending &= ~members;
         if (__popcll(members) < kGroupMin) continue;
@@ -964,15 +969,14 @@ __global__ void __launch_bounds__(kWinThreads, 5) k_tex_bwd_win(TexBwdArgs A, in
           acc.v = 0.0f;
           acc.on = true;
         }
-        const float wt[4] = {q[0].w00, q[0].w10, q[0].w01, q[0].w11};
-        float val[4 * CT];
+        // all the weight is on tap 0 (one texel): four sums, one per channel
+        float x[4];
 #pragma unroll
-        for (int c = 0; c < CT; ++c) {
-          const float gc = g[c] * q[0].scale;
-#pragma unroll
-          for (int t = 0; t < 4; ++t) val[4 * c + t] = wt[t] * gc;
-        }
-        acc_add(acc, val, same);
+        for (int c = 0; c < 4; ++c)
+          x[c] = (c < CT && same) ? q[0].w00 * (g[c < CT ? c : 0] * q[0].scale) : 0.0f;
+        const float z = wave_sum4(x);  // lane l: total of value l & 3
+        const float zc = __shfl(z, (lane >> 2) & 3, kWave);
+        if (lane < 4 * CT && (lane & 3) == 0) acc.v += zc;  // lane 4c: channel c, tap 0
         if (same) hot = true;
       }
     }
