@@ -345,13 +345,56 @@ __device__ __forceinline__ TriRec load_rec(const TriRec* __restrict__ rec, int64
 constexpr int kMaxPerTileCap = 1024;
 constexpr int kRankMax = 4096;
 
-// Rasterize.swift:371-599.  One workgroup per (image, 16x16 tile); wave w
-// owns the 8x8 quadrant (w&1, w>>1).  Each triangle of the tile's list is
-// first tested against the quadrant's pixel-centre box by its bounding box
-// (exact: the pixel -> NDC map is monotonic), 64 triangles at a time, one
-// per lane; only the survivors are tested against the quadrant's 64 pixels.
-// (A conservative edge-function test of the box, in fp64 or fp32, removed
-// more candidates but cost more than the survivor tests it saved.)
+// Triangle-parallel coverage: candidates staged per round, pixels per work
+// item, work items per pass.
+constexpr int kRChunk = 128;
+constexpr int kRSub = 4;
+constexpr int kRItems = 2048;
+
+// Smallest i in [0, n) with p(i) for p false then true (n if none), and
+// largest i in [0, n) with p(i) for p true then false (-1 if none), from a
+// guess i0 (a few steps when the guess is close; at most n).
+template <typename P>
+__device__ __forceinline__ int first_true(int i0, int n, P p) {
+  int i = min(max(i0, 0), n);
+  while (i > 0 && p(i - 1)) --i;
+  while (i < n && !p(i)) ++i;
+  return i;
+}
+template <typename P>
+__device__ __forceinline__ int last_true(int i0, int n, P p) {
+  int i = min(max(i0, -1), n - 1);
+  while (i < n - 1 && p(i + 1)) ++i;
+  while (i >= 0 && !p(i)) --i;
+  return i;
+}
+
+// Pixel coordinate of a bounding-box edge, clamped to a range where the
+// float -> int conversion is exact (only a guess for first/last_true).
+__device__ __forceinline__ int px_guess(float v) {
+  return f2i(fminf(fmaxf(v, -4.0e6f), 4.0e6f));
+}
+
+// Depth-then-index key of a covering triangle: the float depth mapped to an
+// unsigned order (-0 taken as +0, as the reference's == compares it) above
+// `id` (the triangle index, or index << 7 | LDS slot while indices fit in
+// 25 bits), so the smallest key is the reference's winner (the lower index
+// on equal depth).
+__device__ __forceinline__ unsigned long long zkey(float z, uint32_t id) {
+  uint32_t b = z == 0.0f ? 0u : __float_as_uint(z);
+  b ^= (uint32_t)((int32_t)b >> 31) | 0x80000000u;
+  return ((unsigned long long)b << 32) | id;
+}
+
+// Rasterize.swift:371-599.  One workgroup per (image, 16x16 tile); the
+// tile's candidates are taken triangle-parallel.  Each candidate gets the
+// exact set of tile pixels the reference's bounding-box test keeps (a
+// rectangle: pixel centres are monotonic in the pixel index), its pixels
+// are cut into work items of kRSub and the items are dealt out evenly over
+// the workgroup; each covering pixel folds (depth, triangle) into a 64-bit
+// LDS z-buffer by atomic min.  A last pass gives each thread its pixel and
+// recomputes the winner's barycentrics with the same expressions, so every
+// output equals a sequential scan's.
 //
 // CAPPED (max_per_tile > 0): the reference's per-tile limit
 // (Rasterize.swift:164-171, 227-239, 410) with its appends in triangle
@@ -364,109 +407,85 @@ __global__ void __launch_bounds__(256) k_raster(
     const TriRec* __restrict__ rec, const int4* __restrict__ rect, Items it, int64_t rec_stride,
     const int* __restrict__ cnt, const int* __restrict__ list, int cap,
     const float* __restrict__ peel, int N, int H, int W, int ntx, int nty, int max_per_tile,
-    float* __restrict__ rast, float* __restrict__ rast_db) {
-  __shared__ TriRec s_rec[4][kWave];
-  __shared__ int s_t[4][kWave];
+    int slot_keys, float* __restrict__ rast, float* __restrict__ rast_db) {
+  __shared__ TriRec s_rec[kRChunk];
+  __shared__ int s_t[kRChunk];
+  __shared__ int s_box[kRChunk];             // x0 | y0 << 4 | (w - 1) << 8 | (h - 1) << 12
+  __shared__ uint16_t s_item[kRItems];       // candidate << 6 | piece
+  __shared__ unsigned long long s_zb[256];   // per tile pixel: smallest zkey, ~0 = none
+  __shared__ float s_x[16], s_y[16];         // pixel-centre x of tile columns, y of rows
+  __shared__ float s_pz[PEEL ? 256 : 1];     // depth of the peeled layer (-1e30 = none)
   __shared__ int s_keep[CAPPED ? kMaxPerTileCap : 1];
+  __shared__ int s_all[CAPPED ? kRankMax : 1];
+  __shared__ int s_total[2];                 // work items of the round, by round parity
   const int tiles = ntx * nty;
   const int B = tiles * N;
   const int b = xcd_remap((int)blockIdx.x, B);
   const int n = b / tiles;
   const int tile = b - n * tiles;
   const int ty = tile / ntx, tx = tile - ty * ntx;
-  const int wave = threadIdx.x >> 6;
-  const int lane = threadIdx.x & 63;
+  const int tid = threadIdx.x;
   const int64_t j = (int64_t)n * tiles + tile;
-  int count = cnt[j];
   const int* ids = list + j * (int64_t)cap;
+  // the first round's ids are read together with the count (slots past the
+  // count hold stale ids and are not used)
+  const int t_first = tid < kRChunk && tid < cap ? ids[tid] : 0;
+  int count = cnt[j];
+  bool ranked = false;
   int scan_limit = 0x7fffffff;  // full scan: stop after this many tile candidates
   if (CAPPED && count > max_per_tile) {  // uniform over the workgroup
     if (count <= cap && count <= kRankMax) {
       // rank every id of the complete list (ids of one tile are distinct);
       // the max_per_tile lowest land in s_keep in ascending order
-      int* s_all = reinterpret_cast<int*>(&s_rec[0][0]);  // kRankMax ints
-      for (int i = threadIdx.x; i < count; i += blockDim.x) s_all[i] = ids[i];
+      for (int i = tid; i < count; i += blockDim.x) s_all[i] = ids[i];
       __syncthreads();
-      for (int i = threadIdx.x; i < count; i += blockDim.x) {
+      for (int i = tid; i < count; i += blockDim.x) {
         const int v = s_all[i];
         int r = 0;
         for (int k = 0; k < count; ++k) r += s_all[k] < v;
         if (r < max_per_tile) s_keep[r] = v;
       }
-      __syncthreads();  // s_all (the record slots) is free again after this
+      __syncthreads();
       ids = s_keep;
       count = max_per_tile;
+      ranked = true;
     } else {
       count = cap + 1;  // take the ordered full scan
       scan_limit = max_per_tile;
     }
   }
-  const int qx0 = tx * kTile + (wave & 1) * 8;
-  const int qy0 = ty * kTile + (wave >> 1) * 8;
-  if (qx0 >= W || qy0 >= H) return;  // whole quadrant outside the image
-  const int pw = qx0 + (lane & 7);
-  const int ph = qy0 + (lane >> 3);
-  const bool valid = pw < W && ph < H;
-  const int qx1 = min(qx0 + 7, W - 1), qy1 = min(qy0 + 7, H - 1);
-
-  const float x = 2.0f * ((float)pw + 0.5f) / (float)W - 1.0f;
-  const float y = 1.0f - 2.0f * ((float)ph + 0.5f) / (float)H;
-  const float xw0 = 2.0f * ((float)qx0 + 0.5f) / (float)W - 1.0f;
-  const float xw1 = 2.0f * ((float)qx1 + 0.5f) / (float)W - 1.0f;
-  const float yw1 = 1.0f - 2.0f * ((float)qy0 + 0.5f) / (float)H;  // top row: largest y
-  const float yw0 = 1.0f - 2.0f * ((float)qy1 + 0.5f) / (float)H;
-
-  const int64_t pix = ((int64_t)n * H + ph) * W + pw;
+  const int x0t = tx * kTile, y0t = ty * kTile;
+  const int nx = min(kTile, W - x0t), ny = min(kTile, H - y0t);  // tile pixels inside the image
+  const int lx = tid & 15, ly = tid >> 4;
+  const int pw = x0t + lx, ph = y0t + ly;
+  const bool valid = lx < nx && ly < ny;
+  const int64_t pix = ((int64_t)n * H + min(ph, H - 1)) * W + min(pw, W - 1);
+  const int64_t rbase = (int64_t)n * rec_stride;
   float peel_z = -1e30f;
   if (PEEL && valid) {
     const float4 pl = *reinterpret_cast<const float4*>(peel + pix * 4);
     if (pl.w > 0.0f) peel_z = pl.z;
   }
-  Best best = {1e30f, 0.0f, 0.0f, -1};
-  const int64_t rbase = (int64_t)n * rec_stride;
-  if (count <= cap) {
-    // 64 candidates at a time: each lane loads one candidate's record
-    // (vector gathers, one round trip for all 64) and tests it against the
-    // quadrant's box; the survivors are then taken one by one, their
-    // records read back from the wave's LDS slots at a uniform address (a
-    // broadcast read; cheaper than 17 readlanes and their SGPR hazards).
-    for (int c0 = 0; c0 < count; c0 += kWave) {
-      const int nb = min(kWave, count - c0);
-      int myt = 0;
-      TriRec Rl;
-      bool hit = false;
-      if (lane < nb) {
-        myt = ids[c0 + lane];
-        Rl = load_rec(rec, rbase + myt);
-        hit = !(Rl.r3.y < xw0 || Rl.r3.x > xw1 || Rl.r3.w < yw0 || Rl.r3.z > yw1);
-      }
-      uint64_t m = __ballot(hit);
-      if (hit) {
-        s_rec[wave][lane] = Rl;
-        s_t[wave][lane] = myt;
-      }
-      // LDS is ordered within a wave; the barrier keeps the compiler from
-      // moving the reads above the writes
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-      while (m) {
-        const int j = __ffsll((long long)m) - 1;
-        m &= m - 1;
-        const int t = s_t[wave][j];
-        const TriRec R = s_rec[wave][j];
-        if (valid) test_tri(R, t, x, y, peel_z, best);
-      }
-      __builtin_amdgcn_wave_barrier();  // reads done before the next chunk writes
-    }
-  } else {
+  // the pixel centre as the reference computes it
+  const float x = 2.0f * ((float)pw + 0.5f) / (float)W - 1.0f;
+  const float y = 1.0f - 2.0f * ((float)ph + 0.5f) / (float)H;
+
+  if (count > cap) {
     // The tile's list overflowed its capacity (sized from an earlier
-    // call): scan the image's whole triangle range with the same tile test
-    // the binning uses (same candidate set, so the same result).
+    // call): each thread scans the image's whole triangle range for its
+    // pixel with the same tile test the binning uses (same candidate set,
+    // so the same result), wave-uniform up to its 16x4 strip's box.
+    const int sy0 = min(y0t + (tid >> 6) * 4, H - 1), sy1 = min(sy0 + 3, H - 1);
+    const float xw0 = 2.0f * ((float)x0t + 0.5f) / (float)W - 1.0f;
+    const float xw1 = 2.0f * ((float)(x0t + nx - 1) + 0.5f) / (float)W - 1.0f;
+    const float yw1 = 1.0f - 2.0f * ((float)sy0 + 0.5f) / (float)H;
+    const float yw0 = 1.0f - 2.0f * ((float)sy1 + 0.5f) / (float)H;
     int t0 = 0, t1 = it.T;
     if (it.prefix != nullptr) {
       t0 = (int)it.start[n];
       t1 = t0 + (int)(it.prefix[n + 1] - it.prefix[n]);
     }
+    Best best = {1e30f, 0.0f, 0.0f, -1};
     int taken = 0;  // tile candidates so far, in triangle order
     for (int t = t0; t < t1; ++t) {
       const int4 rc = rect[rbase + t];
@@ -476,22 +495,125 @@ __global__ void __launch_bounds__(256) k_raster(
       if (R.r3.y < xw0 || R.r3.x > xw1 || R.r3.w < yw0 || R.r3.z > yw1) continue;
       if (valid) test_tri(R, t, x, y, peel_z, best);
     }
+    if (!valid) return;
+    float4 o4 = make_float4(0.f, 0.f, 0.f, 0.f), d4 = o4;
+    if (best.t >= 0) {
+      o4 = make_float4(best.u, best.v, best.z, (float)(best.t + 1));
+      if (DB) {  // Rasterize.swift:586-598
+        const TriRec R = load_rec(rec, rbase + best.t);
+        const float k_x = 2.0f / (float)W, k_y = -2.0f / (float)H;
+        d4 = make_float4((R.r1.y - R.r0.y) * R.r2.z * k_x, (R.r0.x - R.r1.x) * R.r2.z * k_y,
+                         (R.r0.y - R.r0.w) * R.r2.z * k_x, (R.r0.z - R.r0.x) * R.r2.z * k_y);
+      }
+    }
+    *reinterpret_cast<float4*>(rast + pix * 4) = o4;
+    if (DB) *reinterpret_cast<float4*>(rast_db + pix * 4) = d4;
+    return;
   }
+
+  s_zb[tid] = ~0ull;
+  if (PEEL) s_pz[tid] = peel_z;
+  if (tid < 16) s_x[tid] = 2.0f * ((float)(x0t + tid) + 0.5f) / (float)W - 1.0f;
+  else if (tid < 32) s_y[tid - 16] = 1.0f - 2.0f * ((float)(y0t + tid - 16) + 0.5f) / (float)H;
+  if (tid == 0) s_total[0] = s_total[1] = 0;
+  // one round: every candidate's record stays in s_rec, and the keys carry
+  // its slot (slot_keys: all record indices below 2^25)
+  const bool slots = slot_keys && count <= kRChunk;
+  for (int c0 = 0, round = 0; c0 < count; c0 += kRChunk, ++round) {
+    const int nb = min(kRChunk, count - c0);
+    __syncthreads();  // s_x / s_y / s_zb set; the previous round's items done
+    // the next round's counter: its last reader (two rounds back) is done
+    if (tid == 0) s_total[(round + 1) & 1] = 0;
+    // 1) one candidate per thread: record, exact pixel box, work items
+    int base = 0, pieces = 0;
+    if (tid < nb) {
+      const int t = c0 == 0 && !ranked ? t_first : ids[c0 + tid];
+      const TriRec R = load_rec(rec, rbase + t);
+      const float minx = R.r3.x, maxx = R.r3.y, miny = R.r3.z, maxy = R.r3.w;
+      const float fW = (float)W * 0.5f, fH = (float)H * 0.5f;
+      const int bx0 = first_true(px_guess(ceilf((minx + 1.0f) * fW - 0.5f)) - x0t, nx,
+                                 [&](int i) { return !(s_x[i] < minx); });
+      const int bx1 = last_true(px_guess(floorf((maxx + 1.0f) * fW - 0.5f)) - x0t, nx,
+                                [&](int i) { return !(s_x[i] > maxx); });
+      const int by0 = first_true(px_guess(ceilf((1.0f - maxy) * fH - 0.5f)) - y0t, ny,
+                                 [&](int i) { return !(s_y[i] > maxy); });
+      const int by1 = last_true(px_guess(floorf((1.0f - miny) * fH - 0.5f)) - y0t, ny,
+                                [&](int i) { return !(s_y[i] < miny); });
+      if (bx0 <= bx1 && by0 <= by1) {
+        const int bw = bx1 - bx0 + 1, bh = by1 - by0 + 1;
+        pieces = (bw * bh + kRSub - 1) / kRSub;
+        base = atomicAdd(&s_total[round & 1], pieces);
+        s_rec[tid] = R;
+        s_t[tid] = t;
+        s_box[tid] = bx0 | (by0 << 4) | ((bw - 1) << 8) | ((bh - 1) << 12);
+        for (int q = 0; q < pieces && base + q < kRItems; ++q)
+          s_item[base + q] = (uint16_t)((tid << 6) | q);
+      }
+    }
+    __syncthreads();
+    const int total = s_total[round & 1];
+    // 2) the work items, kRItems per pass
+    for (int p0 = 0; p0 < total; p0 += kRItems) {
+      if (p0 > 0) {  // later passes (more than kRItems items this round)
+        __syncthreads();
+        for (int q = max(p0 - base, 0); q < pieces && base + q < p0 + kRItems; ++q)
+          s_item[base + q - p0] = (uint16_t)((tid << 6) | q);
+        __syncthreads();
+      }
+      const int np = min(kRItems, total - p0);
+      for (int e = tid; e < np; e += blockDim.x) {
+        const int ie = s_item[e];
+        const int k = ie >> 6, q = ie & 63;
+        const TriRec R = s_rec[k];
+        const int t = s_t[k], bx = s_box[k];
+        const int bx0 = bx & 15, by0 = (bx >> 4) & 15, bw = ((bx >> 8) & 15) + 1;
+        const int bh = ((bx >> 12) & 15) + 1;
+        const int o0 = q * kRSub, o1 = min(o0 + kRSub, bw * bh);
+        // row of o0 (o0 < 256, bw <= 16: the product with the reciprocal
+        // stays well clear of an integer)
+        int ry = f2i(((float)o0 + 0.5f) * __builtin_amdgcn_rcpf((float)bw));
+        int rx = o0 - ry * bw;
+        const float sx0 = R.r0.x, sy0 = R.r0.y, sx1 = R.r0.z, sy1 = R.r0.w;
+        const float sx2 = R.r1.x, sy2 = R.r1.y, sz0 = R.r1.z, sz1 = R.r1.w;
+        const float sz2 = R.r2.x, area = R.r2.y, inv_area = R.r2.z;
+        for (int o = o0; o < o1; ++o) {
+          const int cx = bx0 + rx, cy = by0 + ry;
+          const float px = s_x[cx], py = s_y[cy];
+          // Rasterize.swift:417-462 (the box test holds by construction)
+          const float e0 = (sx1 - px) * (sy2 - py) - (sx2 - px) * (sy1 - py);
+          const float e1 = (sx2 - px) * (sy0 - py) - (sx0 - px) * (sy2 - py);
+          const float e2 = (sx0 - px) * (sy1 - py) - (sx1 - px) * (sy0 - py);
+          if (!((e0 * area) < 0.0f || (e1 * area) < 0.0f || (e2 * area) < 0.0f)) {
+            const float u = e1 * inv_area, v = e2 * inv_area;
+            const float z = e0 * inv_area * sz0 + u * sz1 + v * sz2;
+            const int pi = cy * 16 + cx;
+            if (z >= -1.0f && z <= 1.0f && !(PEEL && z <= s_pz[pi]))
+              atomicMin(&s_zb[pi], zkey(z, slots ? ((uint32_t)t << 7) | (uint32_t)k : (uint32_t)t));
+          }
+          if (++rx == bw) {
+            rx = 0;
+            ++ry;
+          }
+        }
+      }
+    }
+  }
+  __syncthreads();
+  // 3) each thread its pixel: the winner's outputs, recomputed
   if (!valid) return;
-  float4 o4, d4 = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (best.t < 0) {
-    o4 = make_float4(0.f, 0.f, 0.f, 0.f);
-  } else {
-    o4 = make_float4(best.u, best.v, best.z, (float)(best.t + 1));
-    if (DB) {  // Rasterize.swift:586-598
-      const TriRec R = load_rec(rec, rbase + best.t);
-      const float sx0 = R.r0.x, sy0 = R.r0.y, sx1 = R.r0.z, sy1 = R.r0.w;
-      const float sx2 = R.r1.x, sy2 = R.r1.y;
-      const float inv_area = R.r2.z;
-      const float k_x = 2.0f / (float)W;
-      const float k_y = -2.0f / (float)H;
-      d4 = make_float4((sy2 - sy0) * inv_area * k_x, (sx0 - sx2) * inv_area * k_y,
-                       (sy0 - sy1) * inv_area * k_x, (sx1 - sx0) * inv_area * k_y);
+  const unsigned long long key = s_zb[tid];
+  float4 o4 = make_float4(0.f, 0.f, 0.f, 0.f), d4 = o4;
+  if (key != ~0ull) {
+    const uint32_t id = (uint32_t)key;
+    const int t = slots ? (int)(id >> 7) : (int)id;
+    const TriRec R = slots ? s_rec[id & 127] : load_rec(rec, rbase + t);
+    Best best = {1e30f, 0.0f, 0.0f, -1};
+    test_tri(R, t, x, y, -1e30f, best);  // the same expressions as the scan
+    if (best.t >= 0) o4 = make_float4(best.u, best.v, best.z, (float)(t + 1));
+    if (DB && best.t >= 0) {  // Rasterize.swift:586-598
+      const float k_x = 2.0f / (float)W, k_y = -2.0f / (float)H;
+      d4 = make_float4((R.r1.y - R.r0.y) * R.r2.z * k_x, (R.r0.x - R.r1.x) * R.r2.z * k_y,
+                       (R.r0.y - R.r0.w) * R.r2.z * k_x, (R.r0.z - R.r0.x) * R.r2.z * k_y);
     }
   }
   *reinterpret_cast<float4*>(rast + pix * 4) = o4;
@@ -998,9 +1120,11 @@ static int raster_fwd(const float* pos, int64_t pos_batch_stride, const int32_t*
   DR_CHECK_LAUNCH();
   }
   const dim3 grid((unsigned)n_tiles), block(256);
+  const int slot_keys = n_rec <= ((int64_t)1 << 25) ? 1 : 0;  // record indices fit in 25 bits
 #define DR_RASTER(DBV, PV, CV)                                                                    \
   hipLaunchKernelGGL((k_raster<DBV, PV, CV>), grid, block, 0, stream, rec, rect, it, rec_stride, \
-                     fillc, list, C, peel, N, H, W, ntx, nty, max_per_tile, rast, rast_db)
+                     fillc, list, C, peel, N, H, W, ntx, nty, max_per_tile, slot_keys, rast,    \
+                     rast_db)
 #define DR_RASTER_C(DBV, PV)                                 \
   do {                                                       \
     if (max_per_tile > 0) DR_RASTER(DBV, PV, true);          \
