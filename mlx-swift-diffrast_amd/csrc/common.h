@@ -63,11 +63,16 @@ struct Scratch {
   // a call is written into pinned host memory by a kernel after the call; a
   // later call reads it (once that kernel has run) and raises the capacity
   // if needed.
-  int64_t* pinned_total = nullptr;
+  // pinned_total[1] receives the sum of the counts (the list entries) of
+  // the same call, whose (image, triangle) items were stat_items: their
+  // ratio, tiles_per_item, picks the forward kernel of later calls.
+  int64_t* pinned_total = nullptr;      // 2 values
   int64_t* pinned_total_dev = nullptr;  // the same memory as a kernel writes it
   hipEvent_t total_event = nullptr;
   bool total_pending = false;
   int bin_cap = 0;  // slots per tile list, 0 = not known yet
+  int64_t stat_items = 0;
+  double tiles_per_item = 0.0;
   // Range-mode item prefix, staged through a ring of pinned host buffers:
   // a buffer is reused once the copy that read it has run (its event), so
   // a call waits only when it is kStageRing calls ahead of the device.
@@ -93,6 +98,7 @@ struct Scratch {
     bool range = false;
     std::vector<int32_t> ranges;
     int64_t n_items = 0, max_items = 0;
+    bool px = false;  // the forward kernel it ran (k_raster_px)
   } last_raster;
 };
 

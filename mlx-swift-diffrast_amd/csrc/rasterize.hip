@@ -160,26 +160,42 @@ __global__ void __launch_bounds__(256) k_bin_count(Items it, int64_t n_items, in
   for (int k = kHeld; k < nt; ++k) atomicAdd(&cnt[rect_tile(rc, ntx, base, k)], 1);
 }
 
-// Largest per-tile count (sizes the next call's per-tile list capacity).
-// The largest of c[0..n) (counts, >= 0) into *out, by one workgroup: out is
-// the pinned host cell of the capacity protocol, written directly (no
-// device atomics, no copy).
+// Largest per-tile count (sizes the next call's per-tile list capacity)
+// and, when out_sum is given, the sum of the counts (the list entries,
+// which tell how many tiles a triangle spans on average).  By one
+// workgroup: the outputs are the pinned host cells of the capacity
+// protocol, written directly (no device atomics, no copy).
 __global__ void __launch_bounds__(256) k_tile_max(const int* __restrict__ c, int64_t n,
-                                                  int64_t* __restrict__ out) {
+                                                  int64_t* __restrict__ out,
+                                                  int64_t* __restrict__ out_sum) {
   __shared__ int s_m[4];
+  __shared__ long long s_s[4];
   int m0 = 0, m1 = 0, m2 = 0, m3 = 0;
+  long long sum = 0;
   int64_t j = threadIdx.x;
   for (; j + 768 < n; j += 1024) {
-    m0 = max(m0, c[j]);
-    m1 = max(m1, c[j + 256]);
-    m2 = max(m2, c[j + 512]);
-    m3 = max(m3, c[j + 768]);
+    const int a = c[j], b = c[j + 256], d = c[j + 512], e = c[j + 768];
+    m0 = max(m0, a);
+    m1 = max(m1, b);
+    m2 = max(m2, d);
+    m3 = max(m3, e);
+    sum += (long long)a + b + d + e;
   }
-  for (; j < n; j += 256) m0 = max(m0, c[j]);
+  for (; j < n; j += 256) {
+    m0 = max(m0, c[j]);
+    sum += c[j];
+  }
   const int m = wave_max(max(max(m0, m1), max(m2, m3)));
-  if (lane_id() == 0) s_m[threadIdx.x >> 6] = m;
+  for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, kWave);
+  if (lane_id() == 0) {
+    s_m[threadIdx.x >> 6] = m;
+    s_s[threadIdx.x >> 6] = sum;
+  }
   __syncthreads();
-  if (threadIdx.x == 0) *out = max(max(s_m[0], s_m[1]), max(s_m[2], s_m[3]));
+  if (threadIdx.x == 0) {
+    *out = max(max(s_m[0], s_m[1]), max(s_m[2], s_m[3]));
+    if (out_sum) *out_sum = s_s[0] + s_s[1] + s_s[2] + s_s[3];
+  }
 }
 
 // Rasterize.swift:227-239, second half: append t to each touched tile's
@@ -344,6 +360,10 @@ __device__ __forceinline__ TriRec load_rec(const TriRec* __restrict__ rec, int64
 // list that mode ranks in LDS (longer lists take the ordered full scan).
 constexpr int kMaxPerTileCap = 1024;
 constexpr int kRankMax = 4096;
+
+// Forward kernel choice: k_raster_px when triangles span at least this many
+// tiles each on average.
+constexpr double kPxTilesPerItem = 8.0;
 
 // Triangle-parallel coverage: candidates staged per round, pixels per work
 // item, work items per pass.
@@ -614,6 +634,161 @@ __global__ void __launch_bounds__(256) k_raster(
       const float k_x = 2.0f / (float)W, k_y = -2.0f / (float)H;
       d4 = make_float4((R.r1.y - R.r0.y) * R.r2.z * k_x, (R.r0.x - R.r1.x) * R.r2.z * k_y,
                        (R.r0.y - R.r0.w) * R.r2.z * k_x, (R.r0.z - R.r0.x) * R.r2.z * k_y);
+    }
+  }
+  *reinterpret_cast<float4*>(rast + pix * 4) = o4;
+  if (DB) *reinterpret_cast<float4*>(rast_db + pix * 4) = d4;
+}
+
+// The same forward, pixel-parallel, for large triangles (a candidate's box
+// then holds most of the tile, and the work items of k_raster cost more
+// than one test per pixel): Rasterize.swift:371-599.  One workgroup per
+// (image, 16x16 tile); wave w owns the 8x8 quadrant (w&1, w>>1).  Each triangle of the tile's list is
+// first tested against the quadrant's pixel-centre box by its bounding box
+// (exact: the pixel -> NDC map is monotonic), 64 triangles at a time, one
+// per lane; only the survivors are tested against the quadrant's 64 pixels.
+// (A conservative edge-function test of the box, in fp64 or fp32, removed
+// more candidates but cost more than the survivor tests it saved.)
+//
+// CAPPED (max_per_tile > 0): the reference's per-tile limit
+// (Rasterize.swift:164-171, 227-239, 410) with its appends in triangle
+// order, i.e. a tile keeps its max_per_tile lowest triangle indices.  A
+// complete list above the limit is ranked in LDS and only the kept ids are
+// rasterized; a list that overflowed its capacity takes the full scan in
+// triangle order and stops at the limit.
+template <bool DB, bool PEEL, bool CAPPED>
+__global__ void __launch_bounds__(256) k_raster_px(
+    const TriRec* __restrict__ rec, const int4* __restrict__ rect, Items it, int64_t rec_stride,
+    const int* __restrict__ cnt, const int* __restrict__ list, int cap,
+    const float* __restrict__ peel, int N, int H, int W, int ntx, int nty, int max_per_tile,
+    float* __restrict__ rast, float* __restrict__ rast_db) {
+  __shared__ TriRec s_rec[4][kWave];
+  __shared__ int s_t[4][kWave];
+  __shared__ int s_keep[CAPPED ? kMaxPerTileCap : 1];
+  const int tiles = ntx * nty;
+  const int B = tiles * N;
+  const int b = xcd_remap((int)blockIdx.x, B);
+  const int n = b / tiles;
+  const int tile = b - n * tiles;
+  const int ty = tile / ntx, tx = tile - ty * ntx;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int64_t j = (int64_t)n * tiles + tile;
+  int count = cnt[j];
+  const int* ids = list + j * (int64_t)cap;
+  int scan_limit = 0x7fffffff;  // full scan: stop after this many tile candidates
+  if (CAPPED && count > max_per_tile) {  // uniform over the workgroup
+    if (count <= cap && count <= kRankMax) {
+      // rank every id of the complete list (ids of one tile are distinct);
+      // the max_per_tile lowest land in s_keep in ascending order
+      int* s_all = reinterpret_cast<int*>(&s_rec[0][0]);  // kRankMax ints
+      for (int i = threadIdx.x; i < count; i += blockDim.x) s_all[i] = ids[i];
+      __syncthreads();
+      for (int i = threadIdx.x; i < count; i += blockDim.x) {
+        const int v = s_all[i];
+        int r = 0;
+        for (int k = 0; k < count; ++k) r += s_all[k] < v;
+        if (r < max_per_tile) s_keep[r] = v;
+      }
+      __syncthreads();  // s_all (the record slots) is free again after this
+      ids = s_keep;
+      count = max_per_tile;
+    } else {
+      count = cap + 1;  // take the ordered full scan
+      scan_limit = max_per_tile;
+    }
+  }
+  const int qx0 = tx * kTile + (wave & 1) * 8;
+  const int qy0 = ty * kTile + (wave >> 1) * 8;
+  if (qx0 >= W || qy0 >= H) return;  // whole quadrant outside the image
+  const int pw = qx0 + (lane & 7);
+  const int ph = qy0 + (lane >> 3);
+  const bool valid = pw < W && ph < H;
+  const int qx1 = min(qx0 + 7, W - 1), qy1 = min(qy0 + 7, H - 1);
+
+  const float x = 2.0f * ((float)pw + 0.5f) / (float)W - 1.0f;
+  const float y = 1.0f - 2.0f * ((float)ph + 0.5f) / (float)H;
+  const float xw0 = 2.0f * ((float)qx0 + 0.5f) / (float)W - 1.0f;
+  const float xw1 = 2.0f * ((float)qx1 + 0.5f) / (float)W - 1.0f;
+  const float yw1 = 1.0f - 2.0f * ((float)qy0 + 0.5f) / (float)H;  // top row: largest y
+  const float yw0 = 1.0f - 2.0f * ((float)qy1 + 0.5f) / (float)H;
+
+  const int64_t pix = ((int64_t)n * H + ph) * W + pw;
+  float peel_z = -1e30f;
+  if (PEEL && valid) {
+    const float4 pl = *reinterpret_cast<const float4*>(peel + pix * 4);
+    if (pl.w > 0.0f) peel_z = pl.z;
+  }
+  Best best = {1e30f, 0.0f, 0.0f, -1};
+  const int64_t rbase = (int64_t)n * rec_stride;
+  if (count <= cap) {
+    // 64 candidates at a time: each lane loads one candidate's record
+    // (vector gathers, one round trip for all 64) and tests it against the
+    // quadrant's box; the survivors are then taken one by one, their
+    // records read back from the wave's LDS slots at a uniform address (a
+    // broadcast read; cheaper than 17 readlanes and their SGPR hazards).
+    for (int c0 = 0; c0 < count; c0 += kWave) {
+      const int nb = min(kWave, count - c0);
+      int myt = 0;
+      TriRec Rl;
+      bool hit = false;
+      if (lane < nb) {
+        myt = ids[c0 + lane];
+        Rl = load_rec(rec, rbase + myt);
+        hit = !(Rl.r3.y < xw0 || Rl.r3.x > xw1 || Rl.r3.w < yw0 || Rl.r3.z > yw1);
+      }
+      uint64_t m = __ballot(hit);
+      if (hit) {
+        s_rec[wave][lane] = Rl;
+        s_t[wave][lane] = myt;
+      }
+      // LDS is ordered within a wave; the barrier keeps the compiler from
+      // moving the reads above the writes
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+      while (m) {
+        const int j = __ffsll((long long)m) - 1;
+        m &= m - 1;
+        const int t = s_t[wave][j];
+        const TriRec R = s_rec[wave][j];
+        if (valid) test_tri(R, t, x, y, peel_z, best);
+      }
+      __builtin_amdgcn_wave_barrier();  // reads done before the next chunk writes
+    }
+  } else {
+    // The tile's list overflowed its capacity (sized from an earlier
+    // call): scan the image's whole triangle range with the same tile test
+    // the binning uses (same candidate set, so the same result).
+    int t0 = 0, t1 = it.T;
+    if (it.prefix != nullptr) {
+      t0 = (int)it.start[n];
+      t1 = t0 + (int)(it.prefix[n + 1] - it.prefix[n]);
+    }
+    int taken = 0;  // tile candidates so far, in triangle order
+    for (int t = t0; t < t1; ++t) {
+      const int4 rc = rect[rbase + t];
+      if (rc.x < 0 || tx < rc.x || tx > rc.y || ty < rc.z || ty > rc.w) continue;
+      if (CAPPED && ++taken > scan_limit) break;  // uniform: the same tile test everywhere
+      const TriRec R = load_rec(rec, rbase + t);
+      if (R.r3.y < xw0 || R.r3.x > xw1 || R.r3.w < yw0 || R.r3.z > yw1) continue;
+      if (valid) test_tri(R, t, x, y, peel_z, best);
+    }
+  }
+  if (!valid) return;
+  float4 o4, d4 = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (best.t < 0) {
+    o4 = make_float4(0.f, 0.f, 0.f, 0.f);
+  } else {
+    o4 = make_float4(best.u, best.v, best.z, (float)(best.t + 1));
+    if (DB) {  // Rasterize.swift:586-598
+      const TriRec R = load_rec(rec, rbase + best.t);
+      const float sx0 = R.r0.x, sy0 = R.r0.y, sx1 = R.r0.z, sy1 = R.r0.w;
+      const float sx2 = R.r1.x, sy2 = R.r1.y;
+      const float inv_area = R.r2.z;
+      const float k_x = 2.0f / (float)W;
+      const float k_y = -2.0f / (float)H;
+      d4 = make_float4((sy2 - sy0) * inv_area * k_x, (sx0 - sx2) * inv_area * k_y,
+                       (sy0 - sy1) * inv_area * k_x, (sx1 - sx0) * inv_area * k_y);
     }
   }
   *reinterpret_cast<float4*>(rast + pix * 4) = o4;
@@ -998,7 +1173,7 @@ extern "C" int dr_rasterize_tile_counts(const float* pos, int64_t pos_batch_stri
   if (max_count_host) {
     int64_t* tmax = reinterpret_cast<int64_t*>(small + 8);
     hipLaunchKernelGGL(k_tile_max, dim3(1), dim3(256), 0, stream, (const int*)counts, n_tiles,
-                       tmax);
+                       tmax, (int64_t*)nullptr);
     DR_CHECK_LAUNCH();
     int64_t mx = 0;
     DR_CHECK_HIP(hipMemcpyAsync(&mx, tmax, sizeof(int64_t), hipMemcpyDeviceToHost, stream));
@@ -1091,8 +1266,12 @@ static int raster_fwd(const float* pos, int64_t pos_batch_stride, const int32_t*
   // a full scan, so results never depend on the capacity.
   auto grow = [](int64_t m) { return (int)std::min<int64_t>(((m + m / 4) + 31) / 32 * 32 + 32, 1 << 30); };
   C = sc->bin_cap;
+  auto take_stats = [&](int64_t items) {
+    sc->tiles_per_item = (double)sc->pinned_total[1] / (double)std::max<int64_t>(items, 1);
+  };
   if (sc->total_pending && hipEventQuery(sc->total_event) == hipSuccess) {
-    const int64_t mx = *sc->pinned_total;
+    const int64_t mx = sc->pinned_total[0];
+    take_stats(sc->stat_items);
     sc->total_pending = false;
     if (mx > C) C = grow(mx);
   }
@@ -1101,10 +1280,11 @@ static int raster_fwd(const float* pos, int64_t pos_batch_stride, const int32_t*
     launch_binning(false, it, n_items, max_items, N, rect, ntx, tiles, cnt, nullptr, 0, stream);
     DR_CHECK_LAUNCH();
     hipLaunchKernelGGL(k_tile_max, dim3(1), dim3(256), 0, stream, cnt, n_tiles,
-                       sc->pinned_total_dev);
+                       sc->pinned_total_dev, sc->pinned_total_dev + 1);
     DR_CHECK_LAUNCH();
     DR_CHECK_HIP(hipStreamSynchronize(stream));
-    C = grow(*sc->pinned_total);
+    C = grow(sc->pinned_total[0]);
+    take_stats(n_items);
   }
   // at most 4 GiB of lists (a 16 x 2048^2 batch of a 1.3M-triangle mesh
   // needs ~1,500 slots per tile); a tile above the capacity takes the full
@@ -1121,17 +1301,27 @@ static int raster_fwd(const float* pos, int64_t pos_batch_stride, const int32_t*
   }
   const dim3 grid((unsigned)n_tiles), block(256);
   const int slot_keys = n_rec <= ((int64_t)1 << 25) ? 1 : 0;  // record indices fit in 25 bits
-#define DR_RASTER(DBV, PV, CV)                                                                    \
-  hipLaunchKernelGGL((k_raster<DBV, PV, CV>), grid, block, 0, stream, rec, rect, it, rec_stride, \
-                     fillc, list, C, peel, N, H, W, ntx, nty, max_per_tile, slot_keys, rast,    \
-                     rast_db)
+  // Triangles spanning kPxTilesPerItem tiles or more on average (the last
+  // counted call's list entries per item) are large: pixel-parallel.
+  const bool px = reuse ? L.px : sc->tiles_per_item >= kPxTilesPerItem;
+#define DR_RASTER(DBV, PV, CV)                                                                     \
+  do {                                                                                            \
+    if (px)                                                                                       \
+      hipLaunchKernelGGL((k_raster_px<DBV, PV, CV>), grid, block, 0, stream, rec, rect, it,       \
+                         rec_stride, fillc, list, C, peel, N, H, W, ntx, nty, max_per_tile, rast, \
+                         rast_db);                                                                \
+    else                                                                                          \
+      hipLaunchKernelGGL((k_raster<DBV, PV, CV>), grid, block, 0, stream, rec, rect, it,          \
+                         rec_stride, fillc, list, C, peel, N, H, W, ntx, nty, max_per_tile,       \
+                         slot_keys, rast, rast_db);                                               \
+  } while (0)
 #define DR_RASTER_C(DBV, PV)                                 \
   do {                                                       \
     if (max_per_tile > 0) DR_RASTER(DBV, PV, true);          \
     else DR_RASTER(DBV, PV, false);                          \
   } while (0)
   {
-    DR_TIMED("k_raster", stream);
+    DR_TIMED(px ? "k_raster_px" : "k_raster", stream);
     if (rast_db) {
       if (peel) DR_RASTER_C(true, true); else DR_RASTER_C(true, false);
     } else {
@@ -1142,9 +1332,10 @@ static int raster_fwd(const float* pos, int64_t pos_batch_stride, const int32_t*
 #undef DR_RASTER
   DR_CHECK_LAUNCH();
   if (reuse) return DR_OK;
-  if (!sc->total_pending) {  // largest count of this call, for the next one
+  if (!sc->total_pending) {  // largest count and list entries of this call, for the next one
     hipLaunchKernelGGL(k_tile_max, dim3(1), dim3(256), 0, stream, fillc, n_tiles,
-                       sc->pinned_total_dev);
+                       sc->pinned_total_dev, sc->pinned_total_dev + 1);
+    sc->stat_items = n_items;
     DR_CHECK_LAUNCH();
     DR_CHECK_HIP(hipEventRecord(sc->total_event, stream));
     sc->total_pending = true;
@@ -1159,6 +1350,7 @@ static int raster_fwd(const float* pos, int64_t pos_batch_stride, const int32_t*
   L.n_items = n_items;
   L.max_items = max_items;
   L.C = C;
+  L.px = px;
   L.valid = true;
   return DR_OK;
 }

@@ -30,7 +30,7 @@ Scratch* scratch_for(hipStream_t stream) {
   auto it = g_scratch.find(key);
   if (it != g_scratch.end()) return it->second;
   Scratch* sc = new Scratch();
-  if (hipHostMalloc((void**)&sc->pinned_total, sizeof(int64_t), hipHostMallocDefault) != hipSuccess ||
+  if (hipHostMalloc((void**)&sc->pinned_total, 2 * sizeof(int64_t), hipHostMallocDefault) != hipSuccess ||
       hipHostGetDevicePointer((void**)&sc->pinned_total_dev, sc->pinned_total, 0) != hipSuccess ||
       hipEventCreateWithFlags(&sc->total_event, hipEventDisableTiming) != hipSuccess) {
     set_error("scratch: pinned counter / event allocation failed");
@@ -38,7 +38,7 @@ Scratch* scratch_for(hipStream_t stream) {
     delete sc;
     return nullptr;
   }
-  *sc->pinned_total = 0;
+  sc->pinned_total[0] = sc->pinned_total[1] = 0;
   g_scratch[key] = sc;
   return sc;
 }

@@ -479,3 +479,52 @@ def test_rasterize_again_abi():
                               peelLayer=None if peel is None else host(peel), max_per_tile=0)
         np.testing.assert_array_equal(host(r), rr)
         np.testing.assert_array_equal(host(db), rdb)
+
+
+def _raster_kernels(fn):
+    """fn() with the library's launch timing on: the forward kernels it ran."""
+    import diffrast._lib as L
+    import torch
+    lib = L.load()
+    torch.cuda.synchronize()
+    lib.dr_profile_reset()
+    lib.dr_profile_enable(1)
+    try:
+        fn()
+        torch.cuda.synchronize()
+    finally:
+        lib.dr_profile_enable(0)
+    rep = L.profile_report()
+    return {k for k in ("k_raster", "k_raster_px") if rep.get(k, {}).get("count", 0)}
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("kind", ["small", "large"])
+def test_forward_kernel_choice(kind):
+    """Small triangles (a fine mesh) run the triangle-parallel forward,
+    large ones (two triangles over the whole image) the pixel-parallel one,
+    chosen from the previous call's tiles per triangle; both match the
+    oracle bit for bit, with and without rast_db and a peel layer."""
+    torch = torch_dev()
+    from diffrast import DiffRast
+    H = W = 128
+    if kind == "small":
+        sc = scenes.textured_icosphere(N=2, H=H, W=W, level=4, tex_size=8)
+        pos, tri = sc["pos"], sc["tri"]
+    else:
+        quad = np.array([[-0.9, -0.8, 0.1, 1.0], [0.95, -0.9, 0.3, 1.0],
+                         [0.9, 0.85, 0.5, 1.0], [-0.85, 0.9, 0.2, 1.0]], np.float32)
+        pos = np.stack([quad, quad[[1, 2, 3, 0]] * np.float32([1, 1, 0.5, 1])])
+        tri = np.array([[0, 1, 2], [0, 2, 3]], np.int32)
+    p, t = dev(pos), dev(tri)
+    want = "k_raster" if kind == "small" else "k_raster_px"
+    for _ in range(2):  # the second call sees the first call's statistics
+        ran = _raster_kernels(lambda: DiffRast.rasterize(p, t, (H, W), gradDB=True))
+    assert ran == {want}
+    rast, db = DiffRast.rasterize(p, t, (H, W), gradDB=True)
+    rr, rdb = O.rasterize(pos, tri, (H, W), gradDB=True, max_per_tile=0)
+    np.testing.assert_array_equal(host(rast), rr)
+    np.testing.assert_array_equal(host(db), rdb)
+    r2, _ = DiffRast.rasterize(p, t, (H, W), gradDB=False, peelLayer=rast)
+    rr2, _ = O.rasterize(pos, tri, (H, W), gradDB=False, peelLayer=rr, max_per_tile=0)
+    np.testing.assert_array_equal(host(r2), rr2)
