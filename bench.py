@@ -126,9 +126,10 @@ def _mse_backward(out, target, loss, lib, _lib):
     """MSE loss and its gradient 2/n (out - target) in one kernel, then the
     backward from it."""
     import torch
+    from diffrast.ops import _stream
     d_out = torch.empty_like(out)
     _lib.check(lib.dr_mse_loss(out.data_ptr(), target.data_ptr(), out.numel(), loss.data_ptr(),
-                               d_out.data_ptr(), torch.cuda.current_stream().cuda_stream))
+                               d_out.data_ptr(), _stream()))
     out.backward(d_out)
 
 

@@ -24,6 +24,7 @@ import torch
 
 from . import _lib
 from .ops import DiffRast
+from .ops import _stream as _stream_handle
 
 
 def _ptr(t: Optional[torch.Tensor]):
@@ -31,7 +32,7 @@ def _ptr(t: Optional[torch.Tensor]):
 
 
 def _stream():
-    return torch.cuda.current_stream().cuda_stream
+    return _stream_handle().value
 
 
 # ---------------------------------------------------------------------------

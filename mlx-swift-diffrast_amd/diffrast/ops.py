@@ -68,8 +68,20 @@ def _ptr(t: Optional[torch.Tensor]):
     return None if t is None else ctypes.c_void_p(t.data_ptr())
 
 
+# The current stream's handle.  torch.cuda.current_stream() builds a Stream
+# object per call (~10 us, several calls per op); the raw query returns the
+# same handle directly.
+if hasattr(torch._C, "_cuda_getCurrentRawStream") and hasattr(torch._C, "_cuda_getDevice"):
+    _raw_stream = torch._C._cuda_getCurrentRawStream
+    _cur_device = torch._C._cuda_getDevice
+else:
+    def _raw_stream(index):
+        return torch.cuda.current_stream(index).cuda_stream
+    _cur_device = torch.cuda.current_device
+
+
 def _stream():
-    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    return ctypes.c_void_p(_raw_stream(_cur_device()))
 
 
 def _dev_f32(t: torch.Tensor, name: str) -> torch.Tensor:
@@ -409,7 +421,7 @@ class DiffRast:
         # previous call on this stream, read in place and unchanged since.
         in_place = (isinstance(pos, torch.Tensor) and isinstance(tri, torch.Tensor)
                     and posc.data_ptr() == pos.data_ptr() and tri32.data_ptr() == tri.data_ptr())
-        where = (posc.device.index, torch.cuda.current_stream(posc.device).cuda_stream)
+        where = (posc.device.index, _raw_stream(posc.device.index))
         key = _raster_key(pos, tri, N, H, W, maxPerTile, ranges_host) if in_place else None
         last = _last_raster.get(where)
         again = (peel is not None and key is not None and last is not None
