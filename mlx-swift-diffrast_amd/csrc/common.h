@@ -53,6 +53,7 @@ enum Slot {
   SLOT_AA_REC,        // per (image, triangle) silhouette records (antialias)
   SLOT_DPOS64,        // fp64 accumulator of d_pos (rasterize and antialias backward)
   SLOT_RBWD_REC,      // per (image, triangle) records of the rasterize backward
+  SLOT_DATTR_COPY,    // copies of a small d_attr (interpolate backward)
   SLOT_COUNT
 };
 
@@ -87,6 +88,9 @@ struct Scratch {
   // counts the leading elements of buffer acc64_buf known to be zero.
   const void* acc64_buf = nullptr;
   int64_t acc64_zero = 0;
+  // d_attr copies (SLOT_DATTR_COPY), left zero by k_sum_copies the same way.
+  const void* copy_buf = nullptr;
+  int64_t copy_zero = 0;
   // The previous dr_rasterize_fwd* call on this stream, whose triangle
   // setup and tile lists (SLOT_RAST_*) dr_rasterize_fwd_again may reuse.
   struct {

@@ -144,8 +144,8 @@ __global__ void __launch_bounds__(256) k_interp_bwd(
     const float* __restrict__ rast_db, const int32_t* __restrict__ tri,
     const int32_t* __restrict__ diff_idx, int K_, const float* __restrict__ d_out,
     const float* __restrict__ d_out_da, int N, int H, int W, int ntx, int nty, int V, int T,
-    int A_, float* __restrict__ d_attr, int64_t d_attr_stride, float* __restrict__ d_rast,
-    float* __restrict__ d_rast_db) {
+    int A_, float* __restrict__ d_attr, int64_t d_attr_stride, int ncopy, int64_t copy_stride,
+    float* __restrict__ d_rast, float* __restrict__ d_rast_db) {
   __shared__ LdsTable<(AT > 0 ? AT : 1), 256> tab;  // d_attr rows (or elements) touched by this tile
   __shared__ int s_any[4];  // per wave: a covered pixel
   const int tiles = ntx * nty;
@@ -180,7 +180,8 @@ __global__ void __launch_bounds__(256) k_interp_bwd(
   const float u = r.x, v = r.y;
   const float bw = 1.0f - u - v;
   const float* at = attr + (int64_t)n * attr_stride;
-  float* da = d_attr + (int64_t)n * d_attr_stride;
+  // ncopy > 0: d_attr is copy (workgroup mod ncopy) of ncopy copies
+  float* da = d_attr + (ncopy ? (int64_t)(b % ncopy) * copy_stride : 0) + (int64_t)n * d_attr_stride;
   int i0 = 0, i1 = 0, i2 = 0;
 
   if constexpr (AT > 0) {
@@ -340,6 +341,25 @@ __global__ void __launch_bounds__(256) k_interp_bwd(
   lds_table_flush(tab);
 }
 
+// d_attr[i] = (accumulate ? d_attr[i] : 0) + the sum of the 256 copies'
+// element i, one workgroup per element (thread c reads copy c; the loads
+// are independent, the sum a fixed tree); the copies are left zero.
+__global__ void __launch_bounds__(256) k_sum_copies(float* __restrict__ copies, int64_t n,
+                                                    float* __restrict__ d_attr, int accumulate) {
+  __shared__ float s_w[4];
+  const int64_t i = blockIdx.x;
+  float* p = copies + (int64_t)threadIdx.x * n + i;
+  float v = *p;
+  *p = 0.0f;
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  if ((threadIdx.x & 63) == 0) s_w[threadIdx.x >> 6] = v;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const float s = (s_w[0] + s_w[1]) + (s_w[2] + s_w[3]);
+    d_attr[i] = accumulate ? d_attr[i] + s : s;
+  }
+}
+
 }  // namespace dr
 
 using namespace dr;
@@ -407,13 +427,48 @@ extern "C" int dr_interpolate_bwd(const float* attr, int64_t attr_batch_stride,
   DR_CHECK_ARG(d_attr_batch_stride == 0 || d_attr_batch_stride == (int64_t)V * A,
                "interpolate_bwd: d_attr_batch_stride must be 0 or V*A");
   const int64_t nattr = (d_attr_batch_stride ? (int64_t)N : 1) * V * A;
-  if (!(flags & DR_ACCUMULATE)) DR_CHECK_HIP(fill_async(d_attr, 0.0f, nattr, stream));
   const int ntx = (W + 15) / 16, nty = (H + 15) / 16;
-  const dim3 grid((unsigned)((int64_t)N * ntx * nty));
-  DR_TIMED("k_interp_bwd", stream);
-  DR_INTERP_DISPATCH(k_interp_bwd, grid, attr, attr_batch_stride, rast, rast_db, tri, diff_idx, K,
-                     d_out, d_out_da, N, H, W, ntx, nty, V, T, A, d_attr, d_attr_batch_stride,
-                     d_rast, d_rast_db);
+  const int64_t tiles = (int64_t)N * ntx * nty;
+  const dim3 grid((unsigned)tiles);
+  // A small d_attr (a few shared vertices: every tile adds into the same
+  // few rows, and device atomics on one address are serialised) is summed
+  // into kCopies copies, workgroup b into copy b % kCopies, then added up.
+  constexpr int kCopies = 256;
+  const bool copy = nattr > 0 && nattr <= 4096 && tiles >= 4 * kCopies;
+  float* target = d_attr;
+  if (copy) {
+    Scratch* sc = scratch_for(stream);
+    if (!sc) return DR_ERR_HIP;
+    const int64_t nc = nattr * kCopies;
+    float* c = (float*)scratch_get(sc, stream, SLOT_DATTR_COPY, (size_t)nc * sizeof(float));
+    if (!c) return DR_ERR_MEMORY;
+    if (sc->copy_buf != c) {  // a new buffer: its contents are unknown
+      sc->copy_buf = c;
+      sc->copy_zero = 0;
+    }
+    if (sc->copy_zero < nc) DR_CHECK_HIP(fill_async(c, 0.0f, nc, stream));
+    sc->copy_zero = 0;  // in use until k_sum_copies is queued
+    target = c;
+  } else if (!(flags & DR_ACCUMULATE)) {
+    DR_CHECK_HIP(fill_async(d_attr, 0.0f, nattr, stream));
+  }
+  {
+    DR_TIMED("k_interp_bwd", stream);
+    DR_INTERP_DISPATCH(k_interp_bwd, grid, attr, attr_batch_stride, rast, rast_db, tri, diff_idx,
+                       K, d_out, d_out_da, N, H, W, ntx, nty, V, T, A, target,
+                       d_attr_batch_stride, copy ? kCopies : 0, nattr, d_rast, d_rast_db);
+  }
   DR_CHECK_LAUNCH();
+  if (copy) {
+    {
+      DR_TIMED("k_sum_copies", stream);
+      static_assert(kCopies == 256, "k_sum_copies: one thread per copy");
+      hipLaunchKernelGGL(k_sum_copies, dim3((unsigned)nattr), dim3(kCopies), 0, stream, target,
+                         nattr, d_attr, (flags & DR_ACCUMULATE) ? 1 : 0);
+    }
+    DR_CHECK_LAUNCH();
+    Scratch* sc = scratch_for(stream);
+    if (sc && sc->copy_buf == target) sc->copy_zero = nattr * kCopies;
+  }
   return DR_OK;
 }

@@ -16,14 +16,17 @@ def scene(kind, rng):
     if kind == "icosphere":
         sc = scenes.textured_icosphere(N=2, H=256, W=320, level=4, tex_size=8)
         pos, tri, H, W = sc["pos"], sc["tri"], 256, 320
-    else:
+    elif kind == "hexpie":
         sc = scenes.hex_pie(N=3, H=77, W=131)
         pos, tri, H, W = sc["pos"], sc["tri"], 77, 131
+    else:  # 2,048 tiles on 7 vertices: d_attr summed through its copies
+        sc = scenes.hex_pie(N=2, H=512, W=512)
+        pos, tri, H, W = sc["pos"], sc["tri"], 512, 512
     rast, db = O.rasterize(pos, tri, (H, W), max_per_tile=0)
     return pos, tri, rast, db
 
 
-@pytest.mark.parametrize("kind", ["icosphere", "hexpie"])
+@pytest.mark.parametrize("kind", ["icosphere", "hexpie", "hexpie512"])
 @pytest.mark.parametrize("A,diff,layout", [
     (2, None, "inst"), (2, "all", "shared"), (3, None, "one"), (3, "all", "inst"),
     (4, [1, 3], "shared"), (6, None, "inst"), (5, "all", "one"), (5, [4, 0, 4], "inst")])
@@ -90,3 +93,34 @@ def test_errors():
         DiffRast.interpolate(attr, rast, tri, rastDB=rast, diffAttrs=[2])
     with pytest.raises(ValueError):
         DiffRast.interpolate(dev(np.ones((3, 3, 2), np.float32)), rast, tri)
+
+
+def test_small_d_attr_copies_accumulate():
+    """A d_attr of 7 shared rows over 2,048 tiles is summed through copies;
+    DR_ACCUMULATE adds the call's sum to the buffer, and a second plain
+    call overwrites it (the copies are left zero between calls)."""
+    import ctypes
+    torch = torch_dev()
+    from diffrast import _lib
+    lib = _lib.load()
+    rng = np.random.default_rng(5)
+    pos, tri, rast, db = scene("hexpie512", rng)
+    N, H, W, _ = rast.shape
+    V, A = pos.shape[1], 3
+    attr = rng.normal(size=(V, A)).astype(np.float32)
+    g = rng.normal(size=(N, H, W, A)).astype(np.float32)
+    ref, _, _ = O.interpolate_vjp(attr, rast, tri, g)
+    p = lambda t: ctypes.c_void_p(t.data_ptr())
+    ta, tr, tt, tg = dev(attr), dev(rast), dev(tri), dev(g)
+    d_attr = torch.full((V, A), 1.5, device="cuda")
+    d_rast = torch.empty_like(tr)
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    run = lambda fl: _lib.check(lib.dr_interpolate_bwd(
+        p(ta), 0, p(tr), None, p(tt), None, 0, p(tg), None, N, H, W, V, tri.shape[0], A,
+        p(d_attr), 0, p(d_rast), None, fl, st))
+    run(1)  # accumulate onto 1.5
+    assert_grad_close(host(d_attr) - 1.5, ref, "accumulated d_attr")
+    run(0)
+    assert_grad_close(host(d_attr), ref, "d_attr after the accumulate call")
+    run(0)
+    assert_grad_close(host(d_attr), ref, "d_attr, second plain call")
