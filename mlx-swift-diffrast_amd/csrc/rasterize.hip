@@ -365,11 +365,14 @@ constexpr int kRankMax = 4096;
 // tiles each on average.
 constexpr double kPxTilesPerItem = 8.0;
 
-// Triangle-parallel coverage: candidates staged per round, pixels per work
-// item, work items per pass.
-constexpr int kRChunk = 128;
+// Triangle-parallel coverage: threads per workgroup (each with kRPix of the
+// tile's 256 pixels), candidates staged per round, pixels per work item,
+// work items per pass.
+constexpr int kRThreads = 128;
+constexpr int kRPix = 256 / kRThreads;
+constexpr int kRChunk = 64;
 constexpr int kRSub = 4;
-constexpr int kRItems = 2048;
+constexpr int kRItems = 1024;
 
 // Smallest i in [0, n) with p(i) for p false then true (n if none), and
 // largest i in [0, n) with p(i) for p true then false (-1 if none), from a
@@ -423,7 +426,7 @@ __device__ __forceinline__ unsigned long long zkey(float z, uint32_t id) {
 // rasterized; a list that overflowed its capacity takes the full scan in
 // triangle order and stops at the limit.
 template <bool DB, bool PEEL, bool CAPPED>
-__global__ void __launch_bounds__(256) k_raster(
+__global__ void __launch_bounds__(kRThreads) k_raster(
     const TriRec* __restrict__ rec, const int4* __restrict__ rect, Items it, int64_t rec_stride,
     const int* __restrict__ cnt, const int* __restrict__ list, int cap,
     const float* __restrict__ peel, int N, int H, int W, int ntx, int nty, int max_per_tile,
@@ -476,46 +479,17 @@ __global__ void __launch_bounds__(256) k_raster(
   }
   const int x0t = tx * kTile, y0t = ty * kTile;
   const int nx = min(kTile, W - x0t), ny = min(kTile, H - y0t);  // tile pixels inside the image
-  const int lx = tid & 15, ly = tid >> 4;
-  const int pw = x0t + lx, ph = y0t + ly;
-  const bool valid = lx < nx && ly < ny;
-  const int64_t pix = ((int64_t)n * H + min(ph, H - 1)) * W + min(pw, W - 1);
   const int64_t rbase = (int64_t)n * rec_stride;
-  float peel_z = -1e30f;
-  if (PEEL && valid) {
-    const float4 pl = *reinterpret_cast<const float4*>(peel + pix * 4);
-    if (pl.w > 0.0f) peel_z = pl.z;
-  }
-  // the pixel centre as the reference computes it
-  const float x = 2.0f * ((float)pw + 0.5f) / (float)W - 1.0f;
-  const float y = 1.0f - 2.0f * ((float)ph + 0.5f) / (float)H;
-
-  if (count > cap) {
-    // The tile's list overflowed its capacity (sized from an earlier
-    // call): each thread scans the image's whole triangle range for its
-    // pixel with the same tile test the binning uses (same candidate set,
-    // so the same result), wave-uniform up to its 16x4 strip's box.
-    const int sy0 = min(y0t + (tid >> 6) * 4, H - 1), sy1 = min(sy0 + 3, H - 1);
-    const float xw0 = 2.0f * ((float)x0t + 0.5f) / (float)W - 1.0f;
-    const float xw1 = 2.0f * ((float)(x0t + nx - 1) + 0.5f) / (float)W - 1.0f;
-    const float yw1 = 1.0f - 2.0f * ((float)sy0 + 0.5f) / (float)H;
-    const float yw0 = 1.0f - 2.0f * ((float)sy1 + 0.5f) / (float)H;
-    int t0 = 0, t1 = it.T;
-    if (it.prefix != nullptr) {
-      t0 = (int)it.start[n];
-      t1 = t0 + (int)(it.prefix[n + 1] - it.prefix[n]);
-    }
-    Best best = {1e30f, 0.0f, 0.0f, -1};
-    int taken = 0;  // tile candidates so far, in triangle order
-    for (int t = t0; t < t1; ++t) {
-      const int4 rc = rect[rbase + t];
-      if (rc.x < 0 || tx < rc.x || tx > rc.y || ty < rc.z || ty > rc.w) continue;
-      if (CAPPED && ++taken > scan_limit) break;  // uniform: the same tile test everywhere
-      const TriRec R = load_rec(rec, rbase + t);
-      if (R.r3.y < xw0 || R.r3.x > xw1 || R.r3.w < yw0 || R.r3.z > yw1) continue;
-      if (valid) test_tri(R, t, x, y, peel_z, best);
-    }
-    if (!valid) return;
+  // thread tid has tile pixels tid + q * kRThreads (q < kRPix): column
+  // tid & 15, rows (tid >> 4) + q * kRThreads / 16
+  auto pix_of = [&](int q, int& lx, int& ly, bool& valid) -> int64_t {
+    const int p = tid + q * kRThreads;
+    lx = p & 15;
+    ly = p >> 4;
+    valid = lx < nx && ly < ny;
+    return ((int64_t)n * H + min(y0t + ly, H - 1)) * W + min(x0t + lx, W - 1);
+  };
+  auto write_px = [&](int64_t pix, const Best& best) {
     float4 o4 = make_float4(0.f, 0.f, 0.f, 0.f), d4 = o4;
     if (best.t >= 0) {
       o4 = make_float4(best.u, best.v, best.z, (float)(best.t + 1));
@@ -528,11 +502,70 @@ __global__ void __launch_bounds__(256) k_raster(
     }
     *reinterpret_cast<float4*>(rast + pix * 4) = o4;
     if (DB) *reinterpret_cast<float4*>(rast_db + pix * 4) = d4;
+  };
+  float peel_z[kRPix];
+#pragma unroll
+  for (int q = 0; q < kRPix; ++q) {
+    int lx, ly;
+    bool valid;
+    const int64_t pix = pix_of(q, lx, ly, valid);
+    peel_z[q] = -1e30f;
+    if (PEEL && valid) {
+      const float4 pl = *reinterpret_cast<const float4*>(peel + pix * 4);
+      if (pl.w > 0.0f) peel_z[q] = pl.z;
+    }
+  }
+
+  if (count > cap) {
+    // The tile's list overflowed its capacity (sized from an earlier
+    // call): each thread scans the image's whole triangle range for its
+    // pixels with the same tile test the binning uses (same candidate set,
+    // so the same result), uniform up to the tile's pixel-centre box.
+    const float xw0 = 2.0f * ((float)x0t + 0.5f) / (float)W - 1.0f;
+    const float xw1 = 2.0f * ((float)(x0t + nx - 1) + 0.5f) / (float)W - 1.0f;
+    const float yw1 = 1.0f - 2.0f * ((float)y0t + 0.5f) / (float)H;
+    const float yw0 = 1.0f - 2.0f * ((float)(y0t + ny - 1) + 0.5f) / (float)H;
+    int t0 = 0, t1 = it.T;
+    if (it.prefix != nullptr) {
+      t0 = (int)it.start[n];
+      t1 = t0 + (int)(it.prefix[n + 1] - it.prefix[n]);
+    }
+    Best best[kRPix];
+    float px[kRPix], py[kRPix];
+#pragma unroll
+    for (int q = 0; q < kRPix; ++q) {
+      int lx, ly;
+      bool valid;
+      pix_of(q, lx, ly, valid);
+      best[q] = {1e30f, 0.0f, 0.0f, -1};
+      px[q] = 2.0f * ((float)(x0t + lx) + 0.5f) / (float)W - 1.0f;
+      py[q] = 1.0f - 2.0f * ((float)(y0t + ly) + 0.5f) / (float)H;
+    }
+    int taken = 0;  // tile candidates so far, in triangle order
+    for (int t = t0; t < t1; ++t) {
+      const int4 rc = rect[rbase + t];
+      if (rc.x < 0 || tx < rc.x || tx > rc.y || ty < rc.z || ty > rc.w) continue;
+      if (CAPPED && ++taken > scan_limit) break;  // uniform: the same tile test everywhere
+      const TriRec R = load_rec(rec, rbase + t);
+      if (R.r3.y < xw0 || R.r3.x > xw1 || R.r3.w < yw0 || R.r3.z > yw1) continue;
+#pragma unroll
+      for (int q = 0; q < kRPix; ++q) test_tri(R, t, px[q], py[q], peel_z[q], best[q]);
+    }
+#pragma unroll
+    for (int q = 0; q < kRPix; ++q) {
+      int lx, ly;
+      bool valid;
+      const int64_t pix = pix_of(q, lx, ly, valid);
+      if (valid) write_px(pix, best[q]);
+    }
     return;
   }
 
-  s_zb[tid] = ~0ull;
-  if (PEEL) s_pz[tid] = peel_z;
+#pragma unroll
+  for (int q = 0; q < kRPix; ++q) {
+    s_zb[tid + q * kRThreads] = ~0ull;
+    if (PEEL) s_pz[tid + q * kRThreads] = peel_z[q];
+  }
   if (tid < 16) s_x[tid] = 2.0f * ((float)(x0t + tid) + 0.5f) / (float)W - 1.0f;
   else if (tid < 32) s_y[tid - 16] = 1.0f - 2.0f * ((float)(y0t + tid - 16) + 0.5f) / (float)H;
   if (tid == 0) s_total[0] = s_total[1] = 0;
@@ -561,11 +594,11 @@ __global__ void __launch_bounds__(256) k_raster(
                                 [&](int i) { return !(s_y[i] < miny); });
       if (bx0 <= bx1 && by0 <= by1) {
         const int bw = bx1 - bx0 + 1, bh = by1 - by0 + 1;
-        pieces = (bw * bh + kRSub - 1) / kRSub;
-        base = atomicAdd(&s_total[round & 1], pieces);
         s_rec[tid] = R;
         s_t[tid] = t;
         s_box[tid] = bx0 | (by0 << 4) | ((bw - 1) << 8) | ((bh - 1) << 12);
+        pieces = (bw * bh + kRSub - 1) / kRSub;
+        base = atomicAdd(&s_total[round & 1], pieces);
         for (int q = 0; q < pieces && base + q < kRItems; ++q)
           s_item[base + q] = (uint16_t)((tid << 6) | q);
       }
@@ -619,25 +652,23 @@ __global__ void __launch_bounds__(256) k_raster(
     }
   }
   __syncthreads();
-  // 3) each thread its pixel: the winner's outputs, recomputed
-  if (!valid) return;
-  const unsigned long long key = s_zb[tid];
-  float4 o4 = make_float4(0.f, 0.f, 0.f, 0.f), d4 = o4;
-  if (key != ~0ull) {
-    const uint32_t id = (uint32_t)key;
-    const int t = slots ? (int)(id >> 7) : (int)id;
-    const TriRec R = slots ? s_rec[id & 127] : load_rec(rec, rbase + t);
+  // 3) each thread its pixels: the winner's outputs, recomputed
+#pragma unroll
+  for (int q = 0; q < kRPix; ++q) {
+    int lx, ly;
+    bool valid;
+    const int64_t pix = pix_of(q, lx, ly, valid);
+    if (!valid) continue;
+    const unsigned long long key = s_zb[tid + q * kRThreads];
     Best best = {1e30f, 0.0f, 0.0f, -1};
-    test_tri(R, t, x, y, -1e30f, best);  // the same expressions as the scan
-    if (best.t >= 0) o4 = make_float4(best.u, best.v, best.z, (float)(t + 1));
-    if (DB && best.t >= 0) {  // Rasterize.swift:586-598
-      const float k_x = 2.0f / (float)W, k_y = -2.0f / (float)H;
-      d4 = make_float4((R.r1.y - R.r0.y) * R.r2.z * k_x, (R.r0.x - R.r1.x) * R.r2.z * k_y,
-                       (R.r0.y - R.r0.w) * R.r2.z * k_x, (R.r0.z - R.r0.x) * R.r2.z * k_y);
+    if (key != ~0ull) {
+      const uint32_t id = (uint32_t)key;
+      const int t = slots ? (int)(id >> 7) : (int)id;
+      const TriRec R = slots ? s_rec[id & 127] : load_rec(rec, rbase + t);
+      test_tri(R, t, s_x[lx], s_y[ly], -1e30f, best);  // the same expressions as the scan
     }
+    write_px(pix, best);
   }
-  *reinterpret_cast<float4*>(rast + pix * 4) = o4;
-  if (DB) *reinterpret_cast<float4*>(rast_db + pix * 4) = d4;
 }
 
 // The same forward, pixel-parallel, for large triangles (a candidate's box
@@ -1311,8 +1342,8 @@ static int raster_fwd(const float* pos, int64_t pos_batch_stride, const int32_t*
                          rec_stride, fillc, list, C, peel, N, H, W, ntx, nty, max_per_tile, rast, \
                          rast_db);                                                                \
     else                                                                                          \
-      hipLaunchKernelGGL((k_raster<DBV, PV, CV>), grid, block, 0, stream, rec, rect, it,          \
-                         rec_stride, fillc, list, C, peel, N, H, W, ntx, nty, max_per_tile,       \
+      hipLaunchKernelGGL((k_raster<DBV, PV, CV>), grid, dim3(kRThreads), 0, stream, rec, rect,   \
+                         it, rec_stride, fillc, list, C, peel, N, H, W, ntx, nty, max_per_tile,   \
                          slot_keys, rast, rast_db);                                               \
   } while (0)
 #define DR_RASTER_C(DBV, PV)                                 \
