@@ -528,3 +528,30 @@ def test_forward_kernel_choice(kind):
     r2, _ = DiffRast.rasterize(p, t, (H, W), gradDB=False, peelLayer=rast)
     rr2, _ = O.rasterize(pos, tri, (H, W), gradDB=False, peelLayer=rr, max_per_tile=0)
     np.testing.assert_array_equal(host(r2), rr2)
+
+
+def test_capped_large_triangles_pixel_parallel():
+    """300 full-screen triangles over 64 tiles each take the pixel-parallel
+    forward; with a per-tile cap (ranked in LDS, or the ordered full scan
+    while the list capacity is short) every pixel shows the cap's last
+    triangle, bit-exact against the oracle."""
+    torch = torch_dev()
+    from diffrast import DiffRast, _lib
+    torch.cuda.synchronize()
+    assert _lib.load().dr_release_scratch() == 0
+    sc = scenes.tier1_triangle(H=128, W=128)
+    check_fwd(sc["pos"], sc["tri"], 128, 128)  # a short list capacity first
+    T = 300
+    p = np.tile(np.array([[-3, 3, 0, 1], [-3, -3, 0, 1], [3, 0, 0, 1]], np.float32), (T, 1))
+    p[:, 2] = np.repeat(np.linspace(0.9, -0.9, T), 3)
+    tri = np.arange(3 * T, dtype=np.int32).reshape(T, 3)
+    for cap in (128, 128, 5, 300, 0):
+        if cap:
+            r = check_capped(p[None], tri, 128, 128, cap)
+            assert (r[..., 3] == min(cap, T)).all(), cap
+        else:
+            check_fwd(p[None], tri, 128, 128)
+        torch.cuda.synchronize()
+    ran = _raster_kernels(lambda: DiffRast.rasterize(dev(p[None]), dev(tri), (128, 128),
+                                                     maxPerTile=16))
+    assert ran == {"k_raster_px"}
