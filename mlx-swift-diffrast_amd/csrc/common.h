@@ -74,6 +74,14 @@ struct Scratch {
   int bin_cap = 0;  // slots per tile list, 0 = not known yet
   int64_t stat_items = 0;
   double tiles_per_item = 0.0;
+  // The LDS binning's fill pass writes the same two figures per wave
+  // instead (its largest final tile count, its list entries), here, for up
+  // to kWaveStatsMax waves; the host reduces the stat_waves pairs into
+  // pinned_total once total_event has passed.  No kernel then reduces them.
+  static constexpr int64_t kWaveStatsMax = 16384;
+  int64_t* wave_stats = nullptr;      // 2 * kWaveStatsMax values
+  int64_t* wave_stats_dev = nullptr;  // the same memory as a kernel writes it
+  int64_t stat_waves = 0;
   // Range-mode item prefix, staged through a ring of pinned host buffers:
   // a buffer is reused once the copy that read it has run (its event), so
   // a call waits only when it is kStageRing calls ahead of the device.

@@ -260,11 +260,17 @@ __global__ void __launch_bounds__(256) k_bin_fill(Items it, int64_t n_items, int
 constexpr int kBinChunk = 1024;
 constexpr int kBinLdsTiles = 16384;
 
+// With `wstats` (the fill pass, when the caller wants this call's tile
+// statistics): each wave writes its largest final tile count (the returned
+// count plus its own, for the chunk that adds last) and its list entries to
+// wstats[2 * (4 * workgroup + wave) + {0, 1}], pinned host memory that the
+// host reduces after the kernel has run.  Waves of an empty chunk write 0s.
 template <bool FILL>
 __global__ void __launch_bounds__(256) k_bin_lds(Items it, int chunks,
                                                  const int4* __restrict__ rect, int ntx,
                                                  int tiles, int* __restrict__ cnt,
-                                                 int* __restrict__ list, int cap) {
+                                                 int* __restrict__ list, int cap,
+                                                 int64_t* __restrict__ wstats) {
   extern __shared__ int s_tile[];
   const int n = (int)blockIdx.x / chunks;
   const int c = (int)blockIdx.x - n * chunks;
@@ -280,40 +286,52 @@ __global__ void __launch_bounds__(256) k_bin_lds(Items it, int chunks,
   }
   const int64_t b0 = i0 + (int64_t)c * kBinChunk;
   const int64_t b1 = min(i1, b0 + kBinChunk);
-  if (b0 >= b1) return;  // uniform over the workgroup
   const int tid = threadIdx.x;
-  for (int k = tid; k < tiles; k += 256) s_tile[k] = 0;
-  __syncthreads();
-  for (int64_t i = b0 + tid; i < b1; i += 256) {
-    const int4 rc = rect[r0 + (i - i0)];
-    if (rc.x < 0) continue;
-    for (int y = rc.z; y <= rc.w; ++y)
-      for (int x = rc.x; x <= rc.y; ++x) atomicAdd(&s_tile[y * ntx + x], 1);
-  }
-  __syncthreads();
-  int* cimg = cnt + (int64_t)n * tiles;
-  for (int k = tid; k < tiles; k += 256) {
-    const int v = s_tile[k];
-    if (v > 0) {
-      const int at = atomicAdd(&cimg[k], v);
-      if (FILL) s_tile[k] = at;
+  int m = 0;        // largest final count this workgroup saw
+  long long e = 0;  // list entries this workgroup added
+  if (b0 < b1) {    // uniform over the workgroup
+    for (int k = tid; k < tiles; k += 256) s_tile[k] = 0;
+    __syncthreads();
+    for (int64_t i = b0 + tid; i < b1; i += 256) {
+      const int4 rc = rect[r0 + (i - i0)];
+      if (rc.x < 0) continue;
+      for (int y = rc.z; y <= rc.w; ++y)
+        for (int x = rc.x; x <= rc.y; ++x) atomicAdd(&s_tile[y * ntx + x], 1);
+    }
+    __syncthreads();
+    int* cimg = cnt + (int64_t)n * tiles;
+    for (int k = tid; k < tiles; k += 256) {
+      const int v = s_tile[k];
+      if (v > 0) {
+        const int at = atomicAdd(&cimg[k], v);
+        if (FILL) s_tile[k] = at;
+        m = max(m, at + v);
+        e += v;
+      }
+    }
+    if (FILL) {
+      __syncthreads();
+      int* limg = list + (int64_t)n * tiles * cap;
+      for (int64_t i = b0 + tid; i < b1; i += 256) {
+        const int64_t r = r0 + (i - i0);
+        const int4 rc = rect[r];
+        if (rc.x < 0) continue;
+        const int t = (int)(it.prefix ? r : i - i0);
+        for (int y = rc.z; y <= rc.w; ++y)
+          for (int x = rc.x; x <= rc.y; ++x) {
+            const int j = y * ntx + x;
+            const int p = atomicAdd(&s_tile[j], 1);
+            if (p < cap) limg[(int64_t)j * cap + p] = t;
+          }
+      }
     }
   }
-  if (!FILL) return;
-  __syncthreads();
-  int* limg = list + (int64_t)n * tiles * cap;
-  for (int64_t i = b0 + tid; i < b1; i += 256) {
-    const int64_t r = r0 + (i - i0);
-    const int4 rc = rect[r];
-    if (rc.x < 0) continue;
-    const int t = (int)(it.prefix ? r : i - i0);
-    for (int y = rc.z; y <= rc.w; ++y)
-      for (int x = rc.x; x <= rc.y; ++x) {
-        const int j = y * ntx + x;
-        const int p = atomicAdd(&s_tile[j], 1);
-        if (p < cap) limg[(int64_t)j * cap + p] = t;
-      }
-  }
+  if (wstats == nullptr) return;  // uniform
+  m = wave_max(m);
+  for (int o = 32; o > 0; o >>= 1) e += __shfl_xor(e, o, kWave);
+  if ((tid & 63) == 0)
+    *reinterpret_cast<longlong2*>(wstats + 2 * ((int64_t)blockIdx.x * 4 + (tid >> 6))) =
+        make_longlong2((long long)m, e);
 }
 
 struct Best {
@@ -1138,23 +1156,29 @@ static int bin_lds_chunks(int N, int tiles, int64_t max_items) {
 }
 
 // Per-tile counts (FILL false) or counts and lists (FILL true) of the items.
-static void launch_binning(bool fill, const Items& it, int64_t n_items, int64_t max_items, int N,
-                           const int4* rect, int ntx, int tiles, int* cnt, int* list, int cap,
-                           hipStream_t stream) {
-  if (n_items == 0) return;
+// With `wstats` (room for `wcap` waves), the LDS fill pass also writes the
+// per-wave tile statistics; returns the number of waves that did (0: none,
+// k_tile_max must compute them).
+static int64_t launch_binning(bool fill, const Items& it, int64_t n_items, int64_t max_items,
+                              int N, const int4* rect, int ntx, int tiles, int* cnt, int* list,
+                              int cap, hipStream_t stream, int64_t* wstats = nullptr,
+                              int64_t wcap = 0) {
+  if (n_items == 0) return 0;
   const int chunks = bin_lds_chunks(N, tiles, max_items);
   if (chunks > 0) {
     const dim3 grid((unsigned)((int64_t)N * chunks));
     const size_t lds = (size_t)tiles * sizeof(int);
     if (fill) {
+      const int64_t waves = (int64_t)N * chunks * 4;
+      if (waves > wcap) wstats = nullptr;
       DR_TIMED("k_bin_fill", stream);
       hipLaunchKernelGGL(k_bin_lds<true>, grid, dim3(256), lds, stream, it, chunks, rect, ntx,
-                         tiles, cnt, list, cap);
-    } else {
-      DR_TIMED("k_bin_count", stream);
-      hipLaunchKernelGGL(k_bin_lds<false>, grid, dim3(256), lds, stream, it, chunks, rect, ntx,
-                         tiles, cnt, list, cap);
+                         tiles, cnt, list, cap, wstats);
+      return wstats ? waves : 0;
     }
+    DR_TIMED("k_bin_count", stream);
+    hipLaunchKernelGGL(k_bin_lds<false>, grid, dim3(256), lds, stream, it, chunks, rect, ntx,
+                       tiles, cnt, list, cap, (int64_t*)nullptr);
   } else if (fill) {
     DR_TIMED("k_bin_fill", stream);
     hipLaunchKernelGGL(k_bin_fill, dim3(grid_for(n_items, 256)), dim3(256), 0, stream, it,
@@ -1164,6 +1188,7 @@ static void launch_binning(bool fill, const Items& it, int64_t n_items, int64_t 
     hipLaunchKernelGGL(k_bin_count, dim3(grid_for(n_items, 256)), dim3(256), 0, stream, it,
                        n_items, N, rect, ntx, tiles, cnt);
   }
+  return 0;
 }
 
 extern "C" int dr_rasterize_tile_counts(const float* pos, int64_t pos_batch_stride,
@@ -1258,6 +1283,8 @@ static int raster_fwd(const float* pos, int64_t pos_batch_stride, const int32_t*
   int* fillc;
   int* list;
   int C;
+  bool want_stats = false;
+  int64_t stat_waves = 0;
   if (reuse) {  // the previous call's setup and lists, untouched since
     if (ranges_host) {
       int64_t* d = (int64_t*)sc->ptr[SLOT_RAST_ITEMS];
@@ -1301,6 +1328,15 @@ static int raster_fwd(const float* pos, int64_t pos_batch_stride, const int32_t*
     sc->tiles_per_item = (double)sc->pinned_total[1] / (double)std::max<int64_t>(items, 1);
   };
   if (sc->total_pending && hipEventQuery(sc->total_event) == hipSuccess) {
+    if (sc->stat_waves > 0) {  // the binning's per-wave figures
+      int64_t mx = 0, sum = 0;
+      for (int64_t w = 0; w < sc->stat_waves; ++w) {
+        mx = std::max(mx, sc->wave_stats[2 * w]);
+        sum += sc->wave_stats[2 * w + 1];
+      }
+      sc->pinned_total[0] = mx;
+      sc->pinned_total[1] = sum;
+    }
     const int64_t mx = sc->pinned_total[0];
     take_stats(sc->stat_items);
     sc->total_pending = false;
@@ -1327,7 +1363,12 @@ static int raster_fwd(const float* pos, int64_t pos_batch_stride, const int32_t*
   if (!list) return DR_ERR_MEMORY;
 
   DR_CHECK_HIP(fill_async(fillc, 0, n_tiles, stream));
-  launch_binning(true, it, n_items, max_items, N, rect, ntx, tiles, fillc, list, C, stream);
+  // this call's largest count and list entries, for the next call
+  // (when the previous ones have been read)
+  want_stats = !sc->total_pending;
+  stat_waves = launch_binning(true, it, n_items, max_items, N, rect, ntx, tiles, fillc, list, C,
+                              stream, want_stats ? sc->wave_stats_dev : nullptr,
+                              Scratch::kWaveStatsMax);
   DR_CHECK_LAUNCH();
   }
   const dim3 grid((unsigned)n_tiles), block(256);
@@ -1363,11 +1404,14 @@ static int raster_fwd(const float* pos, int64_t pos_batch_stride, const int32_t*
 #undef DR_RASTER
   DR_CHECK_LAUNCH();
   if (reuse) return DR_OK;
-  if (!sc->total_pending) {  // largest count and list entries of this call, for the next one
-    hipLaunchKernelGGL(k_tile_max, dim3(1), dim3(256), 0, stream, fillc, n_tiles,
-                       sc->pinned_total_dev, sc->pinned_total_dev + 1);
+  if (want_stats) {  // largest count and list entries of this call, for the next one
+    if (stat_waves == 0) {
+      hipLaunchKernelGGL(k_tile_max, dim3(1), dim3(256), 0, stream, fillc, n_tiles,
+                         sc->pinned_total_dev, sc->pinned_total_dev + 1);
+      DR_CHECK_LAUNCH();
+    }
     sc->stat_items = n_items;
-    DR_CHECK_LAUNCH();
+    sc->stat_waves = stat_waves;
     DR_CHECK_HIP(hipEventRecord(sc->total_event, stream));
     sc->total_pending = true;
   }

@@ -32,9 +32,13 @@ Scratch* scratch_for(hipStream_t stream) {
   Scratch* sc = new Scratch();
   if (hipHostMalloc((void**)&sc->pinned_total, 2 * sizeof(int64_t), hipHostMallocDefault) != hipSuccess ||
       hipHostGetDevicePointer((void**)&sc->pinned_total_dev, sc->pinned_total, 0) != hipSuccess ||
+      hipHostMalloc((void**)&sc->wave_stats, 2 * Scratch::kWaveStatsMax * sizeof(int64_t),
+                    hipHostMallocDefault) != hipSuccess ||
+      hipHostGetDevicePointer((void**)&sc->wave_stats_dev, sc->wave_stats, 0) != hipSuccess ||
       hipEventCreateWithFlags(&sc->total_event, hipEventDisableTiming) != hipSuccess) {
     set_error("scratch: pinned counter / event allocation failed");
     if (sc->pinned_total) (void)hipHostFree(sc->pinned_total);
+    if (sc->wave_stats) (void)hipHostFree(sc->wave_stats);
     delete sc;
     return nullptr;
   }
@@ -244,6 +248,7 @@ int dr_release_scratch(void) {
     for (int s = 0; s < dr::SLOT_COUNT; ++s)
       if (sc->ptr[s]) (void)hipFree(sc->ptr[s]);
     if (sc->pinned_total) (void)hipHostFree(sc->pinned_total);
+    if (sc->wave_stats) (void)hipHostFree(sc->wave_stats);
     if (sc->total_event) (void)hipEventDestroy(sc->total_event);
     for (int r = 0; r < dr::Scratch::kStageRing; ++r) {
       if (sc->stage_event[r]) (void)hipEventDestroy(sc->stage_event[r]);
