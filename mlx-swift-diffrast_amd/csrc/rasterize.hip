@@ -507,12 +507,13 @@ __global__ void __launch_bounds__(kRThreads) k_raster(
     valid = lx < nx && ly < ny;
     return ((int64_t)n * H + min(y0t + ly, H - 1)) * W + min(x0t + lx, W - 1);
   };
-  auto write_px = [&](int64_t pix, const Best& best) {
+  // R: the winner's record when the caller has it (else it is loaded)
+  auto write_px = [&](int64_t pix, const Best& best, const TriRec* Rw) {
     float4 o4 = make_float4(0.f, 0.f, 0.f, 0.f), d4 = o4;
     if (best.t >= 0) {
       o4 = make_float4(best.u, best.v, best.z, (float)(best.t + 1));
       if (DB) {  // Rasterize.swift:586-598
-        const TriRec R = load_rec(rec, rbase + best.t);
+        const TriRec R = Rw ? *Rw : load_rec(rec, rbase + best.t);
         const float k_x = 2.0f / (float)W, k_y = -2.0f / (float)H;
         d4 = make_float4((R.r1.y - R.r0.y) * R.r2.z * k_x, (R.r0.x - R.r1.x) * R.r2.z * k_y,
                          (R.r0.y - R.r0.w) * R.r2.z * k_x, (R.r0.z - R.r0.x) * R.r2.z * k_y);
@@ -574,7 +575,7 @@ __global__ void __launch_bounds__(kRThreads) k_raster(
       int lx, ly;
       bool valid;
       const int64_t pix = pix_of(q, lx, ly, valid);
-      if (valid) write_px(pix, best[q]);
+      if (valid) write_px(pix, best[q], nullptr);
     }
     return;
   }
@@ -679,13 +680,14 @@ __global__ void __launch_bounds__(kRThreads) k_raster(
     if (!valid) continue;
     const unsigned long long key = s_zb[tid + q * kRThreads];
     Best best = {1e30f, 0.0f, 0.0f, -1};
+    TriRec R;
     if (key != ~0ull) {
       const uint32_t id = (uint32_t)key;
       const int t = slots ? (int)(id >> 7) : (int)id;
-      const TriRec R = slots ? s_rec[id & 127] : load_rec(rec, rbase + t);
+      R = slots ? s_rec[id & 127] : load_rec(rec, rbase + t);
       test_tri(R, t, s_x[lx], s_y[ly], -1e30f, best);  // the same expressions as the scan
     }
-    write_px(pix, best);
+    write_px(pix, best, &R);  // R is read only when best.t >= 0, i.e. it was set
   }
 }
 
