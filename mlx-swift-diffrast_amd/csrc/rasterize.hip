@@ -30,12 +30,16 @@ struct alignas(16) TriRec {
   float4 r0, r1, r2, r3;
 };
 
-// Rasterize.swift:280-328 (+ the AABB and tile range of :191-223).
+// Rasterize.swift:280-328 (+ the AABB and tile range of :191-223).  The
+// first nzero threads also clear zero[0, nzero) (the fill pass's counters,
+// which nothing reads before the binning), sparing a fill launch.
 __global__ void __launch_bounds__(256) k_setup(const float* __restrict__ pos, int64_t pos_stride,
                                                const int32_t* __restrict__ tri, int Npos, int V,
                                                int T, int H, int W, TriRec* __restrict__ rec,
-                                               int4* __restrict__ rect) {
+                                               int4* __restrict__ rect, int* __restrict__ zero,
+                                               int64_t nzero) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < nzero) zero[i] = 0;
   if (i >= (int64_t)Npos * T) return;
   int64_t n;
   int t;
@@ -1221,7 +1225,7 @@ extern "C" int dr_rasterize_tile_counts(const float* pos, int64_t pos_batch_stri
     DR_TIMED("k_setup", stream);
     hipLaunchKernelGGL(k_setup, dim3(grid_for(n_rec, 256)), dim3(256), 0, stream, pos,
                        ranges_host ? (int64_t)0 : pos_batch_stride, tri, Npos, V, T, H, W, rec,
-                       rect);
+                       rect, (int*)nullptr, (int64_t)0);
     DR_CHECK_LAUNCH();
   }
   DR_CHECK_HIP(fill_async(counts, 0, n_tiles, stream));
@@ -1311,12 +1315,14 @@ static int raster_fwd(const float* pos, int64_t pos_batch_stride, const int32_t*
   int* cnt = (int*)cbuf;
   fillc = cnt + n_tiles;
 
-  if (n_rec > 0) {
+  if (n_rec > 0) {  // also clears the fill pass's counters
     DR_TIMED("k_setup", stream);
-    hipLaunchKernelGGL(k_setup, dim3(grid_for(n_rec, 256)), dim3(256), 0, stream, pos,
-                       ranges_host ? (int64_t)0 : pos_batch_stride, tri, Npos, V, T, H, W, rec,
-                       rect);
+    hipLaunchKernelGGL(k_setup, dim3(grid_for(std::max(n_rec, n_tiles), 256)), dim3(256), 0,
+                       stream, pos, ranges_host ? (int64_t)0 : pos_batch_stride, tri, Npos, V, T,
+                       H, W, rec, rect, fillc, n_tiles);
     DR_CHECK_LAUNCH();
+  } else {
+    DR_CHECK_HIP(fill_async(fillc, 0, n_tiles, stream));
   }
 
   // Per-tile list capacity: the largest tile count seen so far plus a
@@ -1364,9 +1370,8 @@ static int raster_fwd(const float* pos, int64_t pos_batch_stride, const int32_t*
   list = (int*)scratch_get(sc, stream, SLOT_RAST_LIST, (size_t)n_tiles * C * 4);
   if (!list) return DR_ERR_MEMORY;
 
-  DR_CHECK_HIP(fill_async(fillc, 0, n_tiles, stream));
-  // this call's largest count and list entries, for the next call
-  // (when the previous ones have been read)
+  // (fillc was cleared with the setup) this call's largest count and list
+  // entries, for the next call (when the previous ones have been read)
   want_stats = !sc->total_pending;
   stat_waves = launch_binning(true, it, n_items, max_items, N, rect, ntx, tiles, fillc, list, C,
                               stream, want_stats ? sc->wave_stats_dev : nullptr,
