@@ -108,6 +108,15 @@ def _dev_i32(t, name: str, device) -> torch.Tensor:
 _last_raster = {}
 
 
+def _grad_buf(t, zero=False):
+    """A float32 tensor of t's shape with the standard contiguous strides,
+    for a gradient returned to autograd: a size-1 dimension of the input
+    may carry any stride, and autograd copies a returned gradient whose
+    strides differ from the standard ones there instead of keeping it as
+    the leaf's .grad."""
+    return (torch.zeros if zero else torch.empty)(t.shape, device=t.device, dtype=torch.float32)
+
+
 def _raster_key(pos, tri, N, H, W, max_per_tile, ranges_host):
     return (pos._version, tri._version, tuple(pos.shape), tuple(tri.shape), N, H, W,
             int(max_per_tile), None if ranges_host is None else ranges_host.tobytes())
@@ -140,12 +149,12 @@ class _RasterizeFn(torch.autograd.Function):
         pos, tri, rast = ctx.saved_tensors
         range_mode, N, V, H, W, grad_db = ctx.meta
         if d_rast is None:
-            d_rast = torch.zeros_like(rast)
+            d_rast = _grad_buf(rast, zero=True)
         d_rast = d_rast.to(torch.float32).contiguous()
         db = None
         if grad_db and d_rast_db is not None:
             db = d_rast_db.to(torch.float32).contiguous()
-        d_pos = torch.empty_like(pos)
+        d_pos = _grad_buf(pos)
         _lib.check(lib.dr_rasterize_bwd(
             _ptr(pos), 0 if range_mode else V * 4, _ptr(tri), _ptr(rast), _ptr(d_rast), _ptr(db),
             N, V, tri.shape[0], H, W, _ptr(d_pos), 0, _stream()))
@@ -186,9 +195,9 @@ class _InterpolateFn(torch.autograd.Function):
         if K:
             d_out_da = torch.zeros((N, H, W, 2 * K), device=rast.device) if d_out_da is None \
                 else d_out_da.to(torch.float32).contiguous()
-        d_attr = torch.empty_like(attr)
-        d_rast = torch.empty_like(rast)
-        d_rast_db = torch.empty_like(rast) if K else None
+        d_attr = _grad_buf(attr)
+        d_rast = _grad_buf(rast)
+        d_rast_db = _grad_buf(rast) if K else None
         _lib.check(lib.dr_interpolate_bwd(
             _ptr(attr), stride, _ptr(rast), _ptr(rast_db), _ptr(tri), _ptr(diff_idx), K,
             _ptr(d_out), _ptr(d_out_da) if K else None, N, H, W, V, tri.shape[0], A, _ptr(d_attr),
@@ -302,17 +311,17 @@ class _TextureFn(torch.autograd.Function):
         filt, boundary, bias, L, Nt, Ht, Wt, C, dir_grad = ctx.meta
         N, Hi, Wi = uv.shape[0], uv.shape[1], uv.shape[2]
         d_out = d_out.to(torch.float32).contiguous()
-        d_tex = torch.empty_like(tex)
-        d_uv = torch.empty_like(uv) if ctx.needs_input_grad[1] else None
-        d_uv_da = torch.empty_like(uv_da) if (uv_da is not None and ctx.needs_input_grad[2]) else None
-        d_bias = torch.empty_like(bias_map) if (bias_map is not None and ctx.needs_input_grad[3]) \
+        d_tex = _grad_buf(tex)
+        d_uv = _grad_buf(uv) if ctx.needs_input_grad[1] else None
+        d_uv_da = _grad_buf(uv_da) if (uv_da is not None and ctx.needs_input_grad[2]) else None
+        d_bias = _grad_buf(bias_map) if (bias_map is not None and ctx.needs_input_grad[3]) \
             else None
         _lib.check(lib.dr_texture_bwd(
             _ptr(tex), _ptr(pyr), Nt, Ht, Wt, C, L, _ptr(uv), _ptr(uv_da), _ptr(bias_map),
             float(bias), filt, boundary, N, Hi, Wi, _ptr(d_out), _ptr(d_tex), _ptr(d_uv),
             _ptr(d_uv_da), _ptr(d_bias), _lib.DR_CUBE_DIR_GRAD if dir_grad else 0, _stream()))
         if d_uv_da is None and uv_da is not None and ctx.needs_input_grad[2]:
-            d_uv_da = torch.zeros_like(uv_da)
+            d_uv_da = _grad_buf(uv_da, zero=True)
         return d_tex, d_uv, d_uv_da, d_bias, None, None, None, None, None
 
 
@@ -349,8 +358,8 @@ class _AntialiasFn(torch.autograd.Function):
         N, H, W, C = color.shape
         V, T = pos.shape[1], tri.shape[0]
         d_out = d_out.to(torch.float32).contiguous()
-        d_color = torch.empty_like(color) if ctx.needs_input_grad[0] else None
-        d_pos = torch.empty_like(pos) if ctx.needs_input_grad[1] else None
+        d_color = _grad_buf(color) if ctx.needs_input_grad[0] else None
+        d_pos = _grad_buf(pos) if ctx.needs_input_grad[1] else None
         if saved is not None:
             _lib.check(lib.dr_antialias_bwd_saved(_ptr(color), _ptr(rast), _ptr(pos), _ptr(tri),
                                                   _ptr(topo), _ptr(d_out), _ptr(saved), N, H, W,
