@@ -77,7 +77,13 @@ enum {
   DR_ACCUMULATE = 1u,
   /* dr_texture_bwd of a cube map: the direction gradient (an extension; the
    * reference returns zeros, Texture.swift:196-198, which is the default) */
-  DR_CUBE_DIR_GRAD = 2u
+  DR_CUBE_DIR_GRAD = 2u,
+  /* dr_rasterize_bwd: the caller states that the last dr_rasterize_fwd* on
+   * this stream was the call being differentiated and that pos and tri are
+   * unchanged since (no counterpart in the reference; an autograd wrapper
+   * knows both).  Per-triangle values that forward stored are then reused
+   * instead of recomputed. */
+  DR_RASTERIZE_BWD_REUSE = 4u
 };
 
 /* Texture.swift:8-17 (BoundaryMode) */

@@ -111,7 +111,11 @@ struct Scratch {
     std::vector<int32_t> ranges;
     int64_t n_items = 0, max_items = 0;
     bool px = false;  // the forward kernel it ran (k_raster_px)
+    bool brec = false;  // it also wrote the backward's records (SLOT_RBWD_REC)
   } last_raster;
+  // The last dr_rasterize_bwd on this stream used per-triangle records, so
+  // forwards write them with their setup.
+  bool rbwd_want = false;
 };
 
 // A pinned host buffer of the range-mode staging ring holding at least

@@ -30,6 +30,31 @@ struct alignas(16) TriRec {
   float4 r0, r1, r2, r3;
 };
 
+// Per (image, triangle) values of the rasterize backward that do not
+// depend on the pixel (Rasterize.swift:665-690, 790-797), computed once per
+// triangle with the same expressions instead of once per covered pixel:
+//   q0 = (sx0, sy0, sx1, sy1), q1 = (sx2, sy2, sz0, sz1),
+//   q2 = (sz2, 1 / area, 1 / w0, 1 / w1), q3 = (1 / w2, i0, i1, i2)
+// (the vertex ids as int bits; i0 = -1 when an id lies outside [0, V)).
+struct alignas(16) RBwdRec {
+  float4 q0, q1, q2, q3;
+};
+
+// The record of one triangle from its clip-space vertices (ids valid).
+__device__ __forceinline__ RBwdRec rbwd_rec_of(float4 P0, float4 P1, float4 P2, int i0, int i1,
+                                               int i2) {
+  const float sx0 = P0.x / P0.w, sy0 = P0.y / P0.w, sz0 = P0.z / P0.w;
+  const float sx1 = P1.x / P1.w, sy1 = P1.y / P1.w, sz1 = P1.z / P1.w;
+  const float sx2 = P2.x / P2.w, sy2 = P2.y / P2.w, sz2 = P2.z / P2.w;
+  const float area = (sx1 - sx0) * (sy2 - sy0) - (sx2 - sx0) * (sy1 - sy0);
+  RBwdRec r;
+  r.q0 = make_float4(sx0, sy0, sx1, sy1);
+  r.q1 = make_float4(sx2, sy2, sz0, sz1);
+  r.q2 = make_float4(sz2, 1.0f / area, 1.0f / P0.w, 1.0f / P1.w);
+  r.q3 = make_float4(1.0f / P2.w, __int_as_float(i0), __int_as_float(i1), __int_as_float(i2));
+  return r;
+}
+
 // Rasterize.swift:280-328 (+ the AABB and tile range of :191-223).  The
 // first nzero threads also clear zero[0, nzero) (the fill pass's counters,
 // which nothing reads before the binning), sparing a fill launch.
@@ -37,55 +62,84 @@ __global__ void __launch_bounds__(256) k_setup(const float* __restrict__ pos, in
                                                const int32_t* __restrict__ tri, int Npos, int V,
                                                int T, int H, int W, TriRec* __restrict__ rec,
                                                int4* __restrict__ rect, int* __restrict__ zero,
-                                               int64_t nzero) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+                                               int64_t nzero, RBwdRec* __restrict__ brec) {
+  // the workgroup's records are assembled in LDS and written out as
+  // consecutive 16-byte stores (a thread's own 64-byte record would take
+  // four strided stores)
+  __shared__ float4 s_rec[256 * 4];
+  __shared__ float4 s_brec[256 * 4];
+  const int64_t base = (int64_t)blockIdx.x * 256;
+  const int64_t i = base + threadIdx.x;
+  const int64_t n_rec = (int64_t)Npos * T;
   if (i < nzero) zero[i] = 0;
-  if (i >= (int64_t)Npos * T) return;
-  int64_t n;
-  int t;
-  divmod64(i, T, n, t);
-  const float* p = pos + n * pos_stride;
-  const int i0 = tri[t * 3 + 0], i1 = tri[t * 3 + 1], i2 = tri[t * 3 + 2];
-  const bool ok = verts_ok(i0, i1, i2, V);  // else not drawn
-  float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f), v1 = v0, v2 = v0;
-  if (ok) {
-    v0 = *reinterpret_cast<const float4*>(p + (int64_t)i0 * 4);
-    v1 = *reinterpret_cast<const float4*>(p + (int64_t)i1 * 4);
-    v2 = *reinterpret_cast<const float4*>(p + (int64_t)i2 * 4);
-  }
-  TriRec r;
-  int4 rc = make_int4(-1, -1, -1, -1);
-  if (!ok || v0.w <= 0.0f || v1.w <= 0.0f || v2.w <= 0.0f) {
-    r.r0 = r.r1 = r.r2 = r.r3 = make_float4(0.f, 0.f, 0.f, 0.f);
-  } else {
-    const float sx0 = v0.x / v0.w, sy0 = v0.y / v0.w, sz0 = v0.z / v0.w;
-    const float sx1 = v1.x / v1.w, sy1 = v1.y / v1.w, sz1 = v1.z / v1.w;
-    const float sx2 = v2.x / v2.w, sy2 = v2.y / v2.w, sz2 = v2.z / v2.w;
-    const float area = (sx1 - sx0) * (sy2 - sy0) - (sx2 - sx0) * (sy1 - sy0);
-    const float minx = fminf(sx0, fminf(sx1, sx2));
-    const float maxx = fmaxf(sx0, fmaxf(sx1, sx2));
-    const float miny = fminf(sy0, fminf(sy1, sy2));
-    const float maxy = fmaxf(sy0, fmaxf(sy1, sy2));
-    r.r0 = make_float4(sx0, sy0, sx1, sy1);
-    r.r1 = make_float4(sx2, sy2, sz0, sz1);
-    r.r2 = make_float4(sz2, area, 1.0f / area, 0.0f);
-    r.r3 = make_float4(minx, maxx, miny, maxy);
-    if (area != 0.0f) {
-      const float px_min = (minx + 1.0f) * (float)W * 0.5f - 0.5f;
-      const float px_max = (maxx + 1.0f) * (float)W * 0.5f - 0.5f;
-      const float py_min = (1.0f - maxy) * (float)H * 0.5f - 0.5f;
-      const float py_max = (1.0f - miny) * (float)H * 0.5f - 0.5f;
-      int x0 = f2i(floorf(px_min)), x1 = f2i(floorf(px_max));
-      int y0 = f2i(floorf(py_min)), y1 = f2i(floorf(py_max));
-      if (x0 < 0) x0 = 0;
-      if (x1 >= W) x1 = W - 1;
-      if (y0 < 0) y0 = 0;
-      if (y1 >= H) y1 = H - 1;
-      if (x0 <= x1 && y0 <= y1) rc = make_int4(x0 / kTile, x1 / kTile, y0 / kTile, y1 / kTile);
+  if (base >= n_rec) return;  // uniform: a workgroup past the records only clears
+  if (i < n_rec) {
+    int64_t n;
+    int t;
+    divmod64(i, T, n, t);
+    const float* p = pos + n * pos_stride;
+    const int i0 = tri[t * 3 + 0], i1 = tri[t * 3 + 1], i2 = tri[t * 3 + 2];
+    const bool ok = verts_ok(i0, i1, i2, V);  // else not drawn
+    float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f), v1 = v0, v2 = v0;
+    if (ok) {
+      v0 = *reinterpret_cast<const float4*>(p + (int64_t)i0 * 4);
+      v1 = *reinterpret_cast<const float4*>(p + (int64_t)i1 * 4);
+      v2 = *reinterpret_cast<const float4*>(p + (int64_t)i2 * 4);
+    }
+    TriRec r;
+    int4 rc = make_int4(-1, -1, -1, -1);
+    if (!ok || v0.w <= 0.0f || v1.w <= 0.0f || v2.w <= 0.0f) {
+      r.r0 = r.r1 = r.r2 = r.r3 = make_float4(0.f, 0.f, 0.f, 0.f);
+    } else {
+      const float sx0 = v0.x / v0.w, sy0 = v0.y / v0.w, sz0 = v0.z / v0.w;
+      const float sx1 = v1.x / v1.w, sy1 = v1.y / v1.w, sz1 = v1.z / v1.w;
+      const float sx2 = v2.x / v2.w, sy2 = v2.y / v2.w, sz2 = v2.z / v2.w;
+      const float area = (sx1 - sx0) * (sy2 - sy0) - (sx2 - sx0) * (sy1 - sy0);
+      const float minx = fminf(sx0, fminf(sx1, sx2));
+      const float maxx = fmaxf(sx0, fmaxf(sx1, sx2));
+      const float miny = fminf(sy0, fminf(sy1, sy2));
+      const float maxy = fmaxf(sy0, fmaxf(sy1, sy2));
+      r.r0 = make_float4(sx0, sy0, sx1, sy1);
+      r.r1 = make_float4(sx2, sy2, sz0, sz1);
+      r.r2 = make_float4(sz2, area, 1.0f / area, 0.0f);
+      r.r3 = make_float4(minx, maxx, miny, maxy);
+      if (area != 0.0f) {
+        const float px_min = (minx + 1.0f) * (float)W * 0.5f - 0.5f;
+        const float px_max = (maxx + 1.0f) * (float)W * 0.5f - 0.5f;
+        const float py_min = (1.0f - maxy) * (float)H * 0.5f - 0.5f;
+        const float py_max = (1.0f - miny) * (float)H * 0.5f - 0.5f;
+        int x0 = f2i(floorf(px_min)), x1 = f2i(floorf(px_max));
+        int y0 = f2i(floorf(py_min)), y1 = f2i(floorf(py_max));
+        if (x0 < 0) x0 = 0;
+        if (x1 >= W) x1 = W - 1;
+        if (y0 < 0) y0 = 0;
+        if (y1 >= H) y1 = H - 1;
+        if (x0 <= x1 && y0 <= y1) rc = make_int4(x0 / kTile, x1 / kTile, y0 / kTile, y1 / kTile);
+      }
+    }
+    float4* sr = s_rec + threadIdx.x * 4;
+    sr[0] = r.r0; sr[1] = r.r1; sr[2] = r.r2; sr[3] = r.r3;
+    rect[i] = rc;
+    if (brec) {  // the backward's record of the triangle, as k_rbwd_rec writes it
+      RBwdRec z;
+      if (ok) {
+        z = rbwd_rec_of(v0, v1, v2, i0, i1, i2);
+      } else {
+        z.q0 = z.q1 = z.q2 = make_float4(0.f, 0.f, 0.f, 0.f);
+        z.q3 = make_float4(0.f, __int_as_float(-1), 0.f, 0.f);
+      }
+      float4* sb = s_brec + threadIdx.x * 4;
+      sb[0] = z.q0; sb[1] = z.q1; sb[2] = z.q2; sb[3] = z.q3;
     }
   }
-  rec[i] = r;
-  rect[i] = rc;
+  __syncthreads();
+  const int nr = (int)min((int64_t)256, n_rec - base) * 4;
+  float4* dr = reinterpret_cast<float4*>(rec + base);
+  for (int j = threadIdx.x; j < nr; j += 256) dr[j] = s_rec[j];
+  if (brec) {
+    float4* db = reinterpret_cast<float4*>(brec + base);
+    for (int j = threadIdx.x; j < nr; j += 256) db[j] = s_brec[j];
+  }
 }
 
 // Work item -> (image n, triangle t, record index).  Instanced mode: every
@@ -850,31 +904,6 @@ __global__ void __launch_bounds__(256) k_raster_px(
   if (DB) *reinterpret_cast<float4*>(rast_db + pix * 4) = d4;
 }
 
-// Per (image, triangle) values of the rasterize backward that do not
-// depend on the pixel (Rasterize.swift:665-690, 790-797), computed once per
-// triangle with the same expressions instead of once per covered pixel:
-//   q0 = (sx0, sy0, sx1, sy1), q1 = (sx2, sy2, sz0, sz1),
-//   q2 = (sz2, 1 / area, 1 / w0, 1 / w1), q3 = (1 / w2, i0, i1, i2)
-// (the vertex ids as int bits; i0 = -1 when an id lies outside [0, V)).
-struct alignas(16) RBwdRec {
-  float4 q0, q1, q2, q3;
-};
-
-// The record of one triangle from its clip-space vertices (ids valid).
-__device__ __forceinline__ RBwdRec rbwd_rec_of(float4 P0, float4 P1, float4 P2, int i0, int i1,
-                                               int i2) {
-  const float sx0 = P0.x / P0.w, sy0 = P0.y / P0.w, sz0 = P0.z / P0.w;
-  const float sx1 = P1.x / P1.w, sy1 = P1.y / P1.w, sz1 = P1.z / P1.w;
-  const float sx2 = P2.x / P2.w, sy2 = P2.y / P2.w, sz2 = P2.z / P2.w;
-  const float area = (sx1 - sx0) * (sy2 - sy0) - (sx2 - sx0) * (sy1 - sy0);
-  RBwdRec r;
-  r.q0 = make_float4(sx0, sy0, sx1, sy1);
-  r.q1 = make_float4(sx2, sy2, sz0, sz1);
-  r.q2 = make_float4(sz2, 1.0f / area, 1.0f / P0.w, 1.0f / P1.w);
-  r.q3 = make_float4(1.0f / P2.w, __int_as_float(i0), __int_as_float(i1), __int_as_float(i2));
-  return r;
-}
-
 __global__ void __launch_bounds__(256) k_rbwd_rec(const float* __restrict__ pos, int64_t pos_stride,
                                                   const int32_t* __restrict__ tri, int64_t NT,
                                                   int V, int T, RBwdRec* __restrict__ out) {
@@ -1225,7 +1254,7 @@ extern "C" int dr_rasterize_tile_counts(const float* pos, int64_t pos_batch_stri
     DR_TIMED("k_setup", stream);
     hipLaunchKernelGGL(k_setup, dim3(grid_for(n_rec, 256)), dim3(256), 0, stream, pos,
                        ranges_host ? (int64_t)0 : pos_batch_stride, tri, Npos, V, T, H, W, rec,
-                       rect, (int*)nullptr, (int64_t)0);
+                       rect, (int*)nullptr, (int64_t)0, (RBwdRec*)nullptr);
     DR_CHECK_LAUNCH();
   }
   DR_CHECK_HIP(fill_async(counts, 0, n_tiles, stream));
@@ -1291,6 +1320,7 @@ static int raster_fwd(const float* pos, int64_t pos_batch_stride, const int32_t*
   int C;
   bool want_stats = false;
   int64_t stat_waves = 0;
+  RBwdRec* brec = nullptr;
   if (reuse) {  // the previous call's setup and lists, untouched since
     if (ranges_host) {
       int64_t* d = (int64_t*)sc->ptr[SLOT_RAST_ITEMS];
@@ -1315,11 +1345,19 @@ static int raster_fwd(const float* pos, int64_t pos_batch_stride, const int32_t*
   int* cnt = (int*)cbuf;
   fillc = cnt + n_tiles;
 
+  // A backward on this stream used per-triangle records: write this call's
+  // with the setup (the backward of this call then skips k_rbwd_rec; same
+  // record layout as that backward reads when pos is per image or ranged)
+  if (sc->rbwd_want && n_rec > 0 && n_rec * 8 <= (int64_t)N * H * W &&
+      (ranges_host != nullptr || pos_batch_stride != 0)) {
+    brec = (RBwdRec*)scratch_get(sc, stream, SLOT_RBWD_REC, (size_t)n_rec * sizeof(RBwdRec));
+    if (!brec) return DR_ERR_MEMORY;
+  }
   if (n_rec > 0) {  // also clears the fill pass's counters
     DR_TIMED("k_setup", stream);
     hipLaunchKernelGGL(k_setup, dim3(grid_for(std::max(n_rec, n_tiles), 256)), dim3(256), 0,
                        stream, pos, ranges_host ? (int64_t)0 : pos_batch_stride, tri, Npos, V, T,
-                       H, W, rec, rect, fillc, n_tiles);
+                       H, W, rec, rect, fillc, n_tiles, brec);
     DR_CHECK_LAUNCH();
   } else {
     DR_CHECK_HIP(fill_async(fillc, 0, n_tiles, stream));
@@ -1433,6 +1471,7 @@ static int raster_fwd(const float* pos, int64_t pos_batch_stride, const int32_t*
   L.max_items = max_items;
   L.C = C;
   L.px = px;
+  L.brec = brec != nullptr;
   L.valid = true;
   return DR_OK;
 }
@@ -1476,15 +1515,30 @@ extern "C" int dr_rasterize_bwd(const float* pos, int64_t pos_batch_stride, cons
   const int64_t nrec = (pos_batch_stride ? (int64_t)N : 1) * T;
   const bool use_rec = nrec > 0 && nrec * 8 <= (int64_t)N * H * W;
   RBwdRec* trec = nullptr;
+  Scratch* sc = scratch_for(stream);
+  if (!sc) return DR_ERR_HIP;
   if (use_rec) {
-    Scratch* sc = scratch_for(stream);
-    if (!sc) return DR_ERR_HIP;
-    trec = (RBwdRec*)scratch_get(sc, stream, SLOT_RBWD_REC, (size_t)nrec * sizeof(RBwdRec));
-    if (!trec) return DR_ERR_MEMORY;
-    DR_TIMED("k_rbwd_rec", stream);
-    hipLaunchKernelGGL(k_rbwd_rec, dim3((unsigned)((nrec + 255) / 256)), dim3(256), 0, stream,
-                       pos, pos_batch_stride, tri, nrec, V, T, trec);
+    // DR_RASTERIZE_BWD_REUSE: the caller states that the last forward on
+    // this stream was this call's, with pos and tri unchanged since; if
+    // that forward wrote the records, they are used as they are
+    const auto& L = sc->last_raster;
+    const bool reuse = (flags & DR_RASTERIZE_BWD_REUSE) && L.valid && L.brec && L.pos == pos &&
+                       L.tri == tri && L.N == N && L.V == V && L.T == T &&
+                       (L.range ? pos_batch_stride == 0
+                                : pos_batch_stride != 0 && L.pos_stride == pos_batch_stride) &&
+                       sc->ptr[SLOT_RBWD_REC] && sc->cap[SLOT_RBWD_REC] >= (size_t)nrec * sizeof(RBwdRec);
+    if (reuse) {
+      trec = (RBwdRec*)sc->ptr[SLOT_RBWD_REC];
+    } else {
+      trec = (RBwdRec*)scratch_get(sc, stream, SLOT_RBWD_REC, (size_t)nrec * sizeof(RBwdRec));
+      if (!trec) return DR_ERR_MEMORY;
+      sc->last_raster.brec = false;  // the slot now holds this call's records
+      DR_TIMED("k_rbwd_rec", stream);
+      hipLaunchKernelGGL(k_rbwd_rec, dim3((unsigned)((nrec + 255) / 256)), dim3(256), 0, stream,
+                         pos, pos_batch_stride, tri, nrec, V, T, trec);
+    }
   }
+  sc->rbwd_want = use_rec;
   DR_CHECK_LAUNCH();
   {
     DR_TIMED("k_raster_bwd", stream);

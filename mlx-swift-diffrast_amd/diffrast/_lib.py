@@ -58,6 +58,7 @@ SIGNATURES = {
 DR_OK, DR_ERR_ARGUMENT, DR_ERR_HIP, DR_ERR_MEMORY = 0, 1, 2, 3
 DR_ACCUMULATE = 1
 DR_CUBE_DIR_GRAD = 2
+DR_RASTERIZE_BWD_REUSE = 4
 DR_TEXTURE_BWD_NOALLOC_FLOATS = 8 * 1024 * 1024
 ABI_VERSION = 1
 

@@ -106,6 +106,16 @@ def _dev_i32(t, name: str, device) -> torch.Tensor:
 # (same versions), reuses that call's triangle setup and tile lists
 # (dr_rasterize_fwd_again, which also checks every pointer and size itself).
 _last_raster = {}
+# The last rasterize forward per (device, stream), as a token its autograd
+# context also holds: the backward of that call (pos and tri unchanged since,
+# which autograd checks for saved tensors) may reuse per-triangle values the
+# forward stored (DR_RASTERIZE_BWD_REUSE).
+_last_fwd = {}
+
+
+def _where(device):
+    idx = device.index if device.index is not None else _cur_device()
+    return idx, _raw_stream(idx)
 
 
 def _grad_buf(t, zero=False):
@@ -141,6 +151,8 @@ class _RasterizeFn(torch.autograd.Function):
             _ptr(rast), _ptr(rast_db) if grad_db else None, int(max_per_tile), _stream()))
         ctx.save_for_backward(posc, tri, rast)
         ctx.meta = (range_mode, N, V, H, W, grad_db)
+        ctx.token = object()
+        _last_fwd[_where(posc.device)] = ctx.token
         return rast, rast_db
 
     @staticmethod
@@ -155,9 +167,10 @@ class _RasterizeFn(torch.autograd.Function):
         if grad_db and d_rast_db is not None:
             db = d_rast_db.to(torch.float32).contiguous()
         d_pos = _grad_buf(pos)
+        flags = _lib.DR_RASTERIZE_BWD_REUSE if _last_fwd.get(_where(pos.device)) is ctx.token else 0
         _lib.check(lib.dr_rasterize_bwd(
             _ptr(pos), 0 if range_mode else V * 4, _ptr(tri), _ptr(rast), _ptr(d_rast), _ptr(db),
-            N, V, tri.shape[0], H, W, _ptr(d_pos), 0, _stream()))
+            N, V, tri.shape[0], H, W, _ptr(d_pos), flags, _stream()))
         return d_pos, None, None, None, None, None, None, None, None
 
 

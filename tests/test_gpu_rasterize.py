@@ -555,3 +555,82 @@ def test_capped_large_triangles_pixel_parallel():
     ran = _raster_kernels(lambda: DiffRast.rasterize(dev(p[None]), dev(tri), (128, 128),
                                                      maxPerTile=16))
     assert ran == {"k_raster_px"}
+
+
+def _launches(fn, names):
+    """fn() with the library's launch timing on: launches of each kernel."""
+    import diffrast._lib as L
+    import torch
+    lib = L.load()
+    torch.cuda.synchronize()
+    lib.dr_profile_reset()
+    lib.dr_profile_enable(1)
+    try:
+        fn()
+        torch.cuda.synchronize()
+    finally:
+        lib.dr_profile_enable(0)
+    rep = L.profile_report()
+    return {k: rep.get(k, {}).get("count", 0) for k in names}
+
+
+def _bwd_case(rng, pos, tri, H, W, ranges=None):
+    """A forward whose loss weights rast and rast_db with fixed random
+    cotangents; returns (pos leaf, loss, oracle d_pos)."""
+    from diffrast import DiffRast
+    p = dev(pos).requires_grad_(True)
+    r, db = DiffRast.rasterize(p, dev(tri), (H, W), gradDB=True,
+                               ranges=None if ranges is None else torch_dev().as_tensor(ranges))
+    g = rng.normal(size=tuple(r.shape)).astype(np.float32)
+    gdb = rng.normal(size=tuple(r.shape)).astype(np.float32)
+    loss = (r * dev(g)).sum() + (db * dev(gdb)).sum()
+    ref = O.rasterize_vjp(pos, tri, host(r), g, gdb, ranges=ranges)
+    return p, loss, ref
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", ["icosphere", "range"])
+def test_backward_reuses_forward_records(name):
+    """Once a backward has used per-triangle records, later forwards write
+    them with their setup and the backward of the last forward on the
+    stream skips k_rbwd_rec; a backward of an earlier forward (another
+    forward ran since) recomputes them.  Every d_pos matches the oracle."""
+    rng = np.random.default_rng(5)
+    ranges = None
+    if name == "icosphere":
+        sc = scenes.textured_icosphere(N=2, H=256, W=256, level=4, tex_size=8)
+        pos, tri, H, W = sc["pos"], sc["tri"], 256, 256
+    else:
+        sc = scenes.range_batch(N=4, T_per=6)
+        pos, tri, ranges, H, W = sc["pos"], sc["tri"], sc["ranges"], 96, 96
+    names = ("k_rbwd_rec", "k_raster_bwd")
+    import diffrast._lib as L
+    import torch
+    torch.cuda.synchronize()
+    assert L.load().dr_release_scratch() == 0  # a fresh stream state: no records asked for yet
+    # a first step: its backward computes the records (and asks for them)
+    p, loss, ref = _bwd_case(rng, pos, tri, H, W, ranges)
+    assert _launches(loss.backward, names) == {"k_rbwd_rec": 1, "k_raster_bwd": 1}
+    assert_grad_close(host(p.grad), ref, "d_pos first step")
+    # the next step's backward reuses what its forward stored
+    p, loss, ref = _bwd_case(rng, pos, tri, H, W, ranges)
+    assert _launches(loss.backward, names) == {"k_rbwd_rec": 0, "k_raster_bwd": 1}
+    assert_grad_close(host(p.grad), ref, "d_pos with the forward's records")
+    # two forwards, backwards in reverse order: the last forward's backward
+    # reuses, the earlier one's recomputes (its records were overwritten)
+    pos2 = pos.copy()
+    pos2[..., 0] += 0.01 * pos2[..., 3]
+    pa, la, ra = _bwd_case(rng, pos, tri, H, W, ranges)
+    pb, lb, rb = _bwd_case(rng, pos2, tri, H, W, ranges)
+    assert _launches(lb.backward, names) == {"k_rbwd_rec": 0, "k_raster_bwd": 1}
+    assert _launches(la.backward, names) == {"k_rbwd_rec": 1, "k_raster_bwd": 1}
+    assert_grad_close(host(pb.grad), rb, "d_pos of the last forward")
+    assert_grad_close(host(pa.grad), ra, "d_pos of the earlier forward")
+    # backwards in call order: the earlier one recomputes into the slot, so
+    # the last one may not take the slot as its forward's either
+    pa, la, ra = _bwd_case(rng, pos, tri, H, W, ranges)
+    pb, lb, rb = _bwd_case(rng, pos2, tri, H, W, ranges)
+    assert _launches(la.backward, names) == {"k_rbwd_rec": 1, "k_raster_bwd": 1}
+    assert _launches(lb.backward, names) == {"k_rbwd_rec": 1, "k_raster_bwd": 1}
+    assert_grad_close(host(pa.grad), ra, "d_pos of the earlier forward, first")
+    assert_grad_close(host(pb.grad), rb, "d_pos of the last forward, second")
