@@ -1010,6 +1010,15 @@ __global__ void __launch_bounds__(256) k_raster_bwd(
     valid = i0 >= 0;  // the triangle's vertex ids lie in [0, V)
   }
   if (valid) {
+    // Rasterize.swift:694-798, regrouped (equal up to rounding).  With
+    // e1 = area * u and e2 = area * v, u and v depend on a screen vertex
+    // coordinate q through (de1/dq - u * darea/dq) / area, likewise for v,
+    // and z = bw * sz0 + u * sz1 + v * sz2, so the pixel's d_u, d_v, d_z
+    // reach q as (de1/dq * A + de2/dq * B - darea/dq * (u A + v B)) / area
+    // with A = d_u + d_z (sz1 - sz0), B = d_v + d_z (sz2 - sz0).  rast_db
+    // = (dx / area) * (-2/W or 2/H factors) adds -darea/dq * s / area, s its
+    // cotangent's product with rast_db, plus the terms of the edge vectors
+    // themselves.
     const float u_val = r.x, v_val = r.y;
     const float bw_val = 1.0f - u_val - v_val;
     const float d_u = dr.x, d_v = dr.y, d_z = dr.z;
@@ -1018,67 +1027,42 @@ __global__ void __launch_bounds__(256) k_raster_bwd(
     const float Py = 1.0f - 2.0f * ((float)ph + 0.5f) / (float)H;
     const float sx0 = R.q0.x, sy0 = R.q0.y, sx1 = R.q0.z, sy1 = R.q0.w;
     const float sx2 = R.q1.x, sy2 = R.q1.y, sz0 = R.q1.z, sz1 = R.q1.w;
-    const float sz2 = R.q2.x, inv_area = R.q2.y;
-    const float dadsx0 = sy1 - sy2, dadsx1 = sy2 - sy0, dadsx2 = sy0 - sy1;
-    const float dadsy0 = sx2 - sx1, dadsy1 = sx0 - sx2, dadsy2 = sx1 - sx0;
-    const float de1dsx0 = Py - sy2, de1dsx2 = sy0 - Py;
-    const float de1dsy0 = sx2 - Px, de1dsy2 = Px - sx0;
-    const float de2dsx0 = sy1 - Py, de2dsx1 = Py - sy0;
-    const float de2dsy0 = Px - sx1, de2dsy1 = sx0 - Px;
-    const float dudsx0 = (de1dsx0 - u_val * dadsx0) * inv_area;
-    const float dudsx1 = (0.0f - u_val * dadsx1) * inv_area;
-    const float dudsx2 = (de1dsx2 - u_val * dadsx2) * inv_area;
-    const float dudsy0 = (de1dsy0 - u_val * dadsy0) * inv_area;
-    const float dudsy1 = (0.0f - u_val * dadsy1) * inv_area;
-    const float dudsy2 = (de1dsy2 - u_val * dadsy2) * inv_area;
-    const float dvdsx0 = (de2dsx0 - v_val * dadsx0) * inv_area;
-    const float dvdsx1 = (de2dsx1 - v_val * dadsx1) * inv_area;
-    const float dvdsx2 = (0.0f - v_val * dadsx2) * inv_area;
-    const float dvdsy0 = (de2dsy0 - v_val * dadsy0) * inv_area;
-    const float dvdsy1 = (de2dsy1 - v_val * dadsy1) * inv_area;
-    const float dvdsy2 = (0.0f - v_val * dadsy2) * inv_area;
-    const float dsz10 = sz1 - sz0, dsz20 = sz2 - sz0;
-    float dsx0 = d_u * dudsx0 + d_v * dvdsx0 + d_z * (dudsx0 * dsz10 + dvdsx0 * dsz20);
-    float dsx1 = d_u * dudsx1 + d_v * dvdsx1 + d_z * (dudsx1 * dsz10 + dvdsx1 * dsz20);
-    float dsx2 = d_u * dudsx2 + d_v * dvdsx2 + d_z * (dudsx2 * dsz10 + dvdsx2 * dsz20);
-    float dsy0 = d_u * dudsy0 + d_v * dvdsy0 + d_z * (dudsy0 * dsz10 + dvdsy0 * dsz20);
-    float dsy1 = d_u * dudsy1 + d_v * dvdsy1 + d_z * (dudsy1 * dsz10 + dvdsy1 * dsz20);
-    float dsy2 = d_u * dudsy2 + d_v * dvdsy2 + d_z * (dudsy2 * dsz10 + dvdsy2 * dsz20);
+    const float sz2 = R.q2.x, ia = R.q2.y;  // 1 / area
+    const float kx = (2.0f / (float)W) * ia, ky = (-2.0f / (float)H) * ia;
+    const float A = fmaf(d_z, sz1 - sz0, d_u), B = fmaf(d_z, sz2 - sz0, d_v);
+    // s: the rast_db cotangent against rast_db's dependence on area
+    const float s_db = kx * fmaf(d_db0, sy2 - sy0, d_db2 * (sy0 - sy1)) +
+                       ky * fmaf(d_db1, sx0 - sx2, d_db3 * (sx1 - sx0));
+    const float Q = fmaf(u_val, A, fmaf(v_val, B, s_db));
+    const float ex0 = Py - sy2, ex2 = sy0 - Py, fx0 = sy1 - Py, fx1 = Py - sy0;  // de1/dsx, de2/dsx
+    const float ey0 = sx2 - Px, ey2 = Px - sx0, fy0 = Px - sx1, fy1 = sx0 - Px;  // de1/dsy, de2/dsy
+    float dsx0 = ia * fmaf(ex0, A, fmaf(fx0, B, -(sy1 - sy2) * Q));
+    float dsx1 = ia * fmaf(fx1, B, -(sy2 - sy0) * Q);
+    float dsx2 = ia * fmaf(ex2, A, -(sy0 - sy1) * Q);
+    float dsy0 = ia * fmaf(ey0, A, fmaf(fy0, B, -(sx2 - sx1) * Q));
+    float dsy1 = ia * fmaf(fy1, B, -(sx0 - sx2) * Q);
+    float dsy2 = ia * fmaf(ey2, A, -(sx1 - sx0) * Q);
+    // rast_db's own dependence on the edge vectors
+    dsy0 = fmaf(d_db2 - d_db0, kx, dsy0);
+    dsy1 = fmaf(-d_db2, kx, dsy1);
+    dsy2 = fmaf(d_db0, kx, dsy2);
+    dsx0 = fmaf(d_db1 - d_db3, ky, dsx0);
+    dsx1 = fmaf(d_db3, ky, dsx1);
+    dsx2 = fmaf(-d_db1, ky, dsx2);
     const float dsz0_s = d_z * bw_val, dsz1_s = d_z * u_val, dsz2_s = d_z * v_val;
-    const float Kx = 2.0f / (float)W;
-    const float Ky = -2.0f / (float)H;
-    const float rdb0 = (sy2 - sy0) * Kx * inv_area;
-    const float rdb1 = (sx0 - sx2) * Ky * inv_area;
-    const float rdb2 = (sy0 - sy1) * Kx * inv_area;
-    const float rdb3 = (sx1 - sx0) * Ky * inv_area;
-    const float s = d_db0 * rdb0 + d_db1 * rdb1 + d_db2 * rdb2 + d_db3 * rdb3;
-    dsx0 += (-s * dadsx0) * inv_area;
-    dsx1 += (-s * dadsx1) * inv_area;
-    dsx2 += (-s * dadsx2) * inv_area;
-    dsy0 += (-s * dadsy0) * inv_area;
-    dsy1 += (-s * dadsy1) * inv_area;
-    dsy2 += (-s * dadsy2) * inv_area;
-    dsy0 += d_db0 * (-Kx) * inv_area;
-    dsy2 += d_db0 * (Kx) * inv_area;
-    dsx0 += d_db1 * (Ky) * inv_area;
-    dsx2 += d_db1 * (-Ky) * inv_area;
-    dsy0 += d_db2 * (Kx) * inv_area;
-    dsy1 += d_db2 * (-Kx) * inv_area;
-    dsx0 += d_db3 * (-Ky) * inv_area;
-    dsx1 += d_db3 * (Ky) * inv_area;
     const float inv_w0 = R.q2.z, inv_w1 = R.q2.w, inv_w2 = R.q3.x;
     val[0] = dsx0 * inv_w0;
     val[1] = dsy0 * inv_w0;
     val[2] = dsz0_s * inv_w0;
-    val[3] = -(sx0 * dsx0 + sy0 * dsy0 + sz0 * dsz0_s) * inv_w0;
+    val[3] = -fmaf(sx0, dsx0, fmaf(sy0, dsy0, sz0 * dsz0_s)) * inv_w0;
     val[4] = dsx1 * inv_w1;
     val[5] = dsy1 * inv_w1;
     val[6] = dsz1_s * inv_w1;
-    val[7] = -(sx1 * dsx1 + sy1 * dsy1 + sz1 * dsz1_s) * inv_w1;
+    val[7] = -fmaf(sx1, dsx1, fmaf(sy1, dsy1, sz1 * dsz1_s)) * inv_w1;
     val[8] = dsx2 * inv_w2;
     val[9] = dsy2 * inv_w2;
     val[10] = dsz2_s * inv_w2;
-    val[11] = -(sx2 * dsx2 + sy2 * dsy2 + sz2 * dsz2_s) * inv_w2;
+    val[11] = -fmaf(sx2, dsx2, fmaf(sy2, dsy2, sz2 * dsz2_s)) * inv_w2;
   }
   // Lanes of a row on the same triangle add into the same three rows: sum
   // each run first, its last lane adds the total.
