@@ -634,3 +634,58 @@ def test_backward_reuses_forward_records(name):
     assert _launches(lb.backward, names) == {"k_rbwd_rec": 1, "k_raster_bwd": 1}
     assert_grad_close(host(pa.grad), ra, "d_pos of the earlier forward, first")
     assert_grad_close(host(pb.grad), rb, "d_pos of the last forward, second")
+
+
+@pytest.mark.gpu
+def test_backward_reuse_flag_abi_checks_its_inputs():
+    """DR_RASTERIZE_BWD_REUSE through the C-ABI: the library takes the
+    forward's stored records only for the pos and tri that forward drew; a
+    backward that passes the flag with another pos buffer gets its own
+    records (k_rbwd_rec runs) and that pos's d_pos."""
+    import ctypes
+    torch = torch_dev()
+    import diffrast._lib as L
+    lib = L.load()
+    torch.cuda.synchronize()
+    assert lib.dr_release_scratch() == 0
+    sc = scenes.textured_icosphere(N=2, H=256, W=256, level=4, tex_size=8)
+    posa = sc["pos"]
+    posb = posa.copy()
+    posb[..., 1] += 0.02 * posb[..., 3]
+    pa, pb, tri = dev(posa), dev(posb), dev(sc["tri"])
+    N, V, T, H, W = pa.shape[0], pa.shape[1], tri.shape[0], 256, 256
+    P = lambda x: None if x is None else ctypes.c_void_p(x.data_ptr())
+    S = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    rng = np.random.default_rng(8)
+    g = rng.normal(size=(N, H, W, 4)).astype(np.float32)
+    gdb = rng.normal(size=(N, H, W, 4)).astype(np.float32)
+    dg, ddb = dev(g), dev(gdb)
+
+    def fwd(p):
+        r = torch.empty((N, H, W, 4), device="cuda")
+        db = torch.empty((N, H, W, 4), device="cuda")
+        L.check(lib.dr_rasterize_fwd_ex(P(p), V * 4, P(tri), None, None, N, V, T, H, W, P(r),
+                                        P(db), 0, S))
+        return r
+
+    def bwd(p, r, flags):
+        d = torch.empty_like(p)
+        L.check(lib.dr_rasterize_bwd(P(p), V * 4, P(tri), P(r), P(dg), P(ddb), N, V, T, H, W,
+                                     P(d), flags, S))
+        return d
+
+    names = ("k_rbwd_rec",)
+    ra = fwd(pa)
+    bwd(pa, ra, 0)                                  # asks later forwards for the records
+    ra = fwd(pa)                                    # stores them
+    rb = fwd(pb)                                    # stores pos b's instead
+    out = {}
+    # the flag with pos a after pos b's forward: the stored records are b's
+    assert _launches(lambda: out.setdefault("a", bwd(pa, ra, L.DR_RASTERIZE_BWD_REUSE)),
+                     names) == {"k_rbwd_rec": 1}
+    rb = fwd(pb)                                    # pos b's records again
+    assert _launches(lambda: out.setdefault("b", bwd(pb, rb, L.DR_RASTERIZE_BWD_REUSE)),
+                     names) == {"k_rbwd_rec": 0}
+    for key, pos, r in (("a", posa, ra), ("b", posb, rb)):
+        ref = O.rasterize_vjp(pos, sc["tri"], host(r), g, gdb)
+        assert_grad_close(host(out[key]), ref, f"d_pos {key}")
