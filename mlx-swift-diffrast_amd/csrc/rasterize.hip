@@ -1083,8 +1083,12 @@ __global__ void __launch_bounds__(256) k_acc_to_f32(double* __restrict__ acc,
                                                     int accumulate) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
-  const float v = (float)acc[i];
-  acc[i] = 0.0;
+  const double a = acc[i];
+  // only elements that received an addition are written back: the rows of
+  // vertices no pixel reached (most of them, for a peeled layer) stay
+  // untouched in memory
+  if (__double_as_longlong(a) != 0) acc[i] = 0.0;
+  const float v = (float)a;
   dst[i] = accumulate ? dst[i] + v : v;
 }
 
