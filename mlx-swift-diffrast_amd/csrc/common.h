@@ -113,8 +113,8 @@ struct Scratch {
     bool px = false;  // the forward kernel it ran (k_raster_px)
     bool brec = false;  // it also wrote the backward's records (SLOT_RBWD_REC)
   } last_raster;
-  // The last dr_rasterize_bwd on this stream used per-triangle records, so
-  // forwards write them with their setup.
+  // A dr_rasterize_bwd has run on this stream, so forwards write the
+  // backward's per-triangle records with their setup.
   bool rbwd_want = false;
 };
 

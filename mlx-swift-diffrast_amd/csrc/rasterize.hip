@@ -1338,11 +1338,11 @@ static int raster_fwd(const float* pos, int64_t pos_batch_stride, const int32_t*
   int* cnt = (int*)cbuf;
   fillc = cnt + n_tiles;
 
-  // A backward on this stream used per-triangle records: write this call's
-  // with the setup (the backward of this call then skips k_rbwd_rec; same
-  // record layout as that backward reads when pos is per image or ranged)
-  if (sc->rbwd_want && n_rec > 0 && n_rec * 8 <= (int64_t)N * H * W &&
-      (ranges_host != nullptr || pos_batch_stride != 0)) {
+  // A backward ran on this stream: write this call's records with the
+  // setup (a backward of this call then skips k_rbwd_rec, or the per-pixel
+  // record building; same record layout as the backward reads when pos is
+  // per image or ranged)
+  if (sc->rbwd_want && n_rec > 0 && (ranges_host != nullptr || pos_batch_stride != 0)) {
     brec = (RBwdRec*)scratch_get(sc, stream, SLOT_RBWD_REC, (size_t)n_rec * sizeof(RBwdRec));
     if (!brec) return DR_ERR_MEMORY;
   }
@@ -1504,22 +1504,25 @@ extern "C" int dr_rasterize_bwd(const float* pos, int64_t pos_batch_stride, cons
   const int ntx = (W + kTile - 1) / kTile, nty = (H + kTile - 1) / kTile;
   const int64_t blocks = (int64_t)N * ntx * nty;
   // per (image, triangle) records (one set for all images when pos is
-  // shared), when the triangles average at least 8 pixels of the images
+  // shared): those the forward stored, else built here when the triangles
+  // average at least 8 pixels of the images (below that, each pixel builds
+  // its triangle's record itself)
   const int64_t nrec = (pos_batch_stride ? (int64_t)N : 1) * T;
-  const bool use_rec = nrec > 0 && nrec * 8 <= (int64_t)N * H * W;
-  RBwdRec* trec = nullptr;
   Scratch* sc = scratch_for(stream);
   if (!sc) return DR_ERR_HIP;
+  // DR_RASTERIZE_BWD_REUSE: the caller states that the last forward on this
+  // stream drew this pos and tri, unchanged since; if that forward wrote the
+  // records, they are used as they are
+  const auto& L = sc->last_raster;
+  const bool reuse = nrec > 0 && (flags & DR_RASTERIZE_BWD_REUSE) && L.valid && L.brec &&
+                     L.pos == pos && L.tri == tri && L.N == N && L.V == V && L.T == T &&
+                     (L.range ? pos_batch_stride == 0
+                              : pos_batch_stride != 0 && L.pos_stride == pos_batch_stride) &&
+                     sc->ptr[SLOT_RBWD_REC] &&
+                     sc->cap[SLOT_RBWD_REC] >= (size_t)nrec * sizeof(RBwdRec);
+  const bool use_rec = reuse || (nrec > 0 && nrec * 8 <= (int64_t)N * H * W);
+  RBwdRec* trec = nullptr;
   if (use_rec) {
-    // DR_RASTERIZE_BWD_REUSE: the caller states that the last forward on
-    // this stream was this call's, with pos and tri unchanged since; if
-    // that forward wrote the records, they are used as they are
-    const auto& L = sc->last_raster;
-    const bool reuse = (flags & DR_RASTERIZE_BWD_REUSE) && L.valid && L.brec && L.pos == pos &&
-                       L.tri == tri && L.N == N && L.V == V && L.T == T &&
-                       (L.range ? pos_batch_stride == 0
-                                : pos_batch_stride != 0 && L.pos_stride == pos_batch_stride) &&
-                       sc->ptr[SLOT_RBWD_REC] && sc->cap[SLOT_RBWD_REC] >= (size_t)nrec * sizeof(RBwdRec);
     if (reuse) {
       trec = (RBwdRec*)sc->ptr[SLOT_RBWD_REC];
     } else {
@@ -1531,7 +1534,7 @@ extern "C" int dr_rasterize_bwd(const float* pos, int64_t pos_batch_stride, cons
                          pos, pos_batch_stride, tri, nrec, V, T, trec);
     }
   }
-  sc->rbwd_want = use_rec;
+  sc->rbwd_want = true;
   DR_CHECK_LAUNCH();
   {
     DR_TIMED("k_raster_bwd", stream);

@@ -106,11 +106,19 @@ def _dev_i32(t, name: str, device) -> torch.Tensor:
 # (same versions), reuses that call's triangle setup and tile lists
 # (dr_rasterize_fwd_again, which also checks every pointer and size itself).
 _last_raster = {}
-# The last rasterize forward per (device, stream), as a token its autograd
-# context also holds: the backward of that call (pos and tri unchanged since,
-# which autograd checks for saved tensors) may reuse per-triangle values the
-# forward stored (DR_RASTERIZE_BWD_REUSE).
+# The last rasterize forward per (device, stream): its pos and tri buffers
+# (address, shape, strides) and pos's version.  A backward whose pos and tri
+# are those buffers, pos at that version, differentiates a forward over the
+# same data (autograd has checked that its saved pos is unchanged since its
+# own forward; a later in-place change would have bumped the version), so it
+# may reuse the per-triangle values the last forward stored
+# (DR_RASTERIZE_BWD_REUSE; the peel layers of one pos all qualify).
 _last_fwd = {}
+
+
+def _fwd_key(pos, tri):
+    return (pos.data_ptr(), tuple(pos.shape), pos.stride(), pos._version, tri.data_ptr(),
+            tuple(tri.shape))
 
 
 def _where(device):
@@ -151,8 +159,7 @@ class _RasterizeFn(torch.autograd.Function):
             _ptr(rast), _ptr(rast_db) if grad_db else None, int(max_per_tile), _stream()))
         ctx.save_for_backward(posc, tri, rast)
         ctx.meta = (range_mode, N, V, H, W, grad_db)
-        ctx.token = object()
-        _last_fwd[_where(posc.device)] = ctx.token
+        _last_fwd[_where(posc.device)] = _fwd_key(posc, tri)
         return rast, rast_db
 
     @staticmethod
@@ -167,7 +174,8 @@ class _RasterizeFn(torch.autograd.Function):
         if grad_db and d_rast_db is not None:
             db = d_rast_db.to(torch.float32).contiguous()
         d_pos = _grad_buf(pos)
-        flags = _lib.DR_RASTERIZE_BWD_REUSE if _last_fwd.get(_where(pos.device)) is ctx.token else 0
+        flags = _lib.DR_RASTERIZE_BWD_REUSE if _last_fwd.get(_where(pos.device)) == _fwd_key(pos, tri) \
+            else 0
         _lib.check(lib.dr_rasterize_bwd(
             _ptr(pos), 0 if range_mode else V * 4, _ptr(tri), _ptr(rast), _ptr(d_rast), _ptr(db),
             N, V, tri.shape[0], H, W, _ptr(d_pos), flags, _stream()))

@@ -689,3 +689,33 @@ def test_backward_reuse_flag_abi_checks_its_inputs():
     for key, pos, r in (("a", posa, ra), ("b", posb, rb)):
         ref = O.rasterize_vjp(pos, sc["tri"], host(r), g, gdb)
         assert_grad_close(host(out[key]), ref, f"d_pos {key}")
+
+
+@pytest.mark.gpu
+def test_backward_small_triangles_with_forward_records():
+    """Triangles averaging under 8 pixels: a backward builds each pixel's
+    triangle values itself, but once a backward has run, the forward stores
+    the per-triangle records and the next backward reads them (all four
+    peel layers of one pos qualify).  d_pos matches the oracle both ways."""
+    import diffrast._lib as L
+    import torch
+    from diffrast import DiffRast
+    torch.cuda.synchronize()
+    assert L.load().dr_release_scratch() == 0
+    sc = scenes.textured_icosphere(N=2, H=64, W=64, level=5, tex_size=8)
+    pos, tri, H, W = sc["pos"], sc["tri"], 64, 64
+    assert 2 * tri.shape[0] * 8 > 2 * H * W  # below 8 pixels per triangle
+    rng = np.random.default_rng(21)
+    for step in range(2):
+        p = dev(pos).requires_grad_(True)
+        t = dev(tri)
+        layers, prev, loss, refs = [], None, 0.0, []
+        for _ in range(2):
+            r, db = DiffRast.rasterize(p, t, (H, W), gradDB=True, peelLayer=prev)
+            g = rng.normal(size=tuple(r.shape)).astype(np.float32)
+            gdb = rng.normal(size=tuple(r.shape)).astype(np.float32)
+            loss = loss + (r * dev(g)).sum() + (db * dev(gdb)).sum()
+            refs.append(O.rasterize_vjp(pos, tri, host(r), g, gdb))
+            prev = r.detach()
+        loss.backward()
+        assert_grad_close(host(p.grad), refs[0] + refs[1], f"d_pos step {step}")
