@@ -79,10 +79,11 @@ enum {
    * reference returns zeros, Texture.swift:196-198, which is the default) */
   DR_CUBE_DIR_GRAD = 2u,
   /* dr_rasterize_bwd: the caller states that the last dr_rasterize_fwd* on
-   * this stream was the call being differentiated and that pos and tri are
-   * unchanged since (no counterpart in the reference; an autograd wrapper
-   * knows both).  Per-triangle values that forward stored are then reused
-   * instead of recomputed. */
+   * this stream drew this pos and tri, and that neither changed since (no
+   * counterpart in the reference; an autograd wrapper knows both, e.g. for
+   * every peel layer of one pos).  Per-triangle values that forward stored
+   * are then reused instead of recomputed; the library still checks the
+   * buffers and sizes against that forward's. */
   DR_RASTERIZE_BWD_REUSE = 4u
 };
 
