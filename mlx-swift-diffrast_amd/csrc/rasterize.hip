@@ -24,7 +24,10 @@ constexpr int kTile = 16;
 
 // Per-triangle record, 4 x float4:
 //   r0 = (sx0, sy0, sx1, sy1)  r1 = (sx2, sy2, sz0, sz1)
-//   r2 = (sz2, area, 1/area, 0) r3 = (minx, maxx, miny, maxy)
+//   r2 = (sz2, area, 1/area, 0)
+//   r3 = (X0, X1, Y0, Y1) as int bits: the image pixels whose centres lie
+//        in the triangle's bounding box (the reference's box test), columns
+//        X0..X1 and rows Y0..Y1; X0 > X1 or Y0 > Y1 when none does
 // area == 0 marks a triangle the reference zeroes (w <= 0 or degenerate).
 struct alignas(16) TriRec {
   float4 r0, r1, r2, r3;
@@ -53,6 +56,30 @@ __device__ __forceinline__ RBwdRec rbwd_rec_of(float4 P0, float4 P1, float4 P2, 
   r.q2 = make_float4(sz2, 1.0f / area, 1.0f / P0.w, 1.0f / P1.w);
   r.q3 = make_float4(1.0f / P2.w, __int_as_float(i0), __int_as_float(i1), __int_as_float(i2));
   return r;
+}
+
+// Smallest i in [0, n) with p(i) for p false then true (n if none), and
+// largest i in [0, n) with p(i) for p true then false (-1 if none), from a
+// guess i0 (a few steps when the guess is close; at most n).
+template <typename P>
+__device__ __forceinline__ int first_true(int i0, int n, P p) {
+  int i = min(max(i0, 0), n);
+  while (i > 0 && p(i - 1)) --i;
+  while (i < n && !p(i)) ++i;
+  return i;
+}
+template <typename P>
+__device__ __forceinline__ int last_true(int i0, int n, P p) {
+  int i = min(max(i0, -1), n - 1);
+  while (i < n - 1 && p(i + 1)) ++i;
+  while (i >= 0 && !p(i)) --i;
+  return i;
+}
+
+// Pixel coordinate of a bounding-box edge, clamped to a range where the
+// float -> int conversion is exact (only a guess for first/last_true).
+__device__ __forceinline__ int px_guess(float v) {
+  return f2i(fminf(fmaxf(v, -4.0e6f), 4.0e6f));
 }
 
 // Rasterize.swift:280-328 (+ the AABB and tile range of :191-223).  The
@@ -89,7 +116,9 @@ __global__ void __launch_bounds__(256) k_setup(const float* __restrict__ pos, in
     TriRec r;
     int4 rc = make_int4(-1, -1, -1, -1);
     if (!ok || v0.w <= 0.0f || v1.w <= 0.0f || v2.w <= 0.0f) {
-      r.r0 = r.r1 = r.r2 = r.r3 = make_float4(0.f, 0.f, 0.f, 0.f);
+      r.r0 = r.r1 = r.r2 = make_float4(0.f, 0.f, 0.f, 0.f);
+      r.r3 = make_float4(__int_as_float(1), __int_as_float(0), __int_as_float(1),
+                         __int_as_float(0));  // no pixel
     } else {
       const float sx0 = v0.x / v0.w, sy0 = v0.y / v0.w, sz0 = v0.z / v0.w;
       const float sx1 = v1.x / v1.w, sy1 = v1.y / v1.w, sz1 = v1.z / v1.w;
@@ -102,7 +131,20 @@ __global__ void __launch_bounds__(256) k_setup(const float* __restrict__ pos, in
       r.r0 = make_float4(sx0, sy0, sx1, sy1);
       r.r1 = make_float4(sx2, sy2, sz0, sz1);
       r.r2 = make_float4(sz2, area, 1.0f / area, 0.0f);
-      r.r3 = make_float4(minx, maxx, miny, maxy);
+      // pixel centres as every kernel computes them (monotonic in the index)
+      const float fW = (float)W * 0.5f, fH = (float)H * 0.5f;
+      auto cx = [&](int X) { return 2.0f * ((float)X + 0.5f) / (float)W - 1.0f; };
+      auto cy = [&](int Y) { return 1.0f - 2.0f * ((float)Y + 0.5f) / (float)H; };
+      const int X0 = first_true(px_guess(ceilf((minx + 1.0f) * fW - 0.5f)), W,
+                                [&](int i) { return !(cx(i) < minx); });
+      const int X1 = last_true(px_guess(floorf((maxx + 1.0f) * fW - 0.5f)), W,
+                               [&](int i) { return !(cx(i) > maxx); });
+      const int Y0 = first_true(px_guess(ceilf((1.0f - maxy) * fH - 0.5f)), H,
+                                [&](int i) { return !(cy(i) > maxy); });
+      const int Y1 = last_true(px_guess(floorf((1.0f - miny) * fH - 0.5f)), H,
+                               [&](int i) { return !(cy(i) < miny); });
+      r.r3 = make_float4(__int_as_float(X0), __int_as_float(X1), __int_as_float(Y0),
+                         __int_as_float(Y1));
       if (area != 0.0f) {
         const float px_min = (minx + 1.0f) * (float)W * 0.5f - 0.5f;
         const float px_max = (maxx + 1.0f) * (float)W * 0.5f - 0.5f;
@@ -403,12 +445,15 @@ struct Best {
 };
 
 // One candidate against one pixel (Rasterize.swift:417-462).
-__device__ __forceinline__ void test_tri(const TriRec& R, int t, float x, float y, float peel_z,
-                                         Best& b) {
+// (x, y): the centre of pixel (X, Y); the box test is the record's pixel box.
+__device__ __forceinline__ void test_tri(const TriRec& R, int t, float x, float y, int X, int Y,
+                                         float peel_z, Best& b) {
   const float sx0 = R.r0.x, sy0 = R.r0.y, sx1 = R.r0.z, sy1 = R.r0.w;
   const float sx2 = R.r1.x, sy2 = R.r1.y, sz0 = R.r1.z, sz1 = R.r1.w;
   const float sz2 = R.r2.x, area = R.r2.y, inv_area = R.r2.z;
-  if (x < R.r3.x || x > R.r3.y || y < R.r3.z || y > R.r3.w) return;
+  if (X < __float_as_int(R.r3.x) || X > __float_as_int(R.r3.y) || Y < __float_as_int(R.r3.z) ||
+      Y > __float_as_int(R.r3.w))
+    return;
   const float e0 = (sx1 - x) * (sy2 - y) - (sx2 - x) * (sy1 - y);
   const float e1 = (sx2 - x) * (sy0 - y) - (sx0 - x) * (sy2 - y);
   const float e2 = (sx0 - x) * (sy1 - y) - (sx1 - x) * (sy0 - y);
@@ -454,30 +499,6 @@ constexpr int kRPix = 256 / kRThreads;
 constexpr int kRChunk = 64;
 constexpr int kRSub = 4;
 constexpr int kRItems = 1024;
-
-// Smallest i in [0, n) with p(i) for p false then true (n if none), and
-// largest i in [0, n) with p(i) for p true then false (-1 if none), from a
-// guess i0 (a few steps when the guess is close; at most n).
-template <typename P>
-__device__ __forceinline__ int first_true(int i0, int n, P p) {
-  int i = min(max(i0, 0), n);
-  while (i > 0 && p(i - 1)) --i;
-  while (i < n && !p(i)) ++i;
-  return i;
-}
-template <typename P>
-__device__ __forceinline__ int last_true(int i0, int n, P p) {
-  int i = min(max(i0, -1), n - 1);
-  while (i < n - 1 && p(i + 1)) ++i;
-  while (i >= 0 && !p(i)) --i;
-  return i;
-}
-
-// Pixel coordinate of a bounding-box edge, clamped to a range where the
-// float -> int conversion is exact (only a guess for first/last_true).
-__device__ __forceinline__ int px_guess(float v) {
-  return f2i(fminf(fmaxf(v, -4.0e6f), 4.0e6f));
-}
 
 // Depth-then-index key of a covering triangle: the float depth mapped to an
 // unsigned order (-0 taken as +0, as the reference's == compares it) above
@@ -603,10 +624,6 @@ __global__ void __launch_bounds__(kRThreads) k_raster(
     // call): each thread scans the image's whole triangle range for its
     // pixels with the same tile test the binning uses (same candidate set,
     // so the same result), uniform up to the tile's pixel-centre box.
-    const float xw0 = 2.0f * ((float)x0t + 0.5f) / (float)W - 1.0f;
-    const float xw1 = 2.0f * ((float)(x0t + nx - 1) + 0.5f) / (float)W - 1.0f;
-    const float yw1 = 1.0f - 2.0f * ((float)y0t + 0.5f) / (float)H;
-    const float yw0 = 1.0f - 2.0f * ((float)(y0t + ny - 1) + 0.5f) / (float)H;
     int t0 = 0, t1 = it.T;
     if (it.prefix != nullptr) {
       t0 = (int)it.start[n];
@@ -629,9 +646,14 @@ __global__ void __launch_bounds__(kRThreads) k_raster(
       if (rc.x < 0 || tx < rc.x || tx > rc.y || ty < rc.z || ty > rc.w) continue;
       if (CAPPED && ++taken > scan_limit) break;  // uniform: the same tile test everywhere
       const TriRec R = load_rec(rec, rbase + t);
-      if (R.r3.y < xw0 || R.r3.x > xw1 || R.r3.w < yw0 || R.r3.z > yw1) continue;
+      if (__float_as_int(R.r3.y) < x0t || __float_as_int(R.r3.x) > x0t + nx - 1 ||
+          __float_as_int(R.r3.w) < y0t || __float_as_int(R.r3.z) > y0t + ny - 1)
+        continue;  // no pixel centre of the tile in its box
 #pragma unroll
-      for (int q = 0; q < kRPix; ++q) test_tri(R, t, px[q], py[q], peel_z[q], best[q]);
+      for (int q = 0; q < kRPix; ++q) {
+        const int p = tid + q * kRThreads;
+        test_tri(R, t, px[q], py[q], x0t + (p & 15), y0t + (p >> 4), peel_z[q], best[q]);
+      }
     }
 #pragma unroll
     for (int q = 0; q < kRPix; ++q) {
@@ -664,16 +686,11 @@ __global__ void __launch_bounds__(kRThreads) k_raster(
     if (tid < nb) {
       const int t = c0 == 0 && !ranked ? t_first : ids[c0 + tid];
       const TriRec R = load_rec(rec, rbase + t);
-      const float minx = R.r3.x, maxx = R.r3.y, miny = R.r3.z, maxy = R.r3.w;
-      const float fW = (float)W * 0.5f, fH = (float)H * 0.5f;
-      const int bx0 = first_true(px_guess(ceilf((minx + 1.0f) * fW - 0.5f)) - x0t, nx,
-                                 [&](int i) { return !(s_x[i] < minx); });
-      const int bx1 = last_true(px_guess(floorf((maxx + 1.0f) * fW - 0.5f)) - x0t, nx,
-                                [&](int i) { return !(s_x[i] > maxx); });
-      const int by0 = first_true(px_guess(ceilf((1.0f - maxy) * fH - 0.5f)) - y0t, ny,
-                                 [&](int i) { return !(s_y[i] > maxy); });
-      const int by1 = last_true(px_guess(floorf((1.0f - miny) * fH - 0.5f)) - y0t, ny,
-                                [&](int i) { return !(s_y[i] < miny); });
+      // the record's pixel box, clipped to the tile
+      const int bx0 = max(__float_as_int(R.r3.x) - x0t, 0);
+      const int bx1 = min(__float_as_int(R.r3.y) - x0t, nx - 1);
+      const int by0 = max(__float_as_int(R.r3.z) - y0t, 0);
+      const int by1 = min(__float_as_int(R.r3.w) - y0t, ny - 1);
       if (bx0 <= bx1 && by0 <= by1) {
         const int bw = bx1 - bx0 + 1, bh = by1 - by0 + 1;
         s_rec[tid] = R;
@@ -748,7 +765,7 @@ __global__ void __launch_bounds__(kRThreads) k_raster(
       const uint32_t id = (uint32_t)key;
       const int t = slots ? (int)(id >> 7) : (int)id;
       R = slots ? s_rec[id & 127] : load_rec(rec, rbase + t);
-      test_tri(R, t, s_x[lx], s_y[ly], -1e30f, best);  // the same expressions as the scan
+      test_tri(R, t, s_x[lx], s_y[ly], x0t + lx, y0t + ly, -1e30f, best);  // as the scan
     }
     write_px(pix, best, &R);  // R is read only when best.t >= 0, i.e. it was set
   }
@@ -822,10 +839,6 @@ __global__ void __launch_bounds__(256) k_raster_px(
 
   const float x = 2.0f * ((float)pw + 0.5f) / (float)W - 1.0f;
   const float y = 1.0f - 2.0f * ((float)ph + 0.5f) / (float)H;
-  const float xw0 = 2.0f * ((float)qx0 + 0.5f) / (float)W - 1.0f;
-  const float xw1 = 2.0f * ((float)qx1 + 0.5f) / (float)W - 1.0f;
-  const float yw1 = 1.0f - 2.0f * ((float)qy0 + 0.5f) / (float)H;  // top row: largest y
-  const float yw0 = 1.0f - 2.0f * ((float)qy1 + 0.5f) / (float)H;
 
   const int64_t pix = ((int64_t)n * H + ph) * W + pw;
   float peel_z = -1e30f;
@@ -849,7 +862,8 @@ __global__ void __launch_bounds__(256) k_raster_px(
       if (lane < nb) {
         myt = ids[c0 + lane];
         Rl = load_rec(rec, rbase + myt);
-        hit = !(Rl.r3.y < xw0 || Rl.r3.x > xw1 || Rl.r3.w < yw0 || Rl.r3.z > yw1);
+        hit = !(__float_as_int(Rl.r3.y) < qx0 || __float_as_int(Rl.r3.x) > qx1 ||
+                __float_as_int(Rl.r3.w) < qy0 || __float_as_int(Rl.r3.z) > qy1);
       }
       uint64_t m = __ballot(hit);
       if (hit) {
@@ -865,7 +879,7 @@ __global__ void __launch_bounds__(256) k_raster_px(
         m &= m - 1;
         const int t = s_t[wave][j];
         const TriRec R = s_rec[wave][j];
-        if (valid) test_tri(R, t, x, y, peel_z, best);
+        if (valid) test_tri(R, t, x, y, pw, ph, peel_z, best);
       }
       __builtin_amdgcn_wave_barrier();  // reads done before the next chunk writes
     }
@@ -884,8 +898,10 @@ __global__ void __launch_bounds__(256) k_raster_px(
       if (rc.x < 0 || tx < rc.x || tx > rc.y || ty < rc.z || ty > rc.w) continue;
       if (CAPPED && ++taken > scan_limit) break;  // uniform: the same tile test everywhere
       const TriRec R = load_rec(rec, rbase + t);
-      if (R.r3.y < xw0 || R.r3.x > xw1 || R.r3.w < yw0 || R.r3.z > yw1) continue;
-      if (valid) test_tri(R, t, x, y, peel_z, best);
+      if (__float_as_int(R.r3.y) < qx0 || __float_as_int(R.r3.x) > qx1 ||
+          __float_as_int(R.r3.w) < qy0 || __float_as_int(R.r3.z) > qy1)
+        continue;
+      if (valid) test_tri(R, t, x, y, pw, ph, peel_z, best);
     }
   }
   if (!valid) return;
