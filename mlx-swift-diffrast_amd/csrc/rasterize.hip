@@ -513,8 +513,8 @@ __device__ __forceinline__ unsigned long long zkey(float z, uint32_t id) {
 
 // Rasterize.swift:371-599.  One workgroup per (image, 16x16 tile); the
 // tile's candidates are taken triangle-parallel.  Each candidate gets the
-// exact set of tile pixels the reference's bounding-box test keeps (a
-// rectangle: pixel centres are monotonic in the pixel index), its pixels
+// exact set of tile pixels the reference's bounding-box test keeps (its
+// record's pixel box clipped to the tile), its pixels
 // are cut into work items of kRSub and the items are dealt out evenly over
 // the workgroup; each covering pixel folds (depth, triangle) into a 64-bit
 // LDS z-buffer by atomic min.  A last pass gives each thread its pixel and
