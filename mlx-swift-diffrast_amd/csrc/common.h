@@ -528,6 +528,69 @@ __device__ __forceinline__ void lds_table_flush(LdsTable<NV, CAP>& t) {
   for (int i = threadIdx.x; i < CAP; i += blockDim.x) t.key[i] = kEmptyKey;
 }
 
+// The same table keeping a list of the entries taken since the last flush,
+// so a flush visits those instead of all CAP entries (for large tables that
+// a tile fills only in part).
+template <int NV, int CAP>
+struct LdsTableU {
+  LdsTable<NV, CAP> t;
+  int n;
+  uint16_t slot[CAP];
+};
+
+template <int NV, int CAP>
+__device__ __forceinline__ void lds_table_clear(LdsTableU<NV, CAP>& u) {
+  lds_table_clear(u.t);
+  if (threadIdx.x == 0) u.n = 0;
+}
+
+template <int NV, int CAP, typename D>
+__device__ __forceinline__ void lds_table_add(LdsTableU<NV, CAP>& u, D* dst, const float* v) {
+  static_assert(CAP <= 65536, "slots are 16-bit");
+  auto& t = u.t;
+  bool any = false;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) any = any || v[j] != 0.0f;
+  if (!any) return;
+  const uint64_t key = (uint64_t)dst;
+  uint32_t h = addr_hash(key) & (CAP - 1);
+#pragma unroll 1
+  for (int probe = 0; probe < kLdsProbes; ++probe) {
+    unsigned long long cur = t.key[h];
+    if (cur == kEmptyKey) {
+      cur = atomicCAS(&t.key[h], kEmptyKey, (unsigned long long)key);
+      if (cur == kEmptyKey) u.slot[atomicAdd(&u.n, 1)] = (uint16_t)h;  // taken here
+    }
+    if (cur == kEmptyKey || cur == key) {
+#pragma unroll
+      for (int j = 0; j < NV; ++j)
+        if (v[j] != 0.0f) atomicAdd(&t.val[j][h], (double)v[j]);
+      return;
+    }
+    h = (h + 1) & (CAP - 1);
+  }
+#pragma unroll
+  for (int j = 0; j < NV; ++j)
+    if (v[j] != 0.0f) unsafeAtomicAdd(dst + j, (D)v[j]);
+}
+
+// Writes the taken entries out (call after a barrier) and leaves the table
+// cleared; the caller's next barrier orders the reset count before new adds.
+template <int NV, int CAP, typename D = float>
+__device__ __forceinline__ void lds_table_flush(LdsTableU<NV, CAP>& u) {
+  auto& t = u.t;
+  const int m = u.n;
+  for (int i = threadIdx.x; i < m * NV; i += blockDim.x) {
+    const int e = u.slot[i / NV], j = i - (i / NV) * NV;
+    const double v = t.val[j][e];
+    if (v != 0.0) unsafeAtomicAdd((D*)t.key[e] + j, (D)v);
+    t.val[j][e] = 0.0;
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < m; i += blockDim.x) t.key[u.slot[i]] = kEmptyKey;
+  if (threadIdx.x == 0) u.n = 0;
+}
+
 // dst = (float)acc, or dst += (float)acc: the one rounding of a gradient
 // summed in fp64 across workgroups (so the result does not depend on the
 // order in which the workgroups' atomics land).

@@ -384,6 +384,8 @@ constexpr int kTexTable = 512;  // LDS aggregation entries per tile (texels)
 
 template <int CT, int CAP = kTexTable>
 using TexTable = LdsTable<(CT > 0 ? CT : 1), CAP>;
+template <int CT, int CAP>
+using TexTableU = LdsTableU<(CT > 0 ? CT : 1), CAP>;
 
 // The cube backward's table: a cube map's footprints spread over more
 // texels per tile (a per-pixel LOD bias splits them over two or three
@@ -392,12 +394,12 @@ using TexTable = LdsTable<(CT > 0 ? CT : 1), CAP>;
 // 91 -> 47 ms with 1,024 entries, 43 ms with 2,048).
 constexpr int kCubeTable = 2048;
 
-template <int CT, bool USE_ACC = true, int CAP = kTexTable>
+template <int CT, bool USE_ACC = true, typename Tab = TexTable<CT>>
 __device__ __forceinline__ void scatter_footprint(bool valid, float* __restrict__ base, int Wk,
                                                   int C, const Bilin& b, const float* g,
                                                   float scale,
                                                   FootAcc<(CT > 0 ? CT : 1)>& acc,
-                                                  TexTable<CT, CAP>& tab) {
+                                                  Tab& tab) {
   float w00 = b.w00, w10 = b.w10, w01 = b.w01, w11 = b.w11;
   if (b.ix1 == b.ix0) {
     w00 += w10;
@@ -1604,7 +1606,7 @@ __global__ void __launch_bounds__(256) k_cube_fwd(CubeArgs A) {
 template <int MODE, int CT>
 __device__ __forceinline__ void cube_bwd_px(const CubeArgs& A, int64_t pix, bool valid, int n,
                                             FootAcc<(CT > 0 ? CT : 1)>& acc0,
-                                            TexTable<CT, kCubeTable>& tab) {
+                                            TexTableU<CT, kCubeTable>& tab) {
   const int C = dimC<CT>(A.C);
   const CubePx p = cube_px<MODE>(A, pix);
   const float* gp = A.d_out + pix * C;
@@ -1628,9 +1630,11 @@ __device__ __forceinline__ void cube_bwd_px(const CubeArgs& A, int64_t pix, bool
     float* dl = cube_dlevel(A, n, s.face, k, Hk, Wk);
     const Bilin b = bilin(p.u, p.v, Wk, Hk, DR_BOUNDARY_CLAMP);
     if (li == 0)
-      scatter_footprint<CT, true, kCubeTable>(on, dl, Wk, C, b, gsrc, scale, acc0, tab);
+      scatter_footprint<CT, true, TexTableU<CT, kCubeTable>>(on, dl, Wk, C, b, gsrc, scale, acc0,
+                                                             tab);
     else
-      scatter_footprint<CT, false, kCubeTable>(on, dl, Wk, C, b, gsrc, scale, acc0, tab);
+      scatter_footprint<CT, false, TexTableU<CT, kCubeTable>>(on, dl, Wk, C, b, gsrc, scale, acc0,
+                                                              tab);
     if (!on) continue;
     float dfx = 0.0f, dfy = 0.0f;
     for (int c = 0; c < C; ++c) {
@@ -1752,7 +1756,7 @@ __device__ __forceinline__ void cube_bwd_px(const CubeArgs& A, int64_t pix, bool
 template <int MODE, int CT>
 __global__ void __launch_bounds__(256) k_cube_bwd(CubeArgs A, int Hi, int Wi, int ntx,
                                                   int total_tiles) {
-  __shared__ TexTable<CT, kCubeTable> tab;
+  __shared__ TexTableU<CT, kCubeTable> tab;
   FootAcc<(CT > 0 ? CT : 1)> acc0;
   acc_init(acc0);
   lds_table_clear(tab);
