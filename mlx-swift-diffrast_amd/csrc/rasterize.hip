@@ -777,9 +777,10 @@ __global__ void __launch_bounds__(kRThreads) k_raster(
 // (image, 16x16 tile); wave w owns the 8x8 quadrant (w&1, w>>1).  Each triangle of the tile's list is
 // first tested against the quadrant's pixel-centre box by its bounding box
 // (exact: the pixel -> NDC map is monotonic), 64 triangles at a time, one
-// per lane; only the survivors are tested against the quadrant's 64 pixels.
-// (A conservative edge-function test of the box, in fp64 or fp32, removed
-// more candidates but cost more than the survivor tests it saved.)
+// per lane, then by a conservative edge-function test of the quadrant's
+// pixel-centre box (edge_excludes: large triangles often cover the box's
+// bounding-box corner but miss the box); only the survivors are tested
+// against the quadrant's 64 pixels.
 //
 // CAPPED (max_per_tile > 0): the reference's per-tile limit
 // (Rasterize.swift:164-171, 227-239, 410) with its appends in triangle
@@ -787,6 +788,31 @@ __global__ void __launch_bounds__(kRThreads) k_raster(
 // complete list above the limit is ranked in LDS and only the kept ids are
 // rasterized; a list that overflowed its capacity takes the full scan in
 // triangle order and stops at the limit.
+// Whether one edge of the triangle keeps every pixel centre of the box
+// [xa, xb] x [ya, yb] outside: the edge function (sa - x)(sb - y) -
+// (sc - x)(sd - y) is affine, (ab - cd) + (d - b) x + (c - a) y, so its
+// largest value (times the sign of the area) over the box is at a corner;
+// in fp64, with a margin above the rounding of the fp32 per-pixel
+// expression (three roundings of products of terms below |s| + 1, pixel
+// centres lying in [-1, 1]), so a rejected triangle fails the per-pixel
+// test at every centre of the box.
+__device__ __forceinline__ bool edge_excludes(const TriRec& R, float xa, float xb, float ya,
+                                              float yb) {
+  const double sx0 = R.r0.x, sy0 = R.r0.y, sx1 = R.r0.z, sy1 = R.r0.w;
+  const double sx2 = R.r1.x, sy2 = R.r1.y;
+  const double sg = R.r2.y > 0.0f ? 1.0 : -1.0;
+  const double e[3][4] = {{sx1, sy2, sx2, sy1}, {sx2, sy0, sx0, sy2}, {sx0, sy1, sx1, sy0}};
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    const double a = e[k][0], b = e[k][1], c = e[k][2], d = e[k][3];
+    const double A = sg * (d - b), B = sg * (c - a), C = sg * (a * b - c * d);
+    const double mx = C + fmax(A * (double)xa, A * (double)xb) + fmax(B * (double)ya, B * (double)yb);
+    const double tol = 0x1p-20 * ((fabs(a) + 1.0) * (fabs(b) + 1.0) + (fabs(c) + 1.0) * (fabs(d) + 1.0));
+    if (mx < -tol) return true;
+  }
+  return false;
+}
+
 template <bool DB, bool PEEL, bool CAPPED>
 __global__ void __launch_bounds__(256) k_raster_px(
     const TriRec* __restrict__ rec, const int4* __restrict__ rect, Items it, int64_t rec_stride,
@@ -839,6 +865,11 @@ __global__ void __launch_bounds__(256) k_raster_px(
 
   const float x = 2.0f * ((float)pw + 0.5f) / (float)W - 1.0f;
   const float y = 1.0f - 2.0f * ((float)ph + 0.5f) / (float)H;
+  // the quadrant's pixel-centre box, with the per-pixel expressions
+  const float cxa = 2.0f * ((float)qx0 + 0.5f) / (float)W - 1.0f;
+  const float cxb = 2.0f * ((float)qx1 + 0.5f) / (float)W - 1.0f;
+  const float cya = 1.0f - 2.0f * ((float)qy1 + 0.5f) / (float)H;
+  const float cyb = 1.0f - 2.0f * ((float)qy0 + 0.5f) / (float)H;
 
   const int64_t pix = ((int64_t)n * H + ph) * W + pw;
   float peel_z = -1e30f;
@@ -864,6 +895,7 @@ __global__ void __launch_bounds__(256) k_raster_px(
         Rl = load_rec(rec, rbase + myt);
         hit = !(__float_as_int(Rl.r3.y) < qx0 || __float_as_int(Rl.r3.x) > qx1 ||
                 __float_as_int(Rl.r3.w) < qy0 || __float_as_int(Rl.r3.z) > qy1);
+        if (hit && fabsf(Rl.r2.y) > 1e-30f) hit = !edge_excludes(Rl, cxa, cxb, cya, cyb);
       }
       uint64_t m = __ballot(hit);
       if (hit) {

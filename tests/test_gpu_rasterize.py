@@ -719,3 +719,34 @@ def test_backward_small_triangles_with_forward_records():
             prev = r.detach()
         loss.backward()
         assert_grad_close(host(p.grad), refs[0] + refs[1], f"d_pos step {step}")
+
+
+@pytest.mark.gpu
+def test_pixel_parallel_edge_cull_keeps_boundary_pixels():
+    """The pixel-parallel forward drops a candidate for an 8x8 quadrant only
+    when one of its edges keeps every pixel centre there outside (with a
+    margin over the fp32 rounding).  Large triangles whose vertices sit on
+    pixel centres put edges exactly through centres (e = 0 counts as
+    inside): the result is still bit-exact against the oracle."""
+    torch = torch_dev()
+    from diffrast import DiffRast
+    H, W, T = 128, 96, 96
+    rng = np.random.default_rng(31)
+    ix = rng.integers(0, W, size=(2, 3 * T))
+    iy = rng.integers(0, H, size=(2, 3 * T))
+    x = (2.0 * (ix.astype(np.float32) + np.float32(0.5)) / np.float32(W) - 1.0).astype(np.float32)
+    y = (1.0 - 2.0 * (iy.astype(np.float32) + np.float32(0.5)) / np.float32(H)).astype(np.float32)
+    z = rng.uniform(-0.9, 0.9, size=(2, 3 * T)).astype(np.float32)
+    pos = np.stack([x, y, z, np.ones_like(x)], -1).astype(np.float32)
+    tri = np.arange(3 * T, dtype=np.int32).reshape(T, 3)
+    p, t = dev(pos), dev(tri)
+    for _ in range(2):  # the second call sees the first call's statistics
+        ran = _raster_kernels(lambda: DiffRast.rasterize(p, t, (H, W), gradDB=True))
+    assert ran == {"k_raster_px"}
+    rast, db = DiffRast.rasterize(p, t, (H, W), gradDB=True)
+    rr, rdb = O.rasterize(pos, tri, (H, W), gradDB=True, max_per_tile=0)
+    np.testing.assert_array_equal(host(rast), rr)
+    np.testing.assert_array_equal(host(db), rdb)
+    r2, _ = DiffRast.rasterize(p, t, (H, W), gradDB=False, peelLayer=rast)
+    rr2, _ = O.rasterize(pos, tri, (H, W), gradDB=False, peelLayer=rr, max_per_tile=0)
+    np.testing.assert_array_equal(host(r2), rr2)
