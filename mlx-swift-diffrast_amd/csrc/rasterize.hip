@@ -368,8 +368,9 @@ constexpr int kBinThreads = 1024;
 // With `wstats` (the fill pass, when the caller wants this call's tile
 // statistics): each wave writes its largest final tile count (the returned
 // count plus its own, for the chunk that adds last) and its list entries to
-// wstats[2 * (kBinThreads / 64 * workgroup + wave) + {0, 1}], pinned host memory that the
-// host reduces after the kernel has run.  Waves of an empty chunk write 0s.
+// wstats[2 * (kBinThreads / 64 * workgroup + wave) + {0, 1}], pinned host
+// memory that the host reduces after the kernel has run.  Waves of an empty
+// chunk write 0s.
 template <bool FILL>
 __global__ void __launch_bounds__(kBinThreads) k_bin_lds(Items it, int chunks,
                                                  const int4* __restrict__ rect, int ntx,
@@ -392,8 +393,8 @@ __global__ void __launch_bounds__(kBinThreads) k_bin_lds(Items it, int chunks,
   const int64_t b0 = i0 + (int64_t)c * kBinChunk;
   const int64_t b1 = min(i1, b0 + kBinChunk);
   const int tid = threadIdx.x;
-  int m = 0;        // largest final count this workgroup saw
-  long long e = 0;  // list entries this workgroup added
+  int m = 0;        // largest final count this thread saw
+  long long e = 0;  // list entries this thread added
   if (b0 < b1) {    // uniform over the workgroup
     for (int k = tid; k < tiles; k += kBinThreads) s_tile[k] = 0;
     __syncthreads();
@@ -778,8 +779,8 @@ __global__ void __launch_bounds__(kRThreads) k_raster(
 // first tested against the quadrant's pixel-centre box by its bounding box
 // (exact: the pixel -> NDC map is monotonic), 64 triangles at a time, one
 // per lane, then by a conservative edge-function test of the quadrant's
-// pixel-centre box (edge_excludes: large triangles often cover the box's
-// bounding-box corner but miss the box); only the survivors are tested
+// pixel-centre box (edge_excludes: a large triangle's bounding box overlaps
+// many quadrants the triangle itself misses); only the survivors are tested
 // against the quadrant's 64 pixels.
 //
 // CAPPED (max_per_tile > 0): the reference's per-tile limit
