@@ -309,7 +309,8 @@ int64_t dr_antialias_saved_bytes(int N, int H, int W, int T);
  * direction d is nonzero (d = 0 +w, 1 +h, 2 -w, 3 -h); the byte of pixel
  * (n, h, w) is at ((n * ceil(H/16) + h/16) * ceil(W/16) + w/16) * 256 +
  * ((h%16)/8 * 2 + (w%16)/8) * 64 + (h%8) * 8 + w%8 (each 8x8 block of
- * pixels is 64 consecutive bytes).  The rest is opaque. */
+ * pixels is 64 consecutive bytes).  The rest is opaque (the pixels' triangle
+ * ids, which the backward reads in place of rast, then the records). */
 int dr_antialias_fwd_save(const float* color, const float* rast, const float* pos,
                           const int32_t* tri, const int32_t* topo, int N, int H, int W, int C,
                           int V, int T, float* out, void* saved, dr_stream_t stream);

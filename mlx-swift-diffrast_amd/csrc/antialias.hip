@@ -384,7 +384,8 @@ __global__ void __launch_bounds__(256) k_aa_fwd(const float* __restrict__ rast,
                                                 const float* __restrict__ color, int H, int W,
                                                 int T, int C, int ntx, int nty,
                                                 float* __restrict__ out,
-                                                uint8_t* __restrict__ blend_mask) {
+                                                uint8_t* __restrict__ blend_mask,
+                                                int* __restrict__ saved_ids) {
   __shared__ int s_tri[18][kTriRow];
   // colours of the tile and its border (CT > 0), so a blend reads its
   // neighbour from LDS rather than in a third global round trip
@@ -436,7 +437,11 @@ __global__ void __launch_bounds__(256) k_aa_fwd(const float* __restrict__ rast,
       }
     }
   }
-  if (blend_mask) blend_mask[mask_index(g.n, g.ph, g.pw, ntx, nty)] = (uint8_t)bits;
+  if (blend_mask) {
+    const int64_t mi = mask_index(g.n, g.ph, g.pw, ntx, nty);
+    blend_mask[mi] = (uint8_t)bits;
+    saved_ids[mi] = tp;
+  }
   if constexpr (CT > 0) {
     if (blend) {
       float acc[CT];
@@ -811,7 +816,7 @@ __device__ __forceinline__ void aa_pair_eval(const AAPairIn<CT>& P, const AATile
 // staged in LDS), then each pair's record, corner factors and colours.
 template <int CT>
 __global__ void __launch_bounds__(256) k_aa_bwd_masked(
-    const float* __restrict__ rast, const AARec* __restrict__ rec,
+    const int* __restrict__ saved_ids, const AARec* __restrict__ rec,
     const AAPersp* __restrict__ persp, const float* __restrict__ color,
     const float* __restrict__ d_out, const uint8_t* __restrict__ blend_mask, int H, int W, int V,
     int T, int C, int ntx, int nty, float* __restrict__ d_color, double* __restrict__ d_pos,
@@ -834,22 +839,27 @@ __global__ void __launch_bounds__(256) k_aa_bwd_masked(
   const int own = (ly + 1) * 18 + (lx + 1);
   // every load before the barriers is issued first: the own pixel's id, mask
   // byte and cotangent, and (lanes 0..15 of each wave) one border pixel's
-  // id, mask byte and cotangent
-  const float own_w = rast[pix * 4 + 3];
-  const int own_m = blend_mask[mask_index(g.n, min(g.ph, H - 1), min(g.pw, W - 1), ntx, nty)];
-  float border_w = 0.0f;
-  int border_m = 0;
+  // id, mask byte and cotangent.  The ids are the forward's (the triangle
+  // ids of rast, 4 bytes a pixel beside the mask instead of rast's 16).
+  const int64_t mi = mask_index(g.n, min(g.ph, H - 1), min(g.pw, W - 1), ntx, nty);
+  const int own_id = saved_ids[mi];
+  const int own_m = blend_mask[mi];
+  int border_id = -1, border_m = 0;
   float gown[CS], gbd[CS];
   if constexpr (CT > 0) ld_px<CT>(d_out + pix * CT, CT, gown);
   if (bd.in) {
-    border_w = rast[bd.q * 4 + 3];
-    border_m = blend_mask[mask_index(g.n, bd.qh, bd.qw, ntx, nty)];
+    const int64_t bi = mask_index(g.n, bd.qh, bd.qw, ntx, nty);
+    border_id = saved_ids[bi];
+    border_m = blend_mask[bi];
     if constexpr (CT > 0) ld_px<CT>(d_out + bd.q * CT, CT, gbd);
   }
   // s_nq = 0 is seen by every wave before its first queue slot is taken
   // (the loads above are in flight meanwhile)
   __syncthreads();
-  aa_store_ids(g, bd, own_w, border_w, T, s_tri);
+  // a saved id outside [0, T) reads as empty, as a rast id does, so no
+  // state content can make a record index go out of range
+  s_tri[ly + 1][lx + 1] = g.inside ? ((unsigned)own_id < (unsigned)T ? own_id : -1) : kOut;
+  if (bd.lane) s_tri[bd.r][bd.c] = bd.in ? ((unsigned)border_id < (unsigned)T ? border_id : -1) : kOut;
   if constexpr (CT > 0) {
 #pragma unroll
     for (int k = 0; k < CT; ++k) s_g[own][k] = gown[k];
@@ -996,6 +1006,9 @@ static int aa_records(const float* pos, const int32_t* tri, const int32_t* topo,
 // Saved state of dr_antialias_fwd_save: the blend mask (one byte per pixel
 // of the image padded to 16x16 tiles, a multiple of 256 bytes), then the
 // per-(image, triangle) records, then their corners' d_pos factors.
+// Saved state of dr_antialias_fwd_save: the blend mask (one byte a pixel,
+// mask_index order), the pixels' triangle ids (int32, same order), then the
+// records and their corner factors.
 static int64_t aa_mask_bytes(int N, int H, int W) {
   return (int64_t)N * ((H + 15) / 16) * ((W + 15) / 16) * 256;
 }
@@ -1033,8 +1046,9 @@ static int aa_fwd(const float* color, const float* rast, const float* pos, const
   DR_CHECK_ARG(out != nullptr, "antialias: null output");
   DR_CHECK_ARG(((uintptr_t)saved & 15) == 0, "antialias_fwd_save: saved must be 16-byte aligned");
   uint8_t* mask = saved;
+  int* saved_ids = saved ? (int*)(saved + aa_mask_bytes(N, H, W)) : nullptr;
   AARec* rec = nullptr;
-  AARec* saved_rec = saved ? (AARec*)(saved + aa_mask_bytes(N, H, W)) : nullptr;
+  AARec* saved_rec = saved ? (AARec*)(saved + 5 * aa_mask_bytes(N, H, W)) : nullptr;
   AAPersp* saved_persp = saved ? (AAPersp*)(saved_rec + (int64_t)N * T) : nullptr;
   int st2 = aa_records(pos, tri, topo, N, V, T, H, W, stream, saved_rec, saved_persp, &rec);
   if (st2) return st2;
@@ -1045,7 +1059,7 @@ static int aa_fwd(const float* color, const float* rast, const float* pos, const
   const dim3 grid((unsigned)total), block(256);
   DR_TIMED("k_aa_fwd", stream);
   DR_AA_DISPATCH(k_aa_fwd, ct, grid, block, 0, stream, rast, rec, color, H, W, T, C, ntx, nty,
-                 out, mask);
+                 out, mask, saved_ids);
   DR_CHECK_LAUNCH();
   return DR_OK;
 }
@@ -1071,7 +1085,7 @@ static int aa_bwd(const float* color, const float* rast, const float* pos, const
   const AARec* rec = nullptr;
   const AAPersp* persp = nullptr;
   if (saved) {  // the forward's records
-    rec = (const AARec*)(saved + aa_mask_bytes(N, H, W));
+    rec = (const AARec*)(saved + 5 * aa_mask_bytes(N, H, W));
     persp = (const AAPersp*)(rec + (int64_t)N * T);
   } else {
     AARec* r = nullptr;
@@ -1087,8 +1101,9 @@ static int aa_bwd(const float* color, const float* rast, const float* pos, const
   {
     DR_TIMED("k_aa_bwd", stream);
     if (saved) {
-      DR_AA_DISPATCH(k_aa_bwd_masked, ct, grid, block, 0, stream, rast, rec, persp, color, d_out,
-                     saved, H, W, V, T, C, ntx, nty, d_color, dpos64, acc ? 1 : 0);
+      DR_AA_DISPATCH(k_aa_bwd_masked, ct, grid, block, 0, stream,
+                     (const int*)(saved + aa_mask_bytes(N, H, W)), rec, persp, color, d_out, saved,
+                     H, W, V, T, C, ntx, nty, d_color, dpos64, acc ? 1 : 0);
     } else {
       DR_AA_DISPATCH(k_aa_bwd, ct, grid, block, 0, stream, rast, rec, pos, color, d_out, H, W,
                      V, T, C, ntx, nty, d_color, dpos64, acc ? 1 : 0);
@@ -1116,7 +1131,7 @@ extern "C" int dr_antialias_bwd(const float* color, const float* rast, const flo
 
 extern "C" int64_t dr_antialias_saved_bytes(int N, int H, int W, int T) {
   if (N < 1 || H < 1 || W < 1 || T < 0) return -1;
-  return aa_mask_bytes(N, H, W) + (int64_t)N * T * (int64_t)(sizeof(AARec) + sizeof(AAPersp));
+  return 5 * aa_mask_bytes(N, H, W) + (int64_t)N * T * (int64_t)(sizeof(AARec) + sizeof(AAPersp));
 }
 
 extern "C" int dr_antialias_fwd_save(const float* color, const float* rast, const float* pos,
