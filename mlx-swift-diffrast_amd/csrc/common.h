@@ -204,6 +204,12 @@ __device__ __forceinline__ uint64_t uni(uint64_t x) {
   const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(x >> 32));
   return ((uint64_t)hi << 32) | lo;
 }
+// x of lane l (l wave-uniform): two scalar reads instead of an LDS permute
+__device__ __forceinline__ uint64_t lane_value(uint64_t x, int l) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)x, l);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(x >> 32), l);
+  return ((uint64_t)hi << 32) | lo;
+}
 
 // Wave reductions with DPP row operations (VALU only) and four readlanes:
 // quad xor 1, quad xor 2, row half-mirror and row mirror leave every lane
@@ -422,8 +428,8 @@ __device__ __forceinline__ void group_atomic_add(bool valid, uint64_t key, float
 #pragma unroll 1
   for (int probe = 0; probe < kProbes && pending; ++probe) {
     const int leader = probe_leader(pending, probe);
-    const uint64_t lkey = __shfl(key, leader, kWave);
-    const uint32_t lkey2 = __shfl(key2, leader, kWave);
+    const uint64_t lkey = lane_value(key, leader);
+    const uint32_t lkey2 = (uint32_t)__builtin_amdgcn_readlane((int)key2, leader);
     const bool member = mine && key == lkey && key2 == lkey2;
     const uint64_t members = __ballot(member);
     pending &= ~members;

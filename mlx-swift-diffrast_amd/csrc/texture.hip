@@ -426,7 +426,19 @@ __device__ __forceinline__ void scatter_footprint(bool valid, float* __restrict_
       val[4 * c + 2] = w01 * gc;
       val[4 * c + 3] = w11 * gc;
     }
-    uint64_t pending = __ballot(valid);
+    // The probes pay where many lanes share a footprint: a magnified
+    // texture (a texel cell three or more pixels wide repeats its taps over
+    // runs of three lanes or more along the pixel rows) or one texel under
+    // a whole wave.  Unless at least two lanes share their first tap with
+    // the lane two before them they are skipped: footprints shared in pairs
+    // only, as under a per-pixel LOD bias, never form a group worth them
+    // (cube backward at 4096 x 256^2: 39.0 -> 36.9 ms).  Every lane executes
+    // the shifts (callers keep the wave convergent).
+    const uint64_t a0 = (uint64_t)p[0];
+    const uint32_t l_lo = (uint32_t)dpp_shift<0x112>((int)(uint32_t)a0);
+    const uint32_t l_hi = (uint32_t)dpp_shift<0x112>((int)(uint32_t)(a0 >> 32));
+    const bool run3 = valid && (lane_id() & 15) >= 2 && (((uint64_t)l_hi << 32) | l_lo) == a0;
+    uint64_t pending = __popcll(__ballot(run3)) >= 2 ? __ballot(valid) : 0ull;
     bool mine = valid;
     const int lane = lane_id();
 #pragma unroll 1
@@ -436,7 +448,7 @@ __device__ __forceinline__ void scatter_footprint(bool valid, float* __restrict_
       bool same = mine;
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        lp[t] = (float*)__shfl((uint64_t)p[t], leader, kWave);
+        lp[t] = (float*)lane_value((uint64_t)p[t], leader);
         same = same && p[t] == lp[t];
       }
       const uint64_t members = __ballot(same);

@@ -220,3 +220,47 @@ def test_antialias_saved_mask_superset():
                                        _stream()))
     assert_grad_close(host(dc), d_color, "d_color, full mask")
     assert_grad_close(host(dp), d_pos, "d_pos, full mask")
+
+
+def test_antialias_saved_ids_stay_in_bounds():
+    """The saved state's triangle ids (int32 in the blend mask's pixel order,
+    after the mask) equal rast's; ids outside [0, T) read as empty, as rast
+    ids do, so garbage there, with every mask bit set, changes the gradients
+    but sends no record or vertex read out of range."""
+    torch = torch_dev()
+    import diffrast._lib as L
+    from diffrast import DiffRast
+    from diffrast.ops import _ptr, _stream
+    lib = L.load()
+    rng = np.random.default_rng(11)
+    pos, tri, H, W = aa_scene("tier1")  # ragged 61 x 47
+    rast, _ = O.rasterize(pos, tri, (H, W), gradDB=False, max_per_tile=0)
+    N, V, T, C = pos.shape[0], pos.shape[1], tri.shape[0], 4
+    color = rng.random((N, H, W, C)).astype(np.float32)
+    g = rng.normal(size=color.shape).astype(np.float32)
+    c, r, p, t, gd = dev(color), dev(rast), dev(pos), dev(tri), dev(g)
+    topo = DiffRast.antialiasConstructTopologyHash(t)
+    out = torch.empty_like(c)
+    saved = torch.empty(lib.dr_antialias_saved_bytes(N, H, W, T), dtype=torch.uint8, device="cuda")
+    L.check(lib.dr_antialias_fwd_save(_ptr(c), _ptr(r), _ptr(p), _ptr(t), _ptr(topo), N, H, W, C,
+                                      V, T, _ptr(out), _ptr(saved), _stream()))
+    nty, ntx = -(-H // 16), -(-W // 16)
+    mask_bytes = N * nty * ntx * 256
+    ids = saved[mask_bytes:5 * mask_bytes].view(torch.int32)
+    h, w = np.meshgrid(np.arange(H), np.arange(W), indexing="ij")
+    idx = ((h // 16) * ntx + w // 16) * 256 + ((h % 16) // 8 * 2 + (w % 16) // 8) * 64 + \
+        (h % 8) * 8 + w % 8
+    got = host(ids)
+    got = np.stack([got[n * nty * ntx * 256 + idx] for n in range(N)])
+    want = rast[..., 3].astype(np.int64) - 1  # rast ids are triangle + 1, 0 = empty
+    np.testing.assert_array_equal(got, want)
+    assert (want >= 0).any() and (want < 0).any()
+    ids.copy_(torch.randint(-2 ** 31, 2 ** 31 - 1, ids.shape, dtype=torch.int32, device="cuda"))
+    ids[::7] = torch.arange(ids[::7].numel(), dtype=torch.int32, device="cuda") % max(T, 1)
+    saved[:mask_bytes].fill_(0xFF)
+    dc, dp = torch.empty_like(c), torch.empty_like(p)
+    L.check(lib.dr_antialias_bwd_saved(_ptr(c), _ptr(r), _ptr(p), _ptr(t), _ptr(topo), _ptr(gd),
+                                       _ptr(saved), N, H, W, C, V, T, _ptr(dc), _ptr(dp), 0,
+                                       _stream()))
+    torch.cuda.synchronize()
+    assert np.isfinite(host(dc)).all()

@@ -59,6 +59,32 @@ def test_cube_mip(filt, C, Nt):
     assert_grad_close_lod(host(b.grad), d_bm, sw, "d_biasMap")
 
 
+def test_cube_mip_shared_footprints():
+    """Rows of pixels on one direction share their footprints on both
+    levels: whole rows go through the backward's wave grouping (the
+    per-wave accumulator and the grouped atomics) instead of the table."""
+    torch = torch_dev()
+    from diffrast import DiffRast
+    rng = np.random.default_rng(77)
+    N, S, C, Hi, Wi = 1, 32, 3, 20, 40
+    tex, dirs, dd = cube_inputs(rng, N, 1, S, C, Hi, Wi)
+    dirs[:, 3:9] = np.array([1.0, 0.3, -0.2], np.float32)
+    dd[:, 3:9] = np.float32(0.02)
+    bm = rng.uniform(-1, 1, size=(N, Hi, Wi)).astype(np.float32)
+    bm[:, 3:9] = 0.0
+    t = dev(tex).requires_grad_(True)
+    out = DiffRast.texture(t, dev(dirs), uvDA=dev(dd), filterMode="linear-mipmap-linear",
+                           boundaryMode="cube", mipLevelBias=0.25, mipLevelBiasMap=dev(bm))
+    ref = O.texture(tex, dirs, uvDA=dd, filterMode="linear-mipmap-linear", boundaryMode="cube",
+                    mipLevelBias=0.25, mipLevelBiasMap=bm)
+    assert_fwd_close(host(out), ref)
+    g = rng.normal(size=ref.shape).astype(np.float32)
+    (out * dev(g)).sum().backward()
+    d_tex = O.texture_vjp(tex, dirs, g, uvDA=dd, filterMode="linear-mipmap-linear",
+                          boundaryMode="cube", mipLevelBias=0.25, mipLevelBiasMap=bm)[0]
+    assert_grad_close(host(t.grad), d_tex, "d_tex")
+
+
 def test_cube_mip_without_dir_grad():
     # the default keeps the reference's zero direction gradient
     torch = torch_dev()
