@@ -1499,6 +1499,7 @@ struct CubeArgs {
   int has_bias;
   int64_t P;
   int HWi;
+  int Wi;      // image width (the forward's 16x16 tiles)
   float* out;  // forward
   // backward
   const float* d_out;
@@ -1569,12 +1570,18 @@ __device__ __forceinline__ CubePx cube_px(const CubeArgs& A, int64_t pix) {
 }
 
 // MODE: 1 = mip-nearest, 2 = trilinear (bilinear cube sampling is k_tex_fwd).
+// One 16x16 pixel tile per workgroup (a 16x4 strip per wave), so a wave's
+// texel gathers share cache lines along both image axes.
 template <int MODE, int CT>
 __global__ void __launch_bounds__(256) k_cube_fwd(CubeArgs A) {
-  const int64_t pix = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (pix >= A.P) return;
+  const int Wi = A.Wi, Hi = A.HWi / Wi;
+  const int ntx = (Wi + 15) >> 4, tiles = ntx * ((Hi + 15) >> 4);
+  const int b = (int)blockIdx.x, n = b / tiles, tile = b - n * tiles;
+  const int ty = tile / ntx, tx = tile - ty * ntx;
+  const int ph = ty * 16 + ((int)threadIdx.x >> 4), pw = tx * 16 + ((int)threadIdx.x & 15);
+  if (ph >= Hi || pw >= Wi) return;
+  const int64_t pix = ((int64_t)n * Hi + ph) * Wi + pw;
   const int C = dimC<CT>(A.C);
-  const int n = (int)(pix / A.HWi);
   const CubePx p = cube_px<MODE>(A, pix);
   float* op = A.out + pix * C;
   float acc[kMaxC];
@@ -2007,9 +2014,13 @@ extern "C" int dr_texture_fwd(const float* tex, const float* pyramid, int Nt, in
     CubeArgs A = cube_args(tex, pyramid, md, tex_stride, Ht, Wt, C, uv, uv_da, bias_map,
                            scale_bias, has_bias, P, Hi * Wi);
     A.out = out;
+    A.Wi = Wi;
+    const int64_t tiles = (int64_t)N * ((Hi + 15) / 16) * ((Wi + 15) / 16);
+    DR_CHECK_ARG(tiles <= INT32_MAX, "texture: too many pixel tiles");
+    const dim3 tgrid((unsigned)tiles);
     DR_TIMED("k_cube_fwd", stream);
-    if (filter == DR_FILTER_LINEAR_MIPMAP_LINEAR) DR_CUBE_DISPATCH(k_cube_fwd, 2, grid, A);
-    else DR_CUBE_DISPATCH(k_cube_fwd, 1, grid, A);
+    if (filter == DR_FILTER_LINEAR_MIPMAP_LINEAR) DR_CUBE_DISPATCH(k_cube_fwd, 2, tgrid, A);
+    else DR_CUBE_DISPATCH(k_cube_fwd, 1, tgrid, A);
     DR_CHECK_LAUNCH();
     return DR_OK;
   }
