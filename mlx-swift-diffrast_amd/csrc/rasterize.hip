@@ -814,6 +814,39 @@ __device__ __forceinline__ bool edge_excludes(const TriRec& R, float xa, float x
   return false;
 }
 
+// Whether the triangle's depth lies above zq at every pixel centre of the
+// box [xa, xb] x [ya, yb], so that it cannot take a pixel whose best depth
+// so far is at most zq (test_tri keeps the smaller depth, and the lower index
+// only on equal depths).  The depth sum_k e_k(x, y) sz_k / area is affine in
+// (x, y), so its smallest value over the box is at a corner; in fp64, less a
+// margin over the rounding of the fp32 per-pixel expression (each edge
+// function within 2^-22 of its two products' magnitudes, scaled by 1/area,
+// then the products with the depths and their sum) of four times its bound.
+__device__ __forceinline__ bool depth_excludes(const TriRec& R, float xa, float xb, float ya,
+                                               float yb, float zq) {
+  const double sx0 = R.r0.x, sy0 = R.r0.y, sx1 = R.r0.z, sy1 = R.r0.w;
+  const double sx2 = R.r1.x, sy2 = R.r1.y;
+  const double sz[3] = {R.r1.z, R.r1.w, R.r2.x};
+  const double inv = 1.0 / (double)R.r2.y;
+  const double e[3][4] = {{sx1, sy2, sx2, sy1}, {sx2, sy0, sx0, sy2}, {sx0, sy1, sx1, sy0}};
+  double z0 = 0.0, zx = 0.0, zy = 0.0, m = 0.0, s = 0.0;
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    const double a = e[k][0], b = e[k][1], c = e[k][2], d = e[k][3];
+    z0 += sz[k] * (a * b - c * d);
+    zx += sz[k] * (d - b);
+    zy += sz[k] * (c - a);
+    m = fmax(m, (fabs(a) + 1.0) * (fabs(b) + 1.0) + (fabs(c) + 1.0) * (fabs(d) + 1.0));
+    s += fabs(sz[k]);
+  }
+  z0 *= inv;
+  zx *= inv;
+  zy *= inv;
+  const double zmin = z0 + fmin(zx * (double)xa, zx * (double)xb) + fmin(zy * (double)ya, zy * (double)yb);
+  const double tol = 0x1p-20 * (1.0 + s) * (1.0 + fabs(inv) * m);
+  return zmin - tol > (double)zq;  // false for NaN
+}
+
 template <bool DB, bool PEEL, bool CAPPED>
 __global__ void __launch_bounds__(256) k_raster_px(
     const TriRec* __restrict__ rec, const int4* __restrict__ rect, Items it, int64_t rec_stride,
@@ -888,6 +921,11 @@ __global__ void __launch_bounds__(256) k_raster_px(
     // broadcast read; cheaper than 17 readlanes and their SGPR hazards).
     for (int c0 = 0; c0 < count; c0 += kWave) {
       const int nb = min(kWave, count - c0);
+      // the quadrant's farthest best depth so far; while a pixel of the
+      // image is still uncovered (depth 1e30) no candidate is culled by it
+      const float zq = __int_as_float(wave_reduce_i(
+          __float_as_int(valid ? best.z : -1e30f),
+          [](int a, int b) { return __float_as_int(fmaxf(__int_as_float(a), __int_as_float(b))); }));
       int myt = 0;
       TriRec Rl;
       bool hit = false;
@@ -896,7 +934,10 @@ __global__ void __launch_bounds__(256) k_raster_px(
         Rl = load_rec(rec, rbase + myt);
         hit = !(__float_as_int(Rl.r3.y) < qx0 || __float_as_int(Rl.r3.x) > qx1 ||
                 __float_as_int(Rl.r3.w) < qy0 || __float_as_int(Rl.r3.z) > qy1);
-        if (hit && fabsf(Rl.r2.y) > 1e-30f) hit = !edge_excludes(Rl, cxa, cxb, cya, cyb);
+        if (hit && fabsf(Rl.r2.y) > 1e-30f) {
+          hit = !edge_excludes(Rl, cxa, cxb, cya, cyb);
+          if (hit && zq <= 1.0f) hit = !depth_excludes(Rl, cxa, cxb, cya, cyb, zq);
+        }
       }
       uint64_t m = __ballot(hit);
       if (hit) {

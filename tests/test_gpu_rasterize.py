@@ -722,6 +722,46 @@ def test_backward_small_triangles_with_forward_records():
 
 
 @pytest.mark.gpu
+def test_pixel_parallel_depth_cull_keeps_ties():
+    """The pixel-parallel forward drops a candidate for an 8x8 quadrant when
+    its smallest depth over the quadrant's pixel centres (less a margin over
+    the fp32 rounding) lies above every pixel's best depth so far.  Exact
+    duplicates (the lower index keeps the pixel) and copies a few ulps
+    nearer or farther in depth, taken in random and in near-to-far order,
+    stay bit-exact against the oracle, forward, rast_db and a peeled layer."""
+    torch = torch_dev()
+    from diffrast import DiffRast
+    H, W = 128, 96
+    rng = np.random.default_rng(57)
+    base = rng.uniform(-1.3, 1.3, size=(120, 3, 2)).astype(np.float32)
+    bz = rng.uniform(-0.9, 0.9, size=(120, 3)).astype(np.float32)
+    pick = rng.choice(120, size=80, replace=False)
+    xy = np.concatenate([base, base[pick]], 0)
+    z = np.concatenate([bz, bz[pick]], 0)
+    for i, k in enumerate(range(160, 200)):  # near ties: 1-3 ulps either way
+        step = (i % 3) + 1
+        toward = np.float32(-2.0) if i % 2 else np.float32(2.0)
+        for _ in range(step):
+            z[k] = np.nextafter(z[k], toward)
+    T = xy.shape[0]
+    order = [np.arange(T), np.argsort(z.mean(1))]  # image 1: near to far
+    pos = np.stack([np.concatenate([xy[o], z[o][..., None], np.ones((T, 3, 1), np.float32)],
+                                   -1).reshape(-1, 4) for o in order]).astype(np.float32)
+    tri = np.arange(3 * T, dtype=np.int32).reshape(T, 3)
+    p, t = dev(pos), dev(tri)
+    for _ in range(2):  # the second call sees the first call's statistics
+        ran = _raster_kernels(lambda: DiffRast.rasterize(p, t, (H, W), gradDB=True))
+    assert ran == {"k_raster_px"}
+    rast, db = DiffRast.rasterize(p, t, (H, W), gradDB=True)
+    rr, rdb = O.rasterize(pos, tri, (H, W), gradDB=True, max_per_tile=0)
+    np.testing.assert_array_equal(host(rast), rr)
+    np.testing.assert_array_equal(host(db), rdb)
+    assert (rr[..., 3] > 0).mean() > 0.9
+    r2, _ = DiffRast.rasterize(p, t, (H, W), gradDB=False, peelLayer=rast)
+    rr2, _ = O.rasterize(pos, tri, (H, W), gradDB=False, peelLayer=rr, max_per_tile=0)
+    np.testing.assert_array_equal(host(r2), rr2)
+
+
 def test_pixel_parallel_edge_cull_keeps_boundary_pixels():
     """The pixel-parallel forward drops a candidate for an 8x8 quadrant only
     when one of its edges keeps every pixel centre there outside (with a
