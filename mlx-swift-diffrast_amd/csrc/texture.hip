@@ -2076,19 +2076,26 @@ static int dpyr_get(const DPyrBuf& buf, int64_t np, hipStream_t stream, float*& 
 }
 
 // The cube extension's backward: one thread per pixel, d_tex / d_pyramid by
-// global atomics, then the pyramid collapse over the Nt*6 faces.
+// global atomics, then the pyramid collapse over the Nt*6 faces.  The first
+// `zero_tex` floats of d_tex are cleared first (0: accumulate), after the
+// pyramid gradient's buffer is known to fit, so a refused call leaves d_tex
+// untouched.
 static int cube_bwd(const float* tex, const float* pyramid, const MipDesc& md, int64_t tex_stride,
                     int Nt, int Ht, int Wt, int C, const float* dir, const float* dir_da,
                     const float* bias_map, float bias, int filter, int N, int Hi, int Wi,
-                    const float* d_out, float* d_tex, float* d_dir, float* d_dir_da,
-                    float* d_bias_map, unsigned flags, const DPyrBuf& pbuf, hipStream_t stream) {
+                    const float* d_out, float* d_tex, int64_t zero_tex, float* d_dir,
+                    float* d_dir_da, float* d_bias_map, unsigned flags, const DPyrBuf& pbuf,
+                    hipStream_t stream) {
   const bool mip = filter >= DR_FILTER_LINEAR_MIPMAP_NEAREST;
   float* d_pyr = nullptr;
   if (mip && md.L > 1) {
     const int64_t np = dr_texture_mip_size(Nt * 6, Ht, Wt, C, md.L);
     const int st = dpyr_get(pbuf, np, stream, d_pyr);
     if (st) return st;
-    DR_CHECK_HIP(fill_async(d_pyr, 0.0f, np, stream));
+    if (zero_tex) DR_CHECK_HIP(fill2_async(d_tex, zero_tex, d_pyr, np, 0.0f, stream));
+    else DR_CHECK_HIP(fill_async(d_pyr, 0.0f, np, stream));
+  } else if (zero_tex) {
+    DR_CHECK_HIP(fill_async(d_tex, 0.0f, zero_tex, stream));
   }
   const int64_t P = (int64_t)N * Hi * Wi;
   CubeArgs A = cube_args(tex, pyramid, md, tex_stride, Ht, Wt, C, dir, dir_da, bias_map,
@@ -2143,10 +2150,9 @@ static int texture_bwd(const float* tex, const float* pyramid, int Nt, int Ht, i
   const int64_t ntex = (int64_t)Nt * (cube ? 6 : 1) * Ht * Wt * C;
   const bool zero_tex = !(flags & DR_ACCUMULATE);
   if (cube && (filter >= DR_FILTER_LINEAR_MIPMAP_NEAREST || (flags & DR_CUBE_DIR_GRAD))) {
-    if (zero_tex) DR_CHECK_HIP(fill_async(d_tex, 0.0f, ntex, stream));
     return cube_bwd(tex, pyramid, md, tex_stride, Nt, Ht, Wt, C, uv, uv_da, bias_map, bias,
-                    filter, N, Hi, Wi, d_out, d_tex, d_uv, d_uv_da, d_bias_map, flags, pbuf,
-                    stream);
+                    filter, N, Hi, Wi, d_out, d_tex, zero_tex ? ntex : 0, d_uv, d_uv_da,
+                    d_bias_map, flags, pbuf, stream);
   }
   const bool mip = !cube && filter >= DR_FILTER_LINEAR_MIPMAP_NEAREST;
   float* d_pyr = nullptr;

@@ -7,8 +7,9 @@ oracle on identical inputs):
   * gradients accumulated by scatter-add (summation order differs):
     |got - ref| <= 1e-4 * |ref| + 1e-4 * max|ref|;
   * the mip filters' LOD-dependent gradients (d_uvDA, d_biasMap, the cube
-    direction gradient) at the gradient tolerance, except on pixels whose
-    LOD sits on a switch (see lod_switch_mask), which must be rare.
+    direction gradient) at the gradient tolerance; on pixels whose LOD sits
+    on a switch (see lod_switch_mask), which must be rare, they must match
+    the oracle on one side of the switch.
 """
 import numpy as np
 import pytest
@@ -64,11 +65,27 @@ def lod_switch_mask(ref, lo, hi, frac=0.25):
     return d > frac * GRAD_RTOL * scale
 
 
-def assert_grad_close_lod(got, ref, switch, what="", max_frac=0.01):
-    """assert_grad_close on the pixels off a LOD switch; the switch pixels
-    may differ, and must be at most `max_frac` of all pixels."""
+def assert_grad_close_lod(got, ref, switch, lo, hi, what="", max_frac=0.01):
+    """assert_grad_close on the pixels off a LOD switch.  A switch pixel
+    (at most `max_frac` of all) must be finite and, over all its channels,
+    match the oracle's value at the LOD it was evaluated at or at the LOD
+    shifted by -+LOD_DELTA (`lo`, `hi`: the two sides of the switch), each at
+    the gradient tolerance."""
     assert switch.mean() <= max_frac, f"{what}: {switch.mean():.4f} of pixels on a LOD switch"
+    got = np.asarray(got)
     keep = ~switch
     scale = float(np.abs(ref).max()) if np.size(ref) else 0.0
-    np.testing.assert_allclose(np.asarray(got)[keep], np.asarray(ref)[keep], rtol=GRAD_RTOL,
-                               atol=GRAD_RTOL * scale + 1e-30, err_msg=what)
+    atol = GRAD_RTOL * scale + 1e-30
+    np.testing.assert_allclose(got[keep], np.asarray(ref)[keep], rtol=GRAD_RTOL, atol=atol,
+                               err_msg=what)
+    g = got[switch].astype(np.float64)
+    if g.size == 0:
+        return
+    assert np.isfinite(g).all(), f"{what}: non-finite gradient on a LOD switch pixel"
+    ok = np.zeros(g.shape[:1], bool)
+    for side in (ref, lo, hi):
+        s = np.asarray(side, np.float64)[switch]
+        close = np.abs(g - s) <= atol + GRAD_RTOL * np.abs(s)
+        ok |= close.reshape(close.shape[0], -1).all(axis=1)
+    assert ok.all(), (f"{what}: {(~ok).sum()} of {ok.size} LOD-switch pixels match neither "
+                      "side of the switch")

@@ -171,3 +171,45 @@ def range_batch(seed=4, N=4096, T_per=512, H=256, W=256):
     ranges = np.stack([np.arange(N) * T_per, np.full(N, T_per)], 1).astype(np.int32)
     d = rng.normal(size=(V, 3)).astype(np.float32)
     return dict(pos=pos, tri=tri, ranges=ranges, dir=d, H=H, W=W)
+
+
+def straight_edges(H=64, W=64):
+    """Four images, one triangle each, whose only on-screen edge is a
+    straight line (the other two edges lie off screen).  Images 0 and 1
+    cross every pixel row at x_e = x0 + s (row + 0.5) (s = 1/4 with the
+    triangle on the left, s = -1/8 with it on the right); images 2 and 3 are
+    the same lines with x and y exchanged, crossing every pixel column.
+    Endpoints, crossings and blend weights are exact in fp32 (offsets in
+    eighths of a pixel, a 256-pixel edge span): the crossings never meet a
+    pixel centre or a pixel border on their own axis, and on the other axis
+    they fall on pixel borders only, where the weight is 0.
+
+    Returns pos [4,3,4], tri [1,3], the blend weight beta [4,H,W] that
+    Antialias.swift:274-309 gives the pixel holding the crossing,
+    0.5 - |x_e - (q + 0.5)| for q = floor(x_e) (float64), and the coverage
+    the line implies (pixel centres on the triangle's side) [4,H,W]."""
+    lines = [(16.25, 0.25, -1.0), (48.125, -0.125, 1.0)]  # x0, slope, side
+    pos = np.zeros((4, 3, 4), np.float64)
+    beta = np.zeros((4, H, W), np.float64)
+    cov = np.zeros((4, H, W), np.float32)
+    r = np.arange(H)[:, None] + 0.5
+    c = np.arange(W)[None, :] + 0.5
+    for i in range(4):
+        x0, s, side = lines[i % 2]
+        # pixel-space vertices (a along the crossing axis, t along the other)
+        pts = [(x0 + s * -64.0, -64.0), (x0 + s * 192.0, 192.0), (x0 + side * 300.0, 64.0)]
+        for v, (a, t) in enumerate(pts):
+            X, Y = (a, t) if i < 2 else (t, a)
+            pos[i, v] = (2.0 * X / W - 1.0, 1.0 - 2.0 * Y / H, 0.0, 1.0)
+        for k in range(H if i < 2 else W):
+            xe = x0 + s * (k + 0.5)
+            q = int(math.floor(xe))
+            b = 0.5 - abs(xe - (q + 0.5))
+            if i < 2:
+                beta[i, k, q] = b
+            else:
+                beta[i, q, k] = b
+        a, t = (c, r) if i < 2 else (r, c)
+        cov[i] = side * (a - (x0 + s * t)) > 0
+    return dict(pos=pos.astype(np.float32), tri=np.array([[0, 1, 2]], np.int32), beta=beta,
+                cov=cov)

@@ -264,3 +264,36 @@ def test_antialias_saved_ids_stay_in_bounds():
                                        _stream()))
     torch.cuda.synchronize()
     assert np.isfinite(host(dc)).all()
+
+
+def test_straight_edge_blend_weights():
+    """The blend weight by value on the GPU: straight silhouette edges
+    crossing every pixel row or column at exact sub-pixel positions
+    (Antialias.swift:274-309).  Coverage from the GPU rasterizer, and the
+    forward of DiffRast.antialias and of both C-ABI forward entry points
+    with a one-hot coverage colour, equal the closed form
+    beta = 0.5 - |x_e - (q + 0.5)| bit for bit; the gradients match the
+    oracle."""
+    torch_dev()
+    from diffrast import DiffRast
+    from test_oracle_antialias import straight_edge_expect
+    H = W = 64
+    sc = scenes.straight_edges(H, W)
+    pos, tri, beta = sc["pos"], sc["tri"], sc["beta"]
+    rast, _ = DiffRast.rasterize(dev(pos), dev(tri), (H, W), gradDB=False)
+    rast = host(rast)
+    cov = (rast[..., 3] > 0).astype(np.float32)
+    np.testing.assert_array_equal(cov, sc["cov"])
+    color = np.stack([cov, 1.0 - cov], -1)
+    expect = straight_edge_expect(color, cov, beta)
+    out = DiffRast.antialias(dev(color), dev(rast), dev(pos), dev(tri))
+    np.testing.assert_array_equal(host(out), expect)
+    g = np.random.default_rng(11).normal(size=color.shape).astype(np.float32)
+    d_color, d_pos = O.antialias_vjp(color, rast, pos, tri, g)
+    for masked in (False, True):
+        o, mask, dc, dp = aa_abi(color, rast, pos, tri, g, masked)
+        np.testing.assert_array_equal(o, expect)
+        assert_grad_close(dc, d_color, f"d_color masked={masked}")
+        assert_grad_close(dp, d_pos, f"d_pos masked={masked}")
+        if masked:
+            np.testing.assert_array_equal(mask != 0, beta > 0)

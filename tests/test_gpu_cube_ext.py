@@ -54,9 +54,9 @@ def test_cube_mip(filt, C, Nt):
               for b in (-LOD_DELTA, LOD_DELTA))
     sw = (lod_switch_mask(d_dir, lo[1], hi[1]) | lod_switch_mask(d_dd, lo[2], hi[2]) |
           lod_switch_mask(d_bm, lo[3], hi[3]))
-    assert_grad_close_lod(host(u.grad), d_dir, sw, "d_dir")
-    assert_grad_close_lod(host(d.grad), d_dd, sw, "d_dirDA")
-    assert_grad_close_lod(host(b.grad), d_bm, sw, "d_biasMap")
+    assert_grad_close_lod(host(u.grad), d_dir, sw, lo[1], hi[1], "d_dir")
+    assert_grad_close_lod(host(d.grad), d_dd, sw, lo[2], hi[2], "d_dirDA")
+    assert_grad_close_lod(host(b.grad), d_bm, sw, lo[3], hi[3], "d_biasMap")
 
 
 def test_cube_mip_shared_footprints():

@@ -57,7 +57,7 @@ def test_texture(filt, bnd, C, Nt):
     if mip:
         lo, hi = (O.texture_vjp(tex, uv, g, uvDA=da, filterMode=filt, boundaryMode=bnd,
                                 mipLevelBias=b)[2] for b in (-LOD_DELTA, LOD_DELTA))
-        assert_grad_close_lod(host(d.grad), d_da, lod_switch_mask(d_da, lo, hi), "d_uvDA")
+        assert_grad_close_lod(host(d.grad), d_da, lod_switch_mask(d_da, lo, hi), lo, hi, "d_uvDA")
 
 
 @pytest.mark.parametrize("filt", ["linear-mipmap-linear", "linear-mipmap-nearest"])
@@ -86,8 +86,8 @@ def test_mip_bias(filt):
     lo, hi = (O.texture_vjp(tex, uv, g, uvDA=da, filterMode=filt, boundaryMode="clamp",
                             mipLevelBias=0.5 + b, mipLevelBiasMap=bm) for b in (-LOD_DELTA, LOD_DELTA))
     sw = lod_switch_mask(d_da, lo[2], hi[2]) | lod_switch_mask(d_bm, lo[3], hi[3])
-    assert_grad_close_lod(host(d.grad), d_da, sw, "d_uvDA")
-    assert_grad_close_lod(host(b.grad), d_bm, sw, "d_biasMap")
+    assert_grad_close_lod(host(d.grad), d_da, sw, lo[2], hi[2], "d_uvDA")
+    assert_grad_close_lod(host(b.grad), d_bm, sw, lo[3], hi[3], "d_biasMap")
 
 
 @pytest.mark.parametrize("C,Nt", [(3, 1), (1, 2), (4, 2)])
@@ -174,7 +174,7 @@ def test_smooth_lod_ramp(filt, bnd):
     if mip:
         lo, hi = (O.texture_vjp(tex, uv, g, uvDA=da, filterMode=filt, boundaryMode=bnd,
                                 mipLevelBias=b)[2] for b in (-LOD_DELTA, LOD_DELTA))
-        assert_grad_close_lod(host(d.grad), d_da, lod_switch_mask(d_da, lo, hi), "d_uvDA")
+        assert_grad_close_lod(host(d.grad), d_da, lod_switch_mask(d_da, lo, hi), lo, hi, "d_uvDA")
 
 
 def test_cached_pyramid():

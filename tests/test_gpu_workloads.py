@@ -12,7 +12,8 @@ import pytest
 
 import oracle as O
 import scenes
-from parity import assert_fwd_close, assert_grad_close, dev, host, torch_dev
+from parity import (LOD_DELTA, assert_fwd_close, assert_grad_close, assert_grad_close_lod, dev, host,
+                    lod_switch_mask, torch_dev)
 
 pytestmark = pytest.mark.gpu
 
@@ -313,7 +314,10 @@ def test_range_batch_cube_4096():
     looked up in a shared 6x512^2x3 cube map with the trilinear filter and a
     per-pixel bias map U[-1,1] (the cube + mip + bias extension), forward and
     backward to the cube map, the directions and pos.  Meshes 0..15 against
-    the oracle; the full batch against those meshes rendered alone."""
+    the oracle (forward, d_cube, the direction gradient and its derivatives'
+    gradient, then d_dir-attribute and d_pos through interpolate and the
+    range-mode rasterize VJP with rast_db); the full batch against those
+    meshes rendered alone."""
     torch = torch_dev()
     from diffrast import DiffRast
     _threads()
@@ -338,6 +342,8 @@ def test_range_batch_cube_4096():
         col = DiffRast.texture(tex, dirs, uvDA=dirs_da, filterMode="linear-mipmap-linear",
                                boundaryMode="cube", mipLevelBiasMap=dev(bias[rows]),
                                dirGrad=True)
+        dirs.retain_grad()
+        dirs_da.retain_grad()
         g = torch.ones_like(col) * 1e-3
         (col * g).sum().backward()
         return rast, dirs, dirs_da, col, p, attr, tex
@@ -366,6 +372,21 @@ def test_range_batch_cube_4096():
                    mipLevelBiasMap=bias[:16])
     assert_fwd_close(host(c16), cr)
     g = np.full(cr.shape, 1e-3, np.float32)
-    d_tex, _, _, _ = O.texture_vjp(cube, dr, g, uvDA=dda, filterMode="linear-mipmap-linear",
-                                   boundaryMode="cube", mipLevelBiasMap=bias[:16], dirGrad=True)
+    vjp = lambda b: O.texture_vjp(cube, dr, g, uvDA=dda, filterMode="linear-mipmap-linear",
+                                  boundaryMode="cube", mipLevelBias=b,
+                                  mipLevelBiasMap=bias[:16], dirGrad=True)
+    d_tex, d_dir, d_dda, _ = vjp(0.0)
     assert_grad_close(host(tex16.grad), d_tex, "d_cube")
+    # the direction gradient and its derivatives' gradient, then through
+    # interpolate and the range-mode rasterize VJP (with rast_db) to pos.
+    # The oracle's chain continues from the GPU's d_dir / d_dirDA, so a LOD
+    # switch pixel (evaluated on either side) is not counted twice.
+    lo, hi = vjp(-LOD_DELTA), vjp(LOD_DELTA)
+    sw = lod_switch_mask(d_dir, lo[1], hi[1]) | lod_switch_mask(d_dda, lo[2], hi[2])
+    assert_grad_close_lod(host(d16.grad), d_dir, sw, lo[1], hi[1], "d_dir")
+    assert_grad_close_lod(host(da16.grad), d_dda, sw, lo[2], hi[2], "d_dirDA")
+    d_attr, d_rast, d_rdb = O.interpolate_vjp(d[:nv], rr, tri[:nt], host(d16.grad), rastDB=rdb,
+                                              diffAttrs="all", d_out_da=host(da16.grad))
+    assert_grad_close(host(a16.grad[:nv]), d_attr, "d_dir attribute")
+    d_pos = O.rasterize_vjp(pos[:nv], tri[:nt], rr, d_rast, d_rdb, ranges=ranges[:16])
+    assert_grad_close(host(p16.grad[:nv]), d_pos, "d_pos")

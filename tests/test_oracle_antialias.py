@@ -163,3 +163,31 @@ def test_alpha_range():
     delta = np.abs(out - color)
     assert delta.max() <= 2.0 + 1e-6
     assert (delta > 0).any()
+
+
+def test_straight_edge_blend_weights():
+    """The blend weight by value (Antialias.swift:274-309): a straight
+    silhouette edge crossing every pixel row (images 0, 1) or column
+    (images 2, 3) at a known sub-pixel position x_e blends exactly the pixel
+    q = floor(x_e) holding the crossing, by beta = 0.5 - |x_e - (q + 0.5)|,
+    towards its neighbour across the edge; no other pixel changes.  Every
+    quantity is exact in fp32, so the oracle must equal the closed form
+    bit for bit (a half-pixel shift of the endpoints, a blend of the other
+    pixel of the pair or a cut measured from the wrong side all fail)."""
+    H = W = 64
+    sc = scenes.straight_edges(H, W)
+    pos, tri, beta = sc["pos"], sc["tri"], sc["beta"]
+    rast, _ = O.rasterize(pos, tri, (H, W), gradDB=False)
+    cov = (rast[..., 3] > 0).astype(np.float32)
+    np.testing.assert_array_equal(cov, sc["cov"])
+    color = np.stack([cov, 1.0 - cov], -1)  # one-hot coverage
+    out = O.antialias(color, rast, pos, tri)
+    np.testing.assert_array_equal(out, straight_edge_expect(color, cov, beta))
+    assert (beta > 0).sum() == 4 * 64 and np.unique(beta[beta > 0]).size == 6
+
+
+def straight_edge_expect(color, cov, beta):
+    """The closed form: the blended pixel moves towards the other side of
+    the edge by beta (the colour is one-hot coverage)."""
+    sign = np.where(cov > 0, -1.0, 1.0)
+    return (color + (sign * beta)[..., None] * np.array([1.0, -1.0])).astype(np.float32)
