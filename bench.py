@@ -25,7 +25,10 @@ input resident on the GPU before timing starts:
       x 3, trilinear, per-pixel bias map, direction gradient), backward from
       fixed cotangents to the cube map, the directions and pos.
 
-Prints one JSON line.  `--gpus N` with N > 1 is not supported (one GPU).
+Options: `--graph` times replays of one step captured into a HIP graph
+(the warm-up runs on the capturing stream); `--max-per-tile 128` rasterizes
+with the reference's per-tile limit.  Prints one JSON line.  `--gpus N`
+with N > 1 is not supported (one GPU).
 """
 from __future__ import annotations
 
@@ -93,6 +96,9 @@ class Workload:
     images = 0
     height = width = 0
     triangles = 0  # drawn per step, over all images
+    # rasterize's maxPerTile: 0 keeps every triangle (this build's default);
+    # 128 is the reference's per-tile limit (Rasterize.swift:164-171)
+    max_per_tile = 0
 
     def config(self):
         raise NotImplementedError
@@ -147,7 +153,8 @@ class Tier1(Workload):
         self.sc = sc = scenes.tier1_triangle(H=256, W=256)
         self.pos, self.tri = _dev(sc["pos"]), _dev(sc["tri"])
         self.attr = _dev(sc["attr"], grad=True)
-        r, _ = DiffRast.rasterize(self.pos, self.tri, (256, 256), gradDB=False)
+        r, _ = DiffRast.rasterize(self.pos, self.tri, (256, 256), gradDB=False,
+                                  maxPerTile=self.max_per_tile)
         self.target = DiffRast.interpolate(_dev(sc["target_attr"]), r, self.tri)[0].detach()
         self.loss = torch.empty((), device="cuda")
         self.lib, self._lib = _lib.load(), _lib
@@ -155,7 +162,8 @@ class Tier1(Workload):
     def step(self):
         from diffrast import DiffRast
         self.attr.grad = None
-        rast, _ = DiffRast.rasterize(self.pos, self.tri, (256, 256), gradDB=False)
+        rast, _ = DiffRast.rasterize(self.pos, self.tri, (256, 256), gradDB=False,
+                                     maxPerTile=self.max_per_tile)
         out, _ = DiffRast.interpolate(self.attr, rast, self.tri)
         _mse_backward(out, self.target, self.loss, self.lib, self._lib)
         return self.loss
@@ -168,12 +176,13 @@ class Tier1(Workload):
     def cpu_baseline(self, threads):
         import oracle as O
         sc = self.sc
+        mpt = self.max_per_tile
         target, _ = O.interpolate(sc["target_attr"], O.rasterize(sc["pos"], sc["tri"], (256, 256),
-                                                                 gradDB=False, max_per_tile=0)[0],
+                                                                 gradDB=False, max_per_tile=mpt)[0],
                                   sc["tri"])
 
         def run():
-            rast, _ = O.rasterize(sc["pos"], sc["tri"], (256, 256), gradDB=False, max_per_tile=0)
+            rast, _ = O.rasterize(sc["pos"], sc["tri"], (256, 256), gradDB=False, max_per_tile=mpt)
             out, _ = O.interpolate(sc["attr"], rast, sc["tri"])
             g = ((2.0 / out.size) * (out - target)).astype(np.float32)
             O.interpolate_vjp(sc["attr"], rast, sc["tri"], g)
@@ -201,7 +210,8 @@ class HexPie(Workload):
     def step(self):
         from diffrast import DiffRast
         self.pos.grad = self.attr.grad = None
-        rast, _ = DiffRast.rasterize(self.pos, self.tri, (512, 512), gradDB=False)
+        rast, _ = DiffRast.rasterize(self.pos, self.tri, (512, 512), gradDB=False,
+                                     maxPerTile=self.max_per_tile)
         col, _ = DiffRast.interpolate(self.attr, rast, self.tri)
         out = DiffRast.antialias(col, rast, self.pos, self.tri, topologyHash=self.topo)
         _mse_backward(out, self.target, self.loss, self.lib, self._lib)
@@ -220,7 +230,8 @@ class HexPie(Workload):
         topo = O.antialiasConstructTopologyHash(tri)
 
         def run():
-            rast, _ = O.rasterize(pos, tri, (512, 512), gradDB=False, max_per_tile=0)
+            rast, _ = O.rasterize(pos, tri, (512, 512), gradDB=False,
+                                  max_per_tile=self.max_per_tile)
             col, _ = O.interpolate(attr, rast, tri)
             out = O.antialias(col, rast, pos, tri, topo)
             g = ((2.0 / (4 * out.size)) * (out - target)).astype(np.float32)
@@ -255,7 +266,8 @@ class Icosphere(Workload):
     def step(self):
         from diffrast import DiffRast
         self.pos.grad = self.attr.grad = self.tex.grad = None
-        rast, rast_db = DiffRast.rasterize(self.pos, self.tri, (1024, 1024), gradDB=True)
+        rast, rast_db = DiffRast.rasterize(self.pos, self.tri, (1024, 1024), gradDB=True,
+                                           maxPerTile=self.max_per_tile)
         uv, uv_da = DiffRast.interpolate(self.attr, rast, self.tri, rastDB=rast_db,
                                          diffAttrs="all")
         col = DiffRast.texture(self.tex, uv, uvDA=uv_da, filterMode="linear-mipmap-linear",
@@ -286,7 +298,7 @@ class Icosphere(Workload):
         topo = O.antialiasConstructTopologyHash(tri)
 
         def run():
-            rast, db = O.rasterize(pos, tri, (1024, 1024), max_per_tile=0)
+            rast, db = O.rasterize(pos, tri, (1024, 1024), max_per_tile=self.max_per_tile)
             uv, uvda = O.interpolate(uva, rast, tri, rastDB=db, diffAttrs="all")
             col = O.texture(tex, uv, uvDA=uvda, filterMode="linear-mipmap-linear",
                             boundaryMode="clamp")
@@ -330,7 +342,7 @@ class DisplacedSphere(Workload):
         prev, outs = None, []
         for _ in range(self.layers):
             r, _ = DiffRast.rasterize(self.pos, self.tri, (2048, 2048), gradDB=False,
-                                      peelLayer=prev)
+                                      peelLayer=prev, maxPerTile=self.max_per_tile)
             out, _ = DiffRast.interpolate(self.attr, r, self.tri)
             outs.append(out)
             prev = r.detach()
@@ -362,7 +374,7 @@ class DisplacedSphere(Workload):
             prev = None
             for _ in range(self.layers):
                 r, _ = O.rasterize(pos, tri, (2048, 2048), gradDB=False, peelLayer=prev,
-                                   max_per_tile=0)
+                                   max_per_tile=self.max_per_tile)
                 O.interpolate(attr, r, tri)
                 _, d_rast, _ = O.interpolate_vjp(attr, r, tri, g)
                 O.rasterize_vjp(pos, tri, r, d_rast)
@@ -401,7 +413,8 @@ class RangeCube(Workload):
         self.g = torch.randn((4096, 256, 256, 3), device="cuda", generator=g) * 1e-3
 
     def _chain(self, DiffRast, pos, tri, dirs_attr, cube, bias, ranges, env):
-        rast, db = DiffRast.rasterize(pos, tri, (256, 256), gradDB=True, ranges=ranges)
+        rast, db = DiffRast.rasterize(pos, tri, (256, 256), gradDB=True, ranges=ranges,
+                                      maxPerTile=self.max_per_tile)
         dirs, dirs_da = DiffRast.interpolate(dirs_attr, rast, tri, rastDB=db, diffAttrs="all")
         # empty pixels interpolate to the zero vector, which has no cube face
         # (NaN in the reference too): they look up an environment direction
@@ -444,7 +457,7 @@ class RangeCube(Workload):
 
         def run():
             rast, db = O.rasterize(pos, tri, (256, 256), gradDB=True, ranges=ranges,
-                                   max_per_tile=0)
+                                   max_per_tile=self.max_per_tile)
             dirs, dda = O.interpolate(d, rast, tri, rastDB=db, diffAttrs="all")
             dirs = dirs + (rast[..., 3:4] == 0).astype(np.float32) * env
             O.texture(self.cube_np, dirs, uvDA=dda, **kw)
@@ -477,7 +490,22 @@ def _time_cpu(run, pixels, threads, what, budget_s=12.0, max_reps=40):
             "sample": f"{what}, {reps} rep(s), {per:.3f} s each"}
 
 
-def gpu_run(wl, steps, warmup):
+def gpu_run(wl, steps, warmup, graph=False):
+    """Warm-up, an untimed per-kernel breakdown, then `steps` timed steps:
+    eager calls, or (graph) replays of one step captured into a HIP graph
+    (torch.cuda.graph over the op wrappers, on the stream the warm-up ran
+    on, so the library's scratch for it is sized before capture)."""
+    import torch
+    from diffrast import _lib
+
+    if graph:
+        s = torch.cuda.Stream()
+        with torch.cuda.stream(s):
+            return _gpu_run(wl, steps, warmup, s)
+    return _gpu_run(wl, steps, warmup, None)
+
+
+def _gpu_run(wl, steps, warmup, graph_stream):
     import torch
     from diffrast import _lib
 
@@ -498,6 +526,22 @@ def gpu_run(wl, steps, warmup):
     breakdown = {k: v["total_ms"] / n_break for k, v in rep.items()}
     launches = {k: v["count"] // n_break for k, v in rep.items()}
     dominant = max(breakdown, key=breakdown.get)
+    if graph_stream is not None:
+        # one step captured; the timed region replays it (no events inside a
+        # graph: the dominant kernel's time is the breakdown's)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=graph_stream):
+            res = wl.step()
+        g.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            g.replay()
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        dom = {"count": n_break * launches[dominant], "total_ms": breakdown[dominant] * n_break}
+        assert bool(torch.isfinite(res).all().item())
+        return (t1 - t0) * 1e3 / steps, dominant, dom, breakdown, launches
     # Timed region: only the dominant kernel carries events, on its stream.
     prof.dr_profile_select(dominant.encode())
     prof.dr_profile_reset()
@@ -539,6 +583,11 @@ def main():
     ap.add_argument("--config", type=int, default=3, choices=sorted(WORKLOADS),
                     help="which of the reference's five workloads (3: the headline metric)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--graph", action="store_true",
+                    help="time replays of one step captured into a HIP graph")
+    ap.add_argument("--max-per-tile", type=int, default=0,
+                    help="rasterize with the reference's per-tile triangle limit (128 in the "
+                         "reference; 0, the default, keeps every triangle)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run a 256 MiB copy kernel (HBM counter calibration)")
     args = ap.parse_args()
@@ -548,10 +597,11 @@ def main():
         sys.exit(2)
 
     wl = WORKLOADS[args.config]()
+    wl.max_per_tile = args.max_per_tile
     wl.setup()
     if args.calibrate_copy:
         copy_calibration()
-    ms, dom_name, dom, breakdown, launches = gpu_run(wl, args.steps, args.warmup)
+    ms, dom_name, dom, breakdown, launches = gpu_run(wl, args.steps, args.warmup, args.graph)
     P = wl.images * wl.height * wl.width
     kb = wl.kernel_bytes()
     if "k_raster" in kb:  # the forward runs as k_raster_px for large triangles
@@ -585,7 +635,8 @@ def main():
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
         "data": "synthetic (seeded scenes of the reference's workload shapes)",
-        "config": wl.config(),
+        "config": dict(wl.config(), **({"max_per_tile": wl.max_per_tile} if wl.max_per_tile
+                                           else {}), **({"hip_graph": True} if args.graph else {})),
         "us_per_step": round(ms * 1e3, 1),
         "tris_per_s": round(wl.triangles / (ms * 1e-3), 1),
         "roofline": roofline,

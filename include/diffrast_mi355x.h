@@ -44,6 +44,17 @@
  *     per (device, stream); calls on different streams may overlap.
  *   - Every call returns DR_OK or an error code and never throws; the message
  *     of the last error on the calling thread is dr_get_last_error().
+ *   - HIP graph capture (no counterpart in the reference): a call made while
+ *     its stream is being captured allocates nothing and waits for nothing,
+ *     and is refused with DR_ERR_CAPTURE where it would (scratch that must
+ *     grow, the first rasterize on a stream without dr_rasterize_reserve,
+ *     range mode, whose ranges_host a replay would read stale).  Run each
+ *     call once on the capturing stream first.  A graph uses the scratch of
+ *     the stream it was captured on: replay it on that stream (or ordered
+ *     with it), and not after dr_release_scratch.  Buffers a graph may use
+ *     are kept when later calls grow the scratch, and one call reuses an
+ *     earlier call's work (dr_rasterize_fwd_again, DR_RASTERIZE_BWD_REUSE)
+ *     only within one capture once a stream has been captured.
  *   - Host-memory arguments are named *_host; everything else is device
  *     memory.
  *   - Indices are checked where they are used, so no input makes a kernel
@@ -70,7 +81,12 @@ enum {
   DR_OK = 0,
   DR_ERR_ARGUMENT = 1, /* a shape or argument precondition failed */
   DR_ERR_HIP = 2,      /* a HIP runtime call failed */
-  DR_ERR_MEMORY = 3    /* scratch allocation failed */
+  DR_ERR_MEMORY = 3,   /* scratch allocation failed */
+  /* the call would allocate scratch memory, or wait for the device, while
+   * its stream is being captured into a HIP graph (no counterpart in the
+   * reference): run the same call once on that stream before capturing, or
+   * size the rasterizer's scratch with dr_rasterize_reserve */
+  DR_ERR_CAPTURE = 4
 };
 
 enum {
@@ -128,11 +144,12 @@ int dr_profile_report(char* buf, int len);
  * index.
  * Host synchronisation: the first call on a stream counts every tile's
  * candidates exactly and waits for that count (it sizes the per-tile
- * lists); later calls only read back, asynchronously, the largest count
- * of an earlier call.  A call whose scratch memory must grow waits for the
- * stream before freeing the smaller buffer.  Range mode stages ranges_host
- * through pinned memory and does not wait (unless it runs four calls ahead
- * of the device).  Calls otherwise return before their work has run. */
+ * lists), unless dr_rasterize_reserve sized them; later calls only read
+ * back, asynchronously, the largest count of an earlier call.  A call
+ * whose scratch memory must grow waits for the stream before freeing the
+ * smaller buffer.  Range mode stages ranges_host through pinned memory and
+ * does not wait (unless it runs four calls ahead of the device).  Calls
+ * otherwise return before their work has run. */
 int dr_rasterize_fwd(const float* pos, int64_t pos_batch_stride, const int32_t* tri,
                      const int32_t* ranges_host, const float* peel, int N, int V, int T,
                      int H, int W, float* rast, float* rast_db, dr_stream_t stream);
@@ -179,6 +196,20 @@ int dr_rasterize_fwd_again(const float* pos, int64_t pos_batch_stride, const int
 int dr_rasterize_tile_counts(const float* pos, int64_t pos_batch_stride, const int32_t* tri,
                              const int32_t* ranges_host, int N, int V, int T, int H, int W,
                              int32_t* counts, int64_t* max_count_host, dr_stream_t stream);
+
+/* Sizes the rasterizer's scratch on `stream` up front (no counterpart in
+ * the reference, whose buffers MLX allocates per call, Rasterize.swift:
+ * 256-266, 335-349): calls of up to N images of H x W drawing up to T
+ * triangles each (range mode: T in all, N ranges), V vertices per image for
+ * the backward's fp64 d_pos accumulator, and per-tile lists of
+ * `tile_capacity` triangles.  The first forward on the stream then neither
+ * counts its tiles nor waits: a tile with more candidates than the lists
+ * hold takes the full scan (the same result), and the largest count, read
+ * back asynchronously, raises the capacity of later calls.  For callers
+ * that cannot allocate or wait inside their loop (HIP graph capture, serving
+ * loops); every other call sizes the scratch itself. */
+int dr_rasterize_reserve(int N, int V, int T, int H, int W, int tile_capacity,
+                         dr_stream_t stream);
 
 /* VJP of DiffRast.rasterize: d_pos (same layout and batch stride as pos;
  * range mode accumulates all images into the shared [V,4]).  d_rast_db may

@@ -960,9 +960,9 @@ extern "C" int dr_antialias_topology(const int32_t* tri, int T, int32_t* topo,
   uint64_t S = 64;
   while (S < (uint64_t)E * 2) S <<= 1;
   Scratch* sc = scratch_for(stream);
-  if (!sc) return DR_ERR_HIP;
+  if (!sc) return scratch_fail();
   char* buf = (char*)scratch_get(sc, stream, SLOT_TOPO, (size_t)S * 16);
-  if (!buf) return DR_ERR_MEMORY;
+  if (!buf) return scratch_fail();
   unsigned long long* keys = (unsigned long long*)buf;
   int* cnt = (int*)(buf + S * 8);
   int* slot = cnt + S;
@@ -989,9 +989,9 @@ static int aa_records(const float* pos, const int32_t* tri, const int32_t* topo,
   const int64_t nt = (int64_t)N * T;
   if (!rec) {
     Scratch* sc = scratch_for(stream);
-    if (!sc) return DR_ERR_HIP;
+    if (!sc) return scratch_fail();
     rec = (AARec*)scratch_get(sc, stream, SLOT_AA_REC, (size_t)(nt > 0 ? nt : 1) * sizeof(AARec));
-    if (!rec) return DR_ERR_MEMORY;
+    if (!rec) return scratch_fail();
   }
   if (nt > 0) {
     DR_TIMED("k_aa_rec", stream);
@@ -1080,7 +1080,7 @@ static int aa_bwd(const float* color, const float* rast, const float* pos, const
   double* dpos64 = nullptr;
   if (d_pos) {
     dpos64 = acc64_begin(stream, (int64_t)N * V * 4);
-    if (!dpos64) return DR_ERR_MEMORY;
+    if (!dpos64) return scratch_fail();
   }
   const AARec* rec = nullptr;
   const AAPersp* persp = nullptr;

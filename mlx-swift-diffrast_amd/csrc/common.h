@@ -112,10 +112,27 @@ struct Scratch {
     int64_t n_items = 0, max_items = 0;
     bool px = false;  // the forward kernel it ran (k_raster_px)
     bool brec = false;  // it also wrote the backward's records (SLOT_RBWD_REC)
+    uint64_t capture_id = 0;  // the capture it was made in (0: none)
   } last_raster;
+  // Whether last_raster may be reused by the current call (same capture,
+  // or both uncaptured on a stream that never saw a capture).
+  bool last_raster_reusable() const {
+    return last_raster.valid && last_raster.capture_id == cur_capture &&
+           (cur_capture != 0 || !captured);
+  }
   // A dr_rasterize_bwd has run on this stream, so forwards write the
   // backward's per-triangle records with their setup.
   bool rbwd_want = false;
+  // HIP graph capture.  cur_capture: the capture sequence of the current
+  // call (0 when the stream is not being captured), set by scratch_for.
+  // Once a call has been captured on this stream (`captured`), a replay of
+  // that graph may run between any two later calls: buffers a graph may
+  // point at are never freed (a grown slot retires the old buffer until
+  // dr_release_scratch), and one call reuses another's results only within
+  // one capture (last_raster.capture_id), never between uncaptured calls.
+  uint64_t cur_capture = 0;
+  bool captured = false;
+  std::vector<void*> retired;
 };
 
 // A pinned host buffer of the range-mode staging ring holding at least
@@ -128,10 +145,21 @@ int stage_release(Scratch* sc, int slot, hipStream_t stream);
 // Compute units of the current device (cached per device).
 int device_cu_count();
 
-// Returns the scratch record of (current device, stream); nullptr on error.
+// The capture sequence `stream` is being captured into (a HIP graph), or
+// 0 when it is not.  Under capture the library neither allocates nor
+// waits: scratch that would have to grow, a first rasterize call that would
+// count its tiles, and the range-mode staging are refused with
+// DR_ERR_CAPTURE.
+uint64_t stream_capture_id(hipStream_t stream);
+
+// Returns the scratch record of (current device, stream), with its
+// cur_capture set for this call; nullptr on error.
 Scratch* scratch_for(hipStream_t stream);
 // Ensures slot `s` holds at least `bytes`; returns its pointer or nullptr.
 void* scratch_get(Scratch* sc, hipStream_t stream, int s, size_t bytes);
+// The status to return after scratch_for / scratch_get / stage_acquire
+// gave nullptr on this thread: DR_ERR_CAPTURE, DR_ERR_MEMORY or DR_ERR_HIP.
+int scratch_fail();
 
 // ---------------------------------------------------------------------------
 // kernel timing (dr_profile_*): when enabled, each launch made inside a

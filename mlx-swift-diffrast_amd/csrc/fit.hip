@@ -115,9 +115,9 @@ extern "C" int dr_mse_loss(const float* out, const float* target, int64_t n, flo
   DR_CHECK_ARG(n >= 1, "mse_loss: n must be >= 1");
   DR_CHECK_ARG(out && target && loss, "mse_loss: null tensor");
   Scratch* sc = scratch_for(stream);
-  if (!sc) return DR_ERR_MEMORY;
+  if (!sc) return scratch_fail();
   double* partial = (double*)scratch_get(sc, stream, SLOT_LOSS, kMseBlocks * sizeof(double));
-  if (!partial) return DR_ERR_MEMORY;
+  if (!partial) return scratch_fail();
   const float inv_n = 1.0f / (float)n;
   const bool vec =
       (((uintptr_t)out | (uintptr_t)target | (uintptr_t)(d_out ? d_out : out)) & 15) == 0;

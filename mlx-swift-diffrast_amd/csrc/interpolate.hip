@@ -438,10 +438,10 @@ extern "C" int dr_interpolate_bwd(const float* attr, int64_t attr_batch_stride,
   float* target = d_attr;
   if (copy) {
     Scratch* sc = scratch_for(stream);
-    if (!sc) return DR_ERR_HIP;
+    if (!sc) return scratch_fail();
     const int64_t nc = nattr * kCopies;
     float* c = (float*)scratch_get(sc, stream, SLOT_DATTR_COPY, (size_t)nc * sizeof(float));
-    if (!c) return DR_ERR_MEMORY;
+    if (!c) return scratch_fail();
     if (sc->copy_buf != c) {  // a new buffer: its contents are unknown
       sc->copy_buf = c;
       sc->copy_zero = 0;

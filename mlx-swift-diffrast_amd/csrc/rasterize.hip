@@ -1139,7 +1139,7 @@ static int plan_items(Scratch* sc, hipStream_t stream, const int32_t* ranges_hos
   const size_t nh = 2 * (size_t)N + 1;
   int slot = 0;
   int64_t* h = stage_acquire(sc, nh, slot);
-  if (!h) return DR_ERR_HIP;
+  if (!h) return scratch_fail();
   h[0] = 0;
   max_items = 0;
   for (int n = 0; n < N; ++n) {
@@ -1152,7 +1152,7 @@ static int plan_items(Scratch* sc, hipStream_t stream, const int32_t* ranges_hos
   }
   n_items = h[N];
   int64_t* d = (int64_t*)scratch_get(sc, stream, SLOT_RAST_ITEMS, nh * sizeof(int64_t));
-  if (!d) return DR_ERR_MEMORY;
+  if (!d) return scratch_fail();
   DR_CHECK_HIP(hipMemcpyAsync(d, h, nh * sizeof(int64_t), hipMemcpyHostToDevice, stream));
   const int st = stage_release(sc, slot, stream);
   if (st) return st;
@@ -1228,7 +1228,12 @@ extern "C" int dr_rasterize_tile_counts(const float* pos, int64_t pos_batch_stri
   if (st) return st;
   DR_CHECK_ARG(counts, "rasterize_tile_counts: null counts");
   Scratch* sc = scratch_for(stream);
-  if (!sc) return DR_ERR_HIP;
+  if (!sc) return scratch_fail();
+  if (max_count_host && sc->cur_capture) {
+    set_error("rasterize_tile_counts: the largest count is waited for, which a stream being "
+              "captured into a HIP graph cannot do");
+    return DR_ERR_CAPTURE;
+  }
   sc->last_raster.valid = false;  // its setup and item buffers are rewritten here
   const int ntx = (W + kTile - 1) / kTile, nty = (H + kTile - 1) / kTile;
   const int tiles = ntx * nty;
@@ -1242,7 +1247,7 @@ extern "C" int dr_rasterize_tile_counts(const float* pos, int64_t pos_batch_stri
   TriRec* rec = (TriRec*)scratch_get(sc, stream, SLOT_RAST_REC, (size_t)n_rec * sizeof(TriRec));
   int4* rect = (int4*)scratch_get(sc, stream, SLOT_RAST_RECT, (size_t)n_rec * sizeof(int4));
   int* small = (int*)scratch_get(sc, stream, SLOT_SMALL, 64);
-  if (!rec || !rect || !small) return DR_ERR_MEMORY;
+  if (!rec || !rect || !small) return scratch_fail();
   if (n_rec > 0) {
     DR_TIMED("k_setup", stream);
     hipLaunchKernelGGL(k_setup, dim3(grid_for(n_rec, 256)), dim3(256), 0, stream, pos,
@@ -1287,7 +1292,7 @@ static int raster_fwd(const float* pos, int64_t pos_batch_stride, const int32_t*
   DR_CHECK_ARG(max_per_tile >= 0 && max_per_tile <= kMaxPerTileCap,
                "rasterize: max_per_tile must be in [0, 1024] (0: no limit)");
   Scratch* sc = scratch_for(stream);
-  if (!sc) return DR_ERR_HIP;
+  if (!sc) return scratch_fail();
 
   const int ntx = (W + kTile - 1) / kTile, nty = (H + kTile - 1) / kTile;
   const int tiles = ntx * nty;
@@ -1298,7 +1303,8 @@ static int raster_fwd(const float* pos, int64_t pos_batch_stride, const int32_t*
   const int64_t rec_stride = ranges_host ? 0 : T;
   auto& L = sc->last_raster;
   const bool reuse =
-      again && L.valid && L.pos == pos && L.tri == tri && L.pos_stride == pos_batch_stride &&
+      again && sc->last_raster_reusable() && L.pos == pos && L.tri == tri &&
+      L.pos_stride == pos_batch_stride &&
       L.N == N && L.V == V && L.T == T && L.H == H && L.W == W &&
       L.max_per_tile == max_per_tile && L.range == (ranges_host != nullptr) &&
       (!ranges_host || std::equal(L.ranges.begin(), L.ranges.end(), ranges_host));
@@ -1334,7 +1340,7 @@ static int raster_fwd(const float* pos, int64_t pos_batch_stride, const int32_t*
   rec = (TriRec*)scratch_get(sc, stream, SLOT_RAST_REC, (size_t)n_rec * sizeof(TriRec));
   rect = (int4*)scratch_get(sc, stream, SLOT_RAST_RECT, (size_t)n_rec * sizeof(int4));
   char* cbuf = (char*)scratch_get(sc, stream, SLOT_RAST_CNT, (size_t)n_tiles * 16);
-  if (!rec || !rect || !cbuf) return DR_ERR_MEMORY;
+  if (!rec || !rect || !cbuf) return scratch_fail();
   int* cnt = (int*)cbuf;
   fillc = cnt + n_tiles;
 
@@ -1344,7 +1350,7 @@ static int raster_fwd(const float* pos, int64_t pos_batch_stride, const int32_t*
   // per image or ranged)
   if (sc->rbwd_want && n_rec > 0 && (ranges_host != nullptr || pos_batch_stride != 0)) {
     brec = (RBwdRec*)scratch_get(sc, stream, SLOT_RBWD_REC, (size_t)n_rec * sizeof(RBwdRec));
-    if (!brec) return DR_ERR_MEMORY;
+    if (!brec) return scratch_fail();
   }
   if (n_rec > 0) {  // also clears the fill pass's counters
     DR_TIMED("k_setup", stream);
@@ -1366,7 +1372,11 @@ static int raster_fwd(const float* pos, int64_t pos_batch_stride, const int32_t*
   auto take_stats = [&](int64_t items) {
     sc->tiles_per_item = (double)sc->pinned_total[1] / (double)std::max<int64_t>(items, 1);
   };
-  if (sc->total_pending && hipEventQuery(sc->total_event) == hipSuccess) {
+  // Under graph capture nothing is read back or recorded for later calls
+  // (the host must not query the device), and the first call's count,
+  // which waits, is refused.
+  const bool capturing = sc->cur_capture != 0;
+  if (!capturing && sc->total_pending && hipEventQuery(sc->total_event) == hipSuccess) {
     if (sc->stat_waves > 0) {  // the binning's per-wave figures
       int64_t mx = 0, sum = 0;
       for (int64_t w = 0; w < sc->stat_waves; ++w) {
@@ -1380,6 +1390,12 @@ static int raster_fwd(const float* pos, int64_t pos_batch_stride, const int32_t*
     take_stats(sc->stat_items);
     sc->total_pending = false;
     if (mx > C) C = grow(mx);
+  }
+  if (C == 0 && capturing) {
+    set_error("rasterize: the first call on a stream counts its tiles and waits for the count; "
+              "run it once on this stream before capturing into a HIP graph, or size the lists "
+              "with dr_rasterize_reserve");
+    return DR_ERR_CAPTURE;
   }
   if (C == 0) {
     DR_CHECK_HIP(fill_async(cnt, 0, n_tiles, stream));
@@ -1399,11 +1415,11 @@ static int raster_fwd(const float* pos, int64_t pos_batch_stride, const int32_t*
   C = (int)std::min<int64_t>(C, c_budget);
   if (C > sc->bin_cap) sc->bin_cap = C;
   list = (int*)scratch_get(sc, stream, SLOT_RAST_LIST, (size_t)n_tiles * C * 4);
-  if (!list) return DR_ERR_MEMORY;
+  if (!list) return scratch_fail();
 
   // (fillc was cleared with the setup) this call's largest count and list
   // entries, for the next call (when the previous ones have been read)
-  want_stats = !sc->total_pending;
+  want_stats = !sc->total_pending && !capturing;
   stat_waves = launch_binning(true, it, n_items, max_items, N, rect, ntx, tiles, fillc, list, C,
                               stream, want_stats ? sc->wave_stats_dev : nullptr,
                               Scratch::kWaveStatsMax);
@@ -1465,6 +1481,7 @@ static int raster_fwd(const float* pos, int64_t pos_batch_stride, const int32_t*
   L.C = C;
   L.px = px;
   L.brec = brec != nullptr;
+  L.capture_id = sc->cur_capture;
   L.valid = true;
   return DR_OK;
 }
@@ -1487,6 +1504,32 @@ extern "C" int dr_rasterize_fwd_again(const float* pos, int64_t pos_batch_stride
 }
 
 
+extern "C" int dr_rasterize_reserve(int N, int V, int T, int H, int W, int tile_capacity,
+                                    dr_stream_t stream_) {
+  hipStream_t stream = (hipStream_t)stream_;
+  DR_CHECK_ARG(N >= 1 && V >= 0 && T >= 0 && H >= 1 && W >= 1 && tile_capacity >= 1,
+               "rasterize_reserve: bad sizes");
+  Scratch* sc = scratch_for(stream);
+  if (!sc) return scratch_fail();
+  const int ntx = (W + kTile - 1) / kTile, nty = (H + kTile - 1) / kTile;
+  const int64_t n_tiles = (int64_t)N * ntx * nty;
+  const int64_t n_rec = (int64_t)N * std::max(T, 1);
+  // the same list budget as the forward's
+  const int64_t c_budget = std::max<int64_t>(32, ((int64_t)1 << 30) / std::max<int64_t>(n_tiles, 1));
+  const int C = (int)std::min<int64_t>(tile_capacity, c_budget);
+  const bool ok =
+      scratch_get(sc, stream, SLOT_RAST_REC, (size_t)n_rec * sizeof(TriRec)) &&
+      scratch_get(sc, stream, SLOT_RAST_RECT, (size_t)n_rec * sizeof(int4)) &&
+      scratch_get(sc, stream, SLOT_RAST_CNT, (size_t)n_tiles * 16) &&
+      scratch_get(sc, stream, SLOT_RAST_LIST, (size_t)n_tiles * C * 4) &&
+      scratch_get(sc, stream, SLOT_SMALL, 64) &&
+      scratch_get(sc, stream, SLOT_RBWD_REC, (size_t)n_rec * sizeof(RBwdRec)) &&
+      scratch_get(sc, stream, SLOT_DPOS64, (size_t)std::max<int64_t>((int64_t)N * V * 4, 1) * 8);
+  if (!ok) return scratch_fail();
+  if (C > sc->bin_cap) sc->bin_cap = C;
+  return DR_OK;
+}
+
 extern "C" int dr_rasterize_bwd(const float* pos, int64_t pos_batch_stride, const int32_t* tri,
                                 const float* rast, const float* d_rast, const float* d_rast_db,
                                 int N, int V, int T, int H, int W, float* d_pos, unsigned flags,
@@ -1500,7 +1543,7 @@ extern "C" int dr_rasterize_bwd(const float* pos, int64_t pos_batch_stride, cons
   // d_pos is summed in fp64 across workgroups and rounded once, so it does
   // not depend on the order in which their additions land
   double* acc = acc64_begin(stream, npos);
-  if (!acc) return DR_ERR_MEMORY;
+  if (!acc) return scratch_fail();
   const int ntx = (W + kTile - 1) / kTile, nty = (H + kTile - 1) / kTile;
   const int64_t blocks = (int64_t)N * ntx * nty;
   // per (image, triangle) records (one set for all images when pos is
@@ -1509,12 +1552,13 @@ extern "C" int dr_rasterize_bwd(const float* pos, int64_t pos_batch_stride, cons
   // its triangle's record itself)
   const int64_t nrec = (pos_batch_stride ? (int64_t)N : 1) * T;
   Scratch* sc = scratch_for(stream);
-  if (!sc) return DR_ERR_HIP;
+  if (!sc) return scratch_fail();
   // DR_RASTERIZE_BWD_REUSE: the caller states that the last forward on this
   // stream drew this pos and tri, unchanged since; if that forward wrote the
   // records, they are used as they are
   const auto& L = sc->last_raster;
-  const bool reuse = nrec > 0 && (flags & DR_RASTERIZE_BWD_REUSE) && L.valid && L.brec &&
+  const bool reuse = nrec > 0 && (flags & DR_RASTERIZE_BWD_REUSE) && sc->last_raster_reusable() &&
+                     L.brec &&
                      L.pos == pos && L.tri == tri && L.N == N && L.V == V && L.T == T &&
                      (L.range ? pos_batch_stride == 0
                               : pos_batch_stride != 0 && L.pos_stride == pos_batch_stride) &&
@@ -1527,7 +1571,7 @@ extern "C" int dr_rasterize_bwd(const float* pos, int64_t pos_batch_stride, cons
       trec = (RBwdRec*)sc->ptr[SLOT_RBWD_REC];
     } else {
       trec = (RBwdRec*)scratch_get(sc, stream, SLOT_RBWD_REC, (size_t)nrec * sizeof(RBwdRec));
-      if (!trec) return DR_ERR_MEMORY;
+      if (!trec) return scratch_fail();
       sc->last_raster.brec = false;  // the slot now holds this call's records
       DR_TIMED("k_rbwd_rec", stream);
       hipLaunchKernelGGL(k_rbwd_rec, dim3((unsigned)((nrec + 255) / 256)), dim3(256), 0, stream,

@@ -18,17 +18,48 @@ void set_error(const std::string& msg) { g_last_error = msg; }
 
 static std::mutex g_mu;
 static std::map<std::pair<int, hipStream_t>, Scratch*> g_scratch;
+static thread_local int g_scratch_fail = DR_ERR_HIP;
+
+int scratch_fail() { return g_scratch_fail; }
+
+uint64_t stream_capture_id(hipStream_t stream) {
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  unsigned long long id = 0;
+  if (hipStreamGetCaptureInfo(stream, &st, &id) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  return st == hipStreamCaptureStatusActive ? (uint64_t)id | (1ull << 63) : 0;
+}
+
+static void capture_refused(const char* what) {
+  g_scratch_fail = DR_ERR_CAPTURE;
+  set_error(std::string(what) +
+            " while the stream is being captured into a HIP graph: run the same call once on "
+            "this stream before capturing (or size the rasterizer with dr_rasterize_reserve)");
+}
 
 Scratch* scratch_for(hipStream_t stream) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) {
     set_error("hipGetDevice failed");
+    g_scratch_fail = DR_ERR_HIP;
     return nullptr;
   }
+  const uint64_t cap = stream_capture_id(stream);
   std::lock_guard<std::mutex> lk(g_mu);
   auto key = std::make_pair(dev, stream);
   auto it = g_scratch.find(key);
-  if (it != g_scratch.end()) return it->second;
+  if (it != g_scratch.end()) {
+    it->second->cur_capture = cap;
+    if (cap) it->second->captured = true;
+    return it->second;
+  }
+  if (cap) {  // the pinned counters below would be allocated
+    capture_refused("the library's first call on a stream allocates its scratch");
+    return nullptr;
+  }
+  g_scratch_fail = DR_ERR_HIP;
   Scratch* sc = new Scratch();
   if (hipHostMalloc((void**)&sc->pinned_total, 2 * sizeof(int64_t), hipHostMallocDefault) != hipSuccess ||
       hipHostGetDevicePointer((void**)&sc->pinned_total_dev, sc->pinned_total, 0) != hipSuccess ||
@@ -50,13 +81,24 @@ Scratch* scratch_for(hipStream_t stream) {
 void* scratch_get(Scratch* sc, hipStream_t stream, int s, size_t bytes) {
   if (bytes == 0) bytes = 256;
   if (sc->cap[s] >= bytes) return sc->ptr[s];
-  // Grow: the old buffer may still be read by queued work on this stream.
+  if (sc->cur_capture) {
+    capture_refused(("scratch slot " + std::to_string(s) + " would grow to " +
+                     std::to_string(bytes) + " bytes").c_str());
+    return nullptr;
+  }
+  g_scratch_fail = DR_ERR_MEMORY;
+  // Grow: the old buffer may still be read by queued work on this stream,
+  // or by a graph captured on it (then it is kept until dr_release_scratch).
   if (sc->ptr[s]) {
-    if (hipStreamSynchronize(stream) != hipSuccess) {
-      set_error("scratch: stream synchronize failed");
-      return nullptr;
+    if (sc->captured) {
+      sc->retired.push_back(sc->ptr[s]);
+    } else {
+      if (hipStreamSynchronize(stream) != hipSuccess) {
+        set_error("scratch: stream synchronize failed");
+        return nullptr;
+      }
+      (void)hipFree(sc->ptr[s]);
     }
-    (void)hipFree(sc->ptr[s]);
     sc->ptr[s] = nullptr;
     sc->cap[s] = 0;
   }
@@ -74,6 +116,11 @@ void* scratch_get(Scratch* sc, hipStream_t stream, int s, size_t bytes) {
 }
 
 int64_t* stage_acquire(Scratch* sc, size_t n, int& slot) {
+  if (sc->cur_capture) {  // a replay would copy whatever the buffer then holds
+    capture_refused("range mode stages its ranges through host memory");
+    return nullptr;
+  }
+  g_scratch_fail = DR_ERR_HIP;
   slot = sc->stage_next;
   sc->stage_next = (sc->stage_next + 1) % Scratch::kStageRing;
   if (sc->stage_pending[slot]) {
@@ -247,6 +294,7 @@ int dr_release_scratch(void) {
     (void)hipStreamSynchronize(it->first.second);
     for (int s = 0; s < dr::SLOT_COUNT; ++s)
       if (sc->ptr[s]) (void)hipFree(sc->ptr[s]);
+    for (void* p : sc->retired) (void)hipFree(p);
     if (sc->pinned_total) (void)hipHostFree(sc->pinned_total);
     if (sc->wave_stats) (void)hipHostFree(sc->wave_stats);
     if (sc->total_event) (void)hipEventDestroy(sc->total_event);

@@ -2070,9 +2070,9 @@ static int dpyr_get(const DPyrBuf& buf, int64_t np, hipStream_t stream, float*& 
     return DR_OK;
   }
   Scratch* sc = scratch_for(stream);
-  if (!sc) return DR_ERR_HIP;
+  if (!sc) return scratch_fail();
   d_pyr = (float*)scratch_get(sc, stream, SLOT_DPYR, (size_t)np * sizeof(float));
-  return d_pyr ? DR_OK : DR_ERR_MEMORY;
+  return d_pyr ? DR_OK : scratch_fail();
 }
 
 // The cube extension's backward: one thread per pixel, d_tex / d_pyramid by

@@ -30,6 +30,7 @@ SIGNATURES = {
     "dr_rasterize_fwd_ex": ([_p, _i64, _p, _p, _p, _i, _i, _i, _i, _i, _p, _p, _i, _p], _i),
     "dr_rasterize_fwd_again": ([_p, _i64, _p, _p, _p, _i, _i, _i, _i, _i, _p, _p, _i, _p], _i),
     "dr_rasterize_tile_counts": ([_p, _i64, _p, _p, _i, _i, _i, _i, _i, _p, _p, _p], _i),
+    "dr_rasterize_reserve": ([_i, _i, _i, _i, _i, _i, _p], _i),
     "dr_rasterize_bwd": ([_p, _i64, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p, _u, _p], _i),
     "dr_interpolate_fwd": ([_p, _i64, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i, _p, _p, _p],
                            _i),
@@ -55,7 +56,7 @@ SIGNATURES = {
     "dr_adam_step": ([_p, _p, _p, _p, _p, _p, _i64, _i, _f, _f, _f, _f, _p], _i),
 }
 
-DR_OK, DR_ERR_ARGUMENT, DR_ERR_HIP, DR_ERR_MEMORY = 0, 1, 2, 3
+DR_OK, DR_ERR_ARGUMENT, DR_ERR_HIP, DR_ERR_MEMORY, DR_ERR_CAPTURE = 0, 1, 2, 3, 4
 DR_ACCUMULATE = 1
 DR_CUBE_DIR_GRAD = 2
 DR_RASTERIZE_BWD_REUSE = 4
