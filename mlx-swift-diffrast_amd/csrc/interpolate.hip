@@ -30,7 +30,14 @@ __device__ __forceinline__ void st_run(float* __restrict__ p, const float* v, in
   }
 }
 
-constexpr int kInterpPix = 2;  // pixels per thread (more loads in flight)
+// Pixels per thread of the forward (more independent load chains in
+// flight): four for six attributes (a 16 x 2048^2 batch at ~2.5 pixels per
+// triangle waits on its vertex rows: 3.22 -> 3.08 ms per step of four
+// layers), two otherwise (four measured slower at 8 x 1024^2 with A = 2).
+template <int AT>
+constexpr int interp_pix() {
+  return AT >= 6 ? 4 : 2;
+}
 
 template <int AT, int KT>
 __global__ void __launch_bounds__(256) k_interp_fwd(
@@ -38,23 +45,24 @@ __global__ void __launch_bounds__(256) k_interp_fwd(
     const float* __restrict__ rast_db, const int32_t* __restrict__ tri,
     const int32_t* __restrict__ diff_idx, int K_, int64_t P, int HW, int V, int T, int A_,
     float* __restrict__ out, float* __restrict__ out_da) {
+  constexpr int PX = interp_pix<AT>();
   constexpr int NA = AT > 0 ? AT : 8;       // register slots for attributes
   constexpr int NK = KT > 0 ? 2 * KT : 8;   // and for derivative outputs
   const int A = dimA<AT>(A_);
   const int K = KT > 0 ? KT : K_;
-  const int64_t base = (int64_t)blockIdx.x * (256 * kInterpPix) + threadIdx.x;
-  float4 r[kInterpPix];
-  int t[kInterpPix];
+  const int64_t base = (int64_t)blockIdx.x * (256 * PX) + threadIdx.x;
+  float4 r[PX];
+  int t[PX];
 #pragma unroll
-  for (int q = 0; q < kInterpPix; ++q) {
+  for (int q = 0; q < PX; ++q) {
     const int64_t pix = base + q * 256;
     r[q] = pix < P ? *reinterpret_cast<const float4*>(rast + pix * 4) : make_float4(0.f, 0.f, 0.f, 0.f);
     t[q] = pix < P ? f2i(r[q].w) - 1 : -1;
     if (t[q] >= T) t[q] = -1;  // not a triangle of this mesh: empty
   }
-  int iv[kInterpPix][3];
+  int iv[PX][3];
 #pragma unroll
-  for (int q = 0; q < kInterpPix; ++q) {
+  for (int q = 0; q < PX; ++q) {
     iv[q][0] = iv[q][1] = iv[q][2] = 0;
     if (t[q] >= 0) {
       iv[q][0] = tri[t[q] * 3 + 0];
@@ -64,7 +72,7 @@ __global__ void __launch_bounds__(256) k_interp_fwd(
     }
   }
 #pragma unroll
-  for (int q = 0; q < kInterpPix; ++q) {
+  for (int q = 0; q < PX; ++q) {
     const int64_t pix = base + q * 256;
     if (pix >= P) continue;
     float* o = out + pix * A;
@@ -398,10 +406,12 @@ extern "C" int dr_interpolate_fwd(const float* attr, int64_t attr_batch_stride,
   if (st) return st;
   DR_CHECK_ARG(out && (K == 0 || out_da), "interpolate: null output");
   const int64_t P = (int64_t)N * H * W;
-  const dim3 grid(grid_for(P, 256 * kInterpPix));
   DR_TIMED("k_interp_fwd", stream);
   // the compile-time shapes store with 8/16-byte vector writes
   const bool aligned = (((uintptr_t)out | (uintptr_t)(out_da ? out_da : out)) & 15) == 0;
+  // the dispatched kernel's pixels per thread (DR_INTERP_DISPATCH's choice)
+  const int px = aligned && A == 6 && K == 0 ? interp_pix<6>() : interp_pix<0>();
+  const dim3 grid(grid_for(P, 256 * px));
   if (!aligned)
     hipLaunchKernelGGL((k_interp_fwd<0, 0>), grid, dim3(256), 0, stream, attr, attr_batch_stride,
                        rast, rast_db, tri, diff_idx, K, P, H * W, V, T, A, out, out_da);

@@ -502,7 +502,10 @@ __global__ void __launch_bounds__(kRThreads) k_raster(
     const int* __restrict__ cnt, const int* __restrict__ list, int cap,
     const float* __restrict__ peel, int N, int H, int W, int ntx, int nty, int max_per_tile,
     int slot_keys, float* __restrict__ rast, float* __restrict__ rast_db) {
-  __shared__ TriRec s_rec[kRChunk];
+  // the candidates' records, one array per 16-byte row (a record's rows
+  // 64 bytes apart would put the work items' reads of different
+  // candidates on the same few banks)
+  __shared__ float4 s_r0[kRChunk], s_r1[kRChunk], s_r2[kRChunk], s_r3[kRChunk];
   __shared__ int s_t[kRChunk];
   __shared__ int s_box[kRChunk];             // x0 | y0 << 4 | (w - 1) << 8 | (h - 1) << 12
   __shared__ uint16_t s_item[kRItems];       // candidate << 6 | piece
@@ -642,7 +645,7 @@ __global__ void __launch_bounds__(kRThreads) k_raster(
   if (tid < 16) s_x[tid] = 2.0f * ((float)(x0t + tid) + 0.5f) / (float)W - 1.0f;
   else if (tid < 32) s_y[tid - 16] = 1.0f - 2.0f * ((float)(y0t + tid - 16) + 0.5f) / (float)H;
   if (tid == 0) s_total[0] = s_total[1] = 0;
-  // one round: every candidate's record stays in s_rec, and the keys carry
+  // one round: every candidate's record stays in LDS, and the keys carry
   // its slot (slot_keys: all record indices below 2^25)
   const bool slots = slot_keys && count <= kRChunk;
   for (int c0 = 0, round = 0; c0 < count; c0 += kRChunk, ++round) {
@@ -662,7 +665,10 @@ __global__ void __launch_bounds__(kRThreads) k_raster(
       const int by1 = min(__float_as_int(R.r3.w) - y0t, ny - 1);
       if (bx0 <= bx1 && by0 <= by1) {
         const int bw = bx1 - bx0 + 1, bh = by1 - by0 + 1;
-        s_rec[tid] = R;
+        s_r0[tid] = R.r0;
+        s_r1[tid] = R.r1;
+        s_r2[tid] = R.r2;
+        s_r3[tid] = R.r3;
         s_t[tid] = t;
         s_box[tid] = bx0 | (by0 << 4) | ((bw - 1) << 8) | ((bh - 1) << 12);
         pieces = (bw * bh + kRSub - 1) / kRSub;
@@ -685,7 +691,7 @@ __global__ void __launch_bounds__(kRThreads) k_raster(
       for (int e = tid; e < np; e += blockDim.x) {
         const int ie = s_item[e];
         const int k = ie >> 6, q = ie & 63;
-        const TriRec R = s_rec[k];
+        const float4 R0 = s_r0[k], R1 = s_r1[k], R2 = s_r2[k];  // r3 (the box) is not needed
         const int t = s_t[k], bx = s_box[k];
         const int bx0 = bx & 15, by0 = (bx >> 4) & 15, bw = ((bx >> 8) & 15) + 1;
         const int bh = ((bx >> 12) & 15) + 1;
@@ -694,9 +700,9 @@ __global__ void __launch_bounds__(kRThreads) k_raster(
         // stays well clear of an integer)
         int ry = f2i(((float)o0 + 0.5f) * __builtin_amdgcn_rcpf((float)bw));
         int rx = o0 - ry * bw;
-        const float sx0 = R.r0.x, sy0 = R.r0.y, sx1 = R.r0.z, sy1 = R.r0.w;
-        const float sx2 = R.r1.x, sy2 = R.r1.y, sz0 = R.r1.z, sz1 = R.r1.w;
-        const float sz2 = R.r2.x, area = R.r2.y, inv_area = R.r2.z;
+        const float sx0 = R0.x, sy0 = R0.y, sx1 = R0.z, sy1 = R0.w;
+        const float sx2 = R1.x, sy2 = R1.y, sz0 = R1.z, sz1 = R1.w;
+        const float sz2 = R2.x, area = R2.y, inv_area = R2.z;
         for (int o = o0; o < o1; ++o) {
           const int cx = bx0 + rx, cy = by0 + ry;
           const float px = s_x[cx], py = s_y[cy];
@@ -733,7 +739,15 @@ __global__ void __launch_bounds__(kRThreads) k_raster(
     if (key != ~0ull) {
       const uint32_t id = (uint32_t)key;
       const int t = slots ? (int)(id >> 7) : (int)id;
-      R = slots ? s_rec[id & 127] : load_rec(rec, rbase + t);
+      if (slots) {
+        const int sl = id & 127;
+        R.r0 = s_r0[sl];
+        R.r1 = s_r1[sl];
+        R.r2 = s_r2[sl];
+        R.r3 = s_r3[sl];
+      } else {
+        R = load_rec(rec, rbase + t);
+      }
       test_tri(R, t, s_x[lx], s_y[ly], x0t + lx, y0t + ly, -1e30f, best);  // as the scan
     }
     write_px(pix, best, &R);  // R is read only when best.t >= 0, i.e. it was set

@@ -1636,25 +1636,43 @@ __device__ __forceinline__ void cube_bwd_px(const CubeArgs& A, int64_t pix, bool
   }
   const float* gsrc = CT > 0 ? g : gp;  // run-time C reads d_out directly
   const CubeSel& s = p.s;
+  // Trilinear with the LOD inside (0, L-1): the LOD gradient needs both
+  // levels' samples (:1011-1102), and those levels are the two the filter
+  // blends (the same LOD expression), so the texels read here serve it too.
+  float lod_raw = 0.0f, Asq = 0.0f, Bsq = 0.0f;
+  bool lod_in = false;
+  if (MODE > 0) {
+    const float sx = p.da.x * (float)A.Wt, sy = p.da.y * (float)A.Wt;
+    const float tx_ = p.da.z * (float)A.Ht, ty_ = p.da.w * (float)A.Ht;
+    Asq = sx * sx + tx_ * tx_;
+    Bsq = sy * sy + ty_ * ty_;
+    lod_raw = 0.5f * log2f(fmaxf(fmaxf(Asq, Bsq), 1e-20f));
+    lod_in = lod_raw > 0.0f && lod_raw < (float)(A.md.L - 1);
+  }
+  const bool lod_here = MODE == 2 && valid && lod_in;
   // sample position gradient (:934-999) and the pyramid scatter (:870-932);
   // a level of zero weight adds nothing and is skipped (uniformly per wave)
-  float du = 0.0f, dv = 0.0f;
+  float du = 0.0f, dv = 0.0f, d_lod = 0.0f;
   for (int li = 0; li < (MODE == 0 ? 1 : 2); ++li) {
     const int k = li == 0 ? p.ld.k0 : p.ld.k1;
     const float scale = MODE == 0 ? 1.0f : (li == 0 ? (1.0f - p.ld.frac) : p.ld.frac);
     const bool on = valid && scale != 0.0f;
-    if (__ballot(on) == 0ull) continue;
+    const bool rd = on || lod_here;  // the texels are read
+    if (__ballot(rd) == 0ull) continue;
     const int Hk = mip_h(A.md, k), Wk = mip_w(A.md, k);
     const float* lv = cube_level(A, n, s.face, k, Hk, Wk);
     float* dl = cube_dlevel(A, n, s.face, k, Hk, Wk);
     const Bilin b = bilin(p.u, p.v, Wk, Hk, DR_BOUNDARY_CLAMP);
-    if (li == 0)
-      scatter_footprint<CT, true, TexTableU<CT, kCubeTable>>(on, dl, Wk, C, b, gsrc, scale, acc0,
-                                                             tab);
-    else
-      scatter_footprint<CT, false, TexTableU<CT, kCubeTable>>(on, dl, Wk, C, b, gsrc, scale, acc0,
-                                                              tab);
-    if (!on) continue;
+    if (__ballot(on)) {
+      if (li == 0)
+        scatter_footprint<CT, true, TexTableU<CT, kCubeTable>>(on, dl, Wk, C, b, gsrc, scale,
+                                                               acc0, tab);
+      else
+        scatter_footprint<CT, false, TexTableU<CT, kCubeTable>>(on, dl, Wk, C, b, gsrc, scale,
+                                                                acc0, tab);
+    }
+    if (!rd) continue;
+    const float sign = li == 0 ? -1.0f : 1.0f;
     float dfx = 0.0f, dfy = 0.0f;
     for (int c = 0; c < C; ++c) {
       const float t00 = lv[((int64_t)b.iy0 * Wk + b.ix0) * C + c];
@@ -1664,6 +1682,10 @@ __device__ __forceinline__ void cube_bwd_px(const CubeArgs& A, int64_t pix, bool
       const float gs = gsrc[c] * scale;
       dfx += gs * ((1.0f - b.fy) * (t10 - t00) + b.fy * (t11 - t01));
       dfy += gs * ((1.0f - b.fx) * (t01 - t00) + b.fx * (t11 - t10));
+      if (lod_here) {
+        const float sample = b.w00 * t00 + b.w10 * t10 + b.w01 * t01 + b.w11 * t11;
+        d_lod += sign * sample * gsrc[c];
+      }
     }
     du += dfx * (float)Wk;
     dv += dfy * (float)Hk;
@@ -1681,27 +1703,25 @@ __device__ __forceinline__ void cube_bwd_px(const CubeArgs& A, int64_t pix, bool
   if (MODE > 0) {
     const float sx = p.da.x * (float)A.Wt, sy = p.da.y * (float)A.Wt;
     const float tx_ = p.da.z * (float)A.Ht, ty_ = p.da.w * (float)A.Ht;
-    const float Asq = sx * sx + tx_ * tx_;
-    const float Bsq = sy * sy + ty_ * ty_;
     const float rho_sq = fmaxf(Asq, Bsq);
-    const float lod_raw = 0.5f * log2f(fmaxf(rho_sq, 1e-20f));
-    if (lod_raw > 0.0f && lod_raw < (float)(A.md.L - 1)) {
-      const int j0 = f2i(floorf(lod_raw));
-      const int j1 = min(j0 + 1, A.md.L - 1);
-      float d_lod = 0.0f;
-      for (int li = 0; li < 2; ++li) {
-        const int k = li == 0 ? j0 : j1;
-        const float sign = li == 0 ? -1.0f : 1.0f;
-        const int Hk = mip_h(A.md, k), Wk = mip_w(A.md, k);
-        const float* lv = cube_level(A, n, s.face, k, Hk, Wk);
-        const Bilin b = bilin(p.u, p.v, Wk, Hk, DR_BOUNDARY_CLAMP);
-        for (int c = 0; c < C; ++c) {
-          const float t00 = lv[((int64_t)b.iy0 * Wk + b.ix0) * C + c];
-          const float t10 = lv[((int64_t)b.iy0 * Wk + b.ix1) * C + c];
-          const float t01 = lv[((int64_t)b.iy1 * Wk + b.ix0) * C + c];
-          const float t11 = lv[((int64_t)b.iy1 * Wk + b.ix1) * C + c];
-          const float sample = b.w00 * t00 + b.w10 * t10 + b.w01 * t01 + b.w11 * t11;
-          d_lod += sign * sample * g_[c];
+    if (lod_in) {
+      if (MODE == 1) {  // mip-nearest: the LOD's two levels are not the one sampled
+        const int j0 = f2i(floorf(lod_raw));
+        const int j1 = min(j0 + 1, A.md.L - 1);
+        for (int li = 0; li < 2; ++li) {
+          const int k = li == 0 ? j0 : j1;
+          const float sign = li == 0 ? -1.0f : 1.0f;
+          const int Hk = mip_h(A.md, k), Wk = mip_w(A.md, k);
+          const float* lv = cube_level(A, n, s.face, k, Hk, Wk);
+          const Bilin b = bilin(p.u, p.v, Wk, Hk, DR_BOUNDARY_CLAMP);
+          for (int c = 0; c < C; ++c) {
+            const float t00 = lv[((int64_t)b.iy0 * Wk + b.ix0) * C + c];
+            const float t10 = lv[((int64_t)b.iy0 * Wk + b.ix1) * C + c];
+            const float t01 = lv[((int64_t)b.iy1 * Wk + b.ix0) * C + c];
+            const float t11 = lv[((int64_t)b.iy1 * Wk + b.ix1) * C + c];
+            const float sample = b.w00 * t00 + b.w10 * t10 + b.w01 * t01 + b.w11 * t11;
+            d_lod += sign * sample * g_[c];
+          }
         }
       }
       const float ln2 = 0.6931471805599453f;
