@@ -946,7 +946,7 @@ __global__ void __launch_bounds__(kWinThreads, 5) k_tex_bwd_win(TexBwdArgs A, in
       }
     }
 
-    // -- hot footprint of slot 0: big groups on one texel go to the accumulator
+    // -- hot footprint of slot 0: groups on one texel go to the accumulator
     bool hot = false;
     {
       const bool on0 = q[0].w00 != 0.0f || q[0].w10 != 0.0f || q[0].w01 != 0.0f || q[0].w11 != 0.0f;
@@ -954,11 +954,13 @@ __global__ void __launch_bounds__(kWinThreads, 5) k_tex_bwd_win(TexBwdArgs A, in
       const uint64_t key = ((uint64_t)q[0].k << 48) | (uint64_t)((int64_t)q[0].iy0 * Wk + q[0].ix0);
       const uint32_t key2 = ((uint32_t)(q[0].ix1 - q[0].ix0) << 16) ^ (uint32_t)(q[0].iy1 - q[0].iy0);
       // flat footprints only (all the weight on one texel: every background
-      // pixel); other footprints, however many lanes share them, take the
-      // windows' run sums
+      // pixel), in groups of any size: a few background pixels kept out of
+      // the windows keep a tile that mixes them with the object from boxes
+      // spanning both, which the windows cannot hold (their taps then went to
+      // the hash table: 0.299 -> 0.294 ms at 8 x 1024^2); other footprints,
+      // however many lanes share them, take the windows' run sums
       const bool flat = on0 && q[0].ix0 == q[0].ix1 && q[0].iy0 == q[0].iy1;
       uint64_t pending = __ballot(flat);
-      if (__popcll(pending) < kGroupMin) pending = 0;
 #pragma unroll 1
       for (int probe = 0; probe < 2 && pending; ++probe) {
         const int leader = probe_leader(pending, probe);  // wave-uniform: readlane
@@ -968,7 +970,6 @@ __global__ void __launch_bounds__(kWinThreads, 5) k_tex_bwd_win(TexBwdArgs A, in
         const bool same = flat && !hot && key == lkey && key2 == lkey2;
         const uint64_t members = __ballot(same);
         pending &= ~members;
-        if (__popcll(members) < kGroupMin) continue;
         const int lk = __builtin_amdgcn_readlane(q[0].k, leader);
         float* base = dlevel_ptr(lk);
         const int lW = mip_w(md, lk);
