@@ -365,6 +365,14 @@ constexpr int kBinLdsTiles = 16384;
 // as wide as a workgroup goes (0.030 -> 0.027 ms at 8 x 1024^2; 1.34 ->
 // 0.64 ms per step at 16 x 2048^2, 1.3M triangles).
 constexpr int kBinThreads = 1024;
+// The balanced fill (k_bin_lds<true, true>): from this many tiles per
+// triangle on, for images of at most kBinBalTiles tiles (its LDS holds the
+// chunk's rectangles and offsets beside the tile counters) and at most 256
+// triangles (one triangle over 169 tiles: 18 -> 8 us, six triangles per
+// 512^2 image: 17 -> 8 us; 512 per 256^2 image: 0.65 -> 0.75 ms per
+// 4,096 images, so those keep one triangle per thread).
+constexpr double kBinBalTilesPerItem = 4.0;
+constexpr int kBinBalTiles = 8192;
 
 // With `wstats` (the fill pass, when the caller wants this call's tile
 // statistics): each wave writes its largest final tile count (the returned
@@ -372,13 +380,53 @@ constexpr int kBinThreads = 1024;
 // wstats[2 * (kBinThreads / 64 * workgroup + wave) + {0, 1}], pinned host
 // memory that the host reduces after the kernel has run.  Waves of an empty
 // chunk write 0s.
-template <bool FILL>
+// A thread's walk over its run of the chunk's (item, tile) pairs: item k
+// and its tile (x, y), starting at pair u of item k (the item whose pairs
+// hold u); next() steps along the rectangle's rows and on to the next item
+// with pairs.  Called only while a pair follows in the thread's run, so an
+// item with pairs lies ahead (a step past the chunk's last pair would scan
+// every empty item after it).
+struct BalWalk {
+  const int4* rect;
+  const int* off;
+  int k, x, y;
+  int4 rc;
+  __device__ __forceinline__ BalWalk(const int4* r, const int* o, int k0, int u)
+      : rect(r), off(o), k(k0) {
+    rc = rect[k];
+    const int rw = rc.y - rc.x + 1, l = u - off[k];
+    y = rc.z + l / rw;
+    x = rc.x + (l - (l / rw) * rw);
+  }
+  __device__ __forceinline__ void next() {
+    if (++x <= rc.y) return;
+    x = rc.x;
+    if (++y <= rc.w) return;
+    do {
+      ++k;
+    } while (k < kBinThreads && off[k + 1] == off[k]);  // items without pairs
+    if (k < kBinThreads) {
+      rc = rect[k];
+      x = rc.x;
+      y = rc.z;
+    }
+  }
+};
+
+// BAL (large triangles, many tiles each): the workgroup's (item, tile)
+// pairs are dealt out evenly, each thread a contiguous run of them, instead
+// of one item per thread walking its whole tile rectangle (one triangle
+// over 169 tiles took 18 us in one thread).
+template <bool FILL, bool BAL>
 __global__ void __launch_bounds__(kBinThreads) k_bin_lds(Items it, int chunks,
                                                  const int4* __restrict__ rect, int ntx,
                                                  int tiles, int* __restrict__ cnt,
                                                  int* __restrict__ list, int cap,
                                                  int64_t* __restrict__ wstats) {
   extern __shared__ int s_tile[];
+  __shared__ int4 s_rect[BAL ? kBinThreads : 1];  // the chunk's tile rectangles
+  __shared__ int s_off[BAL ? kBinThreads + 1 : 1];  // pairs before each item
+  __shared__ int s_wsum[BAL ? kBinThreads / 64 : 1];
   const int n = (int)blockIdx.x / chunks;
   const int c = (int)blockIdx.x - n * chunks;
   int64_t i0, i1, r0;  // items [i0, i1) of image n; item i uses record r0 + (i - i0)
@@ -398,12 +446,57 @@ __global__ void __launch_bounds__(kBinThreads) k_bin_lds(Items it, int chunks,
   long long e = 0;  // list entries this thread added
   if (b0 < b1) {    // uniform over the workgroup
     for (int k = tid; k < tiles; k += kBinThreads) s_tile[k] = 0;
+    int npairs = 0, ulo = 0, uhi = 0, k0 = 0;
+    if (BAL) {
+      // each item's pair count, and their exclusive prefix over the chunk
+      int4 rc = make_int4(-1, -1, -1, -1);
+      int a = 0;
+      if (b0 + tid < b1) {
+        rc = rect[r0 + (b0 + tid - i0)];
+        if (rc.x >= 0) a = (rc.y - rc.x + 1) * (rc.w - rc.z + 1);
+      }
+      s_rect[tid] = rc;
+      int inc = a;  // inclusive scan within the wave
+#pragma unroll
+      for (int d = 1; d < kWave; d <<= 1) {
+        const int o = __shfl_up(inc, d, kWave);
+        if ((tid & 63) >= d) inc += o;
+      }
+      if ((tid & 63) == 63) s_wsum[tid >> 6] = inc;
+      __syncthreads();
+      int before = 0;
+      for (int w = 0; w < (tid >> 6); ++w) before += s_wsum[w];
+      npairs = 0;
+      for (int w = 0; w < kBinThreads / 64; ++w) npairs += s_wsum[w];
+      s_off[tid] = before + inc - a;
+      if (tid == kBinThreads - 1) s_off[kBinThreads] = npairs;
+      // this thread's pairs [ulo, uhi) and the item of the first
+      ulo = (int)((int64_t)npairs * tid / kBinThreads);
+      uhi = (int)((int64_t)npairs * (tid + 1) / kBinThreads);
+    }
     __syncthreads();
-    for (int64_t i = b0 + tid; i < b1; i += kBinThreads) {
-      const int4 rc = rect[r0 + (i - i0)];
-      if (rc.x < 0) continue;
-      for (int y = rc.z; y <= rc.w; ++y)
-        for (int x = rc.x; x <= rc.y; ++x) atomicAdd(&s_tile[y * ntx + x], 1);
+    if (BAL) {
+      if (ulo < uhi) {  // last item with s_off <= ulo (items of no pairs are skipped over)
+        int lo = 0, hi = kBinThreads - 1;
+        while (lo < hi) {
+          const int mid = (lo + hi + 1) >> 1;
+          if (s_off[mid] <= ulo) lo = mid;
+          else hi = mid - 1;
+        }
+        k0 = lo;
+      }
+      BalWalk wk(s_rect, s_off, k0, ulo);
+      for (int u = ulo; u < uhi; ++u) {
+        atomicAdd(&s_tile[wk.y * ntx + wk.x], 1);
+        if (u + 1 < uhi) wk.next();
+      }
+    } else {
+      for (int64_t i = b0 + tid; i < b1; i += kBinThreads) {
+        const int4 rc = rect[r0 + (i - i0)];
+        if (rc.x < 0) continue;
+        for (int y = rc.z; y <= rc.w; ++y)
+          for (int x = rc.x; x <= rc.y; ++x) atomicAdd(&s_tile[y * ntx + x], 1);
+      }
     }
     __syncthreads();
     int* cimg = cnt + (int64_t)n * tiles;
@@ -419,17 +512,29 @@ __global__ void __launch_bounds__(kBinThreads) k_bin_lds(Items it, int chunks,
     if (FILL) {
       __syncthreads();
       int* limg = list + (int64_t)n * tiles * cap;
-      for (int64_t i = b0 + tid; i < b1; i += kBinThreads) {
-        const int64_t r = r0 + (i - i0);
-        const int4 rc = rect[r];
-        if (rc.x < 0) continue;
-        const int t = (int)(it.prefix ? r : i - i0);
-        for (int y = rc.z; y <= rc.w; ++y)
-          for (int x = rc.x; x <= rc.y; ++x) {
-            const int j = y * ntx + x;
-            const int p = atomicAdd(&s_tile[j], 1);
-            if (p < cap) limg[(int64_t)j * cap + p] = t;
-          }
+      if (BAL) {
+        BalWalk wk(s_rect, s_off, k0, ulo);
+        for (int u = ulo; u < uhi; ++u) {
+          const int64_t r = r0 + (b0 + wk.k - i0);
+          const int t = (int)(it.prefix ? r : b0 + wk.k - i0);
+          const int j = wk.y * ntx + wk.x;
+          const int p = atomicAdd(&s_tile[j], 1);
+          if (p < cap) limg[(int64_t)j * cap + p] = t;
+          if (u + 1 < uhi) wk.next();
+        }
+      } else {
+        for (int64_t i = b0 + tid; i < b1; i += kBinThreads) {
+          const int64_t r = r0 + (i - i0);
+          const int4 rc = rect[r];
+          if (rc.x < 0) continue;
+          const int t = (int)(it.prefix ? r : i - i0);
+          for (int y = rc.z; y <= rc.w; ++y)
+            for (int x = rc.x; x <= rc.y; ++x) {
+              const int j = y * ntx + x;
+              const int p = atomicAdd(&s_tile[j], 1);
+              if (p < cap) limg[(int64_t)j * cap + p] = t;
+            }
+        }
       }
     }
   }
@@ -1201,10 +1306,12 @@ static int bin_lds_chunks(int N, int tiles, int64_t max_items) {
 // With `wstats` (room for `wcap` waves), the LDS fill pass also writes the
 // per-wave tile statistics; returns the number of waves that did (0: none,
 // k_tile_max must compute them).
+// bal: deal the (item, tile) pairs out evenly (large triangles, from the
+// tile statistics of an earlier call)
 static int64_t launch_binning(bool fill, const Items& it, int64_t n_items, int64_t max_items,
                               int N, const int4* rect, int ntx, int tiles, int* cnt, int* list,
                               int cap, hipStream_t stream, int64_t* wstats = nullptr,
-                              int64_t wcap = 0) {
+                              int64_t wcap = 0, bool bal = false) {
   if (n_items == 0) return 0;
   const int chunks = bin_lds_chunks(N, tiles, max_items);
   if (chunks > 0) {
@@ -1213,14 +1320,18 @@ static int64_t launch_binning(bool fill, const Items& it, int64_t n_items, int64
     if (fill) {
       const int64_t waves = (int64_t)N * chunks * (kBinThreads / 64);
       if (waves > wcap) wstats = nullptr;
-      DR_TIMED("k_bin_fill", stream);
-      hipLaunchKernelGGL(k_bin_lds<true>, grid, dim3(kBinThreads), lds, stream, it, chunks, rect, ntx,
-                         tiles, cnt, list, cap, wstats);
+      DR_TIMED(bal ? "k_bin_fill_bal" : "k_bin_fill", stream);
+      if (bal)
+        hipLaunchKernelGGL((k_bin_lds<true, true>), grid, dim3(kBinThreads), lds, stream, it,
+                           chunks, rect, ntx, tiles, cnt, list, cap, wstats);
+      else
+        hipLaunchKernelGGL((k_bin_lds<true, false>), grid, dim3(kBinThreads), lds, stream, it,
+                           chunks, rect, ntx, tiles, cnt, list, cap, wstats);
       return wstats ? waves : 0;
     }
     DR_TIMED("k_bin_count", stream);
-    hipLaunchKernelGGL(k_bin_lds<false>, grid, dim3(kBinThreads), lds, stream, it, chunks, rect, ntx,
-                       tiles, cnt, list, cap, (int64_t*)nullptr);
+    hipLaunchKernelGGL((k_bin_lds<false, false>), grid, dim3(kBinThreads), lds, stream, it, chunks,
+                       rect, ntx, tiles, cnt, list, cap, (int64_t*)nullptr);
   } else if (fill) {
     DR_TIMED("k_bin_fill", stream);
     hipLaunchKernelGGL(k_bin_fill, dim3(grid_for(n_items, 256)), dim3(256), 0, stream, it,
@@ -1434,9 +1545,14 @@ static int raster_fwd(const float* pos, int64_t pos_batch_stride, const int32_t*
   // (fillc was cleared with the setup) this call's largest count and list
   // entries, for the next call (when the previous ones have been read)
   want_stats = !sc->total_pending && !capturing;
+  // a few large triangles per image (4 tiles each or more on average, in
+  // the last counted call, and at most a quarter of a workgroup's threads):
+  // the fill pass deals their (triangle, tile) pairs out evenly
+  const bool bal = sc->tiles_per_item >= kBinBalTilesPerItem && tiles <= kBinBalTiles &&
+                   max_items <= kBinThreads / 4;
   stat_waves = launch_binning(true, it, n_items, max_items, N, rect, ntx, tiles, fillc, list, C,
                               stream, want_stats ? sc->wave_stats_dev : nullptr,
-                              Scratch::kWaveStatsMax);
+                              Scratch::kWaveStatsMax, bal);
   DR_CHECK_LAUNCH();
   }
   const dim3 grid((unsigned)n_tiles), block(256);

@@ -790,3 +790,52 @@ def test_pixel_parallel_edge_cull_keeps_boundary_pixels():
     r2, _ = DiffRast.rasterize(p, t, (H, W), gradDB=False, peelLayer=rast)
     rr2, _ = O.rasterize(pos, tri, (H, W), gradDB=False, peelLayer=rr, max_per_tile=0)
     np.testing.assert_array_equal(host(r2), rr2)
+
+
+def _fill_launches(fn):
+    """fn() with the library's launch timing on: {binning fill kind: launches}."""
+    import diffrast._lib as L
+    import torch
+    lib = L.load()
+    torch.cuda.synchronize()
+    lib.dr_profile_reset()
+    lib.dr_profile_enable(1)
+    try:
+        fn()
+        torch.cuda.synchronize()
+    finally:
+        lib.dr_profile_enable(0)
+    rep = L.profile_report()
+    return {k: rep.get(k, {}).get("count", 0) for k in ("k_bin_fill", "k_bin_fill_bal")}
+
+
+@pytest.mark.parametrize("kind", ["one", "range", "capped", "small"])
+def test_balanced_binning(kind):
+    """A few large triangles per image (4 tiles each or more on average,
+    counted by the first call on a stream or read back from an earlier one):
+    the binning deals the (triangle, tile) pairs out evenly over the
+    workgroup (k_bin_fill_bal); the lists it builds rasterize bit-exactly as
+    the oracle's, uncapped and with the reference's per-tile limit (whose
+    ranking needs complete lists).  Small triangles keep one triangle per
+    thread (k_bin_fill)."""
+    torch_dev()
+    from diffrast import _lib
+    assert _lib.load().dr_release_scratch() == 0  # no statistics from earlier calls
+    if kind == "one":  # one triangle over most of a 256^2 image
+        sc = scenes.tier1_triangle(H=256, W=256)
+        pos, tri, ranges, H, W = sc["pos"], sc["tri"], None, 256, 256
+    elif kind == "small":  # ~1 tile per triangle
+        sc = scenes.textured_icosphere(N=2, H=128, W=128, level=4, tex_size=8)
+        pos, tri, ranges, H, W = sc["pos"], sc["tri"], None, 128, 128
+    else:  # 24 images of 96 random triangles, most of them over most tiles
+        sc = scenes.range_batch(N=24, T_per=96, H=80, W=112)  # (at most 256 per image)
+        pos, tri, ranges, H, W = sc["pos"], sc["tri"], sc["ranges"], 80, 112
+    for call in range(3):
+        if kind == "capped":
+            n = _fill_launches(lambda: check_capped(pos, tri, H, W, 32, ranges=ranges))
+        else:
+            n = _fill_launches(lambda: check_fwd(pos, tri, H, W, ranges=ranges))
+        if kind == "small":
+            assert n == {"k_bin_fill": 1, "k_bin_fill_bal": 0}, (call, n)
+        else:
+            assert n == {"k_bin_fill": 0, "k_bin_fill_bal": 1}, (call, n)
