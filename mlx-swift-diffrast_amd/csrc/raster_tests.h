@@ -57,23 +57,27 @@ DR_RT_FN void test_tri(const Rec& R, int t, float x, float y, int X, int Y, floa
 // Whether one edge of the triangle keeps every pixel centre of the box
 // [xa, xb] x [ya, yb] outside: the edge function (sa - x)(sb - y) -
 // (sc - x)(sd - y) is affine, (ab - cd) + (d - b) x + (c - a) y, so its
-// largest value (times the sign of the area) over the box is at a corner;
-// in fp64, with a margin above the rounding of the fp32 per-pixel
-// expression (three roundings of products of terms below |s| + 1, pixel
-// centres lying in [-1, 1]), so a rejected triangle fails the per-pixel
-// test at every centre of the box.
+// largest value (times the sign of the area) over the box is at a corner.
+// Evaluated in fp32 at the corners; the margin, 2^-19 of S = (|a| + 1)(|b| +
+// 1) + (|c| + 1)(|d| + 1), is twice the sum of two bounds: the rounding of
+// that corner evaluation (below 2^-21 S: the products, their difference and
+// the three-term sum, each term below S) and that of the per-pixel fp32
+// expression (below 2^-22 S: four differences, two products, one
+// difference, pixel centres lying in [-1, 1]).  So a rejected triangle fails
+// the per-pixel test at every centre of the box.  An overflow or NaN
+// anywhere makes the comparison false (no cull).
 template <typename Rec>
 DR_RT_FN bool edge_excludes(const Rec& R, float xa, float xb, float ya, float yb) {
-  const double sx0 = R.r0.x, sy0 = R.r0.y, sx1 = R.r0.z, sy1 = R.r0.w;
-  const double sx2 = R.r1.x, sy2 = R.r1.y;
-  const double sg = R.r2.y > 0.0f ? 1.0 : -1.0;
-  const double e[3][4] = {{sx1, sy2, sx2, sy1}, {sx2, sy0, sx0, sy2}, {sx0, sy1, sx1, sy0}};
+  const float sx0 = R.r0.x, sy0 = R.r0.y, sx1 = R.r0.z, sy1 = R.r0.w;
+  const float sx2 = R.r1.x, sy2 = R.r1.y;
+  const float sg = R.r2.y > 0.0f ? 1.0f : -1.0f;
+  const float e[3][4] = {{sx1, sy2, sx2, sy1}, {sx2, sy0, sx0, sy2}, {sx0, sy1, sx1, sy0}};
 #pragma unroll
   for (int k = 0; k < 3; ++k) {
-    const double a = e[k][0], b = e[k][1], c = e[k][2], d = e[k][3];
-    const double A = sg * (d - b), B = sg * (c - a), C = sg * (a * b - c * d);
-    const double mx = C + fmax(A * (double)xa, A * (double)xb) + fmax(B * (double)ya, B * (double)yb);
-    const double tol = 0x1p-20 * ((fabs(a) + 1.0) * (fabs(b) + 1.0) + (fabs(c) + 1.0) * (fabs(d) + 1.0));
+    const float a = e[k][0], b = e[k][1], c = e[k][2], d = e[k][3];
+    const float A = sg * (d - b), B = sg * (c - a), C = sg * (a * b - c * d);
+    const float mx = C + fmaxf(A * xa, A * xb) + fmaxf(B * ya, B * yb);
+    const float tol = 0x1p-19f * ((fabsf(a) + 1.0f) * (fabsf(b) + 1.0f) + (fabsf(c) + 1.0f) * (fabsf(d) + 1.0f));
     if (mx < -tol) return true;
   }
   return false;
@@ -83,34 +87,35 @@ DR_RT_FN bool edge_excludes(const Rec& R, float xa, float xb, float ya, float yb
 // box [xa, xb] x [ya, yb], so that it cannot take a pixel whose best depth
 // so far is at most zq (test_tri keeps the smaller depth, and the lower index
 // only on equal depths).  The depth sum_k e_k(x, y) sz_k / area is affine in
-// (x, y), so its smallest value over the box is at a corner; in fp64, less a
-// margin over the rounding of the fp32 per-pixel expression (each edge
-// function within 2^-22 of its two products' magnitudes, scaled by 1/area,
-// then the products with the depths and their sum) of four times its bound.
+// (x, y), so its smallest value over the box is at a corner.  Evaluated in
+// fp32 at the corners, each edge's coefficients scaled by the record's
+// 1/area first (as the per-pixel expression scales the edge functions);
+// the margin, 2^-17 (1 + sum |sz_k|)(1 + |1/area| max_k S_k) with S_k as
+// above, is at least four times the sum of the corner evaluation's rounding
+// and the per-pixel expression's (each below 2^-20 of that product: edge
+// functions within 2^-21 S_k, the scaling, the products with the depths and
+// their sum).  An overflow or NaN anywhere makes the comparison false.
 template <typename Rec>
 DR_RT_FN bool depth_excludes(const Rec& R, float xa, float xb, float ya, float yb,
                              float zq) {
-  const double sx0 = R.r0.x, sy0 = R.r0.y, sx1 = R.r0.z, sy1 = R.r0.w;
-  const double sx2 = R.r1.x, sy2 = R.r1.y;
-  const double sz[3] = {R.r1.z, R.r1.w, R.r2.x};
-  const double inv = 1.0 / (double)R.r2.y;
-  const double e[3][4] = {{sx1, sy2, sx2, sy1}, {sx2, sy0, sx0, sy2}, {sx0, sy1, sx1, sy0}};
-  double z0 = 0.0, zx = 0.0, zy = 0.0, m = 0.0, s = 0.0;
+  const float sx0 = R.r0.x, sy0 = R.r0.y, sx1 = R.r0.z, sy1 = R.r0.w;
+  const float sx2 = R.r1.x, sy2 = R.r1.y;
+  const float sz[3] = {R.r1.z, R.r1.w, R.r2.x};
+  const float inv = R.r2.z;
+  const float e[3][4] = {{sx1, sy2, sx2, sy1}, {sx2, sy0, sx0, sy2}, {sx0, sy1, sx1, sy0}};
+  float z0 = 0.0f, zx = 0.0f, zy = 0.0f, m = 0.0f, s = 0.0f;
 #pragma unroll
   for (int k = 0; k < 3; ++k) {
-    const double a = e[k][0], b = e[k][1], c = e[k][2], d = e[k][3];
-    z0 += sz[k] * (a * b - c * d);
-    zx += sz[k] * (d - b);
-    zy += sz[k] * (c - a);
-    m = fmax(m, (fabs(a) + 1.0) * (fabs(b) + 1.0) + (fabs(c) + 1.0) * (fabs(d) + 1.0));
-    s += fabs(sz[k]);
+    const float a = e[k][0], b = e[k][1], c = e[k][2], d = e[k][3];
+    z0 += sz[k] * ((a * b - c * d) * inv);
+    zx += sz[k] * ((d - b) * inv);
+    zy += sz[k] * ((c - a) * inv);
+    m = fmaxf(m, (fabsf(a) + 1.0f) * (fabsf(b) + 1.0f) + (fabsf(c) + 1.0f) * (fabsf(d) + 1.0f));
+    s += fabsf(sz[k]);
   }
-  z0 *= inv;
-  zx *= inv;
-  zy *= inv;
-  const double zmin = z0 + fmin(zx * (double)xa, zx * (double)xb) + fmin(zy * (double)ya, zy * (double)yb);
-  const double tol = 0x1p-20 * (1.0 + s) * (1.0 + fabs(inv) * m);
-  return zmin - tol > (double)zq;  // false for NaN
+  const float zmin = z0 + fminf(zx * xa, zx * xb) + fminf(zy * ya, zy * yb);
+  const float tol = 0x1p-17f * (1.0f + s) * (1.0f + fabsf(inv) * m);
+  return zmin - tol > zq;  // false for NaN
 }
 
 }  // namespace dr

@@ -867,8 +867,12 @@ __global__ void __launch_bounds__(kRThreads) k_raster(
 // (exact: the pixel -> NDC map is monotonic), 64 triangles at a time, one
 // per lane, then by a conservative edge-function test of the quadrant's
 // pixel-centre box (edge_excludes: a large triangle's bounding box overlaps
-// many quadrants the triangle itself misses); only the survivors are tested
-// against the quadrant's 64 pixels.
+// many quadrants the triangle itself misses) and, once every pixel of the
+// quadrant holds a triangle, a conservative depth test (depth_excludes);
+// only the survivors are tested against the quadrant's 64 pixels.  Both
+// culls are fp32 corner evaluations with margins over the rounding
+// (raster_tests.h; in fp64 they took 11.6 ms of the 4096 x 256^2 batch's
+// 72 ms per step, in fp32 8.5: fp64 issues at half the fp32 rate).
 //
 // CAPPED (max_per_tile > 0): the reference's per-tile limit
 // (Rasterize.swift:164-171, 227-239, 410) with its appends in triangle
