@@ -384,8 +384,6 @@ constexpr int kTexTable = 512;  // LDS aggregation entries per tile (texels)
 
 template <int CT, int CAP = kTexTable>
 using TexTable = LdsTable<(CT > 0 ? CT : 1), CAP>;
-template <int CT, int CAP>
-using TexTableU = LdsTableU<(CT > 0 ? CT : 1), CAP>;
 
 // The cube backward's table: a cube map's footprints spread over more
 // texels per tile (a per-pixel LOD bias splits them over two or three
@@ -393,6 +391,8 @@ using TexTableU = LdsTableU<(CT > 0 ? CT : 1), CAP>;
 // device atomics (4096 x 256^2, 6 x 512^2 x 3 with a random bias map:
 // 91 -> 47 ms with 1,024 entries, 43 ms with 2,048).
 constexpr int kCubeTable = 2048;
+template <int CT>
+using CubeTable = LdsTableU<(CT > 0 ? CT : 1), kCubeTable>;
 
 template <int CT, bool USE_ACC = true, typename Tab = TexTable<CT>>
 __device__ __forceinline__ void scatter_footprint(bool valid, float* __restrict__ base, int Wk,
@@ -1626,14 +1626,15 @@ __global__ void __launch_bounds__(256) k_cube_fwd(CubeArgs A) {
 template <int MODE, int CT>
 __device__ __forceinline__ void cube_bwd_px(const CubeArgs& A, int64_t pix, bool valid, int n,
                                             FootAcc<(CT > 0 ? CT : 1)>& acc0,
-                                            TexTableU<CT, kCubeTable>& tab) {
+                                            CubeTable<CT>& tab) {
   const int C = dimC<CT>(A.C);
   const CubePx p = cube_px<MODE>(A, pix);
   const float* gp = A.d_out + pix * C;
   float g[CT > 0 ? CT : 1];
-  if (CT > 0) {
+  if constexpr (CT > 0) {
+    load_texel<CT>(gp, C, g);  // pix is clamped into the image
 #pragma unroll
-    for (int c = 0; c < (CT > 0 ? CT : 1); ++c) g[c] = valid ? gp[c] : 0.0f;
+    for (int c = 0; c < CT; ++c) g[c] = valid ? g[c] : 0.0f;
   }
   const float* gsrc = CT > 0 ? g : gp;  // run-time C reads d_out directly
   const CubeSel& s = p.s;
@@ -1666,20 +1667,27 @@ __device__ __forceinline__ void cube_bwd_px(const CubeArgs& A, int64_t pix, bool
     const Bilin b = bilin(p.u, p.v, Wk, Hk, DR_BOUNDARY_CLAMP);
     if (__ballot(on)) {
       if (li == 0)
-        scatter_footprint<CT, true, TexTableU<CT, kCubeTable>>(on, dl, Wk, C, b, gsrc, scale,
-                                                               acc0, tab);
+        scatter_footprint<CT, true, CubeTable<CT>>(on, dl, Wk, C, b, gsrc, scale, acc0, tab);
       else
-        scatter_footprint<CT, false, TexTableU<CT, kCubeTable>>(on, dl, Wk, C, b, gsrc, scale,
-                                                                acc0, tab);
+        scatter_footprint<CT, false, CubeTable<CT>>(on, dl, Wk, C, b, gsrc, scale, acc0, tab);
     }
     if (!rd) continue;
     const float sign = li == 0 ? -1.0f : 1.0f;
     float dfx = 0.0f, dfy = 0.0f;
+    // a texel's channels in one load (CT > 0) rather than one per channel
+    // (4096 x 256^2, 6 x 512^2 x 3: 37.7 -> 36.1 ms)
+    float q00[kMaxC], q10[kMaxC], q01[kMaxC], q11[kMaxC];
+    if constexpr (CT > 0) {
+      load_texel<CT>(lv + ((int64_t)b.iy0 * Wk + b.ix0) * C, C, q00);
+      load_texel<CT>(lv + ((int64_t)b.iy0 * Wk + b.ix1) * C, C, q10);
+      load_texel<CT>(lv + ((int64_t)b.iy1 * Wk + b.ix0) * C, C, q01);
+      load_texel<CT>(lv + ((int64_t)b.iy1 * Wk + b.ix1) * C, C, q11);
+    }
     for (int c = 0; c < C; ++c) {
-      const float t00 = lv[((int64_t)b.iy0 * Wk + b.ix0) * C + c];
-      const float t10 = lv[((int64_t)b.iy0 * Wk + b.ix1) * C + c];
-      const float t01 = lv[((int64_t)b.iy1 * Wk + b.ix0) * C + c];
-      const float t11 = lv[((int64_t)b.iy1 * Wk + b.ix1) * C + c];
+      const float t00 = CT > 0 ? q00[c] : lv[((int64_t)b.iy0 * Wk + b.ix0) * C + c];
+      const float t10 = CT > 0 ? q10[c] : lv[((int64_t)b.iy0 * Wk + b.ix1) * C + c];
+      const float t01 = CT > 0 ? q01[c] : lv[((int64_t)b.iy1 * Wk + b.ix0) * C + c];
+      const float t11 = CT > 0 ? q11[c] : lv[((int64_t)b.iy1 * Wk + b.ix1) * C + c];
       const float gs = gsrc[c] * scale;
       dfx += gs * ((1.0f - b.fy) * (t10 - t00) + b.fy * (t11 - t01));
       dfy += gs * ((1.0f - b.fx) * (t01 - t00) + b.fx * (t11 - t10));
@@ -1796,7 +1804,7 @@ __device__ __forceinline__ void cube_bwd_px(const CubeArgs& A, int64_t pix, bool
 template <int MODE, int CT>
 __global__ void __launch_bounds__(256) k_cube_bwd(CubeArgs A, int Hi, int Wi, int ntx,
                                                   int total_tiles) {
-  __shared__ TexTableU<CT, kCubeTable> tab;
+  __shared__ CubeTable<CT> tab;
   FootAcc<(CT > 0 ? CT : 1)> acc0;
   acc_init(acc0);
   lds_table_clear(tab);
