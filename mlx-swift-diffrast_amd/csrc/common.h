@@ -286,6 +286,10 @@ __device__ __forceinline__ int wave_max(int v) {
   return wave_reduce_i(v, [](int a, int b) { return a > b ? a : b; });
 }
 
+__device__ __forceinline__ int wave_or(int v) {
+  return wave_reduce_i(v, [](int a, int b) { return a | b; });
+}
+
 // Runs of equal keys along each 16-lane row (the row of pixels a wave row
 // holds): every lane's v[] becomes the sum of its run's values up to
 // itself (a segmented Hillis-Steele scan over DPP row shifts), and the
@@ -418,13 +422,13 @@ __device__ __forceinline__ int wave_min(int v) {
 }
 
 // Per-half minimum of two signed 16-bit values packed in an int.
-__device__ __forceinline__ int wave_min_pk16(int v) {
+__device__ __forceinline__ int pk16_min(int a, int b) {
   typedef short short2_t __attribute__((ext_vector_type(2)));
-  return wave_reduce_i(v, [](int a, int b) {
-    return __builtin_bit_cast(int, __builtin_elementwise_min(__builtin_bit_cast(short2_t, a),
-                                                             __builtin_bit_cast(short2_t, b)));
-  });
+  return __builtin_bit_cast(int, __builtin_elementwise_min(__builtin_bit_cast(short2_t, a),
+                                                           __builtin_bit_cast(short2_t, b)));
 }
+
+__device__ __forceinline__ int wave_min_pk16(int v) { return wave_reduce_i(v, pk16_min); }
 
 __device__ __forceinline__ int pack16(int lo, int hi) {
   return (int)(((uint32_t)(uint16_t)(int16_t)lo) | ((uint32_t)(uint16_t)(int16_t)hi << 16));

@@ -783,8 +783,8 @@ __global__ void __launch_bounds__(kWinThreads, 5) k_tex_bwd_win(TexBwdArgs A, in
   // neighbouring texels then add 8 bytes apart, spread over the banks,
   // rather than 8 * CT bytes apart on a few of them
   __shared__ double win[kWinTexels * CT];
-  __shared__ int s_wk[kWinWaves];          // per wave: lowest level in use
-  __shared__ int s_wbox[kWinWaves][2][4];  // per wave: boxes on that level and the next
+  __shared__ __align__(16) int s_lmask[kWinWaves];  // per wave: the levels in use (bit mask)
+  __shared__ int2 s_lbox[kWinWaves][kMaxLevels];     // per wave and level: packed box
   __shared__ int s_tab_used[2];    // per tile parity: the table took entries
   __shared__ LdsTable<CT, kWinFallback> tab;
   FootAcc<CT> acc;
@@ -1003,109 +1003,104 @@ __global__ void __launch_bounds__(kWinThreads, 5) k_tex_bwd_win(TexBwdArgs A, in
       }
     }
 
-    // -- per wave: lowest level in use and the boxes on it and the next; the
-    //    block's windows are the two lowest levels over all waves ------------
+    // -- per wave: the levels in use and the box on each; the block's windows
+    //    cover every level any wave uses ------------------------------------
     const bool use0 = !hot && (q[0].w00 != 0.0f || q[0].w10 != 0.0f || q[0].w01 != 0.0f || q[0].w11 != 0.0f);
     const bool use1 = q[1].w00 != 0.0f || q[1].w10 != 0.0f || q[1].w01 != 0.0f || q[1].w11 != 0.0f;
     const int par = it & 1;
     {
-      int kmin = 0x7fffffff;
-      if (use0) kmin = q[0].k;
-      if (use1) kmin = min(kmin, q[1].k);
-      const int kw = wave_min(kmin);
-      // (a wave with no slot in use, kw = INT_MAX, leaves its boxes unread)
-#pragma unroll
-      for (int j = 0; j < 2 && kw != 0x7fffffff; ++j) {
+      const int lm = wave_or((use0 ? 1 << q[0].k : 0) | (use1 ? 1 << q[1].k : 0));
+#pragma unroll 1
+      for (int rem = lm; rem != 0; rem &= rem - 1) {  // uniform: one level at a time
+        const int L = __builtin_ctz(rem);
         // texel coordinates fit in 16 bits (window path needs sizes <= 32767):
         // (x0, -x1) and (y0, -y1) are reduced as packed 16-bit minima
         int x0 = 32767, x1 = -32767, y0 = 32767, y1 = -32767;
 #pragma unroll
         for (int li = 0; li < 2; ++li) {
           const bool u = li == 0 ? use0 : use1;
-          if (!u || q[li].k - kw != j) continue;
+          if (!u || q[li].k != L) continue;
           int a0, a1, b0, b1;
           slot_box(q[li], a0, a1, b0, b1);
           x0 = min(x0, a0); x1 = max(x1, a1); y0 = min(y0, b0); y1 = max(y1, b1);
         }
-        int px = pack16(32767, 32767), py = px;  // an empty box
-        if (__ballot(x1 >= 0)) {  // some lane has a slot on this level
-          px = wave_min_pk16(pack16(x0, -x1));
-          py = wave_min_pk16(pack16(y0, -y1));
-        }
-        if (lane == 0) {
-          const int X1 = -unpack16_hi(px), Y1 = -unpack16_hi(py);
-          s_wbox[wave][j][0] = unpack16_lo(px); s_wbox[wave][j][1] = X1 < 0 ? -1 : X1;
-          s_wbox[wave][j][2] = unpack16_lo(py); s_wbox[wave][j][3] = Y1 < 0 ? -1 : Y1;
-        }
+        const int px = wave_min_pk16(pack16(x0, -x1));
+        const int py = wave_min_pk16(pack16(y0, -y1));
+        if (lane == 0) s_lbox[wave][L] = make_int2(px, py);
       }
-      if (lane == 0) s_wk[wave] = kw;
+      if (lane == 0) s_lmask[wave] = lm;
     }
     __syncthreads();
     if (tid == 0) s_tab_used[par ^ 1] = 0;  // read by every thread before the last barrier
-    // the window selection is uniform: its LDS inputs go to scalar registers
-    auto su = [](int x) { return __builtin_amdgcn_readfirstlane(x); };
-    int wk[kWinWaves];
-#pragma unroll
-    for (int v = 0; v < kWinWaves; ++v) wk[v] = su(s_wk[v]);
-    int ka = wk[0];
-#pragma unroll
-    for (int v = 1; v < kWinWaves; ++v) ka = min(ka, wk[v]);
-    int wsel[2];
-#pragma unroll
-    for (int li = 0; li < 2; ++li) {
-      const bool u = li == 0 ? use0 : use1;
-      wsel[li] = !u ? -2 : (q[li].k == ka ? 0 : (q[li].k - ka == 1 ? 1 : -1));
-    }
-    int bx0[2], bw[2], by0[2], bh[2], wbase[2];
-    bool usable[2];
-    int64_t area[2];
-#pragma unroll
-    for (int w = 0; w < 2; ++w) {
-      int x0 = 0x7fffffff, x1 = -1, y0 = 0x7fffffff, y1 = -1;
+    // Level L's window, in lane L of each 16-lane row: the union of the
+    // waves' boxes on L and its place in the pool (levels in ascending
+    // order; a box larger than the pool is left out).  A lane then takes
+    // its slots' windows from the lanes of their levels.
+    const int4 wm = *reinterpret_cast<const int4*>(s_lmask);
+    const int lmask = __builtin_amdgcn_readfirstlane(wm.x | wm.y | wm.z | wm.w);
+    int wxy, wwh, wbase;  // (x0 | y0 << 16), (width | height << 16), pool offset or -1
+    {
+      const int L = lane & 15;
+      int px = pack16(32767, 32767), py = px;
 #pragma unroll
       for (int v = 0; v < kWinWaves; ++v) {
-        const int kv = wk[v];
-        const int j = w - (kv - ka);  // wave v's box j lies on level ka + w
-        if (kv == 0x7fffffff || j < 0 || j > 1) continue;
-        x0 = min(x0, su(s_wbox[v][j][0])); x1 = max(x1, su(s_wbox[v][j][1]));
-        y0 = min(y0, su(s_wbox[v][j][2])); y1 = max(y1, su(s_wbox[v][j][3]));
+        const int mv = v == 0 ? wm.x : v == 1 ? wm.y : v == 2 ? wm.z : wm.w;
+        if ((mv >> L) & 1) {
+          const int2 b = s_lbox[v][L];
+          px = pk16_min(px, b.x);
+          py = pk16_min(py, b.y);
+        }
       }
-      bx0[w] = x0;
-      by0[w] = y0;
-      bw[w] = x1 - x0 + 1;
-      bh[w] = y1 - y0 + 1;
-      area[w] = x1 >= 0 ? (int64_t)bw[w] * bh[w] : 0;
-      usable[w] = x1 >= 0;
+      const int x0 = unpack16_lo(px), x1 = -unpack16_hi(px);
+      const int y0 = unpack16_lo(py), y1 = -unpack16_hi(py);
+      const bool present = L < kMaxLevels && ((lmask >> L) & 1) && x1 >= x0 && y1 >= y0;
+      const int area = present ? (x1 - x0 + 1) * (y1 - y0 + 1) : 0;
+      const int fit = area <= kWinTexels ? area : 0;
+      // inclusive prefix sum of the fitting areas along the row
+      int incl = fit;
+      int t = dpp_shift<0x111>(incl);
+      incl += t;
+      t = dpp_shift<0x112>(incl);
+      incl += t;
+      t = dpp_shift<0x114>(incl);
+      incl += t;
+      t = dpp_shift<0x118>(incl);
+      incl += t;
+      const bool usable = present && area == fit && incl <= kWinTexels;
+      wxy = x0 | (y0 << 16);
+      wwh = (x1 - x0 + 1) | ((y1 - y0 + 1) << 16);
+      wbase = usable ? incl - fit : -1;
     }
-    usable[0] = usable[0] && area[0] <= kWinTexels;
-    wbase[0] = 0;
-    usable[1] = usable[1] && (usable[0] ? area[0] : 0) + area[1] <= kWinTexels;
-    wbase[1] = usable[0] ? (int)area[0] : 0;  // in texels
 
     // -- accumulate: runs of one footprint along a pixel row are summed
     //    first (lanes of one LDS atomic on one address are serialised), the
     //    run's last lane adds the totals ----------------------------------------
 #pragma unroll
     for (int li = 0; li < 2; ++li) {
-      const int w = wsel[li];
-      if (__ballot(w != -2) == 0) continue;  // no lane uses this slot (uniform)
+      const bool u = li == 0 ? use0 : use1;
+      if (__ballot(u) == 0) continue;  // no lane uses this slot (uniform)
+      const int k = q[li].k;
+      // the window of level k (every lane executes the permutes)
+      const int sxy = __builtin_amdgcn_ds_bpermute(k << 2, wxy);
+      const int swh = __builtin_amdgcn_ds_bpermute(k << 2, wwh);
+      const int sbase = __builtin_amdgcn_ds_bpermute(k << 2, wbase);
       const float sc = mip ? q[li].scale : 1.0f;
       // level and the four texel coordinates (each < 32767 on the window
       // path) fix the taps; an unused slot gets a key no footprint has
       const uint64_t key =
-          w == -2 ? (0x7FFFull << 45) | (uint64_t)lane
-                  : ((uint64_t)q[li].k << 60) | ((uint64_t)q[li].ix0 << 45) |
-                        ((uint64_t)q[li].ix1 << 30) | ((uint64_t)q[li].iy0 << 15) | (uint64_t)q[li].iy1;
+          !u ? (0x7FFFull << 45) | (uint64_t)lane
+             : ((uint64_t)k << 60) | ((uint64_t)q[li].ix0 << 45) | ((uint64_t)q[li].ix1 << 30) |
+                   ((uint64_t)q[li].iy0 << 15) | (uint64_t)q[li].iy1;
       const RowRun run = row_run(key);
       const int maxlen = wave_max(run.li - run.s + 1);  // longest run in the wave
-      const bool adds = w != -2 && run.tail;
-      const bool in_win = w >= 0 && usable[w];
+      const bool adds = u && run.tail;
+      const bool in_win = sbase >= 0;
       // the 16 values (tap-major) of the footprint, then one segmented scan
       // over all of them
       const float wt[4] = {q[li].w00, q[li].w10, q[li].w01, q[li].w11};
       float gs[CT];
 #pragma unroll
-      for (int c = 0; c < CT; ++c) gs[c] = w == -2 ? 0.0f : g[c] * sc;
+      for (int c = 0; c < CT; ++c) gs[c] = !u ? 0.0f : g[c] * sc;
       float v[4 * CT];
 #pragma unroll
       for (int t = 0; t < 4; ++t)
@@ -1118,24 +1113,22 @@ __global__ void __launch_bounds__(kWinThreads, 5) k_tex_bwd_win(TexBwdArgs A, in
         // in all of them (a texel column or row with zero weight, outside
         // the image for the zero boundary) may lie outside it, and its
         // coordinates are clamped into the box, where it adds 0.
-        const int wx = w == 0 ? bx0[0] : bx0[1], wy = w == 0 ? by0[0] : by0[1];
-        const int ww = w == 0 ? bw[0] : bw[1], wh = w == 0 ? bh[0] : bh[1];
-        const int wo = w == 0 ? wbase[0] : wbase[1];
+        const int wx = sxy & 0xffff, wy = sxy >> 16, ww = swh & 0xffff, wh = swh >> 16;
         const int cx0 = min(max(q[li].ix0 - wx, 0), ww - 1);
         const int cx1 = min(max(q[li].ix1 - wx, 0), ww - 1);
-        const int r0 = wo + min(max(q[li].iy0 - wy, 0), wh - 1) * ww;
-        const int r1 = wo + min(max(q[li].iy1 - wy, 0), wh - 1) * ww;
-        const int o[4] = {r0 + cx0, r0 + cx1, r1 + cx0, r1 + cx1};  // < wo + area[w]
+        const int r0 = sbase + min(max(q[li].iy0 - wy, 0), wh - 1) * ww;
+        const int r1 = sbase + min(max(q[li].iy1 - wy, 0), wh - 1) * ww;
+        const int o[4] = {r0 + cx0, r0 + cx1, r1 + cx0, r1 + cx1};  // < sbase + area
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
           for (int c = 0; c < CT; ++c)
             atomicAdd(win + c * kWinTexels + o[t], (double)v[t * CT + c]);
       }
-      if (adds && !in_win) {  // other levels, or boxes too large for a window
+      if (adds && !in_win) {  // boxes that the pool could not hold
         s_tab_used[par] = 1;
-        float* base = dlevel_ptr(q[li].k);
-        const int Wk = mip_w(md, q[li].k);
+        float* base = dlevel_ptr(k);
+        const int Wk = mip_w(md, k);
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
           const int tx_ = (t & 1) ? q[li].ix1 : q[li].ix0;
@@ -1147,16 +1140,18 @@ __global__ void __launch_bounds__(kWinThreads, 5) k_tex_bwd_win(TexBwdArgs A, in
     __syncthreads();
 
     // -- write the windows out, row by row -----------------------------------
-#pragma unroll
-    for (int w = 0; w < 2; ++w) {
-      if (!usable[w]) continue;
-      const int k = ka + w;
-      if (k >= md.L) continue;
+#pragma unroll 1
+    for (int rem = lmask; rem != 0; rem &= rem - 1) {  // uniform
+      const int k = __builtin_ctz(rem);
+      const int base_k = __builtin_amdgcn_readlane(wbase, k);
+      if (base_k < 0) continue;
+      const int xy = __builtin_amdgcn_readlane(wxy, k), wh = __builtin_amdgcn_readlane(wwh, k);
+      const int bx0 = xy & 0xffff, by0 = xy >> 16, bw = wh & 0xffff, bh = wh >> 16;
       float* base = dlevel_ptr(k);
       const int Wk = mip_w(md, k);
-      const int row = bw[w] * CT;
-      const int total = row * bh[w];
-      double* wb = win + wbase[w];
+      const int row = bw * CT;
+      const int total = row * bh;
+      double* wb = win + base_k;
       // consecutive lanes take consecutive channels of a texel, so the
       // device atomics of a row share cache lines; (r, cpos) of element i
       // advance by a uniform step instead of a division per element
@@ -1164,10 +1159,10 @@ __global__ void __launch_bounds__(kWinThreads, 5) k_tex_bwd_win(TexBwdArgs A, in
       int r = tid / row, cpos = tid - r * row;
       for (int i = tid; i < total; i += kWinThreads) {
         const int tx = cpos / CT, c = cpos - tx * CT;
-        double* e = wb + c * kWinTexels + r * bw[w] + tx;
+        double* e = wb + c * kWinTexels + r * bw + tx;
         const double v = *e;
         if (v != 0.0) {
-          unsafeAtomicAdd(base + ((by0[w] + r) * Wk + bx0[w]) * CT + cpos, (float)v);
+          unsafeAtomicAdd(base + ((by0 + r) * Wk + bx0) * CT + cpos, (float)v);
           *e = 0.0;
         }
         r += dr;
