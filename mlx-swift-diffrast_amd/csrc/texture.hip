@@ -1038,7 +1038,10 @@ __global__ void __launch_bounds__(kWinThreads, 5) k_tex_bwd_win(TexBwdArgs A, in
     // its slots' windows from the lanes of their levels.
     const int4 wm = *reinterpret_cast<const int4*>(s_lmask);
     const int lmask = __builtin_amdgcn_readfirstlane(wm.x | wm.y | wm.z | wm.w);
-    int wxy, wwh, wbase;  // (x0 | y0 << 16), (width | height << 16), pool offset or -1
+    // (x0 | y0 << 16) and (width | height << 10 | (pool offset + 1) << 20),
+    // offset + 1 = 0 for no window (a box in the pool has at most 768 texels,
+    // so each of its sides and its offset fit in 10 bits)
+    int wxy, wsz;
     {
       const int L = lane & 15;
       int px = pack16(32767, 32767), py = px;
@@ -1067,9 +1070,9 @@ __global__ void __launch_bounds__(kWinThreads, 5) k_tex_bwd_win(TexBwdArgs A, in
       t = dpp_shift<0x118>(incl);
       incl += t;
       const bool usable = present && area == fit && incl <= kWinTexels;
+      static_assert(kWinTexels < 1024, "window sides and offsets are 10-bit fields");
       wxy = x0 | (y0 << 16);
-      wwh = (x1 - x0 + 1) | ((y1 - y0 + 1) << 16);
-      wbase = usable ? incl - fit : -1;
+      wsz = usable ? (x1 - x0 + 1) | ((y1 - y0 + 1) << 10) | ((incl - fit + 1) << 20) : 0;
     }
 
     // -- accumulate: runs of one footprint along a pixel row are summed
@@ -1082,8 +1085,7 @@ __global__ void __launch_bounds__(kWinThreads, 5) k_tex_bwd_win(TexBwdArgs A, in
       const int k = q[li].k;
       // the window of level k (every lane executes the permutes)
       const int sxy = __builtin_amdgcn_ds_bpermute(k << 2, wxy);
-      const int swh = __builtin_amdgcn_ds_bpermute(k << 2, wwh);
-      const int sbase = __builtin_amdgcn_ds_bpermute(k << 2, wbase);
+      const int ssz = __builtin_amdgcn_ds_bpermute(k << 2, wsz);
       const float sc = mip ? q[li].scale : 1.0f;
       // level and the four texel coordinates (each < 32767 on the window
       // path) fix the taps; an unused slot gets a key no footprint has
@@ -1094,7 +1096,7 @@ __global__ void __launch_bounds__(kWinThreads, 5) k_tex_bwd_win(TexBwdArgs A, in
       const RowRun run = row_run(key);
       const int maxlen = wave_max(run.li - run.s + 1);  // longest run in the wave
       const bool adds = u && run.tail;
-      const bool in_win = sbase >= 0;
+      const bool in_win = ssz != 0;
       // the 16 values (tap-major) of the footprint, then one segmented scan
       // over all of them
       const float wt[4] = {q[li].w00, q[li].w10, q[li].w01, q[li].w11};
@@ -1113,7 +1115,8 @@ __global__ void __launch_bounds__(kWinThreads, 5) k_tex_bwd_win(TexBwdArgs A, in
         // in all of them (a texel column or row with zero weight, outside
         // the image for the zero boundary) may lie outside it, and its
         // coordinates are clamped into the box, where it adds 0.
-        const int wx = sxy & 0xffff, wy = sxy >> 16, ww = swh & 0xffff, wh = swh >> 16;
+        const int wx = sxy & 0xffff, wy = sxy >> 16;
+        const int ww = ssz & 0x3ff, wh = (ssz >> 10) & 0x3ff, sbase = (ssz >> 20) - 1;
         const int cx0 = min(max(q[li].ix0 - wx, 0), ww - 1);
         const int cx1 = min(max(q[li].ix1 - wx, 0), ww - 1);
         const int r0 = sbase + min(max(q[li].iy0 - wy, 0), wh - 1) * ww;
@@ -1143,10 +1146,11 @@ __global__ void __launch_bounds__(kWinThreads, 5) k_tex_bwd_win(TexBwdArgs A, in
 #pragma unroll 1
     for (int rem = lmask; rem != 0; rem &= rem - 1) {  // uniform
       const int k = __builtin_ctz(rem);
-      const int base_k = __builtin_amdgcn_readlane(wbase, k);
-      if (base_k < 0) continue;
-      const int xy = __builtin_amdgcn_readlane(wxy, k), wh = __builtin_amdgcn_readlane(wwh, k);
-      const int bx0 = xy & 0xffff, by0 = xy >> 16, bw = wh & 0xffff, bh = wh >> 16;
+      const int sz = __builtin_amdgcn_readlane(wsz, k);
+      if (sz == 0) continue;
+      const int xy = __builtin_amdgcn_readlane(wxy, k);
+      const int bx0 = xy & 0xffff, by0 = xy >> 16, bw = sz & 0x3ff, bh = (sz >> 10) & 0x3ff;
+      const int base_k = (sz >> 20) - 1;
       float* base = dlevel_ptr(k);
       const int Wk = mip_w(md, k);
       const int row = bw * CT;
