@@ -39,25 +39,41 @@ constexpr int interp_pix() {
   return AT >= 6 ? 4 : 2;
 }
 
+// A workgroup covers 16 x (16 * PX) pixels of one image, each wave a 16x4
+// strip per pixel slot (one pixel row per 16 lanes): the strip's triangles
+// share more vertex rows than a 64-pixel row's, so its attribute gathers
+// touch fewer cache lines.
 template <int AT, int KT>
 __global__ void __launch_bounds__(256) k_interp_fwd(
     const float* __restrict__ attr, int64_t attr_stride, const float* __restrict__ rast,
     const float* __restrict__ rast_db, const int32_t* __restrict__ tri,
-    const int32_t* __restrict__ diff_idx, int K_, int64_t P, int HW, int V, int T, int A_,
-    float* __restrict__ out, float* __restrict__ out_da) {
+    const int32_t* __restrict__ diff_idx, int K_, int H, int W, int ntx, int nty, int V, int T,
+    int A_, float* __restrict__ out, float* __restrict__ out_da) {
   constexpr int PX = interp_pix<AT>();
   constexpr int NA = AT > 0 ? AT : 8;       // register slots for attributes
   constexpr int NK = KT > 0 ? 2 * KT : 8;   // and for derivative outputs
   const int A = dimA<AT>(A_);
   const int K = KT > 0 ? KT : K_;
-  const int64_t base = (int64_t)blockIdx.x * (256 * PX) + threadIdx.x;
+  const int tiles = ntx * nty;
+  const int b = (int)blockIdx.x;
+  const int img = b / tiles;
+  const int tile = b - img * tiles;
+  const int ty = tile / ntx, tx = tile - ty * ntx;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int pw = tx * 16 + (lane & 15);
+  const int ph0 = ty * 16 * PX + wave * 4 + (lane >> 4);
+  const float* at = attr + (int64_t)img * attr_stride;
   float4 r[PX];
   int t[PX];
+  int64_t pixq[PX];
+  bool in[PX];
 #pragma unroll
   for (int q = 0; q < PX; ++q) {
-    const int64_t pix = base + q * 256;
-    r[q] = pix < P ? *reinterpret_cast<const float4*>(rast + pix * 4) : make_float4(0.f, 0.f, 0.f, 0.f);
-    t[q] = pix < P ? f2i(r[q].w) - 1 : -1;
+    const int ph = ph0 + q * 16;
+    in[q] = pw < W && ph < H;
+    pixq[q] = ((int64_t)img * H + min(ph, H - 1)) * W + min(pw, W - 1);
+    r[q] = in[q] ? *reinterpret_cast<const float4*>(rast + pixq[q] * 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+    t[q] = in[q] ? f2i(r[q].w) - 1 : -1;
     if (t[q] >= T) t[q] = -1;  // not a triangle of this mesh: empty
   }
   int iv[PX][3];
@@ -73,8 +89,8 @@ __global__ void __launch_bounds__(256) k_interp_fwd(
   }
 #pragma unroll
   for (int q = 0; q < PX; ++q) {
-    const int64_t pix = base + q * 256;
-    if (pix >= P) continue;
+    const int64_t pix = pixq[q];
+    if (!in[q]) continue;
     float* o = out + pix * A;
     float* od = K > 0 ? out_da + pix * 2 * K : nullptr;
     if (AT == 0 || KT == 0 && K > 0) {  // any shape: element by element
@@ -83,7 +99,6 @@ __global__ void __launch_bounds__(256) k_interp_fwd(
         for (int k = 0; k < 2 * K; ++k) od[k] = 0.0f;
         continue;
       }
-      const float* at = attr + (int64_t)(pix / HW) * attr_stride;
       const float* a0p = at + (int64_t)iv[q][0] * A;
       const float* a1p = at + (int64_t)iv[q][1] * A;
       const float* a2p = at + (int64_t)iv[q][2] * A;
@@ -113,9 +128,6 @@ __global__ void __launch_bounds__(256) k_interp_fwd(
 #pragma unroll
     for (int k = 0; k < NK; ++k) odv[k] = 0.0f;
     if (t[q] >= 0) {
-      // image index: 32-bit division while the pixel index fits
-      const int64_t img = pix <= 0x7fffffff ? (int64_t)((int)pix / HW) : pix / HW;
-      const float* at = attr + img * attr_stride;
       float a0[NA], a1[NA], a2[NA];
 #pragma unroll
       for (int a = 0; a < NA; ++a) {
@@ -405,19 +417,21 @@ extern "C" int dr_interpolate_fwd(const float* attr, int64_t attr_batch_stride,
   int st = check_interp(attr, rast, tri, rast_db, K, N, H, W, V, T, A, attr_batch_stride, diff_idx);
   if (st) return st;
   DR_CHECK_ARG(out && (K == 0 || out_da), "interpolate: null output");
-  const int64_t P = (int64_t)N * H * W;
   DR_TIMED("k_interp_fwd", stream);
   // the compile-time shapes store with 8/16-byte vector writes
   const bool aligned = (((uintptr_t)out | (uintptr_t)(out_da ? out_da : out)) & 15) == 0;
   // the dispatched kernel's pixels per thread (DR_INTERP_DISPATCH's choice)
   const int px = aligned && A == 6 && K == 0 ? interp_pix<6>() : interp_pix<0>();
-  const dim3 grid(grid_for(P, 256 * px));
+  const int ntx = (W + 15) / 16, nty = (H + 16 * px - 1) / (16 * px);
+  const int64_t nblk = (int64_t)N * ntx * nty;
+  DR_CHECK_ARG(nblk < ((int64_t)1 << 31), "interpolate: too many pixels");
+  const dim3 grid((unsigned)nblk);
   if (!aligned)
     hipLaunchKernelGGL((k_interp_fwd<0, 0>), grid, dim3(256), 0, stream, attr, attr_batch_stride,
-                       rast, rast_db, tri, diff_idx, K, P, H * W, V, T, A, out, out_da);
+                       rast, rast_db, tri, diff_idx, K, H, W, ntx, nty, V, T, A, out, out_da);
   else
     DR_INTERP_DISPATCH(k_interp_fwd, grid, attr, attr_batch_stride, rast, rast_db, tri, diff_idx,
-                       K, P, H * W, V, T, A, out, out_da);
+                       K, H, W, ntx, nty, V, T, A, out, out_da);
   DR_CHECK_LAUNCH();
   return DR_OK;
 }
