@@ -484,7 +484,7 @@ __global__ void __launch_bounds__(256) k_aa_fwd(const float* __restrict__ rast,
 // Q0, Q1: the edge vertices' (inv_w, x * inv_w, y * inv_w) (persp_of).
 __device__ __forceinline__ void aa_dpos_add(const SilDir& s, int d, int ph, int pw, float d_alpha,
                                             float4 Q0, float4 Q1, double* __restrict__ dp,
-                                            float halfW, float halfH, LdsTable<4, 128>& tab) {
+                                            float halfW, float halfH, LdsTableU<4, 128>& tab) {
   float dade0x, dade0y, dade1x, dade1y;
   const float inv_denom_sq = 1.0f / (s.denom * s.denom);
   if (d == 0 || d == 2) {
@@ -521,7 +521,7 @@ __device__ __forceinline__ bool aa_dpos_terms(const SilDir& s, int d, int ph, in
                                               const float* __restrict__ cpp,
                                               const float* __restrict__ cnp,
                                               const float* __restrict__ p, double* __restrict__ dp,
-                                              float halfW, float halfH, LdsTable<4, 128>& tab) {
+                                              float halfW, float halfH, LdsTableU<4, 128>& tab) {
   float d_alpha = 0.0f;
   for (int k = 0; k < Cn; ++k) d_alpha += gp[k] * (cnp[k] - cpp[k]);
   if (d_alpha == 0.0f) return false;
@@ -557,7 +557,7 @@ __global__ void __launch_bounds__(256) k_aa_bwd(const float* __restrict__ rast,
   __shared__ int s_tri[18][kTriRow];
   __shared__ float s_alpha[4][16][kAlphaRow];
   __shared__ float s_halo[4][16];
-  __shared__ LdsTable<4, 128> tab;  // d_pos rows touched by this tile
+  __shared__ LdsTableU<4, 128> tab;  // d_pos rows touched by this tile
   __shared__ PosItem s_q[kPosQueue];
   __shared__ int s_nq;              // queued partial blends
   __shared__ int s_need;            // the table holds terms
@@ -712,7 +712,7 @@ __global__ void __launch_bounds__(256) k_aa_bwd(const float* __restrict__ rast,
     }
   }
   __syncthreads();
-  lds_table_flush<4, 128, double>(tab);  // contains a barrier
+  lds_table_flush_last<4, 128, double>(tab);  // the taken rows only
 }
 
 constexpr int kMaskQueue = 256 * 4 + 64;
@@ -773,7 +773,7 @@ __device__ __forceinline__ void aa_pair_eval(const AAPairIn<CT>& P, const AATile
                                              const float (*s_g)[CT > 0 ? CT : 1],
                                              const float* __restrict__ color,
                                              const float* __restrict__ d_out,
-                                             double* __restrict__ dpn, LdsTable<4, 128>& tab) {
+                                             double* __restrict__ dpn, LdsTableU<4, 128>& tab) {
   if (!P.ok) return;
   const int rr = P.cell / 18, cc = P.cell - rr * 18, d = P.d;
   const int qph = g.y0 + rr - 1, qpw = g.x0 + cc - 1;
@@ -826,7 +826,7 @@ __global__ void __launch_bounds__(256) k_aa_bwd_masked(
   __shared__ int s_tri[18][kTriRow];
   __shared__ float s_alpha[4][16][kAlphaRow];
   __shared__ float s_halo[4][16];
-  __shared__ LdsTable<4, 128> tab;       // d_pos rows touched by this tile
+  __shared__ LdsTableU<4, 128> tab;      // d_pos rows touched by this tile
   __shared__ uint16_t s_q[kMaskQueue];   // (cell r * 18 + c) << 2 | direction
   __shared__ int s_nq;
   __shared__ float s_g[kCells][CS];  // d_out of the tile and its border (CT > 0)
@@ -943,7 +943,7 @@ __global__ void __launch_bounds__(256) k_aa_bwd_masked(
   }
   if (!d_pos || nq == 0) return;  // uniform: nq was read after the barrier
   __syncthreads();
-  lds_table_flush<4, 128, double>(tab);  // contains a barrier
+  lds_table_flush_last<4, 128, double>(tab);  // the taken rows only
 }
 
 }  // namespace dr

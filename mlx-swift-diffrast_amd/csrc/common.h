@@ -629,6 +629,19 @@ __device__ __forceinline__ void lds_table_flush(LdsTableU<NV, CAP>& u) {
   if (threadIdx.x == 0) u.n = 0;
 }
 
+// The same for the last use of a table in a workgroup that ends after it:
+// no barrier and no reset.
+template <int NV, int CAP, typename D = float>
+__device__ __forceinline__ void lds_table_flush_last(LdsTableU<NV, CAP>& u) {
+  auto& t = u.t;
+  const int m = u.n;
+  for (int i = threadIdx.x; i < m * NV; i += blockDim.x) {
+    const int e = u.slot[i / NV], j = i - (i / NV) * NV;
+    const double v = t.val[j][e];
+    if (v != 0.0) unsafeAtomicAdd((D*)t.key[e] + j, (D)v);
+  }
+}
+
 // dst = (float)acc, or dst += (float)acc: the one rounding of a gradient
 // summed in fp64 across workgroups (so the result does not depend on the
 // order in which the workgroups' atomics land).

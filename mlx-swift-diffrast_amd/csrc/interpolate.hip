@@ -166,7 +166,7 @@ __global__ void __launch_bounds__(256) k_interp_bwd(
     const float* __restrict__ d_out_da, int N, int H, int W, int ntx, int nty, int V, int T,
     int A_, float* __restrict__ d_attr, int64_t d_attr_stride, int ncopy, int64_t copy_stride,
     float* __restrict__ d_rast, float* __restrict__ d_rast_db) {
-  __shared__ LdsTable<(AT > 0 ? AT : 1), 256> tab;  // d_attr rows (or elements) touched by this tile
+  __shared__ LdsTableU<(AT > 0 ? AT : 1), 256> tab;  // d_attr rows (or elements) touched by this tile
   __shared__ int s_any[4];  // per wave: a covered pixel
   const int tiles = ntx * nty;
   const int b = (int)blockIdx.x;
@@ -358,7 +358,7 @@ __global__ void __launch_bounds__(256) k_interp_bwd(
     }
   }
   __syncthreads();
-  lds_table_flush(tab);
+  lds_table_flush_last(tab);  // the taken rows only
 }
 
 // d_attr[i] = (accumulate ? d_attr[i] : 0) + the sum of the 256 copies'

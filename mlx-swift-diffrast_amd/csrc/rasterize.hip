@@ -1077,8 +1077,8 @@ __global__ void __launch_bounds__(256) k_raster_bwd(
     int64_t pos_stride, const int32_t* __restrict__ tri, int V, const float* __restrict__ rast,
     const float* __restrict__ d_rast, const float* __restrict__ d_rast_db, int N, int T, int H,
     int W, int ntx, int nty, double* __restrict__ d_pos) {
-  __shared__ LdsTable<4, 256> tab;  // d_pos rows touched by this tile
-  __shared__ int s_any[4];          // per wave: a covered pixel
+  __shared__ LdsTableU<4, 256> tab;  // d_pos rows touched by this tile
+  __shared__ int s_any[4];           // per wave: a covered pixel
   const int tiles = ntx * nty;
   const int b = xcd_remap((int)blockIdx.x, tiles * N);
   const int n = b / tiles;
@@ -1196,7 +1196,7 @@ __global__ void __launch_bounds__(256) k_raster_bwd(
     lds_table_add(tab, dp + (int64_t)i2 * 4, &val[8]);
   }
   __syncthreads();
-  lds_table_flush<4, 256, double>(tab);
+  lds_table_flush_last<4, 256, double>(tab);  // the taken rows only
 }
 
 // The one rounding of the fp64 sums; the accumulator is left zero for the
