@@ -39,10 +39,21 @@ constexpr int interp_pix() {
   return AT >= 6 ? 4 : 2;
 }
 
-// A workgroup covers 16 x (16 * PX) pixels of one image, each wave a 16x4
-// strip per pixel slot (one pixel row per 16 lanes): the strip's triangles
-// share more vertex rows than a 64-pixel row's, so its attribute gathers
-// touch fewer cache lines.
+// Width of the forward's pixel strips: a wave takes a 16x4 strip when a
+// 16-pixel row of its outputs fills whole 128-byte lines (an even attribute
+// count), since the strip's triangles share more vertex rows than a 64-pixel
+// row's and its attribute gathers touch fewer cache lines (16 x 2048^2 at
+// ~2.5 pixels per triangle, six attributes: 3.09 -> 2.78 ms per step of four
+// layers); otherwise a 64-pixel row, whose output rows stay whole lines
+// (three attributes and their derivatives on 16-pixel rows: 3.6 -> 4.6 ms at
+// 4096 x 256^2).
+template <int AT>
+constexpr int interp_strip() {
+  return (AT == 2 || AT == 4 || AT == 6) ? 16 : 64;
+}
+
+// A workgroup covers SW x (256 / SW * PX) pixels of one image: each wave a
+// strip SW wide and 64 / SW rows tall per pixel slot.
 template <int AT, int KT>
 __global__ void __launch_bounds__(256) k_interp_fwd(
     const float* __restrict__ attr, int64_t attr_stride, const float* __restrict__ rast,
@@ -59,9 +70,9 @@ __global__ void __launch_bounds__(256) k_interp_fwd(
   const int img = b / tiles;
   const int tile = b - img * tiles;
   const int ty = tile / ntx, tx = tile - ty * ntx;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int pw = tx * 16 + (lane & 15);
-  const int ph0 = ty * 16 * PX + wave * 4 + (lane >> 4);
+  constexpr int SW = interp_strip<AT>(), SH = 256 / SW;  // a slot's tile: SW x SH
+  const int pw = tx * SW + ((int)threadIdx.x & (SW - 1));
+  const int ph0 = ty * SH * PX + (int)threadIdx.x / SW;
   const float* at = attr + (int64_t)img * attr_stride;
   float4 r[PX];
   int t[PX];
@@ -69,7 +80,7 @@ __global__ void __launch_bounds__(256) k_interp_fwd(
   bool in[PX];
 #pragma unroll
   for (int q = 0; q < PX; ++q) {
-    const int ph = ph0 + q * 16;
+    const int ph = ph0 + q * SH;
     in[q] = pw < W && ph < H;
     pixq[q] = ((int64_t)img * H + min(ph, H - 1)) * W + min(pw, W - 1);
     r[q] = in[q] ? *reinterpret_cast<const float4*>(rast + pixq[q] * 4) : make_float4(0.f, 0.f, 0.f, 0.f);
@@ -422,7 +433,11 @@ extern "C" int dr_interpolate_fwd(const float* attr, int64_t attr_batch_stride,
   const bool aligned = (((uintptr_t)out | (uintptr_t)(out_da ? out_da : out)) & 15) == 0;
   // the dispatched kernel's pixels per thread (DR_INTERP_DISPATCH's choice)
   const int px = aligned && A == 6 && K == 0 ? interp_pix<6>() : interp_pix<0>();
-  const int ntx = (W + 15) / 16, nty = (H + 16 * px - 1) / (16 * px);
+  // and its strip width: the shapes of DR_INTERP_DISPATCH with an even A
+  const bool even = aligned && (A == 2 || A == 4 || A == 6) &&
+                    ((A == 2 && (K == 0 || (K == 2 && !diff_idx))) || (A != 2 && K == 0));
+  const int sw = even ? interp_strip<2>() : interp_strip<0>(), sh = 256 / sw;
+  const int ntx = (W + sw - 1) / sw, nty = (H + sh * px - 1) / (sh * px);
   const int64_t nblk = (int64_t)N * ntx * nty;
   DR_CHECK_ARG(nblk < ((int64_t)1 << 31), "interpolate: too many pixels");
   const dim3 grid((unsigned)nblk);
