@@ -251,6 +251,14 @@ int dr_profile_reset(void) {
     dr::g_prof_pool.push_back(r.b);
   }
   dr::g_prof.clear();
+  // events for the next 1,024 timed launches are created here, outside the
+  // measured loop (hipEventCreate costs tens of microseconds, as much as a
+  // small workload's whole step)
+  while (dr::g_prof_pool.size() < 2048) {
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) break;
+    dr::g_prof_pool.push_back(e);
+  }
   return DR_OK;
 }
 
