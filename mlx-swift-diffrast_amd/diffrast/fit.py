@@ -108,6 +108,22 @@ class Adam:
                                     self.beta2, self.eps, _stream()))
         return out
 
+    def step_(self, param: torch.Tensor, grad: torch.Tensor,
+              mask: Optional[torch.Tensor] = None) -> None:
+        """`step` written into `param` itself (contiguous float32 tensors of
+        the state's shape, `mask` too): no allocation, one kernel."""
+        for t in (param, grad) + (() if mask is None else (mask,)):
+            if tuple(t.shape) != tuple(self.m.shape) or t.dtype != torch.float32 or \
+                    not t.is_contiguous():
+                raise ValueError(f"Adam.step_: tensors must be contiguous float32 "
+                                 f"{list(self.m.shape)}")
+        lib = _lib.load()
+        self.t += 1
+        _lib.check(lib.dr_adam_step(_ptr(param), _ptr(grad), _ptr(mask), _ptr(self.m),
+                                    _ptr(self.v), _ptr(param), param.numel(), self.t,
+                                    self.learningRate, self.beta1, self.beta2, self.eps,
+                                    _stream()))
+
 
 # ---------------------------------------------------------------------------
 # the three samples
@@ -140,6 +156,44 @@ def _optimise(param, render, target_image, optimizer, steps, mask=None, log_ever
         if log is not None and log_every and (step % log_every == 0 or step == 1):
             log(f"  step {step:3d}  loss = {losses[step - 1].item():.6f}")
     return param, losses.cpu().tolist()
+
+
+def _optimise_graph(param, render, target_image, optimizer, steps, mask=None, log_every=0,
+                    log=None):
+    """The same loop with the loss and its gradient captured once into a HIP
+    graph and replayed each step: the parameter lives in one tensor that
+    Adam updates in place, so a step costs a graph launch, a copy of the
+    loss and the Adam kernel, not the host work of a dozen op calls.
+    Warm-up and capture run on a stream of their own (the library sizes its
+    per-stream scratch there before capture; nothing is allocated or waited
+    for under capture), and so do the replays."""
+    dev = param.device
+    losses = torch.empty(steps, device=dev, dtype=torch.float32)
+    mk = None if mask is None else mask.to(device=dev, dtype=torch.float32).contiguous()
+    caller = torch.cuda.current_stream(dev)
+    s = torch.cuda.Stream(dev)
+    s.wait_stream(caller)
+    with torch.cuda.stream(s):
+        p = param.detach().to(torch.float32).contiguous().clone().requires_grad_(True)
+
+        def loss_and_grad():
+            loss = mse_loss(render(p), target_image)
+            (grad,) = torch.autograd.grad(loss, [p])
+            return loss, grad
+        for _ in range(2):  # every call once on this stream before capture
+            loss_and_grad()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s):
+            s_loss, s_grad = loss_and_grad()
+        for step in range(1, steps + 1):
+            graph.replay()
+            losses[step - 1].copy_(s_loss)
+            optimizer.step_(p.detach(), s_grad, mk)
+            if log is not None and log_every and (step % log_every == 0 or step == 1):
+                log(f"  step {step:3d}  loss = {losses[step - 1].item():.6f}")
+        out = p.detach().clone()
+    caller.wait_stream(s)
+    return out, losses.cpu().tolist()
 
 
 @dataclass
@@ -249,30 +303,32 @@ def make_render(sc: Scene):
     return render
 
 
-def run(sc: Scene, steps: Optional[int] = None, log=None) -> FitResult:
-    """The sample's optimisation: Adam on the parameter for `steps` steps."""
+def run(sc: Scene, steps: Optional[int] = None, log=None, graph: bool = True) -> FitResult:
+    """The sample's optimisation: Adam on the parameter for `steps` steps,
+    as replays of one captured step (graph=True) or as eager steps."""
     render = make_render(sc)
     target_image = render(sc.target).detach()
     opt = Adam(sc.init.shape, learningRate=sc.learning_rate)
-    param, losses = _optimise(sc.init.clone(), render, target_image, opt,
-                              sc.steps if steps is None else steps, mask=sc.mask,
-                              log_every=sc.log_every, log=log)
+    loop = _optimise_graph if graph else _optimise
+    param, losses = loop(sc.init.clone(), render, target_image, opt,
+                         sc.steps if steps is None else steps, mask=sc.mask,
+                         log_every=sc.log_every, log=log)
     return FitResult(losses, param, sc.target, sc.size)
 
 
-def color_fit(steps: Optional[int] = None, log=None) -> FitResult:
+def color_fit(steps: Optional[int] = None, log=None, graph: bool = True) -> FitResult:
     """Tier 1 (ColorFitExample/main.swift)."""
-    return run(color_scene(), steps, log)
+    return run(color_scene(), steps, log, graph)
 
 
-def pose_fit(steps: Optional[int] = None, log=None) -> FitResult:
+def pose_fit(steps: Optional[int] = None, log=None, graph: bool = True) -> FitResult:
     """Tier 2 (PoseFitExample/main.swift)."""
-    return run(pose_scene(), steps, log)
+    return run(pose_scene(), steps, log, graph)
 
 
-def mesh_fit(steps: Optional[int] = None, log=None) -> FitResult:
+def mesh_fit(steps: Optional[int] = None, log=None, graph: bool = True) -> FitResult:
     """Tier 3 (MeshFitExample/main.swift)."""
-    return run(mesh_scene(), steps, log)
+    return run(mesh_scene(), steps, log, graph)
 
 
 SAMPLES = {"color": color_fit, "pose": pose_fit, "mesh": mesh_fit}
@@ -283,10 +339,12 @@ def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description="inverse-rendering samples on the HIP path")
     ap.add_argument("sample", choices=sorted(SAMPLES))
     ap.add_argument("--steps", type=int, default=None)
+    ap.add_argument("--eager", action="store_true",
+                    help="run every step's ops eagerly instead of replaying a captured step")
     args = ap.parse_args(argv)
     fn = SAMPLES[args.sample]
     kw = {} if args.steps is None else {"steps": args.steps}
-    res = fn(log=print, **kw)
+    res = fn(log=print, graph=not args.eager, **kw)
     print(f"first loss {res.losses[0]:.6f}  final loss {res.losses[-1]:.6f}")
     if args.sample != "color":
         d = (res.param - res.target)[0, :, :2].cpu()
