@@ -130,7 +130,7 @@ def test_sample_converges(name):
         assert abs(res.losses[0] - first) <= 0.001
     # every gradient is order-independent (d_pos summed in fp64 across
     # workgroups), so each sample converges to one fixed final loss
-    # (mesh: 0.000192 against the README's 0.0002)
+    # (mesh: 0.000153 against the README's 0.0002)
     assert res.losses[-1] <= final
     if sc.kind == "pose":
         d = host(res.param - res.target)[0, :, :2]
