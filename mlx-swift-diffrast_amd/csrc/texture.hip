@@ -495,16 +495,21 @@ __device__ __forceinline__ void scatter_footprint(bool valid, float* __restrict_
 }
 
 // d_uv terms of one level (Texture.swift:500-520 / :979-995), summed over C.
+// IDX: the element offsets' type, int64_t for any level, or uint32_t where
+// the caller guarantees a level below 2^32 elements (sides at most 32767,
+// C at most 4).
+template <typename IDX = int64_t>
 __device__ __forceinline__ void duv_level(const float* __restrict__ lv, int Wk, int C,
                                           const Bilin& b, const float* g, float scale,
                                           float& dfx, float& dfy, float& dlod_sample) {
   dfx = 0.0f;
   dfy = 0.0f;
   dlod_sample = 0.0f;
-  const float* p00 = lv + (b.iy0 * Wk + b.ix0) * C;
-  const float* p10 = lv + (b.iy0 * Wk + b.ix1) * C;
-  const float* p01 = lv + (b.iy1 * Wk + b.ix0) * C;
-  const float* p11 = lv + (b.iy1 * Wk + b.ix1) * C;
+  const IDX r0 = (IDX)b.iy0 * (IDX)Wk, r1 = (IDX)b.iy1 * (IDX)Wk;
+  const float* p00 = lv + (r0 + (IDX)b.ix0) * (IDX)C;
+  const float* p10 = lv + (r0 + (IDX)b.ix1) * (IDX)C;
+  const float* p01 = lv + (r1 + (IDX)b.ix0) * (IDX)C;
+  const float* p11 = lv + (r1 + (IDX)b.ix1) * (IDX)C;
   for (int c = 0; c < C; ++c) {
     const float r00 = p00[c], r10 = p10[c], r01 = p01[c], r11 = p11[c];
     const float t00 = r00 * b.m00, t10 = r10 * b.m10, t01 = r01 * b.m01, t11 = r11 * b.m11;
@@ -897,7 +902,7 @@ __global__ void __launch_bounds__(kWinThreads, 5) k_tex_bwd_win(TexBwdArgs A, in
       const bool flat = BND != DR_BOUNDARY_ZERO && b.ix0 == b.ix1 && b.iy0 == b.iy1 && lod0;
       if (valid && (li == 0 || need1) && !flat) {
         float dfx, dfy;
-        duv_level(level_ptr(k), Wk, CT, b, g, mip ? q[li].scale : 1.0f, dfx, dfy, samp[li]);
+        duv_level<uint32_t>(level_ptr(k), Wk, CT, b, g, mip ? q[li].scale : 1.0f, dfx, dfy, samp[li]);
         dfx_total += dfx * (float)Wk;
         dfy_total += dfy * (float)Hk;
       }
@@ -921,9 +926,9 @@ __global__ void __launch_bounds__(kWinThreads, 5) k_tex_bwd_win(TexBwdArgs A, in
           const int k1 = min(k0 + 1, md.L - 1);
           float s0 = 0.0f, s1 = 0.0f, u0, u1;
           const Bilin b0 = bilin(uvp.x, uvp.y, mip_w(md, k0), mip_h(md, k0), BND);
-          duv_level(level_ptr(k0), mip_w(md, k0), CT, b0, g, 0.0f, u0, u1, s0);
+          duv_level<uint32_t>(level_ptr(k0), mip_w(md, k0), CT, b0, g, 0.0f, u0, u1, s0);
           const Bilin b1 = bilin(uvp.x, uvp.y, mip_w(md, k1), mip_h(md, k1), BND);
-          duv_level(level_ptr(k1), mip_w(md, k1), CT, b1, g, 0.0f, u0, u1, s1);
+          duv_level<uint32_t>(level_ptr(k1), mip_w(md, k1), CT, b1, g, 0.0f, u0, u1, s1);
           d_lod = -s0 + s1;
         }
         const float ln2 = 0.6931471805599453f;
@@ -1136,7 +1141,7 @@ __global__ void __launch_bounds__(kWinThreads, 5) k_tex_bwd_win(TexBwdArgs A, in
         for (int t = 0; t < 4; ++t) {
           const int tx_ = (t & 1) ? q[li].ix1 : q[li].ix0;
           const int ty_ = (t & 2) ? q[li].iy1 : q[li].iy0;
-          lds_table_add(tab, base + (ty_ * Wk + tx_) * CT, &v[t * CT]);
+          lds_table_add(tab, base + ((int64_t)ty_ * Wk + tx_) * CT, &v[t * CT]);
         }
       }
     }
@@ -1166,7 +1171,7 @@ __global__ void __launch_bounds__(kWinThreads, 5) k_tex_bwd_win(TexBwdArgs A, in
         double* e = wb + c * kWinTexels + r * bw + tx;
         const double v = *e;
         if (v != 0.0) {
-          unsafeAtomicAdd(base + ((by0 + r) * Wk + bx0) * CT + cpos, (float)v);
+          unsafeAtomicAdd(base + ((int64_t)(by0 + r) * Wk + bx0) * CT + cpos, (float)v);
           *e = 0.0;
         }
         r += dr;

@@ -250,3 +250,44 @@ def test_cached_pyramid_stale():
     ref = O.texture(tex + np.float32(0.5), uv, uvDA=da, filterMode="linear-mipmap-linear",
                     boundaryMode="clamp")
     assert_fwd_close(host(out), ref)
+
+
+@pytest.mark.parametrize("C", [4, 5])
+def test_level_above_2g_elements(C):
+    """A texture level of more than 2^31 floats (C = 4: the windowed
+    backward, sides up to 32767; C = 5: the tiled backward): texel offsets
+    are formed in 64 bits (32 bits where a level stays below 2^32 floats).
+    16 pixels sample the last 8x8 texels; their outputs and gradients equal
+    those of the same texels as a texture of their own (the pixels' uv
+    rescaled, so the bilinear fractions differ by the rounding of u * W),
+    and d_tex is zero away from them."""
+    torch = torch_dev()
+    from diffrast import DiffRast
+    S = 23200 if C == 4 else 20800
+    assert S * S * C > 2 ** 31
+    gen = torch.Generator(device="cuda").manual_seed(C)
+    tex = torch.rand((1, S, S, C), device="cuda", generator=gen).requires_grad_(True)
+    rng = np.random.default_rng(C)
+    x = rng.uniform(S - 7.5, S - 0.5, size=(1, 4, 4, 2))   # texel-space sample points
+    uv = dev((x / S).astype(np.float32))
+    g = dev(rng.standard_normal((1, 4, 4, C)).astype(np.float32))
+    uv_big = uv.detach().clone().requires_grad_(True)
+    out = DiffRast.texture(tex, uv_big, filterMode="linear", boundaryMode="clamp")
+    d_tex, d_uv = torch.autograd.grad(out, [tex, uv_big], g)
+    corner = host(d_tex[0, S - 8:, S - 8:, :]).copy()
+    far = host(d_tex[0, :64, :64, :]).copy()
+    got_out, got_duv = host(out).copy(), host(d_uv).copy()
+    crop = tex.detach()[:, S - 8:, S - 8:, :].contiguous().requires_grad_(True)
+    del tex, d_tex, out
+    torch.cuda.empty_cache()
+    uv_c = dev(((x - (S - 8)) / 8).astype(np.float32)).requires_grad_(True)
+    ref = DiffRast.texture(crop, uv_c, filterMode="linear", boundaryMode="clamp")
+    r_tex, r_uv = torch.autograd.grad(ref, [crop, uv_c], g)
+    np.testing.assert_allclose(got_out, host(ref), rtol=0, atol=2e-3)
+    np.testing.assert_allclose(corner, host(r_tex)[0], rtol=0, atol=5e-3 * float(np.abs(host(g)).max()))
+    # d_uv scales with the texture size (u * S against u' * 8); the sample
+    # points differ by up to S * 2^-24 texels between the two, so the
+    # differences are held to 2e-3 of the largest component
+    r_duv = host(r_uv) * (S / 8.0)
+    np.testing.assert_allclose(got_duv, r_duv, rtol=0, atol=2e-3 * float(np.abs(r_duv).max()))
+    assert not far.any()
