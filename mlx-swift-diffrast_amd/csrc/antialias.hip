@@ -955,6 +955,7 @@ extern "C" int dr_antialias_topology(const int32_t* tri, int T, int32_t* topo,
   hipStream_t stream = (hipStream_t)stream_;
   (void)hipGetLastError();
   DR_CHECK_ARG(tri && topo && T >= 0, "antialias_topology: bad arguments");
+  DR_CHECK_ARG(T <= INT32_MAX / 3, "antialias_topology: at most 715827882 triangles (edges are indexed in 32 bits)");
   if (T == 0) return DR_OK;
   const int64_t E = (int64_t)T * 3;
   uint64_t S = 64;
@@ -1017,6 +1018,7 @@ static int check_aa(const float* color, const float* rast, const float* pos, con
                     const int32_t* topo, int N, int H, int W, int C, int V, int T) {
   DR_CHECK_ARG(color && rast && pos && tri && topo, "antialias: null tensor");
   DR_CHECK_ARG(N >= 1 && H >= 1 && W >= 1 && C >= 1 && V >= 0 && T >= 0, "antialias: bad sizes");
+  DR_CHECK_ARG(T <= INT32_MAX / 3, "antialias: at most 715827882 triangles (edges are indexed in 32 bits)");
   return DR_OK;
 }
 

@@ -412,6 +412,7 @@ static int check_interp(const float* attr, const float* rast, const int32_t* tri
   DR_CHECK_ARG(N >= 1 && H >= 1 && W >= 1 && V >= 0 && T >= 0 && A >= 1 && K >= 0,
                "interpolate: bad sizes");
   DR_CHECK_ARG(attr && rast && tri, "interpolate: null tensor");
+  DR_CHECK_ARG(T <= INT32_MAX / 3, "interpolate: at most 715827882 triangles (tri is indexed in 32 bits)");
   DR_CHECK_ARG(attr_stride == 0 || attr_stride == (int64_t)V * A,
                "interpolate: attr_batch_stride must be 0 or V*A");
   DR_CHECK_ARG(K == 0 || rast_db, "interpolate: rastDB is required when diffAttrs is set");

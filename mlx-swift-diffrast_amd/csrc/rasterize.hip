@@ -1293,6 +1293,7 @@ static int check_raster_args(const float* pos, int64_t pos_batch_stride, const i
   DR_CHECK_ARG(ranges_host == nullptr || pos_batch_stride == 0,
                "rasterize: range mode needs a shared pos (pos_batch_stride = 0)");
   DR_CHECK_ARG((int64_t)N * T < (int64_t)1 << 40, "rasterize: too many triangles");
+  DR_CHECK_ARG(T <= INT32_MAX / 3, "rasterize: at most 715827882 triangles (tri is indexed in 32 bits)");
   const int64_t n_tiles =
       (int64_t)N * ((W + kTile - 1) / kTile) * (int64_t)((H + kTile - 1) / kTile);
   DR_CHECK_ARG(n_tiles < (int64_t)1 << 31, "rasterize: too many tiles");

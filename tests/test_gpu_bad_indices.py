@@ -111,3 +111,26 @@ def test_antialias_triangle_with_foreign_vertex():
     out.backward(dev(rng.normal(size=tuple(out.shape)).astype(np.float32)))
     assert np.isfinite(host(out)).all()
     assert np.isfinite(host(color.grad)).all() and np.isfinite(host(p.grad)).all()
+
+
+def test_triangle_count_above_32bit_indexing_is_refused():
+    """tri is indexed as t * 3 + k in 32 bits: a call with more than
+    715,827,882 triangles is refused before any work is queued (the tensors
+    here are small; nothing reads them)."""
+    torch = torch_dev()
+    import diffrast._lib as L
+    from diffrast.ops import _stream
+    lib = L.load()
+    T = 715827883
+    buf = torch.zeros(64, device="cuda")
+    itri = torch.zeros(64, dtype=torch.int32, device="cuda")
+    p, t = buf.data_ptr(), itri.data_ptr()
+    rc = lib.dr_rasterize_fwd(p, 12, t, None, None, 1, 3, T, 8, 8, p, None, _stream())
+    assert rc == L.DR_ERR_ARGUMENT and b"715827882" in lib.dr_get_last_error()
+    rc = lib.dr_interpolate_fwd(p, 0, p, None, t, None, 0, 1, 8, 8, 3, T, 1, p, None, _stream())
+    assert rc == L.DR_ERR_ARGUMENT and b"715827882" in lib.dr_get_last_error()
+    rc = lib.dr_antialias_topology(t, T, t, _stream())
+    assert rc == L.DR_ERR_ARGUMENT and b"715827882" in lib.dr_get_last_error()
+    rc = lib.dr_antialias_fwd(p, p, p, t, t, 1, 8, 8, 1, 3, T, p, _stream())
+    assert rc == L.DR_ERR_ARGUMENT and b"715827882" in lib.dr_get_last_error()
+    torch.cuda.synchronize()
