@@ -63,6 +63,9 @@
  *     id is outside [0, T) is empty for interpolate and the backward passes;
  *     a diff_idx entry outside [0, A) gives zero derivatives.  (The
  *     reference reads out of range in these cases.)
+ *   - Sizes: at most 715,827,882 triangles a call (tri is indexed as
+ *     t * 3 + k in 32 bits; more returns DR_ERR_ARGUMENT) and fewer than 2^31
+ *     16x16 pixel tiles; textures of any size.
  */
 #ifndef DIFFRAST_MI355X_H
 #define DIFFRAST_MI355X_H
