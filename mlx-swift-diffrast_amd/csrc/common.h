@@ -223,6 +223,34 @@ __device__ __forceinline__ int xcd_remap(int b, int B) {
 
 __device__ __forceinline__ int lane_id() { return (int)__lane_id(); }
 
+// Streaming accesses with the non-temporal hint: per-pixel inputs read
+// once and outputs the next kernel streams in again leave L2's reused lines
+// (texels, vertex rows, triangle records) in place.  Measured on the
+// 8 x 1024^2 chain: texture forward 0.080 -> 0.071 ms, interpolate forward
+// 0.084 -> 0.081 ms, the step 1.153 -> 1.130 ms.  Not used where the next
+// kernel reads the output while it may still be cached and would then
+// have to fetch it again (antialias out before the loss, the interpolate
+// backward's d_rast before the rasterize backward: both measured slower).
+typedef float dr_f4v __attribute__((ext_vector_type(4)));
+typedef float dr_f2v __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float4 ld_nt4(const float* p) {
+  const dr_f4v v = __builtin_nontemporal_load(reinterpret_cast<const dr_f4v*>(p));
+  return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ float2 ld_nt2(const float* p) {
+  const dr_f2v v = __builtin_nontemporal_load(reinterpret_cast<const dr_f2v*>(p));
+  return make_float2(v.x, v.y);
+}
+__device__ __forceinline__ void st_nt4(float* p, float4 v) {
+  dr_f4v x = {v.x, v.y, v.z, v.w};
+  __builtin_nontemporal_store(x, reinterpret_cast<dr_f4v*>(p));
+}
+__device__ __forceinline__ void st_nt2(float* p, float2 v) {
+  dr_f2v x = {v.x, v.y};
+  __builtin_nontemporal_store(x, reinterpret_cast<dr_f2v*>(p));
+}
+
+
 // Wave-uniform values: keep them in scalar registers.
 __device__ __forceinline__ float uni(float x) {
   return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(x)));

@@ -22,9 +22,9 @@ __device__ __forceinline__ int dimA(int A) { return AT > 0 ? AT : A; }
 template <int NC>
 __device__ __forceinline__ void st_run(float* __restrict__ p, const float* v, int n) {
   if constexpr (NC == 2) {
-    *reinterpret_cast<float2*>(p) = make_float2(v[0], v[1]);
+    st_nt2(p, make_float2(v[0], v[1]));
   } else if constexpr (NC == 4) {
-    *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+    st_nt4(p, make_float4(v[0], v[1], v[2], v[3]));
   } else {
     for (int i = 0; i < n; ++i) p[i] = v[i];
   }
@@ -83,7 +83,7 @@ __global__ void __launch_bounds__(256) k_interp_fwd(
     const int ph = ph0 + q * SH;
     in[q] = pw < W && ph < H;
     pixq[q] = ((int64_t)img * H + min(ph, H - 1)) * W + min(pw, W - 1);
-    r[q] = in[q] ? *reinterpret_cast<const float4*>(rast + pixq[q] * 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+    r[q] = in[q] ? ld_nt4(rast + pixq[q] * 4) : make_float4(0.f, 0.f, 0.f, 0.f);
     t[q] = in[q] ? f2i(r[q].w) - 1 : -1;
     if (t[q] >= T) t[q] = -1;  // not a triangle of this mesh: empty
   }

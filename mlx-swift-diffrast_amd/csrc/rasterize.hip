@@ -680,8 +680,8 @@ __global__ void __launch_bounds__(kRThreads) k_raster(
                          (R.r0.y - R.r0.w) * R.r2.z * k_x, (R.r0.z - R.r0.x) * R.r2.z * k_y);
       }
     }
-    *reinterpret_cast<float4*>(rast + pix * 4) = o4;
-    if (DB) *reinterpret_cast<float4*>(rast_db + pix * 4) = d4;
+    st_nt4(rast + pix * 4, o4);
+    if (DB) st_nt4(rast_db + pix * 4, d4);
   };
   float peel_z[kRPix];
 #pragma unroll

@@ -217,7 +217,7 @@ __device__ __forceinline__ void tex_fwd_px(
     }
     return;
   }
-  const float2 uvp = *reinterpret_cast<const float2*>(uv + pix * 2);
+  const float2 uvp = ld_nt2(uv + pix * 2);
   if (FILTER == DR_FILTER_NEAREST) {  // Texture.swift:545-572
     const int tx = f2i(floorf(uvp.x * (float)Wt));
     const int ty = f2i(floorf(uvp.y * (float)Ht));
@@ -253,7 +253,7 @@ __device__ __forceinline__ void tex_fwd_px(
     return;
   }
   // Mip filters (Texture.swift:795-863).
-  float4 da = *reinterpret_cast<const float4*>(uv_da + pix * 4);
+  float4 da = ld_nt4(uv_da + pix * 4);
   const float s = bias_scale(bias_map, pix, scale_bias, has_bias != 0);
   if (bias_map || has_bias) da = make_float4(da.x * s, da.y * s, da.z * s, da.w * s);
   const Lod ld = mip_lod(da, Ht, Wt, md.L, FILTER == DR_FILTER_LINEAR_MIPMAP_LINEAR);
@@ -605,7 +605,7 @@ __device__ __forceinline__ void tex_bwd_tile(const TexBwdArgs& A, int bidx,
     return;
   }
 
-  const float2 uvp = *reinterpret_cast<const float2*>(uv + pix * 2);
+  const float2 uvp = ld_nt2(uv + pix * 2);
   if (FILTER == DR_FILTER_NEAREST) {  // Texture.swift:576-605; d_uv = 0 (:234)
     const int txi = f2i(floorf(uvp.x * (float)Wt));
     const int tyi = f2i(floorf(uvp.y * (float)Ht));
@@ -843,10 +843,15 @@ __global__ void __launch_bounds__(kWinThreads, 5) k_tex_bwd_win(TexBwdArgs A, in
 
     // -- per pixel: footprints, gradients of uv / uvDA ------------------------
     float g[CT];
-    load_texel<CT>(A.d_out + pix * CT, CT, g);  // one vector load for CT = 4
+    if constexpr (CT == 4) {  // one vector load
+      const float4 q4 = ld_nt4(A.d_out + pix * 4);
+      g[0] = q4.x; g[1 % CT] = q4.y; g[2 % CT] = q4.z; g[3 % CT] = q4.w;
+    } else {
+      load_texel<CT>(A.d_out + pix * CT, CT, g);
+    }
 #pragma unroll
     for (int c = 0; c < CT; ++c) g[c] = valid ? g[c] : 0.0f;
-    const float2 uvp = *reinterpret_cast<const float2*>(A.uv + pix * 2);
+    const float2 uvp = ld_nt2(A.uv + pix * 2);
     TapSlot q[2];
     float4 da_in = make_float4(0.f, 0.f, 0.f, 0.f), da = da_in;
     float s = 1.0f;
@@ -858,7 +863,7 @@ __global__ void __launch_bounds__(kWinThreads, 5) k_tex_bwd_win(TexBwdArgs A, in
     bool need1 = false;
     bool lod0 = true;  // LOD clamped to 0: no d_lod sample is needed
     if (mip) {
-      da_in = *reinterpret_cast<const float4*>(A.uv_da + pix * 4);
+      da_in = ld_nt4(A.uv_da + pix * 4);
       if (BIAS) {
         s = bias_scale(A.bias_map, pix, A.scale_bias, A.has_bias != 0);
         scaled = true;
@@ -908,7 +913,7 @@ __global__ void __launch_bounds__(kWinThreads, 5) k_tex_bwd_win(TexBwdArgs A, in
       }
     }
     if (valid && A.d_uv)
-      *reinterpret_cast<float2*>(A.d_uv + pix * 2) = make_float2(dfx_total, dfy_total);
+      st_nt2(A.d_uv + pix * 2, make_float2(dfx_total, dfy_total));
     if (mip && valid && (A.d_uv_da || A.d_bias)) {  // Texture.swift:1011-1102
       const float sx = da.x * (float)A.Wt, sy = da.y * (float)A.Wt;
       const float tx_ = da.z * (float)A.Ht, ty_ = da.w * (float)A.Ht;
@@ -943,7 +948,7 @@ __global__ void __launch_bounds__(kWinThreads, 5) k_tex_bwd_win(TexBwdArgs A, in
       }
       if (A.d_uv_da) {
         const float4 o = scaled ? make_float4(d_eff.x * s, d_eff.y * s, d_eff.z * s, d_eff.w * s) : d_eff;
-        *reinterpret_cast<float4*>(A.d_uv_da + pix * 4) = o;
+        st_nt4(A.d_uv_da + pix * 4, o);
       }
       if (BIAS && A.d_bias && A.bias_map) {
         const float gm = d_eff.x * da_in.x + d_eff.y * da_in.y + d_eff.z * da_in.z + d_eff.w * da_in.w;
