@@ -41,9 +41,10 @@ __global__ __launch_bounds__(256) void k_mse(const float* __restrict__ out,
   if (VEC) {
     const int64_t n4 = n >> 2;
     const float4* o4 = reinterpret_cast<const float4*>(out);
-    const float4* t4 = reinterpret_cast<const float4*>(target);
     for (int64_t i = tid; i < n4; i += stride) {
-      const float4 a = o4[i], b = t4[i];
+      // the target is streamed once a call (non-temporal): 1.133 -> 1.127 ms
+      // a step at 8 x 1024^2, whose antialias output `out` is still in cache
+      const float4 a = o4[i], b = ld_nt4(target + 4 * i);
       const float dx = a.x - b.x, dy = a.y - b.y, dz = a.z - b.z, dw = a.w - b.w;
       const float sx = dx * dx, sy = dy * dy, sz = dz * dz, sw = dw * dw;
       acc += (double)sx + (double)sy + (double)sz + (double)sw;
