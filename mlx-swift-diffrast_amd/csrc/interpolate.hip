@@ -41,13 +41,13 @@ __device__ __forceinline__ void st_run(float* __restrict__ p, const float* v, in
   }
 }
 
-// Pixels per thread of the forward (more independent load chains in
-// flight): four for six attributes (a 16 x 2048^2 batch at ~2.5 pixels per
-// triangle waits on its vertex rows: 3.22 -> 3.08 ms per step of four
-// layers), two otherwise (four measured slower at 8 x 1024^2 with A = 2).
+// Pixels per thread of the forward: two, each round of their loads issued
+// together (16 x 2048^2 at ~2.5 pixels per triangle, six attributes: 2.46
+// -> 2.39 ms per step of four layers against four pixels a thread; 4096 x
+// 256^2, three attributes and their derivatives: 3.54 -> 3.43 ms).
 template <int AT>
 constexpr int interp_pix() {
-  return AT >= 6 ? 4 : 2;
+  return 2;
 }
 
 // Width of the forward's pixel strips: a wave takes a 16x4 strip when a
@@ -89,33 +89,60 @@ __global__ void __launch_bounds__(256) k_interp_fwd(
   int t[PX];
   int64_t pixq[PX];
   bool in[PX];
+  // Every slot's loads of one round (rast, triangle ids, vertex rows) are
+  // issued before any of them is used: a select, check or store between the
+  // slots' loads makes the wave wait for each slot's round trip in turn.  So
+  // the loads are not predicated per lane: a lane outside the image reads
+  // its clamped pixel, and in a wave where some lane has a triangle, lanes
+  // without one read triangle 0 and vertex row 0 (the values are dropped).
 #pragma unroll
   for (int q = 0; q < PX; ++q) {
     const int ph = ph0 + q * SH;
     in[q] = pw < W && ph < H;
     pixq[q] = ((int64_t)img * H + min(ph, H - 1)) * W + min(pw, W - 1);
-    r[q] = in[q] ? ld_nt4(rast + pixq[q] * 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  // (addresses first: a register of a pending load that the code does not
+  // read, such as rast's depth, is not reused for them, which would wait)
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int q = 0; q < PX; ++q) r[q] = ld_nt4(rast + pixq[q] * 4);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int q = 0; q < PX; ++q) {
     t[q] = in[q] ? f2i(r[q].w) - 1 : -1;
     if (t[q] >= T) t[q] = -1;  // not a triangle of this mesh: empty
   }
+  bool any = false;
+#pragma unroll
+  for (int q = 0; q < PX; ++q) any = any || t[q] >= 0;
+  const bool wave_any = __ballot(any) != 0ull;  // uniform: then T > 0
   int iv[PX][3];
 #pragma unroll
-  for (int q = 0; q < PX; ++q) {
-    iv[q][0] = iv[q][1] = iv[q][2] = 0;
-    if (t[q] >= 0) {
-      iv[q][0] = tri[t[q] * 3 + 0];
-      iv[q][1] = tri[t[q] * 3 + 1];
-      iv[q][2] = tri[t[q] * 3 + 2];
-      if (!verts_ok(iv[q][0], iv[q][1], iv[q][2], V)) t[q] = -1;
+  for (int q = 0; q < PX; ++q) iv[q][0] = iv[q][1] = iv[q][2] = 0;
+  if (wave_any) {
+#pragma unroll
+    for (int q = 0; q < PX; ++q) {
+      const int tt = t[q] >= 0 ? t[q] : 0;
+      iv[q][0] = tri[tt * 3 + 0];
+      iv[q][1] = tri[tt * 3 + 1];
+      iv[q][2] = tri[tt * 3 + 2];
     }
   }
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int q = 0; q < PX; ++q) {
-    const int64_t pix = pixq[q];
-    if (!in[q]) continue;
-    float* o = out + pix * A;
-    float* od = K > 0 ? out_da + pix * 2 * K : nullptr;
-    if (AT == 0 || KT == 0 && K > 0) {  // any shape: element by element
+    if (!(t[q] >= 0 && verts_ok(iv[q][0], iv[q][1], iv[q][2], V))) {
+      t[q] = -1;
+      iv[q][0] = iv[q][1] = iv[q][2] = 0;
+    }
+  }
+  if (AT == 0 || KT == 0 && K > 0) {  // any shape: element by element
+#pragma unroll
+    for (int q = 0; q < PX; ++q) {
+      const int64_t pix = pixq[q];
+      if (!in[q]) continue;
+      float* o = out + pix * A;
+      float* od = K > 0 ? out_da + pix * 2 * K : nullptr;
       if (t[q] < 0) {
         for (int a = 0; a < A; ++a) o[a] = 0.0f;
         for (int k = 0; k < 2 * K; ++k) od[k] = 0.0f;
@@ -141,39 +168,58 @@ __global__ void __launch_bounds__(256) k_interp_fwd(
           od[2 * k + 1] = d01 * db.y + d02 * db.w;
         }
       }
-      continue;
     }
-    // compile-time shape (identity diff_idx when KT > 0)
+    return;
+  }
+  // compile-time shape (identity diff_idx when KT > 0)
+  bool rows = false;
+#pragma unroll
+  for (int q = 0; q < PX; ++q) rows = rows || t[q] >= 0;
+  const bool wave_rows = __ballot(rows) != 0ull;  // uniform: then V > 0
+  float a0[PX][NA], a1[PX][NA], a2[PX][NA];
+  float4 db[PX];
+#pragma unroll
+  for (int q = 0; q < PX; ++q) {
+#pragma unroll
+    for (int a = 0; a < NA; ++a) a0[q][a] = a1[q][a] = a2[q][a] = 0.0f;
+    db[q] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  if (wave_rows) {
+#pragma unroll
+    for (int q = 0; q < PX; ++q) {
+#pragma unroll
+      for (int a = 0; a < NA; ++a) {
+        a0[q][a] = at[(int64_t)iv[q][0] * NA + a];
+        a1[q][a] = at[(int64_t)iv[q][1] * NA + a];
+        a2[q][a] = at[(int64_t)iv[q][2] * NA + a];
+      }
+      if (KT > 0) db[q] = *reinterpret_cast<const float4*>(rast_db + pixq[q] * 4);
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < PX; ++q) {
+    if (!in[q]) continue;
+    const int64_t pix = pixq[q];
     float ov[NA], odv[NK];
 #pragma unroll
     for (int a = 0; a < NA; ++a) ov[a] = 0.0f;
 #pragma unroll
     for (int k = 0; k < NK; ++k) odv[k] = 0.0f;
     if (t[q] >= 0) {
-      float a0[NA], a1[NA], a2[NA];
-#pragma unroll
-      for (int a = 0; a < NA; ++a) {
-        a0[a] = at[(int64_t)iv[q][0] * NA + a];
-        a1[a] = at[(int64_t)iv[q][1] * NA + a];
-        a2[a] = at[(int64_t)iv[q][2] * NA + a];
-      }
       const float u = r[q].x, v = r[q].y;
       const float bw = 1.0f - u - v;
 #pragma unroll
-      for (int a = 0; a < NA; ++a) ov[a] = bw * a0[a] + u * a1[a] + v * a2[a];
-      if (KT > 0) {
-        const float4 db = *reinterpret_cast<const float4*>(rast_db + pix * 4);
+      for (int a = 0; a < NA; ++a) ov[a] = bw * a0[q][a] + u * a1[q][a] + v * a2[q][a];
 #pragma unroll
-        for (int k = 0; k < (KT > 0 ? KT : 1); ++k) {
-          const float d01 = a1[k] - a0[k];
-          const float d02 = a2[k] - a0[k];
-          odv[2 * k + 0] = d01 * db.x + d02 * db.z;
-          odv[2 * k + 1] = d01 * db.y + d02 * db.w;
-        }
+      for (int k = 0; k < (KT > 0 ? KT : 0); ++k) {
+        const float d01 = a1[q][k] - a0[q][k];
+        const float d02 = a2[q][k] - a0[q][k];
+        odv[2 * k + 0] = d01 * db[q].x + d02 * db[q].z;
+        odv[2 * k + 1] = d01 * db[q].y + d02 * db[q].w;
       }
     }
-    st_run<NA>(o, ov, NA);
-    if (KT > 0) st_run<NK>(od, odv, NK);
+    st_run<NA>(out + pix * NA, ov, NA);
+    if (KT > 0) st_run<NK>(out_da + pix * NK, odv, NK);
   }
 }
 

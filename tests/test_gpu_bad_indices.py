@@ -71,6 +71,48 @@ def test_interpolate_foreign_ids_read_as_empty():
     np.testing.assert_array_equal(outs[0][4], outs[1][4])
 
 
+@pytest.mark.parametrize("A,diff", [(6, None), (3, "all"), (5, None)])
+def test_interpolate_foreign_vertex_ids_read_as_empty(A, diff):
+    """Pixels of a triangle with a vertex id outside [0, V) interpolate to
+    zero and add no gradient, whatever shares their wave (the forward reads
+    every slot's vertex rows before checking any)."""
+    torch = torch_dev()
+    from diffrast import DiffRast
+    pos, tri, H, W = _scene()
+    V, T = pos.shape[1], tri.shape[0]
+    rast, db = O.rasterize(pos, tri, (H, W), gradDB=True, max_per_tile=0)
+    bad = tri.copy()
+    bad[1] = [0, V + 5, 2]
+    bad[3] = [-7, 1, 2]
+    ids = rast[..., 3].astype(np.int64) - 1
+    emptied, db_e = rast.copy(), db.copy()
+    hit = (ids == 1) | (ids == 3)
+    assert hit.any() and (~hit & (ids >= 0)).any()
+    emptied[hit] = 0.0
+    rng = np.random.default_rng(6 + A)
+    attr = rng.normal(size=(V, A)).astype(np.float32)
+    a = dev(attr).requires_grad_(True)
+    rd = dev(rast).requires_grad_(True)
+    dbd = dev(db).requires_grad_(True)
+    out, out_da = DiffRast.interpolate(a, rd, dev(bad), rastDB=dbd if diff else None,
+                                       diffAttrs=diff)
+    ro, rda = O.interpolate(attr, emptied, tri, rastDB=db_e if diff else None, diffAttrs=diff)
+    np.testing.assert_array_equal(host(out), ro)
+    if diff:
+        np.testing.assert_array_equal(host(out_da), rda)
+    g = rng.normal(size=ro.shape).astype(np.float32)
+    loss = (out * dev(g)).sum()
+    gda = None
+    if diff:
+        gda = rng.normal(size=rda.shape).astype(np.float32)
+        loss = loss + (out_da * dev(gda)).sum()
+    loss.backward()
+    d_attr, d_rast, _ = O.interpolate_vjp(attr, emptied, tri, g, rastDB=db_e if diff else None,
+                                          diffAttrs=diff, d_out_da=gda)
+    assert_grad_close(host(a.grad), d_attr, "d_attr")
+    assert_fwd_close(host(rd.grad), d_rast, "d_rast")
+
+
 def test_interpolate_diff_idx_out_of_range():
     torch = torch_dev()
     from diffrast import DiffRast
