@@ -1548,8 +1548,20 @@ struct CubePx {
 template <int MODE>
 __device__ __forceinline__ CubePx cube_px(const CubeArgs& A, int64_t pix) {
   CubePx p;
+  // the direction, its derivatives and the bias are loaded together, ahead
+  // of the face selection's branches (one round trip instead of two)
   const float* dp = A.dir + pix * 3;
-  p.s = cube_select(dp[0], dp[1], dp[2]);
+  const float x = dp[0], y = dp[1], z = dp[2];
+  float2 a = make_float2(0.f, 0.f), b = a, c = a;
+  float bm = 0.0f;
+  if (MODE > 0) {
+    const float2* q = reinterpret_cast<const float2*>(A.dir_da + pix * 6);
+    a = q[0];
+    b = q[1];
+    c = q[2];
+    if (A.bias_map) bm = A.bias_map[pix];
+  }
+  p.s = cube_select(x, y, z);
   p.inv_ma = 1.0f / p.s.ma;
   p.u = (p.s.sc * p.inv_ma + 1.0f) * 0.5f;
   p.v = (p.s.tc * p.inv_ma + 1.0f) * 0.5f;
@@ -1558,15 +1570,13 @@ __device__ __forceinline__ CubePx cube_px(const CubeArgs& A, int64_t pix) {
   p.scaled = false;
   p.bscale = 1.0f;
   if (MODE > 0) {
-    const float2* q = reinterpret_cast<const float2*>(A.dir_da + pix * 6);
-    const float2 a = q[0], b = q[1], c = q[2];
     p.dd_in.x[0] = a.x; p.dd_in.y[0] = a.y;
     p.dd_in.x[1] = b.x; p.dd_in.y[1] = b.y;
     p.dd_in.x[2] = c.x; p.dd_in.y[2] = c.y;
     p.dd = p.dd_in;
     p.scaled = A.bias_map != nullptr || A.has_bias;
     if (p.scaled) {
-      p.bscale = bias_scale(A.bias_map, pix, A.scale_bias, A.has_bias != 0);
+      p.bscale = A.bias_map ? (A.has_bias ? exp2f(bm) * A.scale_bias : exp2f(bm)) : A.scale_bias;
 #pragma unroll
       for (int i = 0; i < 3; ++i) {
         p.dd.x[i] = p.dd_in.x[i] * p.bscale;
@@ -1637,11 +1647,11 @@ __device__ __forceinline__ void cube_bwd_px(const CubeArgs& A, int64_t pix, bool
                                             FootAcc<(CT > 0 ? CT : 1)>& acc0,
                                             CubeTable<CT>& tab) {
   const int C = dimC<CT>(A.C);
-  const CubePx p = cube_px<MODE>(A, pix);
   const float* gp = A.d_out + pix * C;
   float g[CT > 0 ? CT : 1];
+  if constexpr (CT > 0) load_texel<CT>(gp, C, g);  // pix is clamped into the image
+  const CubePx p = cube_px<MODE>(A, pix);
   if constexpr (CT > 0) {
-    load_texel<CT>(gp, C, g);  // pix is clamped into the image
 #pragma unroll
     for (int c = 0; c < CT; ++c) g[c] = valid ? g[c] : 0.0f;
   }
