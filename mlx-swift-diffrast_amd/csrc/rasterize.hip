@@ -952,6 +952,11 @@ __global__ void __launch_bounds__(256) k_raster_px(
     // quadrant's box; the survivors are then taken one by one, their
     // records read back from the wave's LDS slots at a uniform address (a
     // broadcast read; cheaper than 17 readlanes and their SGPR hazards).
+    // The next chunk's ids are loaded with this chunk's records: one round
+    // trip a chunk instead of two (4096 x 256^2: 8.55 -> 8.37 ms a step).
+    // Lanes past the count take the list's last id, so every record read
+    // is a candidate's; a lane past nb ignores its record.
+    int next_t = count > 0 ? ids[min(lane, count - 1)] : 0;
     for (int c0 = 0; c0 < count; c0 += kWave) {
       const int nb = min(kWave, count - c0);
       // the quadrant's farthest best depth so far; while a pixel of the
@@ -959,12 +964,12 @@ __global__ void __launch_bounds__(256) k_raster_px(
       const float zq = __int_as_float(wave_reduce_i(
           __float_as_int(valid ? best.z : -1e30f),
           [](int a, int b) { return __float_as_int(fmaxf(__int_as_float(a), __int_as_float(b))); }));
-      int myt = 0;
+      const int myt = next_t;
       TriRec Rl;
       bool hit = false;
+      next_t = ids[min(c0 + kWave + lane, count - 1)];  // in the list: count <= cap
+      Rl = load_rec(rec, rbase + myt);
       if (lane < nb) {
-        myt = ids[c0 + lane];
-        Rl = load_rec(rec, rbase + myt);
         hit = !(__float_as_int(Rl.r3.y) < qx0 || __float_as_int(Rl.r3.x) > qx1 ||
                 __float_as_int(Rl.r3.w) < qy0 || __float_as_int(Rl.r3.z) > qy1);
         if (hit && fabsf(Rl.r2.y) > 1e-30f) {
