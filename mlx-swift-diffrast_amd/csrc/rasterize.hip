@@ -683,17 +683,23 @@ __global__ void __launch_bounds__(kRThreads) k_raster(
     st_nt4(rast + pix * 4, o4);
     if (DB) st_nt4(rast_db + pix * 4, d4);
   };
+  // the peeled layer's depth at both pixels, loaded together (the pixel
+  // index is clamped into the image)
   float peel_z[kRPix];
+  float4 pl[kRPix];
 #pragma unroll
   for (int q = 0; q < kRPix; ++q) {
     int lx, ly;
     bool valid;
     const int64_t pix = pix_of(q, lx, ly, valid);
-    peel_z[q] = -1e30f;
-    if (PEEL && valid) {
-      const float4 pl = *reinterpret_cast<const float4*>(peel + pix * 4);
-      if (pl.w > 0.0f) peel_z[q] = pl.z;
-    }
+    if (PEEL) pl[q] = *reinterpret_cast<const float4*>(peel + pix * 4);
+  }
+#pragma unroll
+  for (int q = 0; q < kRPix; ++q) {
+    int lx, ly;
+    bool valid;
+    pix_of(q, lx, ly, valid);
+    peel_z[q] = PEEL && valid && pl[q].w > 0.0f ? pl[q].z : -1e30f;
   }
 
   if (count > cap) {
@@ -753,6 +759,10 @@ __global__ void __launch_bounds__(kRThreads) k_raster(
   // one round: every candidate's record stays in LDS, and the keys carry
   // its slot (slot_keys: all record indices below 2^25)
   const bool slots = slot_keys && count <= kRChunk;
+  // a round's ids were loaded with the previous round's records (one round
+  // trip a round instead of two); threads past the count take the list's
+  // last id, whose record they do not read
+  int t_cur = ranked ? ids[min(tid, count - 1)] : t_first;
   for (int c0 = 0, round = 0; c0 < count; c0 += kRChunk, ++round) {
     const int nb = min(kRChunk, count - c0);
     __syncthreads();  // s_x / s_y / s_zb set; the previous round's items done
@@ -760,21 +770,24 @@ __global__ void __launch_bounds__(kRThreads) k_raster(
     if (tid == 0) s_total[(round + 1) & 1] = 0;
     // 1) one candidate per thread: record, exact pixel box, work items
     int base = 0, pieces = 0;
+    const int t = t_cur;
+    t_cur = ids[min(c0 + kRChunk + tid, count - 1)];
     if (tid < nb) {
-      const int t = c0 == 0 && !ranked ? t_first : ids[c0 + tid];
       const TriRec R = load_rec(rec, rbase + t);
       // the record's pixel box, clipped to the tile
       const int bx0 = max(__float_as_int(R.r3.x) - x0t, 0);
       const int bx1 = min(__float_as_int(R.r3.y) - x0t, nx - 1);
       const int by0 = max(__float_as_int(R.r3.z) - y0t, 0);
       const int by1 = min(__float_as_int(R.r3.w) - y0t, ny - 1);
+      // stored whatever the box (a slot without work items is not read), so
+      // the record's four rows load together rather than its box row first
+      s_r0[tid] = R.r0;
+      s_r1[tid] = R.r1;
+      s_r2[tid] = R.r2;
+      s_r3[tid] = R.r3;
+      s_t[tid] = t;
       if (bx0 <= bx1 && by0 <= by1) {
         const int bw = bx1 - bx0 + 1, bh = by1 - by0 + 1;
-        s_r0[tid] = R.r0;
-        s_r1[tid] = R.r1;
-        s_r2[tid] = R.r2;
-        s_r3[tid] = R.r3;
-        s_t[tid] = t;
         s_box[tid] = bx0 | (by0 << 4) | ((bw - 1) << 8) | ((bh - 1) << 12);
         pieces = (bw * bh + kRSub - 1) / kRSub;
         base = atomicAdd(&s_total[round & 1], pieces);
