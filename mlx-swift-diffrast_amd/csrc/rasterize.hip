@@ -560,6 +560,44 @@ __device__ __forceinline__ TriRec load_rec(const TriRec* __restrict__ rec, int64
 // list that mode ranks in LDS (longer lists take the ordered full scan).
 constexpr int kMaxPerTileCap = 1024;
 constexpr int kRankMax = 4096;
+// The triangle-parallel kernel's bound: its ranking buffer (4 KiB of LDS,
+// in the capped variant only) also holds the kept ids, so the workgroup
+// stays small enough for full occupancy (a 16 KiB buffer and a separate
+// kept list held 29 KiB: 8 x 1024^2 with the limit 128, rasterize 0.197 ms
+// against 0.106 uncapped).  Longer lists take the ordered full scan.
+constexpr int kRankMaxTri = 1024;
+
+// The `keep` lowest of a tile's `count` distinct candidate ids (keep <
+// count, count at most the buffer's size, a power of two) into s_keep,
+// ascending (s_keep may be s_all): a bitonic sort of the list, padded with
+// INT_MAX to a power of two, in s_all by the whole workgroup;
+// log2(n)(log2(n)+1)/2 compare-exchange stages instead of count^2
+// comparisons.
+__device__ __forceinline__ void keep_lowest(const int* ids, int count, int keep, int* s_all,
+                                            int* s_keep) {
+  int n2 = 2;
+  while (n2 < count) n2 <<= 1;
+  for (int i = (int)threadIdx.x; i < n2; i += (int)blockDim.x)
+    s_all[i] = i < count ? ids[i] : 0x7fffffff;
+  __syncthreads();
+  for (int k = 2; k <= n2; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int i = (int)threadIdx.x; i < n2; i += (int)blockDim.x) {
+        const int l = i ^ j;
+        if (l > i) {
+          const int a = s_all[i], b = s_all[l];
+          if ((a > b) == ((i & k) == 0)) {
+            s_all[i] = b;
+            s_all[l] = a;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+  for (int i = (int)threadIdx.x; i < keep; i += (int)blockDim.x) s_keep[i] = s_all[i];
+  __syncthreads();
+}
 
 // Forward kernel choice: k_raster_px when triangles span at least this many
 // tiles each on average.
@@ -617,8 +655,7 @@ __global__ void __launch_bounds__(kRThreads) k_raster(
   __shared__ unsigned long long s_zb[256];   // per tile pixel: smallest zkey, ~0 = none
   __shared__ float s_x[16], s_y[16];         // pixel-centre x of tile columns, y of rows
   __shared__ float s_pz[PEEL ? 256 : 1];     // depth of the peeled layer (-1e30 = none)
-  __shared__ int s_keep[CAPPED ? kMaxPerTileCap : 1];
-  __shared__ int s_all[CAPPED ? kRankMax : 1];
+  __shared__ int s_all[CAPPED ? kRankMaxTri : 1];  // ranking buffer, then the kept ids
   __shared__ int s_total[2];                 // work items of the round, by round parity
   const int tiles = ntx * nty;
   const int B = tiles * N;
@@ -636,19 +673,11 @@ __global__ void __launch_bounds__(kRThreads) k_raster(
   bool ranked = false;
   int scan_limit = 0x7fffffff;  // full scan: stop after this many tile candidates
   if (CAPPED && count > max_per_tile) {  // uniform over the workgroup
-    if (count <= cap && count <= kRankMax) {
-      // rank every id of the complete list (ids of one tile are distinct);
-      // the max_per_tile lowest land in s_keep in ascending order
-      for (int i = tid; i < count; i += blockDim.x) s_all[i] = ids[i];
-      __syncthreads();
-      for (int i = tid; i < count; i += blockDim.x) {
-        const int v = s_all[i];
-        int r = 0;
-        for (int k = 0; k < count; ++k) r += s_all[k] < v;
-        if (r < max_per_tile) s_keep[r] = v;
-      }
-      __syncthreads();
-      ids = s_keep;
+    if (count <= cap && count <= kRankMaxTri) {
+      // the max_per_tile lowest ids of the complete list, ascending, in
+      // place at the front of s_all
+      keep_lowest(ids, count, max_per_tile, s_all, s_all);
+      ids = s_all;
       count = max_per_tile;
       ranked = true;
     } else {
@@ -902,6 +931,7 @@ __global__ void __launch_bounds__(256) k_raster_px(
   __shared__ TriRec s_rec[4][kWave];
   __shared__ int s_t[4][kWave];
   __shared__ int s_keep[CAPPED ? kMaxPerTileCap : 1];
+  static_assert(sizeof(s_rec) >= kRankMax * sizeof(int), "the ranking's buffer");
   const int tiles = ntx * nty;
   const int B = tiles * N;
   const int b = xcd_remap((int)blockIdx.x, B);
@@ -916,18 +946,9 @@ __global__ void __launch_bounds__(256) k_raster_px(
   int scan_limit = 0x7fffffff;  // full scan: stop after this many tile candidates
   if (CAPPED && count > max_per_tile) {  // uniform over the workgroup
     if (count <= cap && count <= kRankMax) {
-      // rank every id of the complete list (ids of one tile are distinct);
-      // the max_per_tile lowest land in s_keep in ascending order
-      int* s_all = reinterpret_cast<int*>(&s_rec[0][0]);  // kRankMax ints
-      for (int i = threadIdx.x; i < count; i += blockDim.x) s_all[i] = ids[i];
-      __syncthreads();
-      for (int i = threadIdx.x; i < count; i += blockDim.x) {
-        const int v = s_all[i];
-        int r = 0;
-        for (int k = 0; k < count; ++k) r += s_all[k] < v;
-        if (r < max_per_tile) s_keep[r] = v;
-      }
-      __syncthreads();  // s_all (the record slots) is free again after this
+      // the max_per_tile lowest ids of the complete list, ascending (the
+      // record slots serve as the sort's buffer, free again after it)
+      keep_lowest(ids, count, max_per_tile, reinterpret_cast<int*>(&s_rec[0][0]), s_keep);
       ids = s_keep;
       count = max_per_tile;
     } else {
