@@ -316,6 +316,16 @@ def test_capped_tile_overflow():
         r = check_capped(p[None], tri, 32, 32, cap)
         assert (r[..., 3] == min(cap, T)).all(), cap
         torch.cuda.synchronize()
+    # 1,500 per tile: above the triangle-parallel kernel's 1,024-id sort, so
+    # even a complete list takes the ordered scan that stops at the cap
+    T2 = 1500
+    p2 = np.tile(np.array([[-3, 3, 0, 1], [-3, -3, 0, 1], [3, 0, 0, 1]], np.float32), (T2, 1))
+    p2[:, 2] = np.repeat(np.linspace(0.9, -0.9, T2), 3)
+    tri2 = np.arange(3 * T2, dtype=np.int32).reshape(T2, 3)
+    for cap in (128, 128, 1024):
+        r = check_capped(p2[None], tri2, 32, 32, cap)
+        assert (r[..., 3] == cap).all(), cap
+        torch.cuda.synchronize()
     # range mode: image 1 draws triangles [100, 300) and keeps [100, 228)
     ranges = np.array([[0, 300], [100, 200], [250, 10]], np.int32)
     r = check_capped(p, tri, 32, 32, 128, ranges=ranges)
