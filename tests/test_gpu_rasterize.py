@@ -301,7 +301,8 @@ def test_capped_tile_overflow():
     """300 full-screen triangles per tile, nearest last: with a per-tile cap
     every pixel shows the cap's last triangle.  The first call after a
     sparse scene has list capacity below 300 (ordered full scan stopping at
-    the cap); later calls rank the complete list in LDS."""
+    the cap); later calls sort the complete list in LDS or, above 1,024
+    ids, take the same ordered scan."""
     torch = torch_dev()
     from diffrast import _lib
     torch.cuda.synchronize()
